@@ -1,0 +1,75 @@
+"""Builds lib/libcheddar_amd.so (HIP kernels for gfx950 + C++ host + C-ABI).
+
+Usage: python cheddar-fhe_amd/build.py [--jobs N]
+Compiles every source each time it is called (hipcc, no cache).
+"""
+import argparse
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+OUT_DIR = os.path.join(PKG, "lib")
+OBJ_DIR = os.path.join(PKG, "_build")
+LIB = os.path.join(OUT_DIR, "libcheddar_amd.so")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+COMMON = [
+    "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-result",
+    "-I" + os.path.join(ROOT, "include"),
+    "-I" + os.path.join(PKG, "csrc"),
+    "-I" + os.path.join(PKG, "host"),
+]
+# device code: gfx950 only, packed-fp32 instruction selection disabled
+DEVICE = ["-x", "hip", "--offload-arch=" + ARCH,
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+SOURCES = [
+    ("csrc/ntt.hip", True),
+    ("csrc/bconv.hip", True),
+    ("csrc/elementwise.hip", True),
+    ("host/device_tables.cpp", False),
+    ("host/cheddar.cpp", False),
+    ("host/capi.cpp", False),
+]
+
+
+def compile_one(rel, device):
+    src = os.path.join(PKG, rel)
+    obj = os.path.join(OBJ_DIR, rel.replace("/", "_") + ".o")
+    if device:
+        cmd = [HIPCC] + COMMON + DEVICE + ["-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC] + COMMON + ["-D__HIP_PLATFORM_AMD__", "-c", src, "-o",
+                                  obj]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("compile failed: %s\n%s\n%s" %
+                           (" ".join(cmd), res.stdout, res.stderr))
+    return obj
+
+
+def build(jobs=8):
+    os.makedirs(OUT_DIR, exist_ok=True)
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: compile_one(*s), SOURCES))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, "-shared", "--offload-arch=" + ARCH, "-o", tmp] + objs
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("link failed: %s\n%s" % (res.stdout, res.stderr))
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=8)
+    a = ap.parse_args()
+    print(build(a.jobs))
+    sys.exit(0)

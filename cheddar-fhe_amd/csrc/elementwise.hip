@@ -1,0 +1,287 @@
+// Element-wise kernels of the key-switch path (HBM-bound): Tensor,
+// CPAccum/CPAccumAdd (the evaluation-key inner product), Permute.
+//
+// One thread owns 4 consecutive coefficients of one limb (128-bit loads and
+// stores); grid (N / 1024, limbs). Arithmetic is the reference's signed
+// Montgomery product MontMul(a, b) = a b 2^-32 mod q, canonical outputs.
+#include "chd_device.h"
+#include "cheddar_kernels.h"
+#include "kernel_common.h"
+
+namespace chd {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kPerThread = 4;
+constexpr int kCoefPerBlock = kThreads * kPerThread;
+
+struct LimbIdx {
+  int l;
+  bool aux;
+  uint32_t q;
+  int32_t qinv;
+};
+
+__device__ __forceinline__ LimbIdx limb_of(const chd_tables &t,
+                                           const chd_limb_map &m) {
+  LimbIdx r;
+  r.l = blockIdx.y + (static_cast<int>(blockIdx.y) >= m.skip_lo ? m.skip_len : 0);
+  r.aux = r.l >= m.num_q;
+  int ti = m.tab_off + r.l + (r.aux ? m.tab_gap : 0);
+  r.q = t.q[ti];
+  r.qinv = t.qinv[ti];
+  return r;
+}
+
+__device__ __forceinline__ uint4 ld4(const uint32_t *p) {
+  return *reinterpret_cast<const uint4 *>(p);
+}
+__device__ __forceinline__ void st4(uint32_t *p, uint4 v) {
+  *reinterpret_cast<uint4 *>(p) = v;
+}
+__device__ __forceinline__ uint32_t get(const uint4 &v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Tensor (ElementWise.cu:504-546)
+__global__ __launch_bounds__(kThreads) void tensor_kernel(
+    chd_tables t, chd_limb_map m, uint32_t *bx, uint32_t *ax, uint32_t *rx,
+    const uint32_t *b1, const uint32_t *a1, const uint32_t *b2,
+    const uint32_t *a2) {
+  LimbIdx li = limb_of(t, m);
+  size_t o = (static_cast<size_t>(li.l) << kLogN) +
+             blockIdx.x * kCoefPerBlock + threadIdx.x * kPerThread;
+  size_t si = o + (li.aux ? static_cast<size_t>(m.src_gap) << kLogN : 0);
+  uint4 vb1 = ld4(b1 + si), va1 = ld4(a1 + si);
+  uint4 vb2 = ld4(b2 + si), va2 = ld4(a2 + si);
+  uint32_t ob[4], oa[4], orr[4];
+  const int32_t q = static_cast<int32_t>(li.q);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int32_t x1 = get(vb1, i), y1 = get(va1, i);
+    int32_t x2 = get(vb2, i), y2 = get(va2, i);
+    int32_t s1 = (x1 - q) + y1;  // [-q, q-2]
+    int32_t s2 = (x2 - q) + y2;
+    uint32_t mid = mont_mul(s1, s2, li.q, li.qinv);
+    uint32_t bb = mont_mul(x1, x2, li.q, li.qinv);
+    uint32_t aa = mont_mul(y1, y2, li.q, li.qinv);
+    mid = sub_mod(mid, bb, li.q);
+    mid = sub_mod(mid, aa, li.q);
+    ob[i] = bb;
+    oa[i] = mid;
+    orr[i] = aa;
+  }
+  st4(bx + o, make_uint4(ob[0], ob[1], ob[2], ob[3]));
+  st4(ax + o, make_uint4(oa[0], oa[1], oa[2], oa[3]));
+  st4(rx + o, make_uint4(orr[0], orr[1], orr[2], orr[3]));
+}
+
+// TensorSquare (ElementWise.cu:549-575)
+__global__ __launch_bounds__(kThreads) void tensor_square_kernel(
+    chd_tables t, chd_limb_map m, uint32_t *bx, uint32_t *ax, uint32_t *rx,
+    const uint32_t *b1, const uint32_t *a1) {
+  LimbIdx li = limb_of(t, m);
+  size_t o = (static_cast<size_t>(li.l) << kLogN) +
+             blockIdx.x * kCoefPerBlock + threadIdx.x * kPerThread;
+  size_t si = o + (li.aux ? static_cast<size_t>(m.src_gap) << kLogN : 0);
+  uint4 vb = ld4(b1 + si), va = ld4(a1 + si);
+  uint32_t ob[4], oa[4], orr[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int32_t x = get(vb, i), y = get(va, i);
+    ob[i] = mont_mul(x, x, li.q, li.qinv);
+    uint32_t xy = mont_mul(x, y, li.q, li.qinv);
+    oa[i] = add_mod(xy, xy, li.q);
+    orr[i] = mont_mul(y, y, li.q, li.qinv);
+  }
+  st4(bx + o, make_uint4(ob[0], ob[1], ob[2], ob[3]));
+  st4(ax + o, make_uint4(oa[0], oa[1], oa[2], oa[3]));
+  st4(rx + o, make_uint4(orr[0], orr[1], orr[2], orr[3]));
+}
+
+struct AccumArgs {
+  uint32_t *dst[CHD_MAX_POLY];
+  const uint32_t *src0[CHD_MAX_POLY];
+  long long src0_gap;
+  chd_accum_src s[CHD_MAX_ACCUM];
+};
+
+// CPAccum / CPAccumAdd (ElementWise.cu:225-366)
+template <int kPoly, bool kConst, bool kHasSrc0>
+__global__ __launch_bounds__(kThreads) void cpaccum_kernel(chd_tables t,
+                                                           chd_limb_map m,
+                                                           AccumArgs a,
+                                                           int num_accum) {
+  LimbIdx li = limb_of(t, m);
+  const int c0 = blockIdx.x * kCoefPerBlock + threadIdx.x * kPerThread;
+  const size_t o = (static_cast<size_t>(li.l) << kLogN) + c0;
+  uint32_t acc[kPoly][4];
+#pragma unroll
+  for (int p = 0; p < kPoly; p++) {
+    if constexpr (kHasSrc0) {
+      uint4 v = ld4(a.src0[p] + o + (li.aux ? a.src0_gap : 0));
+      acc[p][0] = v.x;
+      acc[p][1] = v.y;
+      acc[p][2] = v.z;
+      acc[p][3] = v.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[p][i] = 0;
+    }
+  }
+  for (int j = 0; j < num_accum; j++) {
+    const chd_accum_src &s = a.s[j];
+    const size_t so = o + (li.aux ? s.src_gap : 0);
+    uint32_t cm[4];
+    if constexpr (kConst) {
+      uint32_t cv = s.common[li.l + (li.aux ? s.common_gap : 0)];
+#pragma unroll
+      for (int i = 0; i < 4; i++) cm[i] = cv;
+    } else {
+      uint4 cv = ld4(s.common + o + (li.aux ? s.common_gap : 0));
+      cm[0] = cv.x;
+      cm[1] = cv.y;
+      cm[2] = cv.z;
+      cm[3] = cv.w;
+    }
+#pragma unroll
+    for (int p = 0; p < kPoly; p++) {
+      uint4 v = ld4(s.src[p] + so);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        uint32_t mm = mont_mul(static_cast<int32_t>(cm[i]),
+                               static_cast<int32_t>(get(v, i)), li.q, li.qinv);
+        acc[p][i] = add_mod(acc[p][i], mm, li.q);
+      }
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < kPoly; p++)
+    st4(a.dst[p] + o, make_uint4(acc[p][0], acc[p][1], acc[p][2], acc[p][3]));
+}
+
+struct PermArgs {
+  uint32_t *dst[CHD_MAX_POLY];
+  const uint32_t *src[CHD_MAX_POLY];
+};
+
+// Permute (ElementWise.cu:370-391)
+template <int kPoly>
+__global__ __launch_bounds__(kThreads) void permute_kernel(chd_limb_map m,
+                                                           PermArgs a,
+                                                           uint32_t galois) {
+  const int l = blockIdx.y;
+  const bool aux = l >= m.num_q;
+  const size_t base = static_cast<size_t>(l) << kLogN;
+  const size_t sbase = base + (aux ? static_cast<size_t>(m.src_gap) << kLogN : 0);
+  const int c0 = blockIdx.x * kCoefPerBlock + threadIdx.x * kPerThread;
+  uint32_t idx[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    uint32_t x = c0 + i;
+    uint32_t e = (__brev(x) >> (32 - (kLogN + 1))) + 1;
+    idx[i] = __brev(e * galois - 1) >> (32 - (kLogN + 1));
+  }
+#pragma unroll
+  for (int p = 0; p < kPoly; p++) {
+    const uint32_t *s = a.src[p] + sbase;
+    st4(a.dst[p] + base + c0,
+        make_uint4(s[idx[0]], s[idx[1]], s[idx[2]], s[idx[3]]));
+  }
+}
+
+}  // namespace
+}  // namespace chd
+
+using namespace chd;
+
+extern "C" int chd_k_tensor(const chd_tables *t, const chd_limb_map *m,
+                            uint32_t *bx, uint32_t *ax, uint32_t *rx,
+                            const uint32_t *b1, const uint32_t *a1,
+                            const uint32_t *b2, const uint32_t *a2,
+                            int num_limbs, void *stream) {
+  if (!t || !m || !bx || !ax || !rx || !b1 || !a1 || !b2 || !a2 ||
+      num_limbs < 0)
+    return set_error(CHD_ERR_ARG, "chd_k_tensor: invalid argument");
+  if (num_limbs == 0) return 0;
+  dim3 g(kN / kCoefPerBlock, num_limbs);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (b1 == b2 && a1 == a2)
+    hipLaunchKernelGGL(tensor_square_kernel, g, dim3(kThreads), 0, s, *t, *m,
+                       bx, ax, rx, b1, a1);
+  else
+    hipLaunchKernelGGL(tensor_kernel, g, dim3(kThreads), 0, s, *t, *m, bx, ax,
+                       rx, b1, a1, b2, a2);
+  return check_launch("chd_k_tensor");
+}
+
+extern "C" int chd_k_cpaccum(const chd_tables *t, const chd_limb_map *m,
+                             uint32_t *const *dst, int num_polys,
+                             const uint32_t *const *src0, long long src0_gap,
+                             const chd_accum_src *srcs, int num_accum,
+                             int const_accum, int num_limbs, void *stream) {
+  if (!t || !m || !dst || !srcs || num_polys < 1 ||
+      num_polys > CHD_MAX_POLY || num_accum < 1 || num_accum > CHD_MAX_ACCUM ||
+      num_limbs < 0)
+    return set_error(CHD_ERR_ARG, "chd_k_cpaccum: invalid argument");
+  if (num_limbs == 0) return 0;
+  AccumArgs a{};
+  for (int p = 0; p < num_polys; p++) {
+    a.dst[p] = dst[p];
+    a.src0[p] = src0 ? src0[p] : nullptr;
+  }
+  a.src0_gap = src0_gap;
+  for (int j = 0; j < num_accum; j++) a.s[j] = srcs[j];
+  dim3 g(kN / kCoefPerBlock, num_limbs);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  bool has0 = src0 != nullptr;
+#define CHD_ACCUM_LAUNCH(P, C, S0)                                          \
+  hipLaunchKernelGGL((cpaccum_kernel<P, C, S0>), g, dim3(kThreads), 0, s, \
+                     *t, *m, a, num_accum)
+#define CHD_ACCUM_POLY(P)                         \
+  if (const_accum) {                              \
+    if (has0) CHD_ACCUM_LAUNCH(P, true, true);    \
+    else CHD_ACCUM_LAUNCH(P, true, false);        \
+  } else {                                        \
+    if (has0) CHD_ACCUM_LAUNCH(P, false, true);   \
+    else CHD_ACCUM_LAUNCH(P, false, false);       \
+  }
+  if (num_polys == 1) {
+    CHD_ACCUM_POLY(1)
+  } else if (num_polys == 2) {
+    CHD_ACCUM_POLY(2)
+  } else {
+    CHD_ACCUM_POLY(3)
+  }
+#undef CHD_ACCUM_POLY
+#undef CHD_ACCUM_LAUNCH
+  return check_launch("chd_k_cpaccum");
+}
+
+extern "C" int chd_k_permute(const chd_limb_map *m, uint32_t *const *dst,
+                             const uint32_t *const *src, int num_polys,
+                             int num_limbs, uint32_t galois, void *stream) {
+  if (!m || !dst || !src || num_polys < 1 || num_polys > CHD_MAX_POLY ||
+      num_limbs < 0 || (galois & 1u) == 0)
+    return set_error(CHD_ERR_ARG, "chd_k_permute: invalid argument");
+  if (num_limbs == 0) return 0;
+  PermArgs a{};
+  for (int p = 0; p < num_polys; p++) {
+    if (dst[p] == src[p])
+      return set_error(CHD_ERR_ARG, "chd_k_permute: in-place not supported");
+    a.dst[p] = dst[p];
+    a.src[p] = src[p];
+  }
+  dim3 g(kN / kCoefPerBlock, num_limbs);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (num_polys == 1)
+    hipLaunchKernelGGL(permute_kernel<1>, g, dim3(kThreads), 0, s, *m, a,
+                       galois);
+  else if (num_polys == 2)
+    hipLaunchKernelGGL(permute_kernel<2>, g, dim3(kThreads), 0, s, *m, a,
+                       galois);
+  else
+    hipLaunchKernelGGL(permute_kernel<3>, g, dim3(kThreads), 0, s, *m, a,
+                       galois);
+  return check_launch("chd_k_permute");
+}

@@ -1,0 +1,425 @@
+// Public C-ABI (include/cheddar_amd.h) over the C++ host classes, plus the
+// error plumbing shared with the kernel-level ABI.
+#include <climits>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "cheddar.h"
+#include "cheddar_amd.h"
+#include "kernel_common.h"
+#include "prime_math.h"
+
+namespace {
+thread_local std::string g_err;
+}
+
+namespace chd {
+int set_error(int code, const std::string &msg) {
+  g_err = msg;
+  return code;
+}
+int check_launch(const char *where) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(CHD_ERR_HIP, std::string(where) + ": " +
+                                      hipGetErrorString(e));
+  return 0;
+}
+}  // namespace chd
+
+using cheddar::Context;
+using cheddar::Parameter;
+using chd::set_error;
+using word = uint32_t;
+
+struct chd_ntt_plan {
+  std::unique_ptr<cheddar::ChainTables> chain;
+};
+
+struct chd_bconv_plan {
+  std::unique_ptr<cheddar::ChainTables> dst_chain;
+  std::vector<word> const1;
+  std::vector<int32_t> const2;
+  cheddar::DevBuf table;
+  int src_len = 0, dst_len = 0;
+};
+
+struct chd_param {
+  std::unique_ptr<Parameter<word>> p;
+};
+
+struct chd_context {
+  std::shared_ptr<Context<word>> c;
+};
+
+#define CHD_TRY try {
+#define CHD_CATCH(name)                                            \
+  }                                                                \
+  catch (const std::exception &e) {                                \
+    return set_error(CHD_ERR_STATE, std::string(name ": ") + e.what()); \
+  }
+
+extern "C" const char *chd_last_error(void) { return g_err.c_str(); }
+extern "C" const char *chd_version(void) { return "cheddar-amd 0.1 gfx950"; }
+
+// ------------------------------------------------------------ NTT plans --
+extern "C" int chd_ntt_plan_create(chd_ntt_plan **out, int log_degree,
+                                   const uint32_t *primes, int num_primes) {
+  if (!out || !primes || num_primes < 1)
+    return set_error(CHD_ERR_ARG, "chd_ntt_plan_create: invalid argument");
+  CHD_TRY
+  auto plan = std::make_unique<chd_ntt_plan>();
+  plan->chain = std::make_unique<cheddar::ChainTables>(
+      log_degree, std::vector<word>(primes, primes + num_primes));
+  *out = plan.release();
+  return 0;
+  CHD_CATCH("chd_ntt_plan_create")
+}
+
+extern "C" void chd_ntt_plan_destroy(chd_ntt_plan *plan) { delete plan; }
+
+extern "C" const void *chd_ntt_plan_tables(const chd_ntt_plan *plan) {
+  return plan ? &plan->chain->tables() : nullptr;
+}
+
+static chd_limb_map PlainMap(int num_limbs) {
+  chd_limb_map m{};
+  m.num_q = num_limbs;
+  m.skip_lo = INT_MAX;
+  return m;
+}
+
+extern "C" int chd_ntt_forward(const chd_ntt_plan *plan, uint32_t *dst,
+                               const uint32_t *src, int num_limbs,
+                               int num_polys, int mont_conv, void *stream) {
+  if (!plan || !dst || !src || num_limbs < 1 ||
+      num_limbs > plan->chain->size() || num_polys < 1)
+    return set_error(CHD_ERR_ARG, "chd_ntt_forward: invalid argument");
+  chd_limb_map m = PlainMap(num_limbs);
+  const long long ps = static_cast<long long>(num_limbs) << 16;
+  return chd_k_ntt_fwd(&plan->chain->tables(), &m, dst, ps, src, ps,
+                       num_limbs, num_polys,
+                       mont_conv ? plan->chain->mont_converter() : nullptr,
+                       stream);
+}
+
+extern "C" int chd_ntt_inverse(const chd_ntt_plan *plan, uint32_t *dst,
+                               const uint32_t *src, int num_limbs,
+                               int num_polys, int mont_conv, void *stream) {
+  if (!plan || !dst || !src || num_limbs < 1 ||
+      num_limbs > plan->chain->size() || num_polys < 1)
+    return set_error(CHD_ERR_ARG, "chd_ntt_inverse: invalid argument");
+  chd_limb_map m = PlainMap(num_limbs);
+  const long long ps = static_cast<long long>(num_limbs) << 16;
+  return chd_k_ntt_inv(&plan->chain->tables(), &m, dst, ps, src, ps,
+                       num_limbs, num_polys,
+                       mont_conv ? plan->chain->inv_degree()
+                                 : plan->chain->inv_degree_mont(),
+                       0, stream);
+}
+
+// ---------------------------------------------------------- BConv plans --
+extern "C" int chd_bconv_plan_create(chd_bconv_plan **out, int log_degree,
+                                     const uint32_t *src_primes, int src_len,
+                                     const uint32_t *dst_primes,
+                                     int dst_len) {
+  if (!out || !src_primes || !dst_primes || src_len < 1 || src_len > 16 ||
+      dst_len < 1)
+    return set_error(CHD_ERR_ARG, "chd_bconv_plan_create: invalid argument");
+  CHD_TRY
+  namespace pm = cheddar::pm;
+  auto plan = std::make_unique<chd_bconv_plan>();
+  std::vector<word> src(src_primes, src_primes + src_len);
+  std::vector<word> dst(dst_primes, dst_primes + dst_len);
+  plan->dst_chain = std::make_unique<cheddar::ChainTables>(log_degree, dst);
+  plan->src_len = src_len;
+  plan->dst_len = dst_len;
+  plan->const1.assign(src_len, 1);
+  plan->const2.assign(static_cast<size_t>(src_len) * dst_len, 0);
+  const word n = 1u << log_degree;
+  // PopulateModSwitchConstants (src/core/ModSwitch.cu:320-370)
+  for (int i = 0; i < src_len; i++) {
+    word v = 1;
+    for (int j = 0; j < src_len; j++)
+      if (j != i) v = pm::mulmod(v, src[j], src[i]);
+    plan->const1[i] = pm::invmod(pm::mulmod(v, n, src[i]), src[i]);
+  }
+  for (int k = 0; k < dst_len; k++)
+    for (int i = 0; i < src_len; i++) {
+      word acc = 1;
+      for (int j = 0; j < src_len; j++)
+        if (j != i) acc = pm::mulmod(acc, src[j], dst[k]);
+      acc = pm::to_mont(pm::to_mont(acc, dst[k]), dst[k]);
+      plan->const2[static_cast<size_t>(k) * src_len + i] =
+          pm::normalize(acc, dst[k]);
+    }
+  std::vector<unsigned char> packed(
+      static_cast<size_t>(chd_bconv_table_size(src_len, dst_len)));
+  int st = chd_bconv_table_pack(packed.data(), plan->const2.data(), dst.data(),
+                                src_len, dst_len);
+  if (st != 0) return st;
+  plan->table.Resize(packed.size());
+  plan->table.Upload(packed.data(), packed.size());
+  *out = plan.release();
+  return 0;
+  CHD_CATCH("chd_bconv_plan_create")
+}
+
+extern "C" void chd_bconv_plan_destroy(chd_bconv_plan *plan) { delete plan; }
+
+extern "C" int chd_bconv_plan_constants(const chd_bconv_plan *plan,
+                                        uint32_t *const1, int32_t *const2) {
+  if (!plan) return set_error(CHD_ERR_ARG, "chd_bconv_plan_constants");
+  if (const1)
+    std::memcpy(const1, plan->const1.data(), plan->const1.size() * 4);
+  if (const2)
+    std::memcpy(const2, plan->const2.data(), plan->const2.size() * 4);
+  return 0;
+}
+
+extern "C" int chd_bconv_apply(const chd_bconv_plan *plan, uint32_t *dst,
+                               const int32_t *src, void *stream) {
+  if (!plan || !dst || !src)
+    return set_error(CHD_ERR_ARG, "chd_bconv_apply: invalid argument");
+  chd_limb_map m = PlainMap(plan->dst_len);
+  return chd_k_bconv(&plan->dst_chain->tables(), &m, dst, src, plan->src_len,
+                     plan->dst_len, plan->table.as<void>(), stream);
+}
+
+// ---------------------------------------------------- Parameter/Context --
+extern "C" int chd_param_create(chd_param **out, int log_degree,
+                                double base_scale,
+                                int default_encryption_level,
+                                const int *level_config, int num_levels,
+                                const uint32_t *main_primes, int num_main,
+                                const uint32_t *aux_primes, int num_aux,
+                                const uint32_t *ter_primes, int num_ter) {
+  if (!out || !level_config || num_levels < 1 || !main_primes ||
+      num_main < 1 || !aux_primes || num_aux < 1 || num_ter < 0 ||
+      (num_ter > 0 && !ter_primes))
+    return set_error(CHD_ERR_ARG, "chd_param_create: invalid argument");
+  CHD_TRY
+  std::vector<std::pair<int, int>> lc;
+  for (int i = 0; i < num_levels; i++)
+    lc.emplace_back(level_config[2 * i], level_config[2 * i + 1]);
+  auto p = std::make_unique<chd_param>();
+  p->p = std::make_unique<Parameter<word>>(
+      log_degree, base_scale, default_encryption_level, lc,
+      std::vector<word>(main_primes, main_primes + num_main),
+      std::vector<word>(aux_primes, aux_primes + num_aux),
+      std::vector<word>(ter_primes, ter_primes + num_ter));
+  *out = p.release();
+  return 0;
+  CHD_CATCH("chd_param_create")
+}
+
+extern "C" void chd_param_destroy(chd_param *param) { delete param; }
+
+extern "C" int chd_param_num_q(const chd_param *param, int level) {
+  if (!param || level < 0 || level > param->p->max_level_) return -1;
+  return param->p->LevelToNP(level).GetNumQ();
+}
+
+extern "C" int chd_param_alpha(const chd_param *param) {
+  return param ? param->p->alpha_ : -1;
+}
+
+extern "C" int chd_param_max_level(const chd_param *param) {
+  return param ? param->p->max_level_ : -1;
+}
+
+extern "C" int chd_param_evk_limbs(const chd_param *param) {
+  if (!param) return -1;
+  return param->p->GetMaxNumMain() + param->p->GetMaxNumTer() +
+         param->p->alpha_;
+}
+
+extern "C" int chd_context_create(chd_context **out, const chd_param *param) {
+  if (!out || !param)
+    return set_error(CHD_ERR_ARG, "chd_context_create: invalid argument");
+  CHD_TRY
+  auto c = std::make_unique<chd_context>();
+  c->c = Context<word>::Create(*param->p);
+  *out = c.release();
+  return 0;
+  CHD_CATCH("chd_context_create")
+}
+
+extern "C" void chd_context_destroy(chd_context *ctx) { delete ctx; }
+
+extern "C" int chd_context_beta(const chd_context *ctx, int level) {
+  if (!ctx || level < 0 || level > ctx->c->param_.max_level_) return -1;
+  return ctx->c->mod_switch_handlers_.at(level).GetBeta();
+}
+
+namespace {
+bool LevelOk(const chd_context *ctx, int level) {
+  return ctx && level >= 0 && level <= ctx->c->param_.max_level_;
+}
+
+Context<word>::EvkRef MakeEvk(const chd_context *ctx,
+                              const uint32_t *const *bx,
+                              const uint32_t *const *ax, int beta) {
+  const auto &p = ctx->c->param_;
+  Context<word>::EvkRef r;
+  r.np = cheddar::NPInfo(p.GetMaxNumMain(), p.GetMaxNumTer(), p.alpha_);
+  for (int g = 0; g < beta; g++) {
+    if (!bx[g] || !ax[g]) throw cheddar::Error("null evaluation-key pointer");
+    r.bx.push_back(bx[g]);
+    r.ax.push_back(ax[g]);
+  }
+  return r;
+}
+}  // namespace
+
+#define CHD_CALL(name, cond, ...)                                       \
+  if (!(cond)) return set_error(CHD_ERR_ARG, name ": invalid argument"); \
+  CHD_TRY cheddar::StreamScope scope(static_cast<hipStream_t>(stream));  \
+  __VA_ARGS__;                                                          \
+  return chd::check_launch(name);                                       \
+  CHD_CATCH(name)
+
+extern "C" int chd_tensor(const chd_context *ctx, int level, uint32_t *res_bx,
+                          uint32_t *res_ax, uint32_t *res_rx,
+                          const uint32_t *a_bx, const uint32_t *a_ax,
+                          const uint32_t *b_bx, const uint32_t *b_ax,
+                          void *stream) {
+  CHD_CALL("chd_tensor",
+           LevelOk(ctx, level) && res_bx && res_ax && res_rx && a_bx && a_ax &&
+               b_bx && b_ax,
+           ctx->c->TensorV(level, {res_bx, res_ax, res_rx}, {a_bx, a_ax, nullptr},
+                           {b_bx, b_ax, nullptr}))
+}
+
+extern "C" int chd_mod_up(const chd_context *ctx, int level,
+                          uint32_t *const *dst, const uint32_t *src,
+                          void *stream) {
+  CHD_CALL("chd_mod_up", LevelOk(ctx, level) && dst && src, {
+    const auto &p = ctx->c->param_;
+    const int n = p.degree_, nq = p.LevelToNP(level).GetNumQ();
+    const auto &ms = ctx->c->mod_switch_handlers_.at(level);
+    std::vector<cheddar::DvView<word>> v;
+    for (int g = 0; g < ms.GetBeta(); g++) {
+      if (!dst[g]) throw cheddar::Error("null ModUp destination");
+      v.emplace_back(dst[g], (nq + p.alpha_) * n, p.alpha_ * n);
+    }
+    ms.ModUp(v, cheddar::DvConstView<word>(src, nq * n, 0));
+  })
+}
+
+extern "C" int chd_mod_down(const chd_context *ctx, int level, uint32_t *dst,
+                            const uint32_t *src, void *stream) {
+  CHD_CALL("chd_mod_down", LevelOk(ctx, level) && dst && src, {
+    const auto &p = ctx->c->param_;
+    const int n = p.degree_, nq = p.LevelToNP(level).GetNumQ();
+    cheddar::DvView<word> d(dst, nq * n, 0);
+    ctx->c->mod_switch_handlers_.at(level).ModDown(
+        d, cheddar::DvConstView<word>(src, (nq + p.alpha_) * n, p.alpha_ * n));
+  })
+}
+
+extern "C" int chd_rescale_poly(const chd_context *ctx, int level,
+                                uint32_t *dst, const uint32_t *src,
+                                void *stream) {
+  CHD_CALL("chd_rescale_poly", LevelOk(ctx, level) && level > 0 && dst && src, {
+    const auto &p = ctx->c->param_;
+    const int n = p.degree_, nq = p.LevelToNP(level).GetNumQ();
+    const int nq1 = p.LevelToNP(level - 1).GetNumQ();
+    cheddar::DvView<word> d(dst, nq1 * n, 0);
+    ctx->c->mod_switch_handlers_.at(level).Rescale(
+        d, cheddar::DvConstView<word>(src, nq * n, 0));
+  })
+}
+
+extern "C" int chd_mod_down_and_rescale(const chd_context *ctx, int level,
+                                        uint32_t *dst, const uint32_t *src,
+                                        void *stream) {
+  CHD_CALL("chd_mod_down_and_rescale",
+           LevelOk(ctx, level) && level > 0 && dst && src, {
+             const auto &p = ctx->c->param_;
+             const int n = p.degree_, nq = p.LevelToNP(level).GetNumQ();
+             const int nq1 = p.LevelToNP(level - 1).GetNumQ();
+             cheddar::DvView<word> d(dst, nq1 * n, 0);
+             ctx->c->mod_switch_handlers_.at(level).ModDownAndRescale(
+                 d, cheddar::DvConstView<word>(src, (nq + p.alpha_) * n,
+                                               p.alpha_ * n));
+           })
+}
+
+extern "C" int chd_hmult(const chd_context *ctx, int level, uint32_t *res_bx,
+                         uint32_t *res_ax, const uint32_t *a_bx,
+                         const uint32_t *a_ax, const uint32_t *b_bx,
+                         const uint32_t *b_ax, const uint32_t *const *evk_bx,
+                         const uint32_t *const *evk_ax, int evk_beta,
+                         int rescale, void *stream) {
+  CHD_CALL("chd_hmult",
+           LevelOk(ctx, level) && (!rescale || level > 0) && res_bx &&
+               res_ax && a_bx && a_ax && b_bx && b_ax && evk_bx && evk_ax &&
+               evk_beta > 0,
+           ctx->c->HMultV(level, {res_bx, res_ax, nullptr},
+                          {a_bx, a_ax, nullptr}, {b_bx, b_ax, nullptr},
+                          MakeEvk(ctx, evk_bx, evk_ax, evk_beta),
+                          rescale != 0))
+}
+
+extern "C" int chd_rescale(const chd_context *ctx, int level, uint32_t *res_bx,
+                           uint32_t *res_ax, const uint32_t *a_bx,
+                           const uint32_t *a_ax, void *stream) {
+  CHD_CALL("chd_rescale",
+           LevelOk(ctx, level) && level > 0 && res_bx && res_ax && a_bx &&
+               a_ax && res_bx != a_bx && res_ax != a_ax,
+           ctx->c->RescaleV(level, {res_bx, res_ax, nullptr},
+                            {a_bx, a_ax, nullptr}))
+}
+
+extern "C" int chd_mult_key(const chd_context *ctx, int level,
+                            uint32_t *res_bx, uint32_t *res_ax,
+                            const uint32_t *a_bx, const uint32_t *a_ax,
+                            const uint32_t *const *evk_bx,
+                            const uint32_t *const *evk_ax, int evk_beta,
+                            void *stream) {
+  CHD_CALL("chd_mult_key",
+           LevelOk(ctx, level) && res_bx && res_ax && a_bx && a_ax && evk_bx &&
+               evk_ax && evk_beta > 0,
+           ctx->c->MultKeyV(level, {res_bx, res_ax, nullptr},
+                            {a_bx, a_ax, nullptr},
+                            MakeEvk(ctx, evk_bx, evk_ax, evk_beta)))
+}
+
+extern "C" int chd_hrot(const chd_context *ctx, int level, uint32_t *res_bx,
+                        uint32_t *res_ax, const uint32_t *a_bx,
+                        const uint32_t *a_ax, const uint32_t *const *evk_bx,
+                        const uint32_t *const *evk_ax, int evk_beta, int rot,
+                        int num_slots, void *stream) {
+  CHD_CALL("chd_hrot",
+           LevelOk(ctx, level) && res_bx && res_ax && a_bx && a_ax &&
+               res_bx != a_bx && res_ax != a_ax && evk_bx && evk_ax &&
+               evk_beta > 0 && num_slots > 0,
+           {
+             int r = rot % num_slots;
+             if (r < 0) r += num_slots;
+             if (r == 0) throw cheddar::Error("HRot by 0 is not a rotation");
+             const auto &p = ctx->c->param_;
+             const size_t words =
+                 static_cast<size_t>(p.LevelToNP(level).GetNumQ()) * p.degree_;
+             cheddar::Scratch t(2 * words);
+             ctx->c->MultKeyV(level, {t.data(), t.data() + words, nullptr},
+                              {a_bx, a_ax, nullptr},
+                              MakeEvk(ctx, evk_bx, evk_ax, evk_beta));
+             ctx->c->PermuteV(level, {res_bx, res_ax, nullptr},
+                              {t.data(), t.data() + words, nullptr}, r);
+           })
+}
+
+extern "C" int chd_permute(const chd_context *ctx, int level, uint32_t *res_bx,
+                           uint32_t *res_ax, const uint32_t *a_bx,
+                           const uint32_t *a_ax, int rot, void *stream) {
+  CHD_CALL("chd_permute",
+           LevelOk(ctx, level) && res_bx && res_ax && a_bx && a_ax &&
+               res_bx != a_bx && res_ax != a_ax,
+           ctx->c->PermuteV(level, {res_bx, res_ax, nullptr},
+                            {a_bx, a_ax, nullptr}, rot))
+}

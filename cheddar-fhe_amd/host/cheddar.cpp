@@ -1,0 +1,1024 @@
+// Implementation of the C++ host API (see cheddar.h). Every method cites the
+// reference function whose semantics it keeps.
+#include "cheddar.h"
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+
+#include "cheddar_amd.h"
+#include "prime_math.h"
+
+namespace cheddar {
+
+namespace {
+thread_local hipStream_t g_stream = nullptr;
+
+void K(int status) {
+  if (status != 0) throw Error(chd_last_error());
+}
+
+int DivCeil(int a, int b) { return (a + b - 1) / b; }
+
+chd_limb_map NoSkipMap(const Parameter<uint32_t> &param, const NPInfo &np) {
+  chd_limb_map m{};
+  m.num_q = np.GetNumQ();
+  m.skip_lo = INT_MAX;
+  m.skip_len = 0;
+  m.tab_off = param.TerLeft(np);
+  m.tab_gap = param.MainLeft(np);
+  return m;
+}
+}  // namespace
+
+hipStream_t CurrentStream() { return g_stream; }
+StreamScope::StreamScope(hipStream_t s) : prev_(g_stream) { g_stream = s; }
+StreamScope::~StreamScope() { g_stream = prev_; }
+
+Scratch::Scratch(size_t words) : s_(CurrentStream()) {
+  if (words == 0) return;
+  HipCheck(hipMallocAsync(reinterpret_cast<void **>(&p_),
+                          words * sizeof(uint32_t), s_),
+           "hipMallocAsync");
+}
+Scratch::~Scratch() {
+  if (p_ != nullptr) (void)hipFreeAsync(p_, s_);
+}
+
+NPInfo::NPInfo(int num_main, int num_ter, int num_aux)
+    : num_main_(num_main), num_ter_(num_ter), num_aux_(num_aux) {
+  AssertTrue(num_main >= 0 && num_ter >= 0 && num_aux >= 0,
+             "NPInfo: negative prime count");
+}
+
+// ------------------------------------------------------------ Parameter --
+// src/core/Parameter.cu:20-194
+static int CheckedDnum(size_t main, size_t ter, size_t aux) {
+  AssertTrue(aux > 0, "Parameter: at least one auxiliary prime is required");
+  return static_cast<int>((main + ter + aux - 1) / aux);
+}
+
+Parameter<uint32_t>::Parameter(
+    int log_degree, double base_scale, int default_encryption_level,
+    std::vector<std::pair<int, int>> level_config,
+    const std::vector<word> &main_primes, const std::vector<word> &aux_primes,
+    const std::vector<word> &ter_primes,
+    const std::pair<int, int> &additional_base)
+    : log_degree_(log_degree),
+      degree_(1 << log_degree),
+      dnum_(CheckedDnum(main_primes.size(), ter_primes.size(),
+                        aux_primes.size())),
+      L_(static_cast<int>(main_primes.size() + ter_primes.size())),
+      alpha_(static_cast<int>(aux_primes.size())),
+      base_scale_(base_scale),
+      default_encryption_level_(default_encryption_level),
+      max_level_(static_cast<int>(level_config.size()) - 1),
+      main_primes_(main_primes),
+      ter_primes_(ter_primes),
+      aux_primes_(aux_primes),
+      level_config_(std::move(level_config)) {
+  AssertTrue(log_degree == 16, "Parameter: only log_degree 16 is supported");
+  AssertTrue(ter_primes.empty(),
+             "Parameter: terminal primes are not supported by this build");
+  AssertTrue(additional_base.first == 0 && additional_base.second == 0,
+             "Parameter: additional base (sparse-secret encapsulation) is not "
+             "supported by this build");
+  AssertTrue(max_level_ >= 0, "Parameter: empty level_config");
+  const word ntt_base = 2u * static_cast<word>(degree_);
+  auto check = [&](word p) {
+    // the reference's own bound check is a no-op (Parameter.cu:45-53);
+    // it is enforced here
+    AssertTrue(p < (1u << 31), "Max prime is too large for the word size");
+    AssertTrue(p % ntt_base == 1, "Prime is not NTT-friendly");
+  };
+  for (word p : main_primes_) check(p);
+  for (word p : aux_primes_) check(p);
+  std::pair<int, int> prev{0, 0};
+  for (size_t i = 0; i < level_config_.size(); i++) {
+    const auto &c = level_config_[i];
+    AssertTrue(c.first >= 0 && c.first <= GetMaxNumMain(),
+               "Invalid number of main primes at level " + std::to_string(i));
+    AssertTrue(c.second >= 0 && c.second <= GetMaxNumTer(),
+               "Invalid number of terminal primes at level " +
+                   std::to_string(i));
+    AssertTrue(c.first + c.second > prev.first + prev.second &&
+                   c.first >= prev.first,
+               "Invalid level configuration at level " + std::to_string(i));
+    prev = c;
+  }
+  AssertTrue(level_config_.back().first == GetMaxNumMain(),
+             "Invalid number of main primes at the last level");
+  AssertTrue(default_encryption_level_ >= 0 &&
+                 default_encryption_level_ <= max_level_,
+             "Invalid default encryption level");
+  // galois factors 5^i mod 2N (Parameter.cu:93-101)
+  const int slots = degree_ / 2, m = 2 * degree_;
+  galois_factors_.resize(slots + 1);
+  galois_factors_[0] = 1;
+  galois_factors_[slots] = 1;
+  for (int i = 1; i < slots; i++)
+    galois_factors_[i] = static_cast<int>(
+        (static_cast<int64_t>(galois_factors_[i - 1]) * 5) % m);
+  chain_.insert(chain_.end(), ter_primes_.rbegin(), ter_primes_.rend());
+  chain_.insert(chain_.end(), main_primes_.begin(), main_primes_.end());
+  chain_.insert(chain_.end(), aux_primes_.begin(), aux_primes_.end());
+  // scales (Parameter.cu:149-193), no terminal primes
+  rescale_prime_prod_.assign(max_level_ + 1, 0.0);
+  scale_.assign(default_encryption_level_ + 1, base_scale_);
+  double s = base_scale_;
+  for (int i = 1; i <= max_level_; i++) {
+    double prod = 1.0;
+    for (int j = level_config_[i - 1].first; j < level_config_[i].first; j++)
+      prod *= main_primes_[j];
+    rescale_prime_prod_[i] = prod;
+    if (i <= default_encryption_level_) {
+      s = std::sqrt(s * prod);
+      scale_[i] = s;
+    }
+  }
+}
+
+NPInfo Parameter<uint32_t>::LevelToNP(int level, int num_aux) const {
+  AssertTrue(num_aux >= 0 && num_aux <= alpha_, "Invalid number of aux primes");
+  AssertTrue(level >= 0 && level <= max_level_, "Invalid level");
+  const auto &c = level_config_.at(level);
+  return NPInfo(c.first, c.second, num_aux);
+}
+
+int Parameter<uint32_t>::NPToLevel(const NPInfo &np) const {
+  for (size_t i = 0; i < level_config_.size(); i++)
+    if (level_config_[i].first == np.num_main_ &&
+        level_config_[i].second == np.num_ter_)
+      return static_cast<int>(i);
+  Fail("NPInfo not found");
+}
+
+std::vector<uint32_t> Parameter<uint32_t>::GetPrimeVector(
+    const NPInfo &np) const {
+  std::vector<word> r(chain_.begin() + TerLeft(np),
+                      chain_.begin() + GetMaxNumTer() + np.num_main_);
+  r.insert(r.end(), aux_primes_.begin(), aux_primes_.begin() + np.num_aux_);
+  return r;
+}
+
+int Parameter<uint32_t>::GetGaloisFactor(int i) const {
+  AssertTrue(i >= 0 && i <= degree_ / 2,
+             "GetGaloisFactor: Invalid Galois factor index");
+  return galois_factors_.at(i);
+}
+
+double Parameter<uint32_t>::GetScale(int level) const {
+  AssertTrue(level >= 0 && level <= default_encryption_level_,
+             "GetScale: Invalid level");
+  return scale_.at(level);
+}
+
+double Parameter<uint32_t>::GetRescalePrimeProd(int level) const {
+  AssertTrue(level > 0 && level <= max_level_,
+             "GetRescalePrimeProd: Invalid level");
+  return rescale_prime_prod_.at(level);
+}
+
+// ----------------------------------------------------------- containers --
+Ciphertext<uint32_t>::Ciphertext(const NPInfo &np, bool has_rx) : np_(np) {
+  size_t n = static_cast<size_t>(np.GetNumTotal()) * degree_;
+  bx_.resize(n);
+  ax_.resize(n);
+  if (has_rx) rx_.resize(n);
+}
+
+void Ciphertext<uint32_t>::PrepareRx() {
+  rx_.resize(static_cast<size_t>(np_.GetNumTotal()) * degree_);
+}
+
+void Ciphertext<uint32_t>::RemoveRx() { rx_.resize(0); }
+
+void Ciphertext<uint32_t>::ModifyNP(const NPInfo &np) {
+  np_ = np;
+  size_t n = static_cast<size_t>(np.GetNumTotal()) * degree_;
+  bx_.resize(n);
+  ax_.resize(n);
+  if (rx_.size() != 0) rx_.resize(n);
+}
+
+EvaluationKey<uint32_t>::EvaluationKey(const NPInfo &np, int beta, int degree)
+    : np_(np) {
+  AssertTrue(beta >= 0, "Negative beta given for evaluation key");
+  size_t n = static_cast<size_t>(np.GetNumTotal()) * degree;
+  bx_.resize(beta);
+  ax_.resize(beta);
+  for (int i = 0; i < beta; i++) {
+    bx_[i].resize(n);
+    ax_[i].resize(n);
+  }
+}
+
+// ------------------------------------------------------------ NTTHandler --
+NTTHandler<uint32_t>::NTTHandler(const Parameter<word> &param)
+    : param_(param), chain_(param.log_degree_, param.ChainPrimes()) {}
+
+chd_limb_map NTTHandler<uint32_t>::Map(const NPInfo &np) const {
+  return NoSkipMap(param_, np);
+}
+
+// src/core/NTT.cu:606-671
+void NTTHandler<uint32_t>::NTT(DvView<word> &dst, const NPInfo &np,
+                               const DvConstView<word> &src,
+                               bool montgomery_conversion) const {
+  const int n = param_.degree_;
+  AssertTrue(dst.TotalSize() == np.GetNumTotal() * n, "NTT: Invalid dst size");
+  chd_limb_map m = Map(np);
+  m.src_gap = (src.QSize() - np.GetNumQ() * n) / n;
+  m.cst_gap = param_.MainLeft(np);
+  const word *pre = montgomery_conversion
+                        ? chain_.mont_converter() + param_.TerLeft(np)
+                        : nullptr;
+  K(chd_k_ntt_fwd(&chain_.tables(), &m, dst.data(), 0, src.data(), 0,
+                  np.GetNumTotal(), 1, pre, CurrentStream()));
+}
+
+// src/core/NTT.cu:673-741
+void NTTHandler<uint32_t>::INTT(DvView<word> &dst, const NPInfo &np,
+                                const DvConstView<word> &src,
+                                bool montgomery_conversion) const {
+  const int n = param_.degree_;
+  AssertTrue(dst.TotalSize() == np.GetNumTotal() * n,
+             "INTT: Invalid dst size");
+  chd_limb_map m = Map(np);
+  m.src_gap = (src.QSize() - np.GetNumQ() * n) / n;
+  m.cst_gap = param_.MainLeft(np);
+  const word *cst =
+      (montgomery_conversion ? chain_.inv_degree() : chain_.inv_degree_mont()) +
+      param_.TerLeft(np);
+  K(chd_k_ntt_inv(&chain_.tables(), &m, dst.data(), 0, src.data(), 0,
+                  np.GetNumTotal(), 1, cst, 0, CurrentStream()));
+}
+
+// src/core/NTT.cu:743-813
+void NTTHandler<uint32_t>::INTTAndMultConst(DvView<word> &dst,
+                                            const NPInfo &np,
+                                            const DvConstView<word> &src,
+                                            const DvConstView<word> &src_const,
+                                            bool normalize) const {
+  const int n = param_.degree_;
+  AssertTrue(dst.TotalSize() == np.GetNumTotal() * n,
+             "INTTAndMultConst: Invalid dst size");
+  chd_limb_map m = Map(np);
+  m.src_gap = (src.QSize() - np.GetNumQ() * n) / n;
+  m.cst_gap = src_const.QSize() - np.GetNumQ();
+  K(chd_k_ntt_inv(&chain_.tables(), &m, dst.data(), 0, src.data(), 0,
+                  np.GetNumTotal(), 1, src_const.data(), normalize ? 1 : 0,
+                  CurrentStream()));
+}
+
+// src/core/NTT.cu:815-887
+void NTTHandler<uint32_t>::NTTForModUp(DvView<word> &dst, const NPInfo &np,
+                                       int skip_start, int skip_end,
+                                       const DvConstView<word> &src) const {
+  const int n = param_.degree_;
+  const int num_q = np.GetNumQ();
+  AssertTrue(dst.TotalSize() == np.GetNumTotal() * n,
+             "NTTForModUp: Invalid dst size");
+  AssertTrue(skip_start >= 0 && skip_start < num_q && skip_end >= skip_start &&
+                 skip_end <= num_q,
+             "NTTForModUp: Invalid skip primes");
+  chd_limb_map m = Map(np);
+  m.skip_lo = skip_start;
+  m.skip_len = skip_end - skip_start;
+  m.src_gap = (src.QSize() - num_q * n) / n;
+  K(chd_k_ntt_fwd(&chain_.tables(), &m, dst.data(), 0, src.data(), 0,
+                  np.GetNumTotal() - m.skip_len, 1, nullptr, CurrentStream()));
+}
+
+// src/core/NTT.cu:889-971 (kFuseModDownEpilogue, kFuseMontgomery)
+void NTTHandler<uint32_t>::NTTForModDown(
+    DvView<word> &dst, const NPInfo &np_src1, const NPInfo &np_src2,
+    const DvConstView<word> &src1, const DvConstView<word> &src2,
+    const DvConstView<word> &inv_p_prod,
+    const DvConstView<word> &src2_padding) const {
+  const int n = param_.degree_;
+  const int total = np_src1.GetNumTotal();
+  AssertTrue(dst.TotalSize() == total * n, "NTTForModDown: Invalid dst size");
+  AssertTrue(np_src1.num_aux_ == 0, "NTTForModDown: num_aux should be 0");
+  AssertTrue(np_src2.GetNumQ() <= total, "NTTForModDown: Invalid src2 size");
+  AssertTrue(dst.data() != src2.data(),
+             "NTTForModDown: dst and src2 should be different");
+  AssertTrue(src1.data() == dst.data(),
+             "NTTForModDown: src1 must be dst (in-place NTT)");
+  const int s2_lo = np_src1.num_ter_ - np_src2.num_ter_;
+  const int s2_hi = s2_lo + np_src2.GetNumQ();
+  AssertTrue(s2_hi <= total, "NTTForModDown: Invalid src2 size");
+  chd_limb_map m = Map(np_src1);
+  K(chd_k_ntt_fwd_moddown(&chain_.tables(), &m, dst.data(), total,
+                          src2.data(), s2_lo, s2_hi, inv_p_prod.data(),
+                          src2_padding.data(), CurrentStream()));
+}
+
+// src/core/NTT.cu:973-1071 (case 1: INTT on the upper part only)
+void NTTHandler<uint32_t>::INTTForModDown(
+    DvView<word> &dst, const NPInfo &np_src, const NPInfo &np_non_intt,
+    const DvConstView<word> &src, const DvConstView<word> &src_const) const {
+  const int n = param_.degree_;
+  const int limbs = np_src.GetNumTotal() - np_non_intt.GetNumTotal();
+  AssertTrue(dst.TotalSize() == limbs * n, "INTTForModDown: Invalid dst size");
+  AssertTrue(np_src.GetNumQ() * n == src.QSize() &&
+                 np_src.GetNumTotal() * n == src.TotalSize(),
+             "INTTForModDown: Invalid src size");
+  AssertTrue(np_non_intt.num_aux_ == 0 && np_non_intt.IsSubsetOf(np_src),
+             "INTTForModDown: Invalid np combination");
+  AssertTrue(src.data() != dst.data(),
+             "INTTForModDown: src and dst should be different");
+  AssertTrue(src_const.TotalSize() == limbs,
+             "INTTForModDown: Invalid src_const size");
+  AssertTrue(np_src.num_ter_ == np_non_intt.num_ter_,
+             "INTTForModDown: terminal-prime INTT is not supported");
+  chd_limb_map m{};
+  m.num_q = np_src.num_main_ - np_non_intt.num_main_;
+  m.skip_lo = INT_MAX;
+  m.tab_off = param_.GetMaxNumTer() + np_non_intt.num_main_;
+  m.tab_gap = param_.MainLeft(np_src);
+  const size_t off =
+      static_cast<size_t>(np_src.num_ter_ + np_non_intt.num_main_) * n;
+  K(chd_k_ntt_inv(&chain_.tables(), &m, dst.data(), 0, src.data() + off, 0,
+                  limbs, 1, src_const.data(), 1, CurrentStream()));
+}
+
+// --------------------------------------------------- ElementWiseHandler --
+ElementWiseHandler<uint32_t>::ElementWiseHandler(const Parameter<word> &param,
+                                                 const NTTHandler<word> &ntt)
+    : param_(param), ntt_(ntt) {}
+
+// src/core/ElementWise.cu:921-953
+void ElementWiseHandler<uint32_t>::Tensor(
+    std::vector<DvView<word>> &dst, const NPInfo &np,
+    const std::vector<DvConstView<word>> &src1,
+    const std::vector<DvConstView<word>> &src2) const {
+  AssertTrue(dst.size() == 3 && src1.size() == 2 && src2.size() == 2,
+             "Tensor: Invalid number of polynomials");
+  const int n = param_.degree_;
+  const int q_size = np.GetNumQ() * n;
+  for (auto &d : dst)
+    AssertTrue(d.TotalSize() == np.GetNumTotal() * n, "Tensor: NP mismatch");
+  chd_limb_map m = NoSkipMap(param_, np);
+  m.src_gap = (src1[0].QSize() - q_size) / n;
+  AssertTrue(src2[0].QSize() - q_size == src1[0].QSize() - q_size,
+             "Tensor: source gap mismatch");
+  K(chd_k_tensor(&ntt_.Tables(), &m, dst[0].data(), dst[1].data(),
+                 dst[2].data(), src1[0].data(), src1[1].data(), src2[0].data(),
+                 src2[1].data(), np.GetNumTotal(), CurrentStream()));
+}
+
+// src/core/ElementWise.cu:1437-1643
+void ElementWiseHandler<uint32_t>::CPAccumWorker(
+    bool const_accum, std::vector<DvView<word>> &dst, const NPInfo &np,
+    const std::vector<std::vector<DvConstView<word>>> &ct_srcs,
+    const std::vector<DvConstView<word>> &common_srcs) const {
+  const int num_poly = static_cast<int>(dst.size());
+  const int num_accum = static_cast<int>(common_srcs.size());
+  const bool has_extra_ct = ct_srcs.size() == common_srcs.size() + 1;
+  AssertTrue(num_poly > 0 && num_poly <= CHD_MAX_POLY,
+             "CPAccum: Invalid number of polynomials");
+  AssertTrue(num_accum == static_cast<int>(ct_srcs.size()) || has_extra_ct,
+             "CPAccum: Incompatible ct_srcs/common_srcs size");
+  AssertTrue(num_accum > 0, "CPAccum: Invalid number of accumulations");
+  const int n = param_.degree_;
+  const int q_size = np.GetNumQ() * n;
+  for (auto &d : dst)
+    AssertTrue(d.TotalSize() == np.GetNumTotal() * n, "CPAccum: NP mismatch");
+  for (auto &c : ct_srcs)
+    AssertTrue(static_cast<int>(c.size()) == num_poly,
+               "CPAccum: Incompatible dst/ct_src size");
+  chd_limb_map m = NoSkipMap(param_, np);
+  std::vector<uint32_t *> dptr(num_poly);
+  for (int p = 0; p < num_poly; p++) dptr[p] = dst[p].data();
+  std::vector<const uint32_t *> s0(num_poly);
+  long long s0_gap = 0;
+  bool use_s0 = has_extra_ct;
+  if (has_extra_ct) {
+    for (int p = 0; p < num_poly; p++) s0[p] = ct_srcs.back()[p].data();
+    s0_gap = ct_srcs.back()[0].QSize() - q_size;
+  }
+  // accumulate in chunks of CHD_MAX_ACCUM; later chunks add onto dst
+  for (int base = 0; base < num_accum; base += CHD_MAX_ACCUM) {
+    const int cnt = std::min(CHD_MAX_ACCUM, num_accum - base);
+    chd_accum_src s[CHD_MAX_ACCUM] = {};
+    for (int j = 0; j < cnt; j++) {
+      const auto &ct = ct_srcs[base + j];
+      const auto &cm = common_srcs[base + j];
+      for (int p = 0; p < num_poly; p++) s[j].src[p] = ct[p].data();
+      s[j].src_gap = ct[0].QSize() - q_size;
+      s[j].common = cm.data();
+      s[j].common_gap =
+          const_accum ? cm.QSize() - np.GetNumQ() : cm.QSize() - q_size;
+    }
+    K(chd_k_cpaccum(&ntt_.Tables(), &m, dptr.data(), num_poly,
+                    use_s0 ? s0.data() : nullptr, s0_gap, s, cnt,
+                    const_accum ? 1 : 0, np.GetNumTotal(), CurrentStream()));
+    for (int p = 0; p < num_poly; p++) s0[p] = dptr[p];
+    s0_gap = 0;
+    use_s0 = true;
+  }
+}
+
+void ElementWiseHandler<uint32_t>::PAccum(
+    std::vector<DvView<word>> &dst, const NPInfo &np,
+    const std::vector<std::vector<DvConstView<word>>> &ct_srcs,
+    const std::vector<DvConstView<word>> &common_srcs) const {
+  CPAccumWorker(false, dst, np, ct_srcs, common_srcs);
+}
+
+void ElementWiseHandler<uint32_t>::CAccum(
+    std::vector<DvView<word>> &dst, const NPInfo &np,
+    const std::vector<std::vector<DvConstView<word>>> &ct_srcs,
+    const std::vector<DvConstView<word>> &common_srcs) const {
+  CPAccumWorker(true, dst, np, ct_srcs, common_srcs);
+}
+
+// src/core/ElementWise.cu:955-964
+uint32_t ElementWiseHandler<uint32_t>::PermuteAmountToGaloisFactor(
+    int permute_amount) const {
+  if (permute_amount == -1) return 2u * param_.degree_ - 1;
+  AssertTrue(permute_amount >= 0 && permute_amount <= param_.degree_ / 2,
+             "Permute: Invalid permute amount");
+  return static_cast<uint32_t>(param_.GetGaloisFactor(permute_amount));
+}
+
+// src/core/ElementWise.cu:966-999
+void ElementWiseHandler<uint32_t>::Permute(
+    std::vector<DvView<word>> &dst, const NPInfo &np, int permute_amount,
+    const std::vector<DvConstView<word>> &src1) const {
+  const int num_poly = static_cast<int>(dst.size());
+  AssertTrue(num_poly == static_cast<int>(src1.size()),
+             "Permute: Incompatible dst/src size");
+  AssertTrue(num_poly > 0 && num_poly <= CHD_MAX_POLY,
+             "Permute: Invalid number of polynomials");
+  const int n = param_.degree_;
+  std::vector<uint32_t *> d(num_poly);
+  std::vector<const uint32_t *> s(num_poly);
+  for (int p = 0; p < num_poly; p++) {
+    AssertTrue(dst[p].data() != src1[p].data(),
+               "Permute does not support inplace operation");
+    d[p] = dst[p].data();
+    s[p] = src1[p].data();
+  }
+  chd_limb_map m = NoSkipMap(param_, np);
+  m.src_gap = (src1[0].QSize() - np.GetNumQ() * n) / n;
+  K(chd_k_permute(&m, d.data(), s.data(), num_poly, np.GetNumTotal(),
+                  PermuteAmountToGaloisFactor(permute_amount),
+                  CurrentStream()));
+}
+
+// ----------------------------------------------------- ModSwitchHandler --
+// src/core/ModSwitch.cu:175-318, no terminal primes
+ModSwitchHandler<uint32_t>::ModSwitchHandler(
+    const Parameter<word> &param, int level,
+    const ElementWiseHandler<word> &elem, const NTTHandler<word> &ntt)
+    : level_(level),
+      num_aux_(param.alpha_),
+      beta_(DivCeil(param.LevelToNP(level).num_main_ + param.GetMaxNumTer(),
+                    param.alpha_)),
+      param_(param),
+      elem_(elem),
+      ntt_(ntt) {
+  const NPInfo np = param_.LevelToNP(level_, num_aux_);
+  const int num_q = np.GetNumQ();
+  const std::vector<word> lp = param_.GetPrimeVector(np);
+  std::vector<word> up1(num_q);
+  mod_up_.resize(beta_);
+  for (int i = 0; i < beta_; i++) {
+    const int s0 = i * num_aux_;
+    const int s1 = std::min((i + 1) * num_aux_, num_q);
+    std::vector<word> src(lp.begin() + s0, lp.begin() + s1);
+    std::vector<word> dst(lp.begin(), lp.begin() + s0);
+    dst.insert(dst.end(), lp.begin() + s1, lp.end());
+    BuildSwitch(mod_up_[i], src, dst);
+    std::vector<word> c1(s1 - s0);
+    HipCheck(hipMemcpy(c1.data(), mod_up_[i].const1.data(),
+                       c1.size() * sizeof(word), hipMemcpyDeviceToHost),
+             "hipMemcpy");
+    std::copy(c1.begin(), c1.end(), up1.begin() + s0);
+  }
+  mod_up1_.resize(num_q);
+  HipCheck(hipMemcpy(mod_up1_.data(), up1.data(), num_q * sizeof(word),
+                     hipMemcpyHostToDevice),
+           "hipMemcpy");
+
+  const std::vector<word> qp(lp.begin(), lp.begin() + num_q);
+  const std::vector<word> pp(lp.begin() + num_q, lp.end());
+  BuildSwitch(mod_down_, pp, qp);
+  auto inv_prod = [](const std::vector<word> &src,
+                     const std::vector<word> &dst) {
+    std::vector<word> r(dst.size());
+    for (size_t k = 0; k < dst.size(); k++) {
+      word v = 1;
+      for (word s : src) v = pm::mulmod(v, s, dst[k]);
+      r[k] = pm::to_mont(pm::invmod(v, dst[k]), dst[k]);
+    }
+    return r;
+  };
+  auto upload = [](DeviceVector<word> &dv, const std::vector<word> &h) {
+    dv.resize(h.size());
+    HipCheck(hipMemcpy(dv.data(), h.data(), h.size() * sizeof(word),
+                       hipMemcpyHostToDevice),
+             "hipMemcpy");
+  };
+  upload(inv_prime_prod_, inv_prod(pp, qp));
+  if (level_ == 0) return;
+
+  const NPInfo next = param_.LevelToNP(level_ - 1, num_aux_);
+  const int main_diff = np.num_main_ - next.num_main_;
+  AssertTrue(main_diff > 0, "Invalid rescale amount");
+  const std::vector<word> rdst(lp.begin(), lp.begin() + num_q - main_diff);
+  const std::vector<word> rsrc(lp.begin() + num_q - main_diff,
+                               lp.begin() + num_q);
+  std::vector<word> mdr_src = rsrc;
+  mdr_src.insert(mdr_src.end(), pp.begin(), pp.end());
+  BuildSwitch(rescale_, rsrc, rdst);
+  BuildSwitch(mod_down_rescale_, mdr_src, rdst);
+  upload(rescale_inv_prime_prod_, inv_prod(rsrc, rdst));
+  upload(mod_down_rescale_inv_prime_prod_, inv_prod(mdr_src, rdst));
+  // BitPacker padding with an empty restore range: ToMont(1) per limb
+  std::vector<word> pad(rdst.size());
+  for (size_t k = 0; k < rdst.size(); k++) pad[k] = pm::to_mont(1, rdst[k]);
+  upload(rescale_padding_, pad);
+  upload(mod_down_rescale_padding_, pad);
+}
+
+// PopulateModSwitchConstants (ModSwitch.cu:320-370), restore range empty
+void ModSwitchHandler<uint32_t>::BuildSwitch(
+    SwitchTable &st, const std::vector<word> &src,
+    const std::vector<word> &dst) const {
+  const int sl = static_cast<int>(src.size());
+  const int dl = static_cast<int>(dst.size());
+  std::vector<word> c1(sl, 1);
+  std::vector<int32_t> c2(static_cast<size_t>(sl) * dl);
+  for (int i = 0; i < sl; i++) {
+    word v = 1;
+    for (int j = 0; j < sl; j++)
+      if (j != i) v = pm::mulmod(v, src[j], src[i]);
+    v = pm::mulmod(v, static_cast<word>(param_.degree_), src[i]);
+    c1[i] = pm::invmod(v, src[i]);
+  }
+  for (int k = 0; k < dl; k++)
+    for (int i = 0; i < sl; i++) {
+      word acc = 1;
+      for (int j = 0; j < sl; j++)
+        if (j != i) acc = pm::mulmod(acc, src[j], dst[k]);
+      acc = pm::to_mont(pm::to_mont(acc, dst[k]), dst[k]);
+      c2[static_cast<size_t>(k) * sl + i] = pm::normalize(acc, dst[k]);
+    }
+  st.src_len = sl;
+  st.dst_len = dl;
+  st.const1.resize(sl);
+  HipCheck(hipMemcpy(st.const1.data(), c1.data(), sl * sizeof(word),
+                     hipMemcpyHostToDevice),
+           "hipMemcpy");
+  std::vector<unsigned char> packed(
+      static_cast<size_t>(chd_bconv_table_size(sl, dl)));
+  K(chd_bconv_table_pack(packed.data(), c2.data(), dst.data(), sl, dl));
+  st.table.Resize(packed.size());
+  st.table.Upload(packed.data(), packed.size());
+}
+
+// src/core/ModSwitch.cu:429-509
+void ModSwitchHandler<uint32_t>::ModUp(std::vector<DvView<word>> &dst,
+                                       const DvConstView<word> &src) const {
+  const NPInfo np = param_.LevelToNP(level_, 0);
+  const int num_q = np.GetNumQ();
+  const int n = param_.degree_;
+  AssertTrue(src.QSize() == num_q * n, "ModUp src q size mismatch");
+  AssertTrue(src.AuxSize() == 0, "ModUp src aux size mismatch");
+  AssertTrue(static_cast<int>(dst.size()) == beta_, "ModUp dst size mismatch");
+  Scratch intt(static_cast<size_t>(num_q) * n);
+  DvView<word> intt_view(intt.data(), num_q * n, 0);
+  ntt_.INTTAndMultConst(intt_view, np,
+                        src, DvConstView<word>(mod_up1_.data(), num_q, 0),
+                        true);
+  NPInfo np_aux = np;
+  np_aux.num_aux_ = num_aux_;
+  for (int i = 0; i < beta_; i++) {
+    const int s0 = i * num_aux_;
+    const int s1 = std::min((i + 1) * num_aux_, num_q);
+    AssertTrue(dst[i].AuxSize() == num_aux_ * n &&
+                   dst[i].QSize() == num_q * n,
+               "ModUp dst size mismatch");
+    HipCheck(hipMemcpyAsync(dst[i].data() + static_cast<size_t>(s0) * n,
+                            src.data() + static_cast<size_t>(s0) * n,
+                            static_cast<size_t>(s1 - s0) * n * sizeof(word),
+                            hipMemcpyDeviceToDevice, CurrentStream()),
+             "hipMemcpyAsync");
+  }
+  for (int i = 0; i < beta_; i++) {
+    const int s0 = i * num_aux_;
+    const int s1 = std::min((i + 1) * num_aux_, num_q);
+    const SwitchTable &st = mod_up_[i];
+    chd_limb_map m = NoSkipMap(param_, np_aux);
+    m.skip_lo = s0;
+    m.skip_len = s1 - s0;
+    K(chd_k_bconv(&ntt_.Tables(), &m, dst[i].data(),
+                  reinterpret_cast<const int32_t *>(intt.data()) +
+                      static_cast<size_t>(s0) * n,
+                  st.src_len, st.dst_len, st.table.as<void>(),
+                  CurrentStream()));
+    ntt_.NTTForModUp(dst[i], np_aux, s0, s1, DvConstView<word>(dst[i]));
+  }
+}
+
+void ModSwitchHandler<uint32_t>::ModDown(DvView<word> &dst,
+                                         const DvConstView<word> &src) const {
+  const int n = param_.degree_;
+  const NPInfo np = param_.LevelToNP(level_, num_aux_);
+  AssertTrue(src.AuxSize() == np.num_aux_ * n &&
+                 src.QSize() == np.GetNumQ() * n,
+             "ModDown: src size mismatch");
+  AssertTrue(dst.AuxSize() == 0 && dst.QSize() == np.GetNumQ() * n,
+             "ModDown: dst size mismatch");
+  ModDownWorker(dst, src, Kind::ModDown);
+}
+
+void ModSwitchHandler<uint32_t>::Rescale(DvView<word> &dst,
+                                         const DvConstView<word> &src) const {
+  const int n = param_.degree_;
+  AssertTrue(level_ > 0, "Not enough q primes to rescale");
+  const NPInfo np = param_.LevelToNP(level_);
+  const NPInfo next = param_.LevelToNP(level_ - 1);
+  AssertTrue(src.AuxSize() == 0 && src.QSize() == np.GetNumQ() * n,
+             "Rescale: src size mismatch");
+  AssertTrue(dst.AuxSize() == 0 && dst.QSize() == next.GetNumQ() * n,
+             "Rescale: dst size mismatch");
+  ModDownWorker(dst, src, Kind::Rescale);
+}
+
+void ModSwitchHandler<uint32_t>::ModDownAndRescale(
+    DvView<word> &dst, const DvConstView<word> &src) const {
+  const int n = param_.degree_;
+  AssertTrue(level_ > 0, "Not enough q primes to rescale");
+  const NPInfo np = param_.LevelToNP(level_, num_aux_);
+  const NPInfo next = param_.LevelToNP(level_ - 1);
+  AssertTrue(src.AuxSize() == np.num_aux_ * n &&
+                 src.QSize() == np.GetNumQ() * n,
+             "ModDownAndRescale: src size mismatch");
+  AssertTrue(dst.AuxSize() == 0 && dst.QSize() == next.GetNumQ() * n,
+             "ModDownAndRescale: dst size mismatch");
+  ModDownWorker(dst, src, Kind::ModDownAndRescale);
+}
+
+// src/core/ModSwitch.cu:566-684 (kFuseModDownEpilogue)
+void ModSwitchHandler<uint32_t>::ModDownWorker(DvView<word> &dst,
+                                               const DvConstView<word> &src,
+                                               Kind kind) const {
+  const int n = param_.degree_;
+  const int num_src_aux = kind == Kind::Rescale ? 0 : num_aux_;
+  const NPInfo np_src = param_.LevelToNP(level_, num_src_aux);
+  const NPInfo np_dst =
+      param_.LevelToNP(kind == Kind::ModDown ? level_ : level_ - 1, 0);
+  const NPInfo np_non_intt(std::min(np_src.num_main_, np_dst.num_main_),
+                           std::min(np_src.num_ter_, np_dst.num_ter_), 0);
+  const int src_len = np_src.GetNumTotal() - np_non_intt.GetNumTotal();
+  const int dst_len = np_dst.GetNumTotal();
+  const SwitchTable &st = kind == Kind::ModDown   ? mod_down_
+                          : kind == Kind::Rescale ? rescale_
+                                                  : mod_down_rescale_;
+  AssertTrue(st.src_len == src_len && st.dst_len == dst_len,
+             "ModDown: constant table mismatch");
+  Scratch intt(static_cast<size_t>(src_len) * n);
+  DvView<word> intt_view(intt.data(), src_len * n, 0);
+  ntt_.INTTForModDown(intt_view, np_src, np_non_intt, src,
+                      DvConstView<word>(st.const1.data(), src_len,
+                                        num_src_aux));
+  chd_limb_map m = NoSkipMap(param_, np_dst);
+  K(chd_k_bconv(&ntt_.Tables(), &m, dst.data(),
+                reinterpret_cast<const int32_t *>(intt.data()), src_len,
+                dst_len, st.table.as<void>(), CurrentStream()));
+  const DeviceVector<word> &ipp =
+      kind == Kind::ModDown   ? inv_prime_prod_
+      : kind == Kind::Rescale ? rescale_inv_prime_prod_
+                              : mod_down_rescale_inv_prime_prod_;
+  const word *pad = kind == Kind::ModDown   ? nullptr
+                    : kind == Kind::Rescale ? rescale_padding_.data()
+                                            : mod_down_rescale_padding_.data();
+  const int src2_off = std::max(0, np_src.num_ter_ - np_dst.num_ter_);
+  DvConstView<word> src2(src.data() + static_cast<size_t>(src2_off) * n,
+                         dst_len * n, 0);
+  ntt_.NTTForModDown(dst, np_dst, np_non_intt, DvConstView<word>(dst), src2,
+                     DvConstView<word>(ipp.data(), dst_len, 0),
+                     DvConstView<word>(pad, pad ? dst_len : 0, 0));
+}
+
+// ---------------------------------------------------------------- Context --
+std::shared_ptr<Context<uint32_t>> Context<uint32_t>::Create(
+    const Parameter<word> &param) {
+  return std::shared_ptr<Context<word>>(new Context<word>(param));
+}
+
+// src/core/Context.cpp:68-124
+Context<uint32_t>::Context(const Parameter<word> &param)
+    : param_(param), elem_handler_(param, ntt_handler_), ntt_handler_(param) {
+  Ciphertext<word>::SetDegree(param_.degree_);
+  mod_switch_handlers_.reserve(param_.max_level_ + 1);
+  for (int level = 0; level <= param_.max_level_; level++)
+    mod_switch_handlers_.emplace_back(param_, level, elem_handler_,
+                                      ntt_handler_);
+  const NPInfo np = param_.LevelToNP(param_.max_level_, param_.alpha_);
+  const std::vector<word> primes = param_.GetPrimeVector(np);
+  const int num_q = np.GetNumQ();
+  std::vector<word> h(num_q, 1);
+  for (int i = 0; i < num_q; i++) {
+    for (int j = 0; j < np.num_aux_; j++)
+      h[i] = pm::mulmod(h[i], primes[num_q + j], primes[i]);
+    h[i] = pm::to_mont(h[i], primes[i]);
+  }
+  p_prod_.resize(num_q);
+  HipCheck(hipMemcpy(p_prod_.data(), h.data(), num_q * sizeof(word),
+                     hipMemcpyHostToDevice),
+           "hipMemcpy");
+}
+
+DvConstView<uint32_t> Context<uint32_t>::GetPProd(const NPInfo &np) const {
+  return DvConstView<word>(p_prod_.data() + param_.TerLeft(np), np.GetNumQ(),
+                           0);
+}
+
+void Context<uint32_t>::TensorV(int level, CtRef res, CtCRef a,
+                                CtCRef b) const {
+  const NPInfo np = param_.LevelToNP(level);
+  const int sz = np.GetNumQ() * param_.degree_;
+  std::vector<DvView<word>> d{DvView<word>(res.bx, sz, 0),
+                              DvView<word>(res.ax, sz, 0),
+                              DvView<word>(res.rx, sz, 0)};
+  elem_handler_.Tensor(d, np,
+                       {DvConstView<word>(a.bx, sz, 0),
+                        DvConstView<word>(a.ax, sz, 0)},
+                       {DvConstView<word>(b.bx, sz, 0),
+                        DvConstView<word>(b.ax, sz, 0)});
+}
+
+// src/core/Context.cpp:609-712
+void Context<uint32_t>::KeyMultNoModDownV(int level, word *acc_b, word *acc_a,
+                                          const word *d, const word *cb,
+                                          const word *ca,
+                                          const EvkRef &key) const {
+  const NPInfo a_np = param_.LevelToNP(level);
+  const int n = param_.degree_;
+  const int num_q = a_np.GetNumQ();
+  const int num_aux = key.np.num_aux_;
+  AssertTrue(num_aux == param_.alpha_, "Invalid setting for MultKeyNoModDown");
+  const int prime_offset = param_.GetMaxNumTer() - a_np.num_ter_;
+  const int beta = DivCeil(num_q + prime_offset, num_aux);
+  AssertTrue(static_cast<int>(key.bx.size()) >= beta &&
+                 key.bx.size() == key.ax.size(),
+             "Beta mismatch");
+  const int total = num_q + num_aux;
+  Scratch modup(static_cast<size_t>(beta) * total * n);
+  std::vector<DvView<word>> up_views;
+  for (int g = 0; g < beta; g++)
+    up_views.emplace_back(modup.data() + static_cast<size_t>(g) * total * n,
+                          total * n, num_aux * n);
+  mod_switch_handlers_.at(level).ModUp(up_views,
+                                       DvConstView<word>(d, num_q * n, 0));
+  const NPInfo np(a_np.num_main_, a_np.num_ter_, num_aux);
+  std::vector<DvView<word>> acc{DvView<word>(acc_b, total * n, num_aux * n),
+                                DvView<word>(acc_a, total * n, num_aux * n)};
+  const int key_total = key.np.GetNumTotal() * n - prime_offset * n;
+  std::vector<std::vector<DvConstView<word>>> key_views;
+  std::vector<DvConstView<word>> up_const;
+  for (int g = 0; g < beta; g++) {
+    key_views.push_back(
+        {DvConstView<word>(key.bx[g] + prime_offset * n, key_total,
+                           num_aux * n),
+         DvConstView<word>(key.ax[g] + prime_offset * n, key_total,
+                           num_aux * n)});
+    up_const.emplace_back(up_views[g]);
+  }
+  elem_handler_.PAccum(acc, np, key_views, up_const);
+  // accum.{b,a} (q part) += p_prod * ct.{b,a}
+  std::vector<DvView<word>> cres{DvView<word>(acc_b, num_q * n, 0)};
+  std::vector<DvConstView<word>> ct_part{DvConstView<word>(cb, num_q * n, 0)};
+  std::vector<DvConstView<word>> acc_part{
+      DvConstView<word>(acc_b, total * n, num_aux * n)};
+  if (ca != nullptr) {
+    cres.emplace_back(acc_a, num_q * n, 0);
+    ct_part.emplace_back(ca, num_q * n, 0);
+    acc_part.emplace_back(acc_a, total * n, num_aux * n);
+  }
+  elem_handler_.CAccum(cres, a_np, {ct_part, acc_part}, {GetPProd(a_np)});
+}
+
+// src/core/Context.cpp:862-871 with 714-737 / 559-607
+void Context<uint32_t>::HMultV(int level, CtRef res, CtCRef a, CtCRef b,
+                               const EvkRef &key, bool rescale) const {
+  const NPInfo np = param_.LevelToNP(level);
+  const int n = param_.degree_;
+  const int num_q = np.GetNumQ();
+  const int total = num_q + param_.alpha_;
+  Scratch t(static_cast<size_t>(3) * num_q * n);
+  CtRef tr{t.data(), t.data() + static_cast<size_t>(num_q) * n,
+           t.data() + static_cast<size_t>(2) * num_q * n};
+  TensorV(level, tr, a, b);
+  Scratch acc(static_cast<size_t>(2) * total * n);
+  word *acc_b = acc.data();
+  word *acc_a = acc.data() + static_cast<size_t>(total) * n;
+  KeyMultNoModDownV(level, acc_b, acc_a, tr.rx, tr.bx, tr.ax, key);
+  const auto &ms = mod_switch_handlers_.at(level);
+  DvConstView<word> sb(acc_b, total * n, param_.alpha_ * n);
+  DvConstView<word> sa(acc_a, total * n, param_.alpha_ * n);
+  if (rescale) {
+    const int nq = param_.LevelToNP(level - 1).GetNumQ();
+    DvView<word> db(res.bx, nq * n, 0), da(res.ax, nq * n, 0);
+    ms.ModDownAndRescale(db, sb);
+    ms.ModDownAndRescale(da, sa);
+  } else {
+    DvView<word> db(res.bx, num_q * n, 0), da(res.ax, num_q * n, 0);
+    ms.ModDown(db, sb);
+    ms.ModDown(da, sa);
+  }
+}
+
+// src/core/Context.cpp:739-774
+void Context<uint32_t>::RescaleV(int level, CtRef res, CtCRef a) const {
+  AssertTrue(level > 0, "Not enough q primes to rescale");
+  const int n = param_.degree_;
+  const int nq = param_.LevelToNP(level).GetNumQ();
+  const int nq1 = param_.LevelToNP(level - 1).GetNumQ();
+  const auto &ms = mod_switch_handlers_.at(level);
+  DvView<word> db(res.bx, nq1 * n, 0), da(res.ax, nq1 * n, 0);
+  ms.Rescale(db, DvConstView<word>(a.bx, nq * n, 0));
+  ms.Rescale(da, DvConstView<word>(a.ax, nq * n, 0));
+  if (a.rx != nullptr && res.rx != nullptr) {
+    DvView<word> dr(res.rx, nq1 * n, 0);
+    ms.Rescale(dr, DvConstView<word>(a.rx, nq * n, 0));
+  }
+}
+
+// src/core/Context.cpp:584-607
+void Context<uint32_t>::MultKeyV(int level, CtRef res, CtCRef a,
+                                 const EvkRef &key) const {
+  const int n = param_.degree_;
+  const int num_q = param_.LevelToNP(level).GetNumQ();
+  const int total = num_q + param_.alpha_;
+  Scratch acc(static_cast<size_t>(2) * total * n);
+  word *acc_b = acc.data();
+  word *acc_a = acc.data() + static_cast<size_t>(total) * n;
+  KeyMultNoModDownV(level, acc_b, acc_a, a.ax, a.bx, nullptr, key);
+  const auto &ms = mod_switch_handlers_.at(level);
+  DvView<word> db(res.bx, num_q * n, 0), da(res.ax, num_q * n, 0);
+  ms.ModDown(db, DvConstView<word>(acc_b, total * n, param_.alpha_ * n));
+  ms.ModDown(da, DvConstView<word>(acc_a, total * n, param_.alpha_ * n));
+}
+
+void Context<uint32_t>::PermuteV(int level, CtRef res, CtCRef a,
+                                 int amount) const {
+  const NPInfo np = param_.LevelToNP(level);
+  const int sz = np.GetNumQ() * param_.degree_;
+  std::vector<DvView<word>> d{DvView<word>(res.bx, sz, 0),
+                              DvView<word>(res.ax, sz, 0)};
+  elem_handler_.Permute(d, np, amount,
+                        {DvConstView<word>(a.bx, sz, 0),
+                         DvConstView<word>(a.ax, sz, 0)});
+}
+
+// ------------------------------------------- Ciphertext-level entry points
+namespace {
+Context<uint32_t>::EvkRef RefOf(const EvaluationKey<uint32_t> &k) {
+  Context<uint32_t>::EvkRef r;
+  r.np = k.GetNP();
+  for (int g = 0; g < k.GetBeta(); g++) {
+    r.bx.push_back(k.bx_[g].data());
+    r.ax.push_back(k.ax_[g].data());
+  }
+  return r;
+}
+}  // namespace
+
+void Context<uint32_t>::Mult(Ct &res, const Ct &a, const Ct &b) const {
+  AssertTrue(a.GetNP() == b.GetNP(), "Mult: NP mismatch");
+  AssertTrue(!a.HasRx() && !b.HasRx(),
+             "Relinearization required before Mult Ct x Ct");
+  const int level = param_.NPToLevel(a.GetNP());
+  // Tensor reads a and b fully before res is resized only when res aliases
+  // neither; otherwise go through a temporary
+  Ct tmp(a.GetNP(), true);
+  TensorV(level, {tmp.bx_.data(), tmp.ax_.data(), tmp.rx_.data()},
+          {a.bx_.data(), a.ax_.data(), nullptr},
+          {b.bx_.data(), b.ax_.data(), nullptr});
+  tmp.SetNumSlots(std::max(a.GetNumSlots(), b.GetNumSlots()));
+  tmp.SetScale(a.GetScale() * b.GetScale());
+  res = std::move(tmp);
+}
+
+void Context<uint32_t>::Relinearize(Ct &res, const Ct &a,
+                                    const Evk &key) const {
+  AssertTrue(a.HasRx(), "Relinearize requires aux");
+  const int level = param_.NPToLevel(a.GetNP());
+  const int n = param_.degree_;
+  const int num_q = a.GetNP().GetNumQ();
+  const int total = num_q + param_.alpha_;
+  Ct out(a.GetNP());
+  Scratch acc(static_cast<size_t>(2) * total * n);
+  KeyMultNoModDownV(level, acc.data(), acc.data() + static_cast<size_t>(total) * n,
+                    a.rx_.data(), a.bx_.data(), a.ax_.data(), RefOf(key));
+  const auto &ms = mod_switch_handlers_.at(level);
+  DvView<word> db = out.bx_.View(), da = out.ax_.View();
+  ms.ModDown(db, DvConstView<word>(acc.data(), total * n, param_.alpha_ * n));
+  ms.ModDown(da, DvConstView<word>(acc.data() + static_cast<size_t>(total) * n,
+                                   total * n, param_.alpha_ * n));
+  out.SetScale(a.GetScale());
+  out.SetNumSlots(a.GetNumSlots());
+  res = std::move(out);
+}
+
+void Context<uint32_t>::RelinearizeRescale(Ct &res, const Ct &a,
+                                           const Evk &key) const {
+  AssertTrue(a.HasRx(), "RelinearizeRescale requires aux");
+  const int level = param_.NPToLevel(a.GetNP());
+  const int n = param_.degree_;
+  const int num_q = a.GetNP().GetNumQ();
+  const int total = num_q + param_.alpha_;
+  Ct out(param_.LevelToNP(level - 1));
+  Scratch acc(static_cast<size_t>(2) * total * n);
+  KeyMultNoModDownV(level, acc.data(), acc.data() + static_cast<size_t>(total) * n,
+                    a.rx_.data(), a.bx_.data(), a.ax_.data(), RefOf(key));
+  const auto &ms = mod_switch_handlers_.at(level);
+  DvView<word> db = out.bx_.View(), da = out.ax_.View();
+  ms.ModDownAndRescale(
+      db, DvConstView<word>(acc.data(), total * n, param_.alpha_ * n));
+  ms.ModDownAndRescale(
+      da, DvConstView<word>(acc.data() + static_cast<size_t>(total) * n,
+                            total * n, param_.alpha_ * n));
+  out.SetScale(a.GetScale() / param_.GetRescalePrimeProd(level));
+  out.SetNumSlots(a.GetNumSlots());
+  res = std::move(out);
+}
+
+void Context<uint32_t>::HMult(Ct &res, const Ct &a, const Ct &b,
+                              const Evk &mult_key, bool rescale) const {
+  Mult(res, a, b);
+  if (rescale)
+    RelinearizeRescale(res, res, mult_key);
+  else
+    Relinearize(res, res, mult_key);
+}
+
+void Context<uint32_t>::MultKey(Ct &res, const Ct &a, const Evk &key) const {
+  const int level = param_.NPToLevel(a.GetNP());
+  Ct out(a.GetNP());
+  MultKeyV(level, {out.bx_.data(), out.ax_.data(), nullptr},
+           {a.bx_.data(), a.ax_.data(), nullptr}, RefOf(key));
+  out.SetScale(a.GetScale());
+  out.SetNumSlots(a.GetNumSlots());
+  res = std::move(out);
+}
+
+void Context<uint32_t>::Rescale(Ct &res, const Ct &a) const {
+  AssertTrue(a.GetNP().num_aux_ == 0,
+             "Rescale is not supported for ciphertexts with p primes");
+  const int level = param_.NPToLevel(a.GetNP());
+  AssertTrue(level > 0, "Not enough q primes to rescale");
+  Ct out(param_.LevelToNP(level - 1), a.HasRx());
+  RescaleV(level, {out.bx_.data(), out.ax_.data(),
+                   a.HasRx() ? out.rx_.data() : nullptr},
+           {a.bx_.data(), a.ax_.data(), a.HasRx() ? a.rx_.data() : nullptr});
+  out.SetNumSlots(a.GetNumSlots());
+  out.SetScale(a.GetScale() / param_.GetRescalePrimeProd(level));
+  res = std::move(out);
+}
+
+void Context<uint32_t>::Permute(Ct &res, const Ct &a, int rot_dist) const {
+  int slots = a.GetNumSlots();
+  int r = rot_dist % slots;
+  if (r < 0) r += slots;
+  const int level = param_.NPToLevel(a.GetNP());
+  Ct out(a.GetNP());
+  if (r == 0) {
+    const size_t bytes = a.bx_.size() * sizeof(word);
+    HipCheck(hipMemcpyAsync(out.bx_.data(), a.bx_.data(), bytes,
+                            hipMemcpyDeviceToDevice, CurrentStream()),
+             "hipMemcpyAsync");
+    HipCheck(hipMemcpyAsync(out.ax_.data(), a.ax_.data(), bytes,
+                            hipMemcpyDeviceToDevice, CurrentStream()),
+             "hipMemcpyAsync");
+  } else {
+    PermuteV(level, {out.bx_.data(), out.ax_.data(), nullptr},
+             {a.bx_.data(), a.ax_.data(), nullptr}, r);
+  }
+  out.SetNumSlots(a.GetNumSlots());
+  out.SetScale(a.GetScale());
+  res = std::move(out);
+}
+
+// src/core/Context.cpp:776-791: key switch first, then permute
+void Context<uint32_t>::HRot(Ct &res, const Ct &a, const Evk &rot_key,
+                             int rot_dist) const {
+  int slots = a.GetNumSlots();
+  int r = rot_dist % slots;
+  if (r < 0) r += slots;
+  Ct tmp;
+  if (r == 0) {
+    Permute(res, a, 0);
+    return;
+  }
+  MultKey(tmp, a, rot_key);
+  Permute(res, tmp, r);
+}
+
+}  // namespace cheddar

@@ -1,0 +1,397 @@
+// C++ host API of the MI355X key-switch path, mirroring the reference's
+// classes and entry points so existing callers compile against it:
+//   Parameter          include/core/Parameter.h:22-253
+//   NPInfo             include/core/NPInfo.h
+//   DvView/DeviceVector include/core/DeviceVector.h:27-125
+//   Ciphertext/EvaluationKey include/core/Container.h:132-345
+//   NTTHandler         include/core/NTT.h:56-81
+//   ModSwitchHandler   include/core/ModSwitch.h:40-44
+//   ElementWiseHandler include/core/ElementWise.h:88-109 (key-switch subset)
+//   Context            include/core/Context.h:70-423 (key-switch subset)
+// Only word = uint32_t is provided, N = 2^16, no terminal primes (a
+// Parameter with terminal primes is rejected with an error).
+// Failures throw cheddar::Error (the reference prints and exits); the C-ABI
+// (include/cheddar_amd.h) converts them into status codes.
+// Kernels are reached through the kernel C-ABI (include/cheddar_kernels.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "cheddar_kernels.h"
+#include "device_tables.h"
+
+namespace cheddar {
+
+struct Error : std::runtime_error {
+  explicit Error(const std::string &m) : std::runtime_error(m) {}
+};
+inline void AssertTrue(bool c, const std::string &msg) {
+  if (!c) throw Error("ERROR: " + msg);
+}
+[[noreturn]] inline void Fail(const std::string &msg) {
+  throw Error("ERROR: " + msg);
+}
+
+// Stream the library launches on (the reference uses the legacy default
+// stream; the C-ABI sets the caller's stream for the duration of a call).
+hipStream_t CurrentStream();
+class StreamScope {
+ public:
+  explicit StreamScope(hipStream_t s);
+  ~StreamScope();
+
+ private:
+  hipStream_t prev_;
+};
+
+struct NPInfo {
+  int num_main_ = 0;
+  int num_ter_ = 0;
+  int num_aux_ = 0;
+  explicit NPInfo(int num_main = 0, int num_ter = 0, int num_aux = 0);
+  int GetNumQ() const { return num_main_ + num_ter_; }
+  int GetNumTotal() const { return num_main_ + num_ter_ + num_aux_; }
+  bool operator==(const NPInfo &o) const {
+    return num_main_ == o.num_main_ && num_ter_ == o.num_ter_ &&
+           num_aux_ == o.num_aux_;
+  }
+  bool IsSubsetOf(const NPInfo &o) const {
+    return num_main_ <= o.num_main_ && num_ter_ <= o.num_ter_ &&
+           num_aux_ <= o.num_aux_;
+  }
+};
+
+template <typename word>
+class Parameter;
+
+template <>
+class Parameter<uint32_t> {
+ public:
+  using word = uint32_t;
+  Parameter(int log_degree, double base_scale, int default_encryption_level,
+            std::vector<std::pair<int, int>> level_config,
+            const std::vector<word> &main_primes,
+            const std::vector<word> &aux_primes,
+            const std::vector<word> &ter_primes = std::vector<word>{},
+            const std::pair<int, int> &additional_base = {0, 0});
+
+  const int log_degree_;
+  const int degree_;
+  const int dnum_;
+  const int L_;
+  const int alpha_;
+  const double base_scale_;
+  const int default_encryption_level_;
+  const int max_level_;
+
+  NPInfo LevelToNP(int level, int num_aux = 0) const;
+  int NPToLevel(const NPInfo &np) const;
+  std::vector<word> GetPrimeVector(const NPInfo &np) const;
+  int GetMaxNumMain() const { return static_cast<int>(main_primes_.size()); }
+  int GetMaxNumTer() const { return static_cast<int>(ter_primes_.size()); }
+  int GetMaxNumAux() const { return alpha_; }
+  int GetGaloisFactor(int rot) const;
+  double GetScale(int level) const;
+  double GetRescalePrimeProd(int level) const;
+  // chain position of limb 0 of np / aux gap (the reference's ter_left and
+  // main_left, src/core/NTT.cu:620-621)
+  int TerLeft(const NPInfo &np) const { return GetMaxNumTer() - np.num_ter_; }
+  int MainLeft(const NPInfo &np) const {
+    return GetMaxNumMain() - np.num_main_;
+  }
+  // the full chain: ter reversed, main, aux (Parameter.cu:103-111)
+  const std::vector<word> &ChainPrimes() const { return chain_; }
+
+ private:
+  std::vector<word> main_primes_, ter_primes_, aux_primes_;
+  std::vector<std::pair<int, int>> level_config_;
+  std::vector<word> chain_;
+  std::vector<int> galois_factors_;
+  std::vector<double> scale_, rescale_prime_prod_;
+};
+
+// Non-owning views: (pointer, total words, aux words) (DeviceVector.h:27-72)
+template <typename word>
+class DvView {
+ public:
+  DvView(word *p = nullptr, int total = 0, int aux = 0)
+      : p_(p), total_(total), aux_(aux) {}
+  word *data() const { return p_; }
+  int TotalSize() const { return total_; }
+  int AuxSize() const { return aux_; }
+  int QSize() const { return total_ - aux_; }
+
+ private:
+  word *p_;
+  int total_, aux_;
+};
+
+template <typename word>
+class DvConstView {
+ public:
+  DvConstView(const word *p = nullptr, int total = 0, int aux = 0)
+      : p_(p), total_(total), aux_(aux) {}
+  DvConstView(const DvView<word> &v)  // NOLINT: implicit like the reference
+      : p_(v.data()), total_(v.TotalSize()), aux_(v.AuxSize()) {}
+  const word *data() const { return p_; }
+  int TotalSize() const { return total_; }
+  int AuxSize() const { return aux_; }
+  int QSize() const { return total_ - aux_; }
+
+ private:
+  const word *p_;
+  int total_, aux_;
+};
+
+// Owning device vector (hipMalloc; the reference uses an RMM pool).
+template <typename word>
+class DeviceVector {
+ public:
+  DeviceVector() = default;
+  explicit DeviceVector(size_t n) { resize(n); }
+  void resize(size_t n) {
+    buf_.Resize(n * sizeof(word));
+    n_ = n;
+  }
+  size_t size() const { return n_; }
+  word *data() { return buf_.as<word>(); }
+  const word *data() const { return buf_.as<word>(); }
+  DvView<word> View(int aux_size = 0, int front = 0) {
+    return DvView<word>(data() + front, static_cast<int>(n_) - front, aux_size);
+  }
+  DvConstView<word> ConstView(int aux_size = 0, int front = 0) const {
+    return DvConstView<word>(data() + front, static_cast<int>(n_) - front,
+                             aux_size);
+  }
+
+ private:
+  DevBuf buf_;
+  size_t n_ = 0;
+};
+
+template <typename word>
+class Ciphertext;
+template <>
+class Ciphertext<uint32_t> {
+ public:
+  using word = uint32_t;
+  explicit Ciphertext(const NPInfo &np = NPInfo{}, bool has_rx = false);
+  DeviceVector<word> bx_, ax_, rx_;
+  bool HasRx() const { return rx_.size() != 0; }
+  void PrepareRx();
+  void RemoveRx();
+  NPInfo GetNP() const { return np_; }
+  void ModifyNP(const NPInfo &np);
+  int GetNumSlots() const { return num_slots_; }
+  void SetNumSlots(int n) { num_slots_ = n; }
+  double GetScale() const { return scale_; }
+  void SetScale(double s) { scale_ = s; }
+  static void SetDegree(int degree) { degree_ = degree; }
+
+ private:
+  static inline int degree_ = 1 << 16;
+  NPInfo np_;
+  int num_slots_ = (1 << 16) / 2;
+  double scale_ = 1.0;
+};
+
+template <typename word>
+class EvaluationKey;
+template <>
+class EvaluationKey<uint32_t> {
+ public:
+  using word = uint32_t;
+  EvaluationKey(const NPInfo &np, int beta, int degree = 1 << 16);
+  std::vector<DeviceVector<word>> bx_, ax_;
+  int GetBeta() const { return static_cast<int>(bx_.size()); }
+  NPInfo GetNP() const { return np_; }
+
+ private:
+  NPInfo np_;
+};
+
+template <typename word>
+class NTTHandler;
+template <>
+class NTTHandler<uint32_t> {
+ public:
+  using word = uint32_t;
+  explicit NTTHandler(const Parameter<word> &param);
+  void NTT(DvView<word> &dst, const NPInfo &np, const DvConstView<word> &src,
+           bool montgomery_conversion = false) const;
+  void INTT(DvView<word> &dst, const NPInfo &np, const DvConstView<word> &src,
+            bool montgomery_conversion = true) const;
+  void INTTAndMultConst(DvView<word> &dst, const NPInfo &np,
+                        const DvConstView<word> &src,
+                        const DvConstView<word> &src_const,
+                        bool normalize = false) const;
+  void NTTForModUp(DvView<word> &dst, const NPInfo &np, int skip_start,
+                   int skip_end, const DvConstView<word> &src) const;
+  void NTTForModDown(DvView<word> &dst, const NPInfo &np_src1,
+                     const NPInfo &np_src2, const DvConstView<word> &src1,
+                     const DvConstView<word> &src2,
+                     const DvConstView<word> &inv_p_prod,
+                     const DvConstView<word> &src2_padding =
+                         DvConstView<word>(nullptr, 0)) const;
+  void INTTForModDown(DvView<word> &dst, const NPInfo &np_src,
+                      const NPInfo &np_non_intt, const DvConstView<word> &src,
+                      const DvConstView<word> &src_const) const;
+  const chd_tables &Tables() const { return chain_.tables(); }
+
+ private:
+  chd_limb_map Map(const NPInfo &np) const;
+  const Parameter<word> &param_;
+  ChainTables chain_;
+};
+
+template <typename word>
+class ElementWiseHandler;
+template <>
+class ElementWiseHandler<uint32_t> {
+ public:
+  using word = uint32_t;
+  ElementWiseHandler(const Parameter<word> &param,
+                     const NTTHandler<word> &ntt);
+  void Tensor(std::vector<DvView<word>> &dst, const NPInfo &np,
+              const std::vector<DvConstView<word>> &src1,
+              const std::vector<DvConstView<word>> &src2) const;
+  void PAccum(std::vector<DvView<word>> &dst, const NPInfo &np,
+              const std::vector<std::vector<DvConstView<word>>> &ct_srcs,
+              const std::vector<DvConstView<word>> &common_srcs) const;
+  void CAccum(std::vector<DvView<word>> &dst, const NPInfo &np,
+              const std::vector<std::vector<DvConstView<word>>> &ct_srcs,
+              const std::vector<DvConstView<word>> &common_srcs) const;
+  void Permute(std::vector<DvView<word>> &dst, const NPInfo &np,
+               int permute_amount,
+               const std::vector<DvConstView<word>> &src1) const;
+  uint32_t PermuteAmountToGaloisFactor(int permute_amount) const;
+
+ private:
+  void CPAccumWorker(bool const_accum, std::vector<DvView<word>> &dst,
+                     const NPInfo &np,
+                     const std::vector<std::vector<DvConstView<word>>> &ct_srcs,
+                     const std::vector<DvConstView<word>> &common_srcs) const;
+  const Parameter<word> &param_;
+  const NTTHandler<word> &ntt_;
+};
+
+template <typename word>
+class ModSwitchHandler;
+template <>
+class ModSwitchHandler<uint32_t> {
+ public:
+  using word = uint32_t;
+  ModSwitchHandler(const Parameter<word> &param, int level,
+                   const ElementWiseHandler<word> &elem,
+                   const NTTHandler<word> &ntt);
+  void ModUp(std::vector<DvView<word>> &dst,
+             const DvConstView<word> &src) const;
+  void ModDown(DvView<word> &dst, const DvConstView<word> &src) const;
+  void Rescale(DvView<word> &dst, const DvConstView<word> &src) const;
+  void ModDownAndRescale(DvView<word> &dst,
+                         const DvConstView<word> &src) const;
+  int GetBeta() const { return beta_; }
+
+ private:
+  enum class Kind { ModDown, Rescale, ModDownAndRescale };
+  struct SwitchTable {       // one source set -> destination set
+    DeviceVector<word> const1;   // (N prod_{j!=i} s_j)^-1 mod s_i
+    DevBuf table;                // packed BConv table (chd_bconv_table_pack)
+    int src_len = 0, dst_len = 0;
+  };
+  void BuildSwitch(SwitchTable &st, const std::vector<word> &src,
+                   const std::vector<word> &dst) const;
+  void ModDownWorker(DvView<word> &dst, const DvConstView<word> &src,
+                     Kind kind) const;
+  const int level_;
+  const int num_aux_;
+  const int beta_;
+  const Parameter<word> &param_;
+  const ElementWiseHandler<word> &elem_;
+  const NTTHandler<word> &ntt_;
+  DeviceVector<word> mod_up1_;
+  std::vector<SwitchTable> mod_up_;
+  SwitchTable mod_down_, rescale_, mod_down_rescale_;
+  DeviceVector<word> inv_prime_prod_, rescale_inv_prime_prod_,
+      mod_down_rescale_inv_prime_prod_, rescale_padding_,
+      mod_down_rescale_padding_;
+};
+
+template <typename word>
+class Context;
+template <>
+class Context<uint32_t> {
+ public:
+  using word = uint32_t;
+  using Ct = Ciphertext<word>;
+  using Evk = EvaluationKey<word>;
+  static std::shared_ptr<Context<word>> Create(const Parameter<word> &param);
+
+  // reference entry points (Context.h:302-423)
+  void Mult(Ct &res, const Ct &a, const Ct &b) const;
+  void HMult(Ct &res, const Ct &a, const Ct &b, const Evk &mult_key,
+             bool rescale = true) const;
+  void Relinearize(Ct &res, const Ct &a, const Evk &key) const;
+  void RelinearizeRescale(Ct &res, const Ct &a, const Evk &key) const;
+  void MultKey(Ct &res, const Ct &a, const Evk &key) const;
+  void Rescale(Ct &res, const Ct &a) const;
+  void HRot(Ct &res, const Ct &a, const Evk &rot_key, int rot_dist) const;
+  void Permute(Ct &res, const Ct &a, int rot_dist) const;
+
+  // view-level core used by the C++ API above and by the C-ABI
+  struct CtRef {           // polynomials of num_q limbs (rx optional)
+    word *bx = nullptr, *ax = nullptr, *rx = nullptr;
+  };
+  struct CtCRef {
+    const word *bx = nullptr, *ax = nullptr, *rx = nullptr;
+  };
+  struct EvkRef {          // beta pairs of evk_limbs limbs each
+    std::vector<const word *> bx, ax;
+    NPInfo np;
+  };
+  void TensorV(int level, CtRef res, CtCRef a, CtCRef b) const;
+  // accum (b, a) of num_q + alpha limbs = KS of d, plus p_prod * (cb, ca)
+  void KeyMultNoModDownV(int level, word *acc_b, word *acc_a, const word *d,
+                         const word *cb, const word *ca,
+                         const EvkRef &key) const;
+  void HMultV(int level, CtRef res, CtCRef a, CtCRef b, const EvkRef &key,
+              bool rescale) const;
+  void RescaleV(int level, CtRef res, CtCRef a) const;
+  void MultKeyV(int level, CtRef res, CtCRef a, const EvkRef &key) const;
+  void PermuteV(int level, CtRef res, CtCRef a, int galois_amount) const;
+
+  const Parameter<word> &param_;
+  ElementWiseHandler<word> elem_handler_;
+  NTTHandler<word> ntt_handler_;
+  std::vector<ModSwitchHandler<word>> mod_switch_handlers_;
+
+ private:
+  explicit Context(const Parameter<word> &param);
+  DvConstView<word> GetPProd(const NPInfo &np) const;
+  DeviceVector<word> p_prod_;
+};
+
+// Stream-ordered scratch allocation (hipMallocAsync / hipFreeAsync on the
+// current stream), the counterpart of the reference's per-call RMM
+// temporaries (ModSwitch.cu:442,597; Context.cpp:670-682).
+class Scratch {
+ public:
+  explicit Scratch(size_t words);
+  ~Scratch();
+  Scratch(const Scratch &) = delete;
+  Scratch &operator=(const Scratch &) = delete;
+  uint32_t *data() const { return p_; }
+
+ private:
+  uint32_t *p_ = nullptr;
+  hipStream_t s_;
+};
+
+}  // namespace cheddar

@@ -1,0 +1,96 @@
+#include "device_tables.h"
+
+#include "prime_math.h"
+
+namespace cheddar {
+
+void HipCheck(hipError_t e, const char *what) {
+  if (e != hipSuccess)
+    throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void DevBuf::Resize(size_t bytes) {
+  if (bytes == bytes_) return;
+  Release();
+  if (bytes == 0) return;
+  HipCheck(hipMalloc(&ptr_, bytes), "hipMalloc");
+  bytes_ = bytes;
+}
+
+void DevBuf::Upload(const void *host, size_t bytes) {
+  if (bytes > bytes_) throw std::runtime_error("DevBuf::Upload: overflow");
+  HipCheck(hipMemcpy(ptr_, host, bytes, hipMemcpyHostToDevice), "hipMemcpy");
+}
+
+void DevBuf::Release() {
+  if (ptr_ != nullptr) (void)hipFree(ptr_);
+  ptr_ = nullptr;
+  bytes_ = 0;
+}
+
+ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
+    : log_degree_(log_degree), primes_(primes) {
+  if (log_degree != 16)
+    throw std::invalid_argument("only log_degree 16 is supported");
+  const int n = 1 << log_degree;
+  const size_t T = primes.size();
+  std::vector<int32_t> qinv(T);
+  std::vector<double> qd(T), qinvd(T);
+  std::vector<uint32_t> rinv(T), ninv(T), ninv_mont(T), r2(T);
+  std::vector<double> tw_lo(T * 512), itw_lo(T * 512);
+  std::vector<uint32_t> tw(T * n), itw(T * n);
+  for (size_t i = 0; i < T; i++) {
+    const uint32_t q = primes[i];
+    if (q >= (1u << 31) || q % (2u * n) != 1)
+      throw std::invalid_argument("prime " + std::to_string(q) +
+                                  " is not an NTT-friendly prime below 2^31");
+    qinv[i] = pm::inv_mod_base(q);
+    qd[i] = static_cast<double>(q);
+    qinvd[i] = 1.0 / static_cast<double>(q);
+    rinv[i] = pm::invmod(static_cast<uint32_t>((1ull << 32) % q), q);
+    ninv[i] = pm::invmod(static_cast<uint32_t>(n % q), q);
+    ninv_mont[i] = pm::to_mont(ninv[i], q);
+    r2[i] = pm::to_mont(pm::to_mont(1, q), q);
+    const uint32_t psi = pm::primitive_root(2u * n, q);
+    const uint32_t psi_inv = pm::invmod(psi, q);
+    uint64_t p = 1, pi = 1;
+    uint32_t *t = tw.data() + i * n;
+    uint32_t *it = itw.data() + i * n;
+    for (int j = 0; j < n; j++) {
+      const uint32_t r = pm::bitrev(static_cast<uint32_t>(j), log_degree);
+      t[r] = static_cast<uint32_t>(p);
+      it[r] = static_cast<uint32_t>(pi);
+      p = p * psi % q;
+      pi = pi * psi_inv % q;
+    }
+    for (int j = 0; j < 256; j++) {
+      tw_lo[i * 512 + 2 * j] = static_cast<double>(t[j]);
+      tw_lo[i * 512 + 2 * j + 1] = static_cast<double>(t[j]) / qd[i];
+      itw_lo[i * 512 + 2 * j] = static_cast<double>(it[j]);
+      itw_lo[i * 512 + 2 * j + 1] = static_cast<double>(it[j]) / qd[i];
+    }
+  }
+  q_.Upload(primes);
+  qinv_.Upload(qinv);
+  qd_.Upload(qd);
+  qinvd_.Upload(qinvd);
+  rinv_.Upload(rinv);
+  tw_lo_.Upload(tw_lo);
+  itw_lo_.Upload(itw_lo);
+  tw_.Upload(tw);
+  itw_.Upload(itw);
+  ninv_.Upload(ninv);
+  ninv_mont_.Upload(ninv_mont);
+  r2_.Upload(r2);
+  tab_.q = q_.as<uint32_t>();
+  tab_.qinv = qinv_.as<int32_t>();
+  tab_.qd = qd_.as<double>();
+  tab_.qinvd = qinvd_.as<double>();
+  tab_.rinv = rinv_.as<uint32_t>();
+  tab_.tw_lo = tw_lo_.as<void>();
+  tab_.itw_lo = itw_lo_.as<void>();
+  tab_.tw = tw_.as<uint32_t>();
+  tab_.itw = itw_.as<uint32_t>();
+}
+
+}  // namespace cheddar

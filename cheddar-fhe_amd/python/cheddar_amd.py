@@ -1,0 +1,251 @@
+"""ctypes binding of libcheddar_amd.so (include/cheddar_amd.h).
+
+Device buffers are torch tensors on the HIP device (torch is only the
+allocator and stream provider here). Every function raises ChdError with
+the library's message on a non-zero status. Importing this module fails
+loudly if the HIP library has not been built.
+"""
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG, "lib", "libcheddar_amd.so")
+LOG_N = 16
+N = 1 << LOG_N
+
+
+class ChdError(RuntimeError):
+    pass
+
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError("libcheddar_amd.so is not built: run "
+                      "python cheddar-fhe_amd/build.py")
+
+_c_u32p = ctypes.POINTER(ctypes.c_uint32)
+_c_i32p = ctypes.POINTER(ctypes.c_int32)
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_pp = ctypes.POINTER(ctypes.c_void_p)
+
+lib = ctypes.CDLL(LIB_PATH)
+_SIGS = {
+    "chd_last_error": (ctypes.c_char_p, []),
+    "chd_version": (ctypes.c_char_p, []),
+    "chd_ntt_plan_create": (_i, [_pp, _i, _c_u32p, _i]),
+    "chd_ntt_plan_destroy": (None, [_vp]),
+    "chd_ntt_plan_tables": (_vp, [_vp]),
+    "chd_ntt_forward": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "chd_ntt_inverse": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "chd_bconv_plan_create": (_i, [_pp, _i, _c_u32p, _i, _c_u32p, _i]),
+    "chd_bconv_plan_destroy": (None, [_vp]),
+    "chd_bconv_plan_constants": (_i, [_vp, _c_u32p, _c_i32p]),
+    "chd_bconv_apply": (_i, [_vp, _vp, _vp, _vp]),
+    "chd_param_create": (_i, [_pp, _i, ctypes.c_double, _i,
+                              ctypes.POINTER(ctypes.c_int), _i, _c_u32p, _i,
+                              _c_u32p, _i, _c_u32p, _i]),
+    "chd_param_destroy": (None, [_vp]),
+    "chd_param_num_q": (_i, [_vp, _i]),
+    "chd_param_alpha": (_i, [_vp]),
+    "chd_param_max_level": (_i, [_vp]),
+    "chd_param_evk_limbs": (_i, [_vp]),
+    "chd_context_create": (_i, [_pp, _vp]),
+    "chd_context_destroy": (None, [_vp]),
+    "chd_context_beta": (_i, [_vp, _i]),
+    "chd_tensor": (_i, [_vp, _i] + [_vp] * 7 + [_vp]),
+    "chd_mod_up": (_i, [_vp, _i, _pp, _vp, _vp]),
+    "chd_mod_down": (_i, [_vp, _i, _vp, _vp, _vp]),
+    "chd_rescale_poly": (_i, [_vp, _i, _vp, _vp, _vp]),
+    "chd_mod_down_and_rescale": (_i, [_vp, _i, _vp, _vp, _vp]),
+    "chd_hmult": (_i, [_vp, _i] + [_vp] * 6 + [_pp, _pp, _i, _i, _vp]),
+    "chd_rescale": (_i, [_vp, _i] + [_vp] * 4 + [_vp]),
+    "chd_mult_key": (_i, [_vp, _i] + [_vp] * 4 + [_pp, _pp, _i, _vp]),
+    "chd_hrot": (_i, [_vp, _i] + [_vp] * 4 + [_pp, _pp, _i, _i, _i, _vp]),
+    "chd_permute": (_i, [_vp, _i] + [_vp] * 4 + [_i, _vp]),
+}
+for _name, (_res, _args) in _SIGS.items():
+    _f = getattr(lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+
+def _check(status):
+    if status != 0:
+        raise ChdError(lib.chd_last_error().decode())
+
+
+def _u32_array(vals):
+    return (ctypes.c_uint32 * len(vals))(*[int(v) for v in vals])
+
+
+def ptr(t):
+    """device pointer of a torch tensor (or None)"""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def ptr_array(ts):
+    return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+
+
+def current_stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class NttPlan:
+    """standalone NTT over an explicit prime chain (configs 1-2)"""
+
+    def __init__(self, primes, log_n=LOG_N):
+        self.primes = [int(p) for p in primes]
+        h = ctypes.c_void_p()
+        _check(lib.chd_ntt_plan_create(ctypes.byref(h), log_n,
+                                       _u32_array(self.primes),
+                                       len(self.primes)))
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib.chd_ntt_plan_destroy(self.h)
+            self.h = None
+
+    def forward(self, dst, src, num_limbs, num_polys=1, mont_conv=False,
+                stream=None):
+        _check(lib.chd_ntt_forward(self.h, ptr(dst), ptr(src), num_limbs,
+                                   num_polys, int(bool(mont_conv)),
+                                   stream if stream is not None else
+                                   current_stream()))
+
+    def inverse(self, dst, src, num_limbs, num_polys=1, mont_conv=True,
+                stream=None):
+        _check(lib.chd_ntt_inverse(self.h, ptr(dst), ptr(src), num_limbs,
+                                   num_polys, int(bool(mont_conv)),
+                                   stream if stream is not None else
+                                   current_stream()))
+
+
+class BconvPlan:
+    """standalone BConv src primes -> dst primes (config 3)"""
+
+    def __init__(self, src_primes, dst_primes, log_n=LOG_N):
+        self.src = [int(p) for p in src_primes]
+        self.dst = [int(p) for p in dst_primes]
+        h = ctypes.c_void_p()
+        _check(lib.chd_bconv_plan_create(ctypes.byref(h), log_n,
+                                         _u32_array(self.src), len(self.src),
+                                         _u32_array(self.dst), len(self.dst)))
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib.chd_bconv_plan_destroy(self.h)
+            self.h = None
+
+    def constants(self):
+        import numpy as np
+        c1 = np.zeros(len(self.src), np.uint32)
+        c2 = np.zeros(len(self.src) * len(self.dst), np.int32)
+        _check(lib.chd_bconv_plan_constants(
+            self.h, c1.ctypes.data_as(_c_u32p), c2.ctypes.data_as(_c_i32p)))
+        return c1, c2.reshape(len(self.dst), len(self.src))
+
+    def apply(self, dst, src_centred, stream=None):
+        _check(lib.chd_bconv_apply(self.h, ptr(dst), ptr(src_centred),
+                                   stream if stream is not None else
+                                   current_stream()))
+
+
+class Param:
+    def __init__(self, main_primes, aux_primes, level_config,
+                 default_encryption_level=None, base_scale=float(1 << 30),
+                 log_n=LOG_N):
+        lc = [int(v) for pair in level_config for v in pair]
+        dl = (len(level_config) - 1 if default_encryption_level is None
+              else default_encryption_level)
+        h = ctypes.c_void_p()
+        _check(lib.chd_param_create(
+            ctypes.byref(h), log_n, base_scale, dl,
+            (ctypes.c_int * len(lc))(*lc), len(level_config),
+            _u32_array(main_primes), len(main_primes),
+            _u32_array(aux_primes), len(aux_primes), None, 0))
+        self.h = h
+        self.main = [int(p) for p in main_primes]
+        self.aux = [int(p) for p in aux_primes]
+        self.alpha = lib.chd_param_alpha(h)
+        self.max_level = lib.chd_param_max_level(h)
+        self.evk_limbs = lib.chd_param_evk_limbs(h)
+
+    def num_q(self, level):
+        return lib.chd_param_num_q(self.h, level)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib.chd_param_destroy(self.h)
+            self.h = None
+
+
+class Context:
+    def __init__(self, param):
+        self.param = param
+        h = ctypes.c_void_p()
+        _check(lib.chd_context_create(ctypes.byref(h), param.h))
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib.chd_context_destroy(self.h)
+            self.h = None
+
+    def beta(self, level):
+        return lib.chd_context_beta(self.h, level)
+
+    def _s(self, stream):
+        return stream if stream is not None else current_stream()
+
+    def tensor(self, level, res, a, b, stream=None):
+        _check(lib.chd_tensor(self.h, level, *[ptr(t) for t in res],
+                              *[ptr(t) for t in a], *[ptr(t) for t in b],
+                              self._s(stream)))
+
+    def mod_up(self, level, dst_list, src, stream=None):
+        _check(lib.chd_mod_up(self.h, level, ptr_array(dst_list), ptr(src),
+                              self._s(stream)))
+
+    def mod_down(self, level, dst, src, stream=None):
+        _check(lib.chd_mod_down(self.h, level, ptr(dst), ptr(src),
+                                self._s(stream)))
+
+    def rescale_poly(self, level, dst, src, stream=None):
+        _check(lib.chd_rescale_poly(self.h, level, ptr(dst), ptr(src),
+                                    self._s(stream)))
+
+    def mod_down_and_rescale(self, level, dst, src, stream=None):
+        _check(lib.chd_mod_down_and_rescale(self.h, level, ptr(dst), ptr(src),
+                                            self._s(stream)))
+
+    def hmult(self, level, res, a, b, evk_b, evk_a, rescale=True,
+              stream=None):
+        _check(lib.chd_hmult(self.h, level, ptr(res[0]), ptr(res[1]),
+                             ptr(a[0]), ptr(a[1]), ptr(b[0]), ptr(b[1]),
+                             ptr_array(evk_b), ptr_array(evk_a), len(evk_b),
+                             int(bool(rescale)), self._s(stream)))
+
+    def rescale(self, level, res, a, stream=None):
+        _check(lib.chd_rescale(self.h, level, ptr(res[0]), ptr(res[1]),
+                               ptr(a[0]), ptr(a[1]), self._s(stream)))
+
+    def mult_key(self, level, res, a, evk_b, evk_a, stream=None):
+        _check(lib.chd_mult_key(self.h, level, ptr(res[0]), ptr(res[1]),
+                                ptr(a[0]), ptr(a[1]), ptr_array(evk_b),
+                                ptr_array(evk_a), len(evk_b),
+                                self._s(stream)))
+
+    def hrot(self, level, res, a, evk_b, evk_a, rot, num_slots=N // 2,
+             stream=None):
+        _check(lib.chd_hrot(self.h, level, ptr(res[0]), ptr(res[1]),
+                            ptr(a[0]), ptr(a[1]), ptr_array(evk_b),
+                            ptr_array(evk_a), len(evk_b), rot, num_slots,
+                            self._s(stream)))
+
+    def permute(self, level, res, a, rot, stream=None):
+        _check(lib.chd_permute(self.h, level, ptr(res[0]), ptr(res[1]),
+                               ptr(a[0]), ptr(a[1]), rot, self._s(stream)))

@@ -1,0 +1,166 @@
+/*
+ * Public C-ABI of the MI355X-native CKKS key-switch path.
+ *
+ * This is the drop-in boundary a foreign caller binds (ctypes / cgo / JNI):
+ * plain pointers and sizes, device pointers for ciphertext data, an explicit
+ * stream (hipStream_t passed as void*, NULL = the null stream, which is the
+ * reference's only stream). The functions wrap the C++ classes of
+ * cheddar-fhe_amd/host (cheddar::Parameter, Context, ...), which keep the
+ * reference's C++ API (include/core/Parameter.h:42-47, Context.h:70-423).
+ *
+ * Conventions (identical to the reference):
+ *  - u32 residues, primes q < 2^31, q = 1 mod 2N, N = 2^16;
+ *  - limb-major polynomials u32[limbs][N], limb order ter (reversed), main,
+ *    aux (include/core/Parameter.h:198-206);
+ *  - ciphertext and key data in the NTT domain, Montgomery form (x 2^32);
+ *  - an evaluation key is beta pairs (bx_g, ax_g), each of
+ *    (max main + max ter + alpha) limbs (include/core/Container.h:289-345).
+ * Every call returns CHD_OK (0) or a negative status; chd_last_error()
+ * returns the message of the last failure on the calling thread. No call
+ * exits the process (the reference's AssertTrue -> exit(1) becomes a status).
+ * Calls that overlap on one stream are ordered by it; a Context is not
+ * thread-safe (as in the reference).
+ */
+#ifndef CHEDDAR_AMD_H
+#define CHEDDAR_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CHD_OK 0
+#define CHD_ERR_INVALID_ARGUMENT (-1)
+#define CHD_ERR_HIP (-2)
+#define CHD_ERR_STATE (-3)
+#define CHD_ERR_ALLOC (-4)
+
+const char *chd_last_error(void);
+const char *chd_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* standalone NTT over an explicit prime chain (configs 1-2)               */
+/* replaces NTTHandler::NTT / INTT (include/core/NTT.h:56-61)              */
+/* ---------------------------------------------------------------------- */
+typedef struct chd_ntt_plan chd_ntt_plan;
+int chd_ntt_plan_create(chd_ntt_plan **out, int log_degree,
+                        const uint32_t *primes, int num_primes);
+void chd_ntt_plan_destroy(chd_ntt_plan *plan);
+/* device tables of the plan (for the kernel-level ABI, cheddar_kernels.h) */
+const void *chd_ntt_plan_tables(const chd_ntt_plan *plan);
+/* [num_polys][num_limbs][N]; limb i uses prime i of the plan.
+ * forward: natural -> bit-reversed, mont_conv multiplies by 2^32 first.
+ * inverse: mont_conv=1 returns intt * 2^-32 (the reference's default),
+ *          0 returns intt exactly. dst may equal src. */
+int chd_ntt_forward(const chd_ntt_plan *plan, uint32_t *dst,
+                    const uint32_t *src, int num_limbs, int num_polys,
+                    int mont_conv, void *stream);
+int chd_ntt_inverse(const chd_ntt_plan *plan, uint32_t *dst,
+                    const uint32_t *src, int num_limbs, int num_polys,
+                    int mont_conv, void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* standalone BConv between explicit prime sets (config 3)                 */
+/* replaces ModSwitchMatrixMult (src/core/ModSwitch.cu:23-171) with the    */
+/* table of PopulateModSwitchConstants (ModSwitch.cu:320-370)              */
+/* ---------------------------------------------------------------------- */
+typedef struct chd_bconv_plan chd_bconv_plan;
+int chd_bconv_plan_create(chd_bconv_plan **out, int log_degree,
+                          const uint32_t *src_primes, int src_len,
+                          const uint32_t *dst_primes, int dst_len);
+void chd_bconv_plan_destroy(chd_bconv_plan *plan);
+/* host copies of the reference-form constants: const1[src_len] =
+ * (N prod_{j!=i} q_j)^-1 mod q_i, const2[dst_len][src_len] =
+ * centre(qhat_i 2^64 mod p_k) */
+int chd_bconv_plan_constants(const chd_bconv_plan *plan, uint32_t *const1,
+                             int32_t *const2);
+/* dst[k] = sum_i src[i] const2[k][i] 2^-32 mod p_k; src centred int32
+ * [src_len][N], dst [dst_len][N] */
+int chd_bconv_apply(const chd_bconv_plan *plan, uint32_t *dst,
+                    const int32_t *src, void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* Parameter / Context (include/core/Parameter.h:42-47, Context.h:70)      */
+/* ---------------------------------------------------------------------- */
+typedef struct chd_param chd_param;
+typedef struct chd_context chd_context;
+
+/* level_config: num_levels pairs (num_main, num_ter), as the JSON
+ * "level_config"; ter_primes may be NULL when num_ter == 0. */
+int chd_param_create(chd_param **out, int log_degree, double base_scale,
+                     int default_encryption_level, const int *level_config,
+                     int num_levels, const uint32_t *main_primes, int num_main,
+                     const uint32_t *aux_primes, int num_aux,
+                     const uint32_t *ter_primes, int num_ter);
+void chd_param_destroy(chd_param *param);
+/* number of q limbs (main + ter) at a level; -1 on error */
+int chd_param_num_q(const chd_param *param, int level);
+int chd_param_alpha(const chd_param *param);
+int chd_param_max_level(const chd_param *param);
+/* limb count of an evaluation key (max main + max ter + alpha) */
+int chd_param_evk_limbs(const chd_param *param);
+
+int chd_context_create(chd_context **out, const chd_param *param);
+void chd_context_destroy(chd_context *ctx);
+/* beta = number of dnum groups of ModUp at this level (ModSwitch.cu:181) */
+int chd_context_beta(const chd_context *ctx, int level);
+
+/* Polynomials below hold num_q(level) limbs unless stated; aux-extended
+ * polynomials hold num_q(level) + alpha limbs. */
+
+/* Context::Mult(Ct,Ct) -> Tensor (Context.cpp:316-330) */
+int chd_tensor(const chd_context *ctx, int level, uint32_t *res_bx,
+               uint32_t *res_ax, uint32_t *res_rx, const uint32_t *a_bx,
+               const uint32_t *a_ax, const uint32_t *b_bx,
+               const uint32_t *b_ax, void *stream);
+/* ModSwitchHandler::ModUp (ModSwitch.cu:429-509): dst[beta] each
+ * num_q + alpha limbs */
+int chd_mod_up(const chd_context *ctx, int level, uint32_t *const *dst,
+               const uint32_t *src, void *stream);
+/* ModDown: (num_q + alpha) -> num_q limbs (ModSwitch.cu:511-527) */
+int chd_mod_down(const chd_context *ctx, int level, uint32_t *dst,
+                 const uint32_t *src, void *stream);
+/* Rescale: num_q -> num_q(level-1) limbs (ModSwitch.cu:529-545) */
+int chd_rescale_poly(const chd_context *ctx, int level, uint32_t *dst,
+                     const uint32_t *src, void *stream);
+/* merged ModDownAndRescale: (num_q + alpha) -> num_q(level-1) limbs
+ * (ModSwitch.cu:547-564) */
+int chd_mod_down_and_rescale(const chd_context *ctx, int level, uint32_t *dst,
+                             const uint32_t *src, void *stream);
+
+/* HMult (Context.cpp:862-871): res = relinearize(a * b), rescaled when
+ * rescale != 0 (res then has num_q(level-1) limbs). evk_bx/evk_ax: beta
+ * device pointers, each chd_param_evk_limbs() limbs. res may alias a. */
+int chd_hmult(const chd_context *ctx, int level, uint32_t *res_bx,
+              uint32_t *res_ax, const uint32_t *a_bx, const uint32_t *a_ax,
+              const uint32_t *b_bx, const uint32_t *b_ax,
+              const uint32_t *const *evk_bx, const uint32_t *const *evk_ax,
+              int evk_beta, int rescale, void *stream);
+/* Context::Rescale of a two-polynomial ciphertext (Context.cpp:739-774) */
+int chd_rescale(const chd_context *ctx, int level, uint32_t *res_bx,
+                uint32_t *res_ax, const uint32_t *a_bx, const uint32_t *a_ax,
+                void *stream);
+/* Context::MultKey (Context.cpp:584-607): (b, a) -> (b + KS_b(a), KS_a(a)) */
+int chd_mult_key(const chd_context *ctx, int level, uint32_t *res_bx,
+                 uint32_t *res_ax, const uint32_t *a_bx, const uint32_t *a_ax,
+                 const uint32_t *const *evk_bx, const uint32_t *const *evk_ax,
+                 int evk_beta, void *stream);
+/* Context::HRot (Context.cpp:776-791): MultKey then Permute by 5^rot;
+ * num_slots as Ciphertext::GetNumSlots (N/2 for a fresh ciphertext).
+ * res must not alias a. */
+int chd_hrot(const chd_context *ctx, int level, uint32_t *res_bx,
+             uint32_t *res_ax, const uint32_t *a_bx, const uint32_t *a_ax,
+             const uint32_t *const *evk_bx, const uint32_t *const *evk_ax,
+             int evk_beta, int rot, int num_slots, void *stream);
+/* Permute of a ciphertext by 5^rot (rot = -1: conjugation), no key switch
+ * (Context.cpp:501-527) */
+int chd_permute(const chd_context *ctx, int level, uint32_t *res_bx,
+                uint32_t *res_ax, const uint32_t *a_bx, const uint32_t *a_ax,
+                int rot, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

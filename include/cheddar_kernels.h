@@ -1,0 +1,116 @@
+/*
+ * Kernel-level C-ABI of the MI355X key-switch path: the thin layer between
+ * the C++ handler classes (cheddar::NTTHandler, ModSwitchHandler,
+ * ElementWiseHandler) and the hand-written gfx950 kernels. Plain C types,
+ * raw device pointers, an explicit stream (hipStream_t passed as void*).
+ * Every call returns 0 on success or a negative chd_status; the message is
+ * available from chd_last_error() (declared in cheddar_amd.h).
+ *
+ * Each entry point replaces the CUDA launch sites named in its comment
+ * (paths relative to the Cheddar reference tree). No entry point allocates
+ * or frees device memory.
+ */
+#ifndef CHEDDAR_KERNELS_H
+#define CHEDDAR_KERNELS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Per-prime device tables of one prime chain (ter reversed, main, aux).
+ * Built by the C++ NTTHandler (src/core/NTT.cu:1233-1299 counterpart). */
+typedef struct chd_tables {
+  const uint32_t *q;        /* [T] primes                                 */
+  const int32_t *qinv;      /* [T] q^-1 mod 2^32 (signed)                 */
+  const double *qd;         /* [T] q as double                            */
+  const double *qinvd;      /* [T] 1/q                                    */
+  const uint32_t *rinv;     /* [T] 2^-32 mod q                            */
+  const void *tw_lo;        /* [T][256] double2 (psi^brev(j), /q)         */
+  const void *itw_lo;       /* [T][256] double2 (psi^-brev(j), /q)        */
+  const uint32_t *tw;       /* [T][N] psi^brev(j) mod q                   */
+  const uint32_t *itw;      /* [T][N] psi^-brev(j) mod q                  */
+} chd_tables;
+
+/* launch limb j -> logical limb l = j + (j >= skip_lo ? skip_len : 0);
+ * aux limbs (l >= num_q) shift src/table/constant indices by their gaps
+ * (the reference's PtrList extra_, include/common/PtrList.h:38-63). */
+typedef struct chd_limb_map {
+  int num_q;
+  int skip_lo, skip_len;
+  int src_gap;
+  int tab_off, tab_gap;
+  int cst_gap;
+} chd_limb_map;
+
+/* Forward NTT of num_limbs x num_polys limbs (NTT.cu:606-671, 815-887).
+ * pre_cst != NULL: input first multiplied by MontMul(x, pre_cst[limb])
+ * (Montgomery conversion). Strides are in words between polynomials. */
+int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
+                  long long dst_pstride, const uint32_t *src,
+                  long long src_pstride, int num_limbs, int num_polys,
+                  const uint32_t *pre_cst, void *stream);
+
+/* Forward NTT of dst in place followed by the ModDown epilogue
+ * out = MontMul(MontMul(src2, pad) - NTT(x), inv_prod) (NTT.cu:889-971,
+ * 456-601). src2 covers logical limbs [src2_lo, src2_hi); pad may be NULL. */
+int chd_k_ntt_fwd_moddown(const chd_tables *t, const chd_limb_map *m,
+                          uint32_t *dst, int num_limbs, const uint32_t *src2,
+                          int src2_lo, int src2_hi, const uint32_t *inv_prod,
+                          const uint32_t *pad, void *stream);
+
+/* Inverse NTT with epilogue MontMul(N*intt(x), cst[limb]), centred into
+ * [-(q-1)/2, (q-1)/2] when centre (NTT.cu:673-813, 973-1128). */
+int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
+                  long long dst_pstride, const uint32_t *src,
+                  long long src_pstride, int num_limbs, int num_polys,
+                  const uint32_t *cst, int centre, void *stream);
+
+/* BConv (src/core/ModSwitch.cu:23-171): for dst position k,
+ * dst[pos(k)] = sum_i src[i] * T[k][i] * 2^-32 mod p_k with centred int32
+ * sources. table = chd_bconv_table_size(src_len, dst_len) bytes made by
+ * chd_bconv_table_pack from the reference-form table T (dst-major).
+ * pos(k) = k + (k >= skip_lo ? skip_len : 0); prime of pos via m->tab_*. */
+long long chd_bconv_table_size(int src_len, int dst_len);
+int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
+                         const uint32_t *dst_primes, int src_len, int dst_len);
+int chd_k_bconv(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
+                const int32_t *src, int src_len, int dst_len,
+                const void *table, void *stream);
+
+/* Tensor (ElementWise.cu:504-575, 921-953): Karatsuba product of
+ * (b1,a1) x (b2,a2) -> (bx, ax, rx) over num_limbs limbs. src2 == src1
+ * selects the squaring kernel. src_gap as in chd_limb_map. */
+int chd_k_tensor(const chd_tables *t, const chd_limb_map *m, uint32_t *bx,
+                 uint32_t *ax, uint32_t *rx, const uint32_t *b1,
+                 const uint32_t *a1, const uint32_t *b2, const uint32_t *a2,
+                 int num_limbs, void *stream);
+
+/* CPAccum / CPAccumAdd (ElementWise.cu:225-366, 1437-1643):
+ * dst[p][i] = (src0[p][i]) + sum_a MontMul(common_a[., i], src_a[p][i]).
+ * const_accum: common_a is one constant per limb; otherwise a polynomial. */
+#define CHD_MAX_ACCUM 8
+#define CHD_MAX_POLY 3
+typedef struct chd_accum_src {
+  const uint32_t *src[CHD_MAX_POLY];
+  const uint32_t *common;
+  long long src_gap;     /* words added to the index of aux limbs */
+  long long common_gap;  /* same for common (limbs if const_accum) */
+} chd_accum_src;
+int chd_k_cpaccum(const chd_tables *t, const chd_limb_map *m,
+                  uint32_t *const *dst, int num_polys, const uint32_t *const *src0,
+                  long long src0_gap, const chd_accum_src *srcs, int num_accum,
+                  int const_accum, int num_limbs, void *stream);
+
+/* Permute (ElementWise.cu:370-391, 966-999): NTT-domain automorphism with
+ * galois factor g: dst[l][x] = src[l][brev(((2 brev(x)+1) g - 1) mod 2N)]. */
+int chd_k_permute(const chd_limb_map *m, uint32_t *const *dst,
+                  const uint32_t *const *src, int num_polys, int num_limbs,
+                  uint32_t galois, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

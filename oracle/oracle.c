@@ -155,6 +155,42 @@ void orc_twiddles(uint32_t q, int log_n, uint32_t *psi_rev,
   }
 }
 
+/* Twiddle-table cache keyed by (q, log_n) so repeated limb transforms (the
+ * CPU baseline) do not rebuild tables; filled under a lock, never evicted
+ * beyond its capacity (then tables are built per call). */
+#define ORC_CACHE 256
+static struct {
+  uint32_t q;
+  int log_n;
+  uint32_t *tw, *itw, c[5];
+} g_cache[ORC_CACHE];
+static int g_cache_n = 0;
+
+static int cached_tables(uint32_t q, int log_n, const uint32_t **tw,
+                         const uint32_t **itw, uint32_t *consts) {
+  int hit = -1;
+#pragma omp critical(orc_cache)
+  {
+    for (int i = 0; i < g_cache_n; i++)
+      if (g_cache[i].q == q && g_cache[i].log_n == log_n) { hit = i; break; }
+    if (hit < 0 && g_cache_n < ORC_CACHE) {
+      uint32_t n = 1u << log_n;
+      hit = g_cache_n;
+      g_cache[hit].tw = (uint32_t *)malloc(sizeof(uint32_t) * n);
+      g_cache[hit].itw = (uint32_t *)malloc(sizeof(uint32_t) * n);
+      orc_twiddles(q, log_n, g_cache[hit].tw, g_cache[hit].itw, g_cache[hit].c);
+      g_cache[hit].q = q;
+      g_cache[hit].log_n = log_n;
+      g_cache_n++;
+    }
+  }
+  if (hit < 0) return 0;
+  *tw = g_cache[hit].tw;
+  *itw = g_cache[hit].itw;
+  if (consts) memcpy(consts, g_cache[hit].c, sizeof(g_cache[hit].c));
+  return 1;
+}
+
 /* ------------------------------------------------------------------------ */
 /* NTT, kernel-faithful: butterflies NTTUtils.cuh:19-60, structure          */
 /* NTT.cu:231-454 (stage order), epilogue NTTUtils.cuh:369-391              */
@@ -164,9 +200,14 @@ void orc_twiddles(uint32_t q, int log_n, uint32_t *psi_rev,
  * psi_rev[m + i] (NTTUtils.cuh:62-87 index tw_idx << (stage-1)). */
 void orc_ntt(uint32_t *x, int log_n, uint32_t q, int mont_conv) {
   uint32_t n = 1u << log_n;
-  uint32_t *tw = (uint32_t *)malloc(sizeof(uint32_t) * n);
   uint32_t c[5];
-  orc_twiddles(q, log_n, tw, NULL, c);
+  const uint32_t *tw, *itw_unused;
+  uint32_t *owned = NULL;
+  if (!cached_tables(q, log_n, &tw, &itw_unused, c)) {
+    owned = (uint32_t *)malloc(sizeof(uint32_t) * n);
+    orc_twiddles(q, log_n, owned, NULL, c);
+    tw = owned;
+  }
   int32_t qinv = orc_inv_mod_base(q);
   int32_t *a = (int32_t *)x;
   if (mont_conv) {
@@ -193,7 +234,7 @@ void orc_ntt(uint32_t *x, int log_n, uint32_t q, int mont_conv) {
   }
   for (uint32_t j = 0; j < n; j++)
     if (a[j] < 0) a[j] += (int32_t)q;
-  free(tw);
+  free(owned);
 }
 
 /* GS inverse without the N^-1 factor (kernels compute N * intt) */
@@ -221,8 +262,13 @@ static void intt_raw(int32_t *a, int log_n, uint32_t q, const uint32_t *itw,
 void orc_intt_mult_const(int32_t *out, const uint32_t *x, int log_n, uint32_t q,
                          uint32_t cst, int normalize) {
   uint32_t n = 1u << log_n;
-  uint32_t *itw = (uint32_t *)malloc(sizeof(uint32_t) * n);
-  orc_twiddles(q, log_n, NULL, itw, NULL);
+  const uint32_t *itw, *tw_unused;
+  uint32_t *owned = NULL;
+  if (!cached_tables(q, log_n, &tw_unused, &itw, NULL)) {
+    owned = (uint32_t *)malloc(sizeof(uint32_t) * n);
+    orc_twiddles(q, log_n, NULL, owned, NULL);
+    itw = owned;
+  }
   int32_t qinv = orc_inv_mod_base(q);
   if ((const void *)out != (const void *)x)
     memcpy(out, x, sizeof(uint32_t) * n);
@@ -233,7 +279,7 @@ void orc_intt_mult_const(int32_t *out, const uint32_t *x, int log_n, uint32_t q,
     if (normalize && v > (int32_t)(q >> 1)) v -= (int32_t)q;
     out[j] = v;
   }
-  free(itw);
+  free(owned);
 }
 
 /* NTT.cu:673-741: epilogue constant N^-1 (mont_conv) or N^-1 R */

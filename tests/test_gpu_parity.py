@@ -1,0 +1,242 @@
+"""GPU parity: the HIP path through the C-ABI against the CPU oracle,
+bit-exact, on seeded inputs at the BASELINE configurations' real sizes."""
+import numpy as np
+import pytest
+
+import _orc
+from gpu_util import (CFG1_Q, N, Q30, Q31, centred_limbs, config4, dev, host,
+                      uniform_limbs, zeros)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def chd():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("no HIP device visible")
+    import cheddar_amd
+    return cheddar_amd
+
+
+def rng(s):
+    return np.random.default_rng(s)
+
+
+# ------------------------------------------------------------------ NTT ----
+def test_ntt_config1_single_limb_roundtrip(chd):
+    plan = chd.NttPlan([CFG1_Q])
+    x = uniform_limbs(rng(1), [CFG1_Q])
+    src = dev(x)
+    y = zeros(N)
+    for mont in (0, 1):
+        plan.forward(y, src, 1, 1, mont_conv=mont)
+        assert np.array_equal(host(y), _orc.ntt(x[0], 16, CFG1_Q, mont))
+        back = zeros(N)
+        plan.inverse(back, y, 1, 1, mont_conv=mont)
+        assert np.array_equal(host(back), x[0])
+
+
+def test_ntt_config2_batch(chd):
+    primes = Q30[:32]
+    plan = chd.NttPlan(primes)
+    x = np.stack([uniform_limbs(rng(10 + p), primes) for p in range(2)])
+    src = dev(x)
+    y = zeros(2, 32, N)
+    plan.forward(y, src, 32, 2)
+    want = np.stack([_orc.ntt_batch(x[p].reshape(-1), 16, primes).reshape(
+        32, N) for p in range(2)])
+    assert np.array_equal(host(y), want)
+    z = zeros(2, 32, N)
+    plan.inverse(z, y, 32, 2, mont_conv=True)
+    want_inv = np.stack([_orc.intt_batch(want[p].reshape(-1), 16, primes,
+                                         1).reshape(32, N) for p in range(2)])
+    assert np.array_equal(host(z), want_inv)
+    plan.inverse(z, y, 32, 2, mont_conv=False)
+    assert np.array_equal(host(z), x)
+    # in place, Montgomery conversion on input
+    y2 = dev(x)
+    plan.forward(y2, y2, 32, 2, mont_conv=True)
+    want_m = np.stack([_orc.ntt_batch(x[p].reshape(-1), 16, primes, 1)
+                       .reshape(32, N) for p in range(2)])
+    assert np.array_equal(host(y2), want_m)
+
+
+@pytest.mark.parametrize("kind", ["zeros", "max", "impulse", "ramp"])
+def test_ntt_edge_inputs(chd, kind):
+    primes = [CFG1_Q, Q31[5], Q30[0], Q30[31]]
+    if kind == "zeros":
+        x = np.zeros((4, N), np.uint32)
+    elif kind == "max":
+        x = np.stack([np.full(N, p - 1, np.uint32) for p in primes])
+    elif kind == "impulse":
+        x = np.zeros((4, N), np.uint32)
+        x[:, 1] = 1
+        x[:, N - 1] = 7
+    else:
+        x = np.stack([(np.arange(N, dtype=np.uint64) * 2654435761 % p)
+                      .astype(np.uint32) for p in primes])
+    plan = chd.NttPlan(primes)
+    y = zeros(4, N)
+    plan.forward(y, dev(x), 4, 1)
+    assert np.array_equal(host(y), _orc.ntt_batch(x.reshape(-1), 16,
+                                                  primes).reshape(4, N))
+    z = zeros(4, N)
+    plan.inverse(z, y, 4, 1, mont_conv=False)
+    assert np.array_equal(host(z), x)
+
+
+# ---------------------------------------------------------------- BConv ----
+def test_bconv_config3(chd):
+    src_p, dst_p = Q30[:8], Q31[:40]
+    plan = chd.BconvPlan(src_p, dst_p)
+    c1, c2 = plan.constants()
+    o1, o2 = _orc.modswitch_consts(src_p, dst_p, 16)
+    assert np.array_equal(c1, o1) and np.array_equal(c2, o2)
+    x = centred_limbs(rng(3), src_p)
+    out = zeros(40, N)
+    plan.apply(out, dev(x.view(np.uint32)))
+    assert np.array_equal(host(out), _orc.bconv(x, o2, dst_p, 16))
+
+
+def test_bconv_extreme_centred_values(chd):
+    src_p, dst_p = Q31[:8], Q31[8:20]
+    plan = chd.BconvPlan(src_p, dst_p)
+    _, o2 = _orc.modswitch_consts(src_p, dst_p, 16)
+    x = np.stack([np.where(np.arange(N) % 2 == 0, (p - 1) // 2,
+                           -((p - 1) // 2)).astype(np.int32) for p in src_p])
+    out = zeros(12, N)
+    plan.apply(out, dev(x.view(np.uint32)))
+    assert np.array_equal(host(out), _orc.bconv(x, o2, dst_p, 16))
+
+
+# --------------------------------------------------- key-switch pipeline ----
+@pytest.fixture(scope="module")
+def ks(chd):
+    main, aux, levels = config4(24)
+    param = chd.Param(main, aux, levels)
+    ctx = chd.Context(param)
+    return param, ctx, main, aux
+
+
+def _evk(r, main, aux, beta):
+    primes = main + aux
+    kb = np.stack([uniform_limbs(r, primes) for _ in range(beta)])
+    ka = np.stack([uniform_limbs(r, primes) for _ in range(beta)])
+    return kb, ka
+
+
+@pytest.mark.parametrize("L", [24, 20, 17])
+def test_mod_up(chd, ks, L):
+    param, ctx, main, aux = ks
+    level = L - 1
+    x = uniform_limbs(rng(100 + L), main[:L])
+    beta = ctx.beta(level)
+    assert beta == (L + 7) // 8
+    outs = [zeros(L + 8, N) for _ in range(beta)]
+    ctx.mod_up(level, outs, dev(x))
+    want = _orc.mod_up(x, main[:L], aux, 16)
+    for g in range(beta):
+        assert np.array_equal(host(outs[g]), want[g]), "group %d" % g
+
+
+@pytest.mark.parametrize("L", [24, 9])
+def test_mod_down_family(chd, ks, L):
+    param, ctx, main, aux = ks
+    level = L - 1
+    primes = main[:L] + aux
+    x = uniform_limbs(rng(200 + L), primes)
+    out = zeros(L, N)
+    ctx.mod_down(level, out, dev(x))
+    assert np.array_equal(host(out), _orc.mod_down(x, primes, L, 16))
+    out2 = zeros(L - 1, N)
+    ctx.mod_down_and_rescale(level, out2, dev(x))
+    assert np.array_equal(host(out2), _orc.mod_down(x, primes, L - 1, 16))
+    xq = np.ascontiguousarray(x[:L])
+    out3 = zeros(L - 1, N)
+    ctx.rescale_poly(level, out3, dev(xq))
+    assert np.array_equal(host(out3), _orc.mod_down(xq, main[:L], L - 1, 16))
+
+
+def test_tensor(chd, ks):
+    param, ctx, main, _ = ks
+    L = 24
+    r = rng(300)
+    b1, a1, b2, a2 = (uniform_limbs(r, main) for _ in range(4))
+    res = [zeros(L, N) for _ in range(3)]
+    ctx.tensor(L - 1, res, (dev(b1), dev(a1)), (dev(b2), dev(a2)))
+    want = _orc.tensor(b1, a1, b2, a2, main, 16)
+    for got, w in zip(res, want):
+        assert np.array_equal(host(got), w)
+    # squaring path (same source pointers)
+    sa, sb = dev(a1), dev(b1)
+    ctx.tensor(L - 1, res, (sb, sa), (sb, sa))
+    want = _orc.tensor(b1, a1, b1, a1, main, 16)
+    for got, w in zip(res, want):
+        assert np.array_equal(host(got), w)
+
+
+@pytest.mark.parametrize("L,rescale", [(24, True), (24, False), (20, True)])
+def test_hmult_config4(chd, ks, L, rescale):
+    param, ctx, main, aux = ks
+    level = L - 1
+    r = rng(400 + L + int(rescale))
+    b1, a1, b2, a2 = (uniform_limbs(r, main[:L]) for _ in range(4))
+    kb, ka = _evk(r, main, aux, 3)
+    out_l = L - 1 if rescale else L
+    res = (zeros(out_l, N), zeros(out_l, N))
+    ctx.hmult(level, res, (dev(b1), dev(a1)), (dev(b2), dev(a2)),
+              [dev(k) for k in kb], [dev(k) for k in ka], rescale=rescale)
+    wb, wa = _orc.hmult(b1, a1, b2, a2, kb, ka, L, 24, main, aux, 16,
+                        1 if rescale else 0)
+    assert np.array_equal(host(res[0]), wb)
+    assert np.array_equal(host(res[1]), wa)
+
+
+def test_hmult_in_place_and_separate_rescale(chd, ks):
+    param, ctx, main, aux = ks
+    L = 24
+    r = rng(450)
+    b1, a1, b2, a2 = (uniform_limbs(r, main) for _ in range(4))
+    kb, ka = _evk(r, main, aux, 3)
+    ta, tb = dev(a1), dev(b1)
+    ctx.hmult(L - 1, (tb, ta), (tb, ta), (dev(b2), dev(a2)),
+              [dev(k) for k in kb], [dev(k) for k in ka], rescale=False)
+    wb, wa = _orc.hmult(b1, a1, b2, a2, kb, ka, L, 24, main, aux, 16, 0)
+    assert np.array_equal(host(tb), wb) and np.array_equal(host(ta), wa)
+    rb, ra = zeros(L - 1, N), zeros(L - 1, N)
+    ctx.rescale(L - 1, (rb, ra), (tb, ta))
+    assert np.array_equal(host(rb), _orc.rescale(wb, main, L, 1, 16))
+    assert np.array_equal(host(ra), _orc.rescale(wa, main, L, 1, 16))
+
+
+@pytest.mark.parametrize("rot", [1, 1234])
+def test_hrot_and_mult_key(chd, ks, rot):
+    param, ctx, main, aux = ks
+    L = 20
+    r = rng(500 + rot)
+    b, a = uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L])
+    kb, ka = _evk(r, main, aux, 3)
+    res = (zeros(L, N), zeros(L, N))
+    ctx.mult_key(L - 1, res, (dev(b), dev(a)), [dev(k) for k in kb],
+                 [dev(k) for k in ka])
+    wb, wa = _orc.mult_key(b, a, kb, ka, L, 24, main, aux, 16)
+    assert np.array_equal(host(res[0]), wb)
+    assert np.array_equal(host(res[1]), wa)
+    ctx.hrot(L - 1, res, (dev(b), dev(a)), [dev(k) for k in kb],
+             [dev(k) for k in ka], rot)
+    hb, ha = _orc.hrot(b, a, kb, ka, L, 24, main, aux, 16, rot)
+    assert np.array_equal(host(res[0]), hb)
+    assert np.array_equal(host(res[1]), ha)
+
+
+def test_permute_conjugate(chd, ks):
+    param, ctx, main, _ = ks
+    L = 5
+    r = rng(600)
+    b, a = uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L])
+    res = (zeros(L, N), zeros(L, N))
+    ctx.permute(L - 1, res, (dev(b), dev(a)), -1)
+    g = 2 * N - 1
+    assert np.array_equal(host(res[0]), _orc.permute(b, 16, g))
+    assert np.array_equal(host(res[1]), _orc.permute(a, 16, g))
