@@ -40,6 +40,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU-baseline leg")
+    ap.add_argument("--only", choices=["ntt_fwd", "ntt_inv", "hmult",
+                                       "bconv"],
+                    help="run only this workload's timed loop (for "
+                         "profiling); prints its average time")
     return ap.parse_args()
 
 
@@ -179,6 +183,33 @@ def cpu_baseline(seconds=10.0):
                       % (done, el)}
 
 
+def run_only(chd, what, steps):
+    """one workload's timed loop, for rocprofv3 runs"""
+    import numpy as np
+    import torch
+    from chd_primes import ntt_primes
+    if what == "hmult":
+        return bench_hmult(chd, steps) * 1e3
+    if what == "bconv":
+        return bench_bconv(chd, steps) * 1e3
+    primes = ntt_primes(30, 32)
+    plan = chd.NttPlan(primes)
+    rng = np.random.default_rng(0xC0FFEE02)
+    host = np.stack([np.stack([rng.integers(0, p, N, dtype=np.uint64)
+                               for p in primes]) for _ in range(2)])
+    src = torch.from_numpy(host.astype(np.uint32).view(np.int32)).cuda()
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    if what == "ntt_fwd":
+        fn = lambda i: plan.forward(dst, src, 32, 2, stream=sp)  # noqa: E731
+    else:
+        fn = lambda i: plan.inverse(dst, src, 32, 2, stream=sp)  # noqa: E731
+    fn(0)
+    torch.cuda.synchronize()
+    return event_time_ms(fn, steps, stream) / steps * 1e3
+
+
 def traffic_from_profile():
     path = os.path.join(ROOT, "profiles", "ntt_fwd_config2_traffic.json")
     if not os.path.exists(path):
@@ -201,6 +232,10 @@ def main():
         sys.exit(1)
     import cheddar_amd as chd
 
+    if args.only:
+        print(json.dumps({"only": args.only,
+                          "us": run_only(chd, args.only, args.steps)}))
+        return
     ms, fwd_ms, inv_ms, warm_ms, ok = bench_ntt(chd, args.steps, args.warmup)
     if not ok:
         print("NTT round trip changed the data", file=sys.stderr)

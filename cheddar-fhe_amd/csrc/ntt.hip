@@ -9,14 +9,17 @@
 //
 // Semantics follow the reference exactly (bit-exact canonical outputs):
 //   forward: y[i] = sum_j x_j psi^{(2 brev(i)+1) j}, twiddle psi_rev[m+i]
-//            for butterfly group i of the stage with m groups
-//            (include/core/NTTUtils.cuh:19-34, 62-87; src/core/NTT.cu:231-454)
+//            (Montgomery form) for butterfly group i of the stage with m
+//            groups (include/core/NTTUtils.cuh:19-34, 62-87;
+//            src/core/NTT.cu:231-454)
 //   inverse: Gentleman-Sande with psi_inv_rev[m+i], computes N*intt; the
 //            N^-1 and any per-limb factor live in the epilogue constant,
 //            applied as MontMul(x, c) (NTT.cu:23-229, 673-813).
-// Butterfly arithmetic is the exact fp64 modular multiply of chd_device.h;
-// values are kept unreduced in fp64 inside a pass (|x| < 2^40) and reduced to
-// canonical u32 at each pass boundary.
+// Arithmetic is the reference's signed lazy Montgomery butterfly
+// (NTTUtils.cuh:19-60) in Montgomery-Shoup form: with w' = w q^-1 mod 2^32,
+// MontMul(b, w) = mulhi(b, w) - mulhi(b w' mod 2^32, q): three 32-bit
+// multiplies, which gfx950 issues at full VALU rate. w' is derived on the
+// fly (one multiply per twiddle; scalar when the twiddle is wave-uniform).
 #include "chd_device.h"
 #include "kernel_common.h"
 #include "ntt.h"
@@ -47,59 +50,178 @@ __device__ __forceinline__ Limb decode(const LimbMap &m, int j) {
   return r;
 }
 
-__device__ __forceinline__ void ct_bfly(double &a, double &b, double w,
-                                        double wq, double q) {
-  double m = mulmod_f64(b, w, wq, q);
-  b = a - m;
-  a = a + m;
+// (b * w * 2^-32) mod q in (-q, q) for |b w| < q 2^31 (Basic.cuh:72-137)
+__device__ __forceinline__ int32_t mont(int32_t b, int32_t w, int32_t wq,
+                                        int32_t q) {
+  int32_t hi = __mulhi(b, w);
+  int32_t t = static_cast<int32_t>(static_cast<uint32_t>(b) *
+                                   static_cast<uint32_t>(wq));
+  return hi - __mulhi(t, q);
 }
 
-__device__ __forceinline__ void gs_bfly(double &a, double &b, double w,
-                                        double wq, double q) {
-  double d = a - b;
-  a = a + b;
-  b = mulmod_f64(d, w, wq, q);
+// [-q, q) -> [0, q) with one add and an unsigned min
+__device__ __forceinline__ int32_t norm(int32_t a, int32_t q) {
+  uint32_t ua = static_cast<uint32_t>(a);
+  uint32_t uq = ua + static_cast<uint32_t>(q);
+  return static_cast<int32_t>(ua < uq ? ua : uq);
 }
 
-// MontMul constant c (reference form) -> plain multiplier c * 2^-32 mod q
-__device__ __forceinline__ double eff_const(uint32_t c, uint32_t rinv,
-                                            double q, double qinv) {
-  double r = static_cast<double>(rinv);
-  double m = mulmod_f64(static_cast<double>(c), r, r * qinv, q);
-  return static_cast<double>(reduce_f64(m, q, qinv));
+// ButterflyNTT (NTTUtils.cuh:19-34): a, b in [-q, q)
+__device__ __forceinline__ void ct_bfly(int32_t &a, int32_t &b, int32_t w,
+                                        int32_t wq, int32_t q) {
+  int32_t m = norm(mont(b, w, wq, q), q);
+  int32_t an = norm(a, q);
+  b = an - m;
+  a = (an - q) + m;
+}
+
+// ButterflyINTT (NTTUtils.cuh:46-60)
+__device__ __forceinline__ void gs_bfly(int32_t &a, int32_t &b, int32_t w,
+                                        int32_t wq, int32_t q) {
+  int32_t an = norm(a, q);
+  int32_t bn = norm(b, q);
+  int32_t d = an - bn;
+  a = (an - q) + bn;
+  b = mont(d, w, wq, q);
+}
+
+// Lazy butterflies for q < 2^30 (4q < 2^32), unsigned values:
+// CT keeps [0, 4q) (Harvey), GS keeps [0, 2q). With d = mulhi(b,w) -
+// mulhi(b w' mod 2^32, q) in (-q, q) congruent to b w 2^-32 (unsigned
+// Montgomery, b < 2^32), the CT outputs are a + q +/- d.
+__device__ __forceinline__ int32_t mont_u(uint32_t b, uint32_t w, uint32_t wq,
+                                          uint32_t q) {
+  uint32_t hi = __umulhi(b, w);
+  uint32_t u = __umulhi(b * wq, q);
+  return static_cast<int32_t>(hi - u);
+}
+
+__device__ __forceinline__ uint32_t umin(uint32_t a, uint32_t b) {
+  return a < b ? a : b;
+}
+
+__device__ __forceinline__ void ct_lazy(uint32_t &a, uint32_t &b, uint32_t w,
+                                        uint32_t wq, uint32_t q) {
+  uint32_t x = umin(a, a - 2 * q) + q;     // [q, 3q)
+  uint32_t d = __umulhi(b, w) - __umulhi(b * wq, q);  // (-q, q) mod 2^32
+  b = x - d;                                // (0, 4q)
+  a = x + d;                                // (0, 4q)
+}
+
+__device__ __forceinline__ void gs_lazy(uint32_t &a, uint32_t &b, uint32_t w,
+                                        uint32_t wq, uint32_t q) {
+  uint32_t s = a + b;                       // [0, 4q)
+  uint32_t t = a + 2 * q - b;               // (0, 4q)
+  a = umin(s, s - 2 * q);                   // [0, 2q)
+  b = static_cast<uint32_t>(mont_u(t, w, wq, q)) + q;  // (0, 2q)
+}
+
+// [0, 4q) -> [0, q)
+__device__ __forceinline__ uint32_t canon4(uint32_t x, uint32_t q) {
+  x = umin(x, x - 2 * q);
+  return umin(x, x - q);
 }
 
 __device__ __forceinline__ int pidx(int i) { return i + (i >> 4); }
 
+// element load/store at a 32-bit byte offset from a wave-uniform base, so the
+// compiler emits the scalar-base + 32-bit-offset addressing form
+template <typename T>
+__device__ __forceinline__ T ld_at(const void *base, uint32_t byte_off) {
+  return *reinterpret_cast<const T *>(static_cast<const char *>(base) +
+                                      byte_off);
+}
+template <typename T>
+__device__ __forceinline__ void st_at(void *base, uint32_t byte_off, T v) {
+  *reinterpret_cast<T *>(static_cast<char *>(base) + byte_off) = v;
+}
+
+// Per-limb arithmetic policy. Values between the two passes of a transform
+// stay unreduced in the policy's range: [0, 4q) (forward, lazy), [0, 2q)
+// (inverse, lazy) or [-q, q) (reference form, any q < 2^31).
+template <bool kLazy>
+struct Arith;
+
+template <>
+struct Arith<true> {
+  using T = uint32_t;
+  uint32_t q;
+  __device__ void ct(T &a, T &b, uint32_t w, uint32_t wq) const {
+    ct_lazy(a, b, w, wq, q);
+  }
+  __device__ void gs(T &a, T &b, uint32_t w, uint32_t wq) const {
+    gs_lazy(a, b, w, wq, q);
+  }
+  // MontMul(x, c) for any representable input, result in (0, 2q)
+  __device__ T mul(T x, uint32_t c, uint32_t cq) const {
+    return static_cast<uint32_t>(mont_u(x, c, cq, q)) + q;
+  }
+  __device__ uint32_t canon_fwd(T x) const { return canon4(x, q); }
+  __device__ uint32_t canon_inv(T x) const { return umin(x, x - q); }
+};
+
+template <>
+struct Arith<false> {
+  using T = int32_t;
+  int32_t q;
+  __device__ void ct(T &a, T &b, uint32_t w, uint32_t wq) const {
+    ct_bfly(a, b, static_cast<int32_t>(w), static_cast<int32_t>(wq), q);
+  }
+  __device__ void gs(T &a, T &b, uint32_t w, uint32_t wq) const {
+    gs_bfly(a, b, static_cast<int32_t>(w), static_cast<int32_t>(wq), q);
+  }
+  __device__ T mul(T x, uint32_t c, uint32_t cq) const {
+    return mont(x, static_cast<int32_t>(c), static_cast<int32_t>(cq), q);
+  }
+  __device__ uint32_t canon_fwd(T x) const {
+    return static_cast<uint32_t>(norm(x, q));
+  }
+  __device__ uint32_t canon_inv(T x) const {
+    return static_cast<uint32_t>(norm(x, q));
+  }
+};
+
+// signed (-q, q) value of a policy value (for epilogue arithmetic)
+__device__ __forceinline__ int32_t to_signed_canon(uint32_t canon) {
+  return static_cast<int32_t>(canon);
+}
+
 // ------------------------------------------------------------------------
-// forward, column pass: stages 0..7
+// Kernel skeleton: each kernel decodes its limb, issues the data loads of the
+// whole tile first (they depend on kernel arguments only), then reads the
+// prime and twiddles and branches to the lazy (q < 2^30) or reference-form
+// body. Twiddles of both half-passes are fetched before the LDS barrier.
+// ------------------------------------------------------------------------
+
+// forward, column pass: stages 0..7 (src -> dst, dst left unreduced)
 // grid (kCols / kTileCols, limbs, polys), block 512
-// ------------------------------------------------------------------------
-template <bool kPre>
-__global__ __launch_bounds__(512) void ntt_fwd_cols(NttArgs a) {
-  __shared__ double xch[kRows * kTileCols];
-  const Limb lb = decode(a.map, blockIdx.y);
-  const uint32_t *src = a.src + blockIdx.z * a.src_pstride +
-                        (static_cast<size_t>(lb.sl) << kLogN);
-  uint32_t *dst =
-      a.dst + blockIdx.z * a.dst_pstride + (static_cast<size_t>(lb.l) << kLogN);
-  const double q = a.tab.qd[lb.ti];
-  const double qinv = a.tab.qinvd[lb.ti];
-  const double2 *tw =
-      static_cast<const double2 *>(a.tab.tw_lo) + lb.ti * 256;
+template <bool kPre, bool kLazy>
+__device__ __forceinline__ void fwd_cols_body(const NttArgs &a, const Limb &lb,
+                                              uint32_t (&xin)[16], uint32_t q,
+                                              uint32_t qinv, void *dst,
+                                              int32_t *xch) {
+  using A = Arith<kLazy>;
+  using T = typename A::T;
+  const A ar{static_cast<T>(q)};
+  const uint32_t *tw = a.tab.tw + (static_cast<size_t>(lb.ti) << kLogN);
   const int c = threadIdx.x & (kTileCols - 1);
   const int rg = threadIdx.x / kTileCols;  // 0..15
-  const int col = blockIdx.x * kTileCols + c;
+  const uint32_t col = blockIdx.x * kTileCols + c;
+  uint32_t w2[15];
+#pragma unroll
+  for (int s = 4, i = 0; s < 8; s++)
+#pragma unroll
+    for (int g = 0; g < (1 << (s - 4)); g++, i++)
+      w2[i] = tw[(1 << s) + (rg << (s - 4)) + g];
 
-  double x[16];
+  T x[16];
 #pragma unroll
-  for (int k = 0; k < 16; k++)
-    x[k] = static_cast<double>(src[(rg + 16 * k) * kCols + col]);
+  for (int k = 0; k < 16; k++) x[k] = static_cast<T>(xin[k]);
   if constexpr (kPre) {
-    double ce = eff_const(a.cst[lb.ci], a.tab.rinv[lb.ti], q, qinv);
-    double ceq = ce * qinv;
+    const uint32_t ce = a.cst[lb.ci];
+    const uint32_t ceq = ce * qinv;
 #pragma unroll
-    for (int k = 0; k < 16; k++) x[k] = mulmod_f64(x[k], ce, ceq, q);
+    for (int k = 0; k < 16; k++) x[k] = ar.mul(x[k], ce, ceq);
   }
   // stages 0..3: rows rg + 16k, twiddles identical for every thread
 #pragma unroll
@@ -107,67 +229,95 @@ __global__ __launch_bounds__(512) void ntt_fwd_cols(NttArgs a) {
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
-      const double2 w = tw[(1 << s) + g];
+      const uint32_t w = tw[(1 << s) + g];
+      const uint32_t wq = w * qinv;
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++)
-        ct_bfly(x[k], x[k + h], w.x, w.y, q);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
     }
   }
+  T *xt = reinterpret_cast<T *>(xch);
 #pragma unroll
-  for (int k = 0; k < 16; k++) xch[(rg + 16 * k) * kTileCols + c] = x[k];
+  for (int k = 0; k < 16; k++) xt[(rg + 16 * k) * kTileCols + c] = x[k];
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = xch[(16 * rg + k) * kTileCols + c];
+  for (int k = 0; k < 16; k++) x[k] = xt[(16 * rg + k) * kTileCols + c];
   // stages 4..7: rows 16 rg + k
 #pragma unroll
-  for (int s = 4; s < 8; s++) {
+  for (int s = 4, i = 0; s < 8; s++) {
     const int h = 8 >> (s - 4);
 #pragma unroll
-    for (int g = 0; g < (1 << (s - 4)); g++) {
-      const double2 w = tw[(1 << s) + (rg << (s - 4)) + g];
+    for (int g = 0; g < (1 << (s - 4)); g++, i++) {
+      const uint32_t w = w2[i];
+      const uint32_t wq = w * qinv;
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++)
-        ct_bfly(x[k], x[k + h], w.x, w.y, q);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
     }
   }
 #pragma unroll
   for (int k = 0; k < 16; k++)
-    dst[(16 * rg + k) * kCols + col] = reduce_f64(x[k], q, qinv);
+    st_at<T>(dst, ((16 * rg + k) * kCols + col) * 4u, x[k]);
 }
 
-// ------------------------------------------------------------------------
+template <bool kPre>
+__global__ __launch_bounds__(512) void ntt_fwd_cols(NttArgs a) {
+  __shared__ int32_t xch[kRows * kTileCols];
+  const Limb lb = decode(a.map, blockIdx.y);
+  const void *src = a.src + blockIdx.z * a.src_pstride +
+                    (static_cast<size_t>(lb.sl) << kLogN);
+  void *dst =
+      a.dst + blockIdx.z * a.dst_pstride + (static_cast<size_t>(lb.l) << kLogN);
+  const uint32_t col = blockIdx.x * kTileCols + (threadIdx.x & (kTileCols - 1));
+  const int rg = threadIdx.x / kTileCols;
+  uint32_t x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++)
+    x[k] = ld_at<uint32_t>(src, ((rg + 16 * k) * kCols + col) * 4u);
+  const uint32_t q = a.tab.q[lb.ti];
+  const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
+  if (q < (1u << 30))
+    fwd_cols_body<kPre, true>(a, lb, x, q, qinv, dst, xch);
+  else
+    fwd_cols_body<kPre, false>(a, lb, x, q, qinv, dst, xch);
+}
+
 // forward, row pass: stages 8..15 (in place on dst) + epilogue
 // grid (kRows / kTileRows, limbs, polys), block 256
-// ------------------------------------------------------------------------
-template <int kEpi>
-__global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
-  __shared__ double xch[kTileRows * kRowPad];
-  const Limb lb = decode(a.map, blockIdx.y);
-  uint32_t *dst =
-      a.dst + blockIdx.z * a.dst_pstride + (static_cast<size_t>(lb.l) << kLogN);
-  const double q = a.tab.qd[lb.ti];
-  const double qinv = a.tab.qinvd[lb.ti];
+template <int kEpi, bool kLazy>
+__device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
+                                              uint32_t (&xin)[16], uint32_t q,
+                                              uint32_t qinv, uint32_t *dst,
+                                              int32_t *xch) {
+  using A = Arith<kLazy>;
+  using T = typename A::T;
+  const A ar{static_cast<T>(q)};
   const uint32_t *tw = a.tab.tw + (static_cast<size_t>(lb.ti) << kLogN);
   const int c = threadIdx.x & 15;
   const int r = threadIdx.x >> 4;
   const int row = blockIdx.x * kTileRows + r;
-  uint32_t *base = dst + row * kCols;
-  double *xr = xch + r * kRowPad;
-
-  double x[16];
+  const uint32_t rbase = static_cast<uint32_t>(row * kCols) * 4u;
+  T *xr = reinterpret_cast<T *>(xch) + r * kRowPad;
+  uint32_t w1[15], w2[15];
 #pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = static_cast<double>(base[c + 16 * k]);
+  for (int s = 0, i = 0; s < 4; s++)
+#pragma unroll
+    for (int g = 0; g < (1 << s); g++, i++) {
+      w1[i] = tw[(256 << s) + (row << s) + g];
+      w2[i] = tw[(4096 << s) + (row << (4 + s)) + (c << s) + g];
+    }
+
+  T x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = static_cast<T>(xin[k]);
   // stages 8..11: columns c + 16k, twiddles depend on the row only
 #pragma unroll
-  for (int s = 0; s < 4; s++) {
+  for (int s = 0, i = 0; s < 4; s++) {
     const int h = 8 >> s;
 #pragma unroll
-    for (int g = 0; g < (1 << s); g++) {
-      const double w = static_cast<double>(tw[(256 << s) + (row << s) + g]);
-      const double wq = w * qinv;
+    for (int g = 0; g < (1 << s); g++, i++) {
+      const uint32_t w = w1[i];
+      const uint32_t wq = w * qinv;
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++)
-        ct_bfly(x[k], x[k + h], w, wq, q);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
     }
   }
 #pragma unroll
@@ -177,96 +327,117 @@ __global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
   for (int k = 0; k < 16; k++) x[k] = xr[pidx(16 * c + k)];
   // stages 12..15: columns 16c + k
 #pragma unroll
-  for (int s = 0; s < 4; s++) {
+  for (int s = 0, i = 0; s < 4; s++) {
     const int h = 8 >> s;
 #pragma unroll
-    for (int g = 0; g < (1 << s); g++) {
-      const double w = static_cast<double>(
-          tw[(4096 << s) + (row << (4 + s)) + (c << s) + g]);
-      const double wq = w * qinv;
+    for (int g = 0; g < (1 << s); g++, i++) {
+      const uint32_t w = w2[i];
+      const uint32_t wq = w * qinv;
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++)
-        ct_bfly(x[k], x[k + h], w, wq, q);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
     }
   }
   uint32_t out[16];
   if constexpr (kEpi == kEpiModDown) {
-    const uint32_t rinv = a.tab.rinv[lb.ti];
-    const double c2 = eff_const(a.cst2[lb.l], rinv, q, qinv);
-    const double c2q = c2 * qinv;
+    // NTTPhase2ForModDown epilogue (NTT.cu:567-600)
+    const int32_t qs = static_cast<int32_t>(q);
+    const int32_t c2 = static_cast<int32_t>(a.cst2[lb.l]);
+    const int32_t c2q = static_cast<int32_t>(static_cast<uint32_t>(c2) * qinv);
     const int s2 = lb.l - a.src2_lo;
     const bool has2 = lb.l >= a.src2_lo && lb.l < a.src2_hi;
     if (has2) {
-      const uint32_t *s2p = a.src2 + blockIdx.z * a.src2_pstride +
-                            (static_cast<size_t>(s2) << kLogN) + row * kCols +
-                            16 * c;
-      double pe = 0.0, peq = 0.0;
+      const int32_t *s2p = reinterpret_cast<const int32_t *>(a.src2) +
+                           blockIdx.z * a.src2_pstride +
+                           (static_cast<size_t>(s2) << kLogN) + row * kCols +
+                           16 * c;
+      int32_t pe = 0, peq = 0;
       if (a.pad != nullptr) {
-        pe = eff_const(a.pad[s2], rinv, q, qinv);
-        peq = pe * qinv;
+        pe = static_cast<int32_t>(a.pad[s2]);
+        peq = static_cast<int32_t>(static_cast<uint32_t>(pe) * qinv);
       }
 #pragma unroll
       for (int k = 0; k < 16; k++) {
-        double v = static_cast<double>(s2p[k]);
-        if (a.pad != nullptr) v = mulmod_f64(v, pe, peq, q);
-        out[k] = reduce_f64(mulmod_f64(v - x[k], c2, c2q, q), q, qinv);
+        int32_t v = s2p[k];
+        if (a.pad != nullptr) v = norm(mont(v, pe, peq, qs), qs);
+        v -= static_cast<int32_t>(ar.canon_fwd(x[k]));
+        out[k] = static_cast<uint32_t>(norm(mont(v, c2, c2q, qs), qs));
       }
     } else {
 #pragma unroll
       for (int k = 0; k < 16; k++)
-        out[k] = reduce_f64(mulmod_f64(-x[k], c2, c2q, q), q, qinv);
+        out[k] = static_cast<uint32_t>(norm(
+            mont(-static_cast<int32_t>(ar.canon_fwd(x[k])), c2, c2q, qs), qs));
     }
   } else {
 #pragma unroll
-    for (int k = 0; k < 16; k++) out[k] = reduce_f64(x[k], q, qinv);
+    for (int k = 0; k < 16; k++) out[k] = ar.canon_fwd(x[k]);
   }
-  uint4 *o4 = reinterpret_cast<uint4 *>(base + 16 * c);
+  uint4 *o4 = reinterpret_cast<uint4 *>(reinterpret_cast<char *>(dst) + rbase +
+                                        64u * c);
 #pragma unroll
   for (int v = 0; v < 4; v++)
     o4[v] = make_uint4(out[4 * v], out[4 * v + 1], out[4 * v + 2],
                        out[4 * v + 3]);
 }
 
-// ------------------------------------------------------------------------
-// inverse, row pass: GS stages 15..8 (src -> dst)
-// ------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void ntt_inv_rows(NttArgs a) {
-  __shared__ double xch[kTileRows * kRowPad];
+template <int kEpi>
+__global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
+  __shared__ int32_t xch[kTileRows * kRowPad];
   const Limb lb = decode(a.map, blockIdx.y);
-  const uint32_t *src = a.src + blockIdx.z * a.src_pstride +
-                        (static_cast<size_t>(lb.sl) << kLogN);
   uint32_t *dst =
       a.dst + blockIdx.z * a.dst_pstride + (static_cast<size_t>(lb.l) << kLogN);
-  const double q = a.tab.qd[lb.ti];
-  const double qinv = a.tab.qinvd[lb.ti];
+  const int c = threadIdx.x & 15;
+  const uint32_t rbase =
+      static_cast<uint32_t>((blockIdx.x * kTileRows + (threadIdx.x >> 4)) *
+                            kCols) * 4u;
+  uint32_t x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = ld_at<uint32_t>(dst, rbase + (c + 16 * k) * 4u);
+  const uint32_t q = a.tab.q[lb.ti];
+  const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
+  if (q < (1u << 30))
+    fwd_rows_body<kEpi, true>(a, lb, x, q, qinv, dst, xch);
+  else
+    fwd_rows_body<kEpi, false>(a, lb, x, q, qinv, dst, xch);
+}
+
+// inverse, row pass: GS stages 15..8 (src -> dst, dst left unreduced)
+template <bool kLazy>
+__device__ __forceinline__ void inv_rows_body(const NttArgs &a, const Limb &lb,
+                                              uint32_t (&xin)[16], uint32_t q,
+                                              uint32_t qinv, uint32_t *dst,
+                                              int32_t *xch) {
+  using A = Arith<kLazy>;
+  using T = typename A::T;
+  const A ar{static_cast<T>(q)};
   const uint32_t *tw = a.tab.itw + (static_cast<size_t>(lb.ti) << kLogN);
   const int c = threadIdx.x & 15;
   const int r = threadIdx.x >> 4;
   const int row = blockIdx.x * kTileRows + r;
-  double *xr = xch + r * kRowPad;
-
-  double x[16];
-  const uint4 *i4 = reinterpret_cast<const uint4 *>(src + row * kCols + 16 * c);
+  const uint32_t rbase = static_cast<uint32_t>(row * kCols) * 4u;
+  T *xr = reinterpret_cast<T *>(xch) + r * kRowPad;
+  uint32_t w1[15], w2[15];
 #pragma unroll
-  for (int v = 0; v < 4; v++) {
-    uint4 u = i4[v];
-    x[4 * v] = u.x;
-    x[4 * v + 1] = u.y;
-    x[4 * v + 2] = u.z;
-    x[4 * v + 3] = u.w;
-  }
+  for (int s = 0, i = 0; s < 4; s++)
+#pragma unroll
+    for (int g = 0; g < (1 << s); g++, i++) {
+      w2[i] = tw[(4096 << s) + (row << (4 + s)) + (c << s) + g];
+      w1[i] = tw[(256 << s) + (row << s) + g];
+    }
+
+  T x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = static_cast<T>(xin[k]);
   // stages 15..12: columns 16c + k
 #pragma unroll
   for (int s = 3; s >= 0; s--) {
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
-      const double w = static_cast<double>(
-          tw[(4096 << s) + (row << (4 + s)) + (c << s) + g]);
-      const double wq = w * qinv;
+      const uint32_t w = w2[(1 << s) - 1 + g];
+      const uint32_t wq = w * qinv;
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++)
-        gs_bfly(x[k], x[k + h], w, wq, q);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
     }
   }
 #pragma unroll
@@ -280,78 +451,126 @@ __global__ __launch_bounds__(256) void ntt_inv_rows(NttArgs a) {
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
-      const double w = static_cast<double>(tw[(256 << s) + (row << s) + g]);
-      const double wq = w * qinv;
+      const uint32_t w = w1[(1 << s) - 1 + g];
+      const uint32_t wq = w * qinv;
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++)
-        gs_bfly(x[k], x[k + h], w, wq, q);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
     }
   }
-  uint32_t *base = dst + row * kCols;
 #pragma unroll
-  for (int k = 0; k < 16; k++) base[c + 16 * k] = reduce_f64(x[k], q, qinv);
+  for (int k = 0; k < 16; k++) st_at<T>(dst, rbase + (c + 16 * k) * 4u, x[k]);
 }
 
-// ------------------------------------------------------------------------
-// inverse, column pass: GS stages 7..0 (in place on dst) + constant epilogue
-// ------------------------------------------------------------------------
-template <int kEpi>
-__global__ __launch_bounds__(512) void ntt_inv_cols(NttArgs a) {
-  __shared__ double xch[kRows * kTileCols];
+__global__ __launch_bounds__(256) void ntt_inv_rows(NttArgs a) {
+  __shared__ int32_t xch[kTileRows * kRowPad];
   const Limb lb = decode(a.map, blockIdx.y);
+  const uint32_t *src = a.src + blockIdx.z * a.src_pstride +
+                        (static_cast<size_t>(lb.sl) << kLogN);
   uint32_t *dst =
       a.dst + blockIdx.z * a.dst_pstride + (static_cast<size_t>(lb.l) << kLogN);
-  const double q = a.tab.qd[lb.ti];
-  const double qinv = a.tab.qinvd[lb.ti];
-  const double2 *tw =
-      static_cast<const double2 *>(a.tab.itw_lo) + lb.ti * 256;
+  const int c = threadIdx.x & 15;
+  const uint32_t rbase =
+      static_cast<uint32_t>((blockIdx.x * kTileRows + (threadIdx.x >> 4)) *
+                            kCols) * 4u;
+  uint32_t x[16];
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    uint4 u = ld_at<uint4>(src, rbase + 64u * c + 16u * v);
+    x[4 * v] = u.x;
+    x[4 * v + 1] = u.y;
+    x[4 * v + 2] = u.z;
+    x[4 * v + 3] = u.w;
+  }
+  const uint32_t q = a.tab.q[lb.ti];
+  const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
+  if (q < (1u << 30))
+    inv_rows_body<true>(a, lb, x, q, qinv, dst, xch);
+  else
+    inv_rows_body<false>(a, lb, x, q, qinv, dst, xch);
+}
+
+// inverse, column pass: GS stages 7..0 (in place on dst) + constant epilogue
+// (INTTPhase2 with MultConst / MultConstNormalize, NTTUtils.cuh:369-391)
+template <int kEpi, bool kLazy>
+__device__ __forceinline__ void inv_cols_body(const NttArgs &a, const Limb &lb,
+                                              uint32_t (&xin)[16], uint32_t q,
+                                              uint32_t qinv, uint32_t *dst,
+                                              int32_t *xch) {
+  using A = Arith<kLazy>;
+  using T = typename A::T;
+  const A ar{static_cast<T>(q)};
+  const uint32_t *tw = a.tab.itw + (static_cast<size_t>(lb.ti) << kLogN);
   const int c = threadIdx.x & (kTileCols - 1);
   const int rg = threadIdx.x / kTileCols;
-  const int col = blockIdx.x * kTileCols + c;
-
-  double x[16];
+  const uint32_t col = blockIdx.x * kTileCols + c;
+  uint32_t w2[15];
 #pragma unroll
-  for (int k = 0; k < 16; k++)
-    x[k] = static_cast<double>(dst[(16 * rg + k) * kCols + col]);
+  for (int s = 4, i = 0; s < 8; s++)
+#pragma unroll
+    for (int g = 0; g < (1 << (s - 4)); g++, i++)
+      w2[i] = tw[(1 << s) + (rg << (s - 4)) + g];
+
+  T x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = static_cast<T>(xin[k]);
 #pragma unroll
   for (int s = 7; s >= 4; s--) {
     const int h = 8 >> (s - 4);
 #pragma unroll
     for (int g = 0; g < (1 << (s - 4)); g++) {
-      const double2 w = tw[(1 << s) + (rg << (s - 4)) + g];
+      const uint32_t w = w2[(1 << (s - 4)) - 1 + g];
+      const uint32_t wq = w * qinv;
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++)
-        gs_bfly(x[k], x[k + h], w.x, w.y, q);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
     }
   }
+  T *xt = reinterpret_cast<T *>(xch);
 #pragma unroll
-  for (int k = 0; k < 16; k++) xch[(16 * rg + k) * kTileCols + c] = x[k];
+  for (int k = 0; k < 16; k++) xt[(16 * rg + k) * kTileCols + c] = x[k];
   __syncthreads();
 #pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = xch[(rg + 16 * k) * kTileCols + c];
+  for (int k = 0; k < 16; k++) x[k] = xt[(rg + 16 * k) * kTileCols + c];
 #pragma unroll
   for (int s = 3; s >= 0; s--) {
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
-      const double2 w = tw[(1 << s) + g];
+      const uint32_t w = tw[(1 << s) + g];
+      const uint32_t wq = w * qinv;
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++)
-        gs_bfly(x[k], x[k + h], w.x, w.y, q);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
     }
   }
-  const double ce = eff_const(a.cst[lb.ci], a.tab.rinv[lb.ti], q, qinv);
-  const double ceq = ce * qinv;
+  const uint32_t ce = a.cst[lb.ci];
+  const uint32_t ceq = ce * qinv;
+  const int32_t qs = static_cast<int32_t>(q);
 #pragma unroll
   for (int k = 0; k < 16; k++) {
-    double v = mulmod_f64(x[k], ce, ceq, q);
-    uint32_t o;
+    int32_t v = static_cast<int32_t>(ar.canon_inv(ar.mul(x[k], ce, ceq)));
     if constexpr (kEpi == kEpiConstCentre)
-      o = static_cast<uint32_t>(centre_f64(v, q, qinv));
-    else
-      o = reduce_f64(v, q, qinv);
-    dst[(rg + 16 * k) * kCols + col] = o;
+      if (v > (qs >> 1)) v -= qs;
+    st_at<int32_t>(dst, ((rg + 16 * k) * kCols + col) * 4u, v);
   }
+}
+
+template <int kEpi>
+__global__ __launch_bounds__(512) void ntt_inv_cols(NttArgs a) {
+  __shared__ int32_t xch[kRows * kTileCols];
+  const Limb lb = decode(a.map, blockIdx.y);
+  uint32_t *dst =
+      a.dst + blockIdx.z * a.dst_pstride + (static_cast<size_t>(lb.l) << kLogN);
+  const uint32_t col = blockIdx.x * kTileCols + (threadIdx.x & (kTileCols - 1));
+  const int rg = threadIdx.x / kTileCols;
+  uint32_t x[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++)
+    x[k] = ld_at<uint32_t>(dst, ((16 * rg + k) * kCols + col) * 4u);
+  const uint32_t q = a.tab.q[lb.ti];
+  const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
+  if (q < (1u << 30))
+    inv_cols_body<kEpi, true>(a, lb, x, q, qinv, dst, xch);
+  else
+    inv_cols_body<kEpi, false>(a, lb, x, q, qinv, dst, xch);
 }
 
 }  // namespace

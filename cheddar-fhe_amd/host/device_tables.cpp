@@ -28,6 +28,7 @@ void DevBuf::Release() {
   bytes_ = 0;
 }
 
+// twiddle tables as in NTTHandler::PopulateTwiddleFactors (NTT.cu:1233-1299)
 ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
     : log_degree_(log_degree), primes_(primes) {
   if (log_degree != 16)
@@ -37,7 +38,6 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
   std::vector<int32_t> qinv(T);
   std::vector<double> qd(T), qinvd(T);
   std::vector<uint32_t> rinv(T), ninv(T), ninv_mont(T), r2(T);
-  std::vector<double> tw_lo(T * 512), itw_lo(T * 512);
   std::vector<uint32_t> tw(T * n), itw(T * n);
   for (size_t i = 0; i < T; i++) {
     const uint32_t q = primes[i];
@@ -58,16 +58,10 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
     uint32_t *it = itw.data() + i * n;
     for (int j = 0; j < n; j++) {
       const uint32_t r = pm::bitrev(static_cast<uint32_t>(j), log_degree);
-      t[r] = static_cast<uint32_t>(p);
-      it[r] = static_cast<uint32_t>(pi);
+      t[r] = pm::to_mont(static_cast<uint32_t>(p), q);
+      it[r] = pm::to_mont(static_cast<uint32_t>(pi), q);
       p = p * psi % q;
       pi = pi * psi_inv % q;
-    }
-    for (int j = 0; j < 256; j++) {
-      tw_lo[i * 512 + 2 * j] = static_cast<double>(t[j]);
-      tw_lo[i * 512 + 2 * j + 1] = static_cast<double>(t[j]) / qd[i];
-      itw_lo[i * 512 + 2 * j] = static_cast<double>(it[j]);
-      itw_lo[i * 512 + 2 * j + 1] = static_cast<double>(it[j]) / qd[i];
     }
   }
   q_.Upload(primes);
@@ -75,8 +69,6 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
   qd_.Upload(qd);
   qinvd_.Upload(qinvd);
   rinv_.Upload(rinv);
-  tw_lo_.Upload(tw_lo);
-  itw_lo_.Upload(itw_lo);
   tw_.Upload(tw);
   itw_.Upload(itw);
   ninv_.Upload(ninv);
@@ -87,8 +79,6 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
   tab_.qd = qd_.as<double>();
   tab_.qinvd = qinvd_.as<double>();
   tab_.rinv = rinv_.as<uint32_t>();
-  tab_.tw_lo = tw_lo_.as<void>();
-  tab_.itw_lo = itw_lo_.as<void>();
   tab_.tw = tw_.as<uint32_t>();
   tab_.itw = itw_.as<uint32_t>();
 }

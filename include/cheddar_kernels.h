@@ -27,10 +27,8 @@ typedef struct chd_tables {
   const double *qd;         /* [T] q as double                            */
   const double *qinvd;      /* [T] 1/q                                    */
   const uint32_t *rinv;     /* [T] 2^-32 mod q                            */
-  const void *tw_lo;        /* [T][256] double2 (psi^brev(j), /q)         */
-  const void *itw_lo;       /* [T][256] double2 (psi^-brev(j), /q)        */
-  const uint32_t *tw;       /* [T][N] psi^brev(j) mod q                   */
-  const uint32_t *itw;      /* [T][N] psi^-brev(j) mod q                  */
+  const uint32_t *tw;       /* [T][N] ToMont(psi^brev(j))                 */
+  const uint32_t *itw;      /* [T][N] ToMont(psi^-brev(j))                */
 } chd_tables;
 
 /* launch limb j -> logical limb l = j + (j >= skip_lo ? skip_len : 0);
