@@ -14,6 +14,7 @@
 //
 // Layout: one thread per coefficient n, all sources held in registers; the
 // table is wave-uniform (scalar loads). grid (N / 256, dst chunks).
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -32,21 +33,28 @@ struct BconvTab {   // per (k, i): {Uhi, Ulo} as doubles
   double hi, lo;
 };
 
+struct BconvBatch {
+  chd_bconv_job job[CHD_MAX_JOBS];
+};
+
 template <int kSrc>
-__global__ __launch_bounds__(kThreads) void bconv_kernel(
-    chd_tables t, chd_limb_map m, uint32_t *__restrict__ dst,
-    const int32_t *__restrict__ src, int src_len, int dst_len,
-    const BconvTab *__restrict__ tab) {
+__global__ __launch_bounds__(kThreads) void bconv_kernel(chd_tables t,
+                                                         chd_limb_map m,
+                                                         BconvBatch b) {
+  const chd_bconv_job &jb = b.job[blockIdx.z];
   const int n = blockIdx.x * kThreads + threadIdx.x;
   const int k0 = blockIdx.y * kDstChunk;
-  const int k1 = min(dst_len, k0 + kDstChunk);
-  const int ns = kSrc > 0 ? kSrc : src_len;
+  const int k1 = min(jb.dst_len, k0 + kDstChunk);
+  if (k0 >= k1) return;
+  const int ns = kSrc > 0 ? kSrc : jb.src_len;
+  const int32_t *__restrict__ src = jb.src;
+  const BconvTab *__restrict__ tab = static_cast<const BconvTab *>(jb.table);
   double c[kMaxSrc];
 #pragma unroll
   for (int i = 0; i < kMaxSrc; i++)
     if (i < ns) c[i] = static_cast<double>(src[(static_cast<size_t>(i) << kLogN) + n]);
   for (int k = k0; k < k1; k++) {
-    const int pos = k + (k >= m.skip_lo ? m.skip_len : 0);
+    const int pos = k + (k >= jb.skip_lo ? jb.skip_len : 0);
     const bool aux = pos >= m.num_q;
     const int ti = m.tab_off + pos + (aux ? m.tab_gap : 0);
     const double p = t.qd[ti];
@@ -63,7 +71,7 @@ __global__ __launch_bounds__(kThreads) void bconv_kernel(
     }
     const double rhi = __builtin_fma(-__builtin_rint(shi * pinv), p, shi);
     const double v = __builtin_fma(rhi, 65536.0, slo);
-    dst[(static_cast<size_t>(pos) << kLogN) + n] = reduce_f64(v, p, pinv);
+    jb.dst[(static_cast<size_t>(pos) << kLogN) + n] = reduce_f64(v, p, pinv);
   }
 }
 
@@ -113,32 +121,49 @@ extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
   return 0;
 }
 
+extern "C" int chd_k_bconv_batch(const chd_tables *t, const chd_limb_map *m,
+                                 const chd_bconv_job *jobs, int num_jobs,
+                                 void *stream) {
+  if (!t || !m || !jobs || num_jobs < 1 || num_jobs > CHD_MAX_JOBS)
+    return set_error(CHD_ERR_ARG, "chd_k_bconv_batch: invalid argument");
+  BconvBatch b{};
+  int max_dst = 0, src_len = jobs[0].src_len;
+  bool same_src = true;
+  for (int j = 0; j < num_jobs; j++) {
+    const chd_bconv_job &jb = jobs[j];
+    if (!jb.dst || !jb.src || !jb.table || jb.src_len < 1 ||
+        jb.src_len > kMaxSrc || jb.dst_len < 1 || jb.skip_len < 0)
+      return set_error(CHD_ERR_ARG, "chd_k_bconv_batch: invalid job");
+    b.job[j] = jb;
+    max_dst = std::max(max_dst, jb.dst_len);
+    same_src = same_src && jb.src_len == src_len;
+  }
+  dim3 g(kN / kThreads, (max_dst + kDstChunk - 1) / kDstChunk, num_jobs);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int sl = same_src ? src_len : 0;
+  switch (sl) {
+    case 1:
+      hipLaunchKernelGGL(bconv_kernel<1>, g, dim3(kThreads), 0, s, *t, *m, b);
+      break;
+    case 8:
+      hipLaunchKernelGGL(bconv_kernel<8>, g, dim3(kThreads), 0, s, *t, *m, b);
+      break;
+    case 9:
+      hipLaunchKernelGGL(bconv_kernel<9>, g, dim3(kThreads), 0, s, *t, *m, b);
+      break;
+    default:
+      hipLaunchKernelGGL(bconv_kernel<0>, g, dim3(kThreads), 0, s, *t, *m, b);
+      break;
+  }
+  return check_launch("chd_k_bconv_batch");
+}
+
 extern "C" int chd_k_bconv(const chd_tables *t, const chd_limb_map *m,
                            uint32_t *dst, const int32_t *src, int src_len,
                            int dst_len, const void *table, void *stream) {
   if (!t || !m || !dst || !src || !table || src_len < 1 ||
       src_len > kMaxSrc || dst_len < 1)
     return set_error(CHD_ERR_ARG, "chd_k_bconv: invalid argument");
-  dim3 g(kN / kThreads, (dst_len + kDstChunk - 1) / kDstChunk);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const BconvTab *tab = static_cast<const BconvTab *>(table);
-  switch (src_len) {
-    case 1:
-      hipLaunchKernelGGL(bconv_kernel<1>, g, dim3(kThreads), 0, s, *t, *m, dst,
-                         src, src_len, dst_len, tab);
-      break;
-    case 8:
-      hipLaunchKernelGGL(bconv_kernel<8>, g, dim3(kThreads), 0, s, *t, *m, dst,
-                         src, src_len, dst_len, tab);
-      break;
-    case 9:
-      hipLaunchKernelGGL(bconv_kernel<9>, g, dim3(kThreads), 0, s, *t, *m, dst,
-                         src, src_len, dst_len, tab);
-      break;
-    default:
-      hipLaunchKernelGGL(bconv_kernel<0>, g, dim3(kThreads), 0, s, *t, *m, dst,
-                         src, src_len, dst_len, tab);
-      break;
-  }
-  return check_launch("chd_k_bconv");
+  chd_bconv_job j{dst, src, table, src_len, dst_len, m->skip_lo, m->skip_len};
+  return chd_k_bconv_batch(t, m, &j, 1, stream);
 }

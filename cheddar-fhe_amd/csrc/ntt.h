@@ -32,7 +32,22 @@ struct NttArgs {
   int src2_lo, src2_hi;   // logical limb range that src2 covers
   const uint32_t *cst2;   // inv prime product per logical limb
   const uint32_t *pad;    // optional padding per src2 limb (nullptr: none)
+  // ModUp group mode (group_alpha > 0): grid.z = dnum group g, whose own
+  // limbs [g alpha, min((g+1) alpha, num_q)) are skipped; every group holds
+  // group_limbs logical limbs (NTTForModUp for all groups in one launch)
+  int group_alpha;
+  int group_limbs;
+  // optional per-polynomial base pointers (used instead of base + z*stride
+  // when dst_list[0] is set): polynomials in separate allocations
+  uint32_t *dst_list[4];
 };
+
+// Fused ModUp row pass + evaluation-key inner product (PAccum) + CAccum.
+constexpr int kMaxGroups = CHD_MAX_JOBS;
+struct KeyAccArgs : chd_keyacc_args {
+  chd_tables tab;
+};
+hipError_t launch_modup_keyacc(const KeyAccArgs &a, hipStream_t s);
 
 // Forward NTT over grid (limbs, polys); pre_const multiplies the input by
 // MontMul(x, cst[limb]) first (Montgomery conversion).
@@ -41,5 +56,10 @@ hipError_t launch_ntt_fwd(const NttArgs &a, int num_limbs, int num_polys,
 // Inverse NTT (kernels compute N * intt; the N^-1 is in the constant)
 hipError_t launch_ntt_inv(const NttArgs &a, int num_limbs, int num_polys,
                           int epilogue, hipStream_t s);
+// column pass only (ModUp group mode uses grid.z = groups)
+hipError_t launch_ntt_fwd_cols(const NttArgs &a, int num_limbs, int num_z,
+                               hipStream_t s);
+hipError_t launch_ntt_fwd_rows(const NttArgs &a, int num_limbs, int num_z,
+                               hipStream_t s);
 
 }  // namespace chd

@@ -20,6 +20,8 @@
 // MontMul(b, w) = mulhi(b, w) - mulhi(b w' mod 2^32, q): three 32-bit
 // multiplies, which gfx950 issues at full VALU rate. w' is derived on the
 // fly (one multiply per twiddle; scalar when the twiddle is wave-uniform).
+#include <algorithm>
+
 #include "chd_device.h"
 #include "kernel_common.h"
 #include "ntt.h"
@@ -123,6 +125,11 @@ __device__ __forceinline__ uint32_t canon4(uint32_t x, uint32_t q) {
 }
 
 __device__ __forceinline__ int pidx(int i) { return i + (i >> 4); }
+
+// base of polynomial z: explicit list or base + z * stride
+__device__ __forceinline__ uint32_t *poly_dst(const NttArgs &a, int z) {
+  return a.dst_list[0] != nullptr ? a.dst_list[z] : a.dst + z * a.dst_pstride;
+}
 
 // element load/store at a 32-bit byte offset from a wave-uniform base, so the
 // compiler emits the scalar-base + 32-bit-offset addressing form
@@ -261,11 +268,19 @@ __device__ __forceinline__ void fwd_cols_body(const NttArgs &a, const Limb &lb,
 template <bool kPre>
 __global__ __launch_bounds__(512) void ntt_fwd_cols(NttArgs a) {
   __shared__ int32_t xch[kRows * kTileCols];
-  const Limb lb = decode(a.map, blockIdx.y);
-  const void *src = a.src + blockIdx.z * a.src_pstride +
-                    (static_cast<size_t>(lb.sl) << kLogN);
+  LimbMap m = a.map;
+  if (a.group_alpha > 0) {
+    m.skip_lo = blockIdx.z * a.group_alpha;
+    m.skip_len = min(a.group_alpha, m.num_q - m.skip_lo);
+    if (static_cast<int>(blockIdx.y) >= a.group_limbs - m.skip_len) return;
+  }
+  const Limb lb = decode(m, blockIdx.y);
+  const uint32_t *sbase =
+      a.dst_list[0] != nullptr ? a.dst_list[blockIdx.z]
+                               : a.src + blockIdx.z * a.src_pstride;
+  const void *src = sbase + (static_cast<size_t>(lb.sl) << kLogN);
   void *dst =
-      a.dst + blockIdx.z * a.dst_pstride + (static_cast<size_t>(lb.l) << kLogN);
+      poly_dst(a, blockIdx.z) + (static_cast<size_t>(lb.l) << kLogN);
   const uint32_t col = blockIdx.x * kTileCols + (threadIdx.x & (kTileCols - 1));
   const int rg = threadIdx.x / kTileCols;
   uint32_t x[16];
@@ -383,9 +398,15 @@ __device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
 template <int kEpi>
 __global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
   __shared__ int32_t xch[kTileRows * kRowPad];
-  const Limb lb = decode(a.map, blockIdx.y);
+  LimbMap m = a.map;
+  if (a.group_alpha > 0) {
+    m.skip_lo = blockIdx.z * a.group_alpha;
+    m.skip_len = min(a.group_alpha, m.num_q - m.skip_lo);
+    if (static_cast<int>(blockIdx.y) >= a.group_limbs - m.skip_len) return;
+  }
+  const Limb lb = decode(m, blockIdx.y);
   uint32_t *dst =
-      a.dst + blockIdx.z * a.dst_pstride + (static_cast<size_t>(lb.l) << kLogN);
+      poly_dst(a, blockIdx.z) + (static_cast<size_t>(lb.l) << kLogN);
   const int c = threadIdx.x & 15;
   const uint32_t rbase =
       static_cast<uint32_t>((blockIdx.x * kTileRows + (threadIdx.x >> 4)) *
@@ -467,7 +488,7 @@ __global__ __launch_bounds__(256) void ntt_inv_rows(NttArgs a) {
   const uint32_t *src = a.src + blockIdx.z * a.src_pstride +
                         (static_cast<size_t>(lb.sl) << kLogN);
   uint32_t *dst =
-      a.dst + blockIdx.z * a.dst_pstride + (static_cast<size_t>(lb.l) << kLogN);
+      poly_dst(a, blockIdx.z) + (static_cast<size_t>(lb.l) << kLogN);
   const int c = threadIdx.x & 15;
   const uint32_t rbase =
       static_cast<uint32_t>((blockIdx.x * kTileRows + (threadIdx.x >> 4)) *
@@ -558,7 +579,7 @@ __global__ __launch_bounds__(512) void ntt_inv_cols(NttArgs a) {
   __shared__ int32_t xch[kRows * kTileCols];
   const Limb lb = decode(a.map, blockIdx.y);
   uint32_t *dst =
-      a.dst + blockIdx.z * a.dst_pstride + (static_cast<size_t>(lb.l) << kLogN);
+      poly_dst(a, blockIdx.z) + (static_cast<size_t>(lb.l) << kLogN);
   const uint32_t col = blockIdx.x * kTileCols + (threadIdx.x & (kTileCols - 1));
   const int rg = threadIdx.x / kTileCols;
   uint32_t x[16];
@@ -573,7 +594,189 @@ __global__ __launch_bounds__(512) void ntt_inv_cols(NttArgs a) {
     inv_cols_body<kEpi, false>(a, lb, x, q, qinv, dst, xch);
 }
 
+
+// ------------------------------------------------------------------------
+// Fused ModUp row pass + evk inner product + CAccum (Context.cpp:609-712):
+//   acc_{b,a}[l] = sum_g MontMul(u_g[l], key_g.{b,a}[l'])
+//                  (+ MontMul(p_prod[l], c{b,a}[l]) for q limbs)
+// where u_g[l] = d[l] for the group's own limbs and otherwise the forward
+// NTT of BConv output (stages 8..15 done here on the column-pass result).
+// The ModUp output never goes back to HBM. grid (kRows/kTileRows, L+alpha).
+// ------------------------------------------------------------------------
+template <bool kLazy>
+__device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
+                                            bool aux, int ti, uint32_t q,
+                                            uint32_t qinv, int32_t *xch) {
+  using A = Arith<kLazy>;
+  using T = typename A::T;
+  const A ar{static_cast<T>(q)};
+  const int32_t qs = static_cast<int32_t>(q);
+  const int32_t qi = static_cast<int32_t>(qinv);
+  const uint32_t *tw = a.tab.tw + (static_cast<size_t>(ti) << kLogN);
+  const int c = threadIdx.x & 15;
+  const int r = threadIdx.x >> 4;
+  const int row = blockIdx.x * kTileRows + r;
+  const uint32_t rbase = static_cast<uint32_t>(row * kCols) * 4u;
+  const uint32_t cbase = rbase + 64u * c;  // this thread's 16 contiguous words
+  T *xr = reinterpret_cast<T *>(xch) + r * kRowPad;
+  uint32_t w1[15], w2[15];
+#pragma unroll
+  for (int s = 0, i = 0; s < 4; s++)
+#pragma unroll
+    for (int g = 0; g < (1 << s); g++, i++) {
+      w1[i] = tw[(256 << s) + (row << s) + g];
+      w2[i] = tw[(4096 << s) + (row << (4 + s)) + (c << s) + g];
+    }
+  const size_t loff = static_cast<size_t>(l) << kLogN;
+  const size_t koff = loff + (aux ? a.key_gap : 0);
+  uint32_t accb[16], acca[16];
+#pragma unroll
+  for (int k = 0; k < 16; k++) accb[k] = acca[k] = 0;
+  bool synced = false;
+  for (int g = 0; g < a.beta; g++) {
+    const int own_lo = g * a.alpha;
+    const int own_hi = min(own_lo + a.alpha, a.num_q);
+    uint32_t u[16];
+    if (l >= own_lo && l < own_hi) {
+      // own limb: the input itself (ModSwitch.cu:466-470 copies it)
+      const uint32_t *dl = a.d + loff;
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        uint4 t = ld_at<uint4>(dl, cbase + 16u * v);
+        u[4 * v] = t.x;
+        u[4 * v + 1] = t.y;
+        u[4 * v + 2] = t.z;
+        u[4 * v + 3] = t.w;
+      }
+    } else {
+      const uint32_t *src = a.modup + g * a.group_stride + loff;
+      T x[16];
+#pragma unroll
+      for (int k = 0; k < 16; k++)
+        x[k] = static_cast<T>(ld_at<uint32_t>(src, rbase + (c + 16 * k) * 4u));
+#pragma unroll
+      for (int s = 0, i = 0; s < 4; s++) {
+        const int h = 8 >> s;
+#pragma unroll
+        for (int gg = 0; gg < (1 << s); gg++, i++) {
+          const uint32_t w = w1[i];
+          const uint32_t wq = w * qinv;
+#pragma unroll
+          for (int k = gg * 2 * h; k < gg * 2 * h + h; k++)
+            ar.ct(x[k], x[k + h], w, wq);
+        }
+      }
+      if (synced) __syncthreads();  // previous group's LDS reads are done
+#pragma unroll
+      for (int k = 0; k < 16; k++) xr[pidx(c + 16 * k)] = x[k];
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 16; k++) x[k] = xr[pidx(16 * c + k)];
+      synced = true;
+#pragma unroll
+      for (int s = 0, i = 0; s < 4; s++) {
+        const int h = 8 >> s;
+#pragma unroll
+        for (int gg = 0; gg < (1 << s); gg++, i++) {
+          const uint32_t w = w2[i];
+          const uint32_t wq = w * qinv;
+#pragma unroll
+          for (int k = gg * 2 * h; k < gg * 2 * h + h; k++)
+            ar.ct(x[k], x[k + h], w, wq);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 16; k++) u[k] = ar.canon_fwd(x[k]);
+    }
+    const uint32_t *kbp = a.kb[g] + koff;
+    const uint32_t *kap = a.ka[g] + koff;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      uint4 tb = ld_at<uint4>(kbp, cbase + 16u * v);
+      uint4 ta = ld_at<uint4>(kap, cbase + 16u * v);
+      const uint32_t kbv[4] = {tb.x, tb.y, tb.z, tb.w};
+      const uint32_t kav[4] = {ta.x, ta.y, ta.z, ta.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int32_t uv = static_cast<int32_t>(u[4 * v + j]);
+        accb[4 * v + j] = add_mod(
+            accb[4 * v + j], mont_mul(uv, static_cast<int32_t>(kbv[j]), q, qi), q);
+        acca[4 * v + j] = add_mod(
+            acca[4 * v + j], mont_mul(uv, static_cast<int32_t>(kav[j]), q, qi), q);
+      }
+    }
+  }
+  if (!aux) {
+    // CAccum (Context.cpp:684-699): acc += p_prod * ct (bx, and ax if given)
+    const int32_t pp = static_cast<int32_t>(a.p_prod[l]);
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      uint4 tb = ld_at<uint4>(a.cb + loff, cbase + 16u * v);
+      const uint32_t cbv[4] = {tb.x, tb.y, tb.z, tb.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        accb[4 * v + j] = add_mod(
+            accb[4 * v + j], mont_mul(pp, static_cast<int32_t>(cbv[j]), q, qi), q);
+      if (a.ca != nullptr) {
+        uint4 ta = ld_at<uint4>(a.ca + loff, cbase + 16u * v);
+        const uint32_t cav[4] = {ta.x, ta.y, ta.z, ta.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          acca[4 * v + j] = add_mod(
+              acca[4 * v + j], mont_mul(pp, static_cast<int32_t>(cav[j]), q, qi), q);
+      }
+    }
+  }
+  (void)qs;
+  uint32_t *ob = a.acc_b + loff;
+  uint32_t *oa = a.acc_a + loff;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    st_at<uint4>(ob, cbase + 16u * v,
+                 make_uint4(accb[4 * v], accb[4 * v + 1], accb[4 * v + 2],
+                            accb[4 * v + 3]));
+    st_at<uint4>(oa, cbase + 16u * v,
+                 make_uint4(acca[4 * v], acca[4 * v + 1], acca[4 * v + 2],
+                            acca[4 * v + 3]));
+  }
+}
+
+__global__ __launch_bounds__(256) void modup_keyacc(KeyAccArgs a) {
+  __shared__ int32_t xch[kTileRows * kRowPad];
+  const int l = blockIdx.y;
+  const bool aux = l >= a.num_q;
+  const int ti = a.tab_off + l + (aux ? a.tab_gap : 0);
+  const uint32_t q = a.tab.q[ti];
+  const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[ti]);
+  if (q < (1u << 30))
+    keyacc_body<true>(a, l, aux, ti, q, qinv, xch);
+  else
+    keyacc_body<false>(a, l, aux, ti, q, qinv, xch);
+}
+
 }  // namespace
+
+hipError_t launch_ntt_fwd_cols(const NttArgs &a, int num_limbs, int num_z,
+                               hipStream_t s) {
+  if (num_limbs <= 0 || num_z <= 0) return hipSuccess;
+  dim3 gc(kCols / kTileCols, num_limbs, num_z);
+  hipLaunchKernelGGL(ntt_fwd_cols<false>, gc, dim3(512), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_ntt_fwd_rows(const NttArgs &a, int num_limbs, int num_z,
+                               hipStream_t s) {
+  if (num_limbs <= 0 || num_z <= 0) return hipSuccess;
+  dim3 gr(kRows / kTileRows, num_limbs, num_z);
+  hipLaunchKernelGGL(ntt_fwd_rows<kEpiStore>, gr, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_modup_keyacc(const KeyAccArgs &a, hipStream_t s) {
+  dim3 g(kRows / kTileRows, a.num_q + a.alpha);
+  hipLaunchKernelGGL(modup_keyacc, g, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
 
 hipError_t launch_ntt_fwd(const NttArgs &a, int num_limbs, int num_polys,
                           bool pre_const, int epilogue, hipStream_t s) {
@@ -687,6 +890,91 @@ extern "C" int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m,
                      static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
     return set_error(CHD_ERR_HIP, std::string("chd_k_ntt_inv: ") +
+                                      hipGetErrorString(e));
+  return 0;
+}
+
+extern "C" int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
+                                    uint32_t *modup, long long group_stride,
+                                    int num_groups, int alpha, int group_limbs,
+                                    int with_rows, void *stream) {
+  if (!t || !m || !modup || num_groups < 1 || alpha < 1 ||
+      group_limbs < m->num_q || (num_groups - 1) * alpha >= m->num_q)
+    return set_error(CHD_ERR_ARG, "chd_k_ntt_fwd_groups: invalid argument");
+  NttArgs a{};
+  a.src = modup;
+  a.dst = modup;
+  a.src_pstride = group_stride;
+  a.dst_pstride = group_stride;
+  a.map = *m;
+  a.map.src_gap = 0;
+  a.tab = *t;
+  a.group_alpha = alpha;
+  a.group_limbs = group_limbs;
+  // grid.y covers the largest group (the smallest skip range)
+  const int min_skip = std::min(alpha, m->num_q - (num_groups - 1) * alpha);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_ntt_fwd_cols(a, group_limbs - min_skip, num_groups, s);
+  if (e == hipSuccess && with_rows)
+    e = launch_ntt_fwd_rows(a, group_limbs - min_skip, num_groups, s);
+  if (e != hipSuccess)
+    return set_error(CHD_ERR_HIP, std::string("chd_k_ntt_fwd_groups: ") +
+                                      hipGetErrorString(e));
+  return 0;
+}
+
+extern "C" int chd_k_modup_keyacc(const chd_tables *t,
+                                  const chd_keyacc_args *args, void *stream) {
+  if (!t || !args || !args->modup || !args->d || !args->p_prod ||
+      !args->cb || !args->acc_b || !args->acc_a || args->alpha < 1 ||
+      args->beta < 1 || args->beta > kMaxGroups ||
+      (args->beta - 1) * args->alpha >= args->num_q ||
+      args->beta * args->alpha < args->num_q)
+    return set_error(CHD_ERR_ARG, "chd_k_modup_keyacc: invalid argument");
+  for (int g = 0; g < args->beta; g++)
+    if (!args->kb[g] || !args->ka[g])
+      return set_error(CHD_ERR_ARG, "chd_k_modup_keyacc: null key pointer");
+  KeyAccArgs a;
+  static_cast<chd_keyacc_args &>(a) = *args;
+  a.tab = *t;
+  hipError_t e = launch_modup_keyacc(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return set_error(CHD_ERR_HIP, std::string("chd_k_modup_keyacc: ") +
+                                      hipGetErrorString(e));
+  return 0;
+}
+
+extern "C" int chd_k_ntt_fwd_moddown_multi(
+    const chd_tables *t, const chd_limb_map *m, uint32_t *const *dst,
+    int num_polys, int num_limbs, const uint32_t *src2,
+    long long src2_pstride, int src2_lo, int src2_hi,
+    const uint32_t *inv_prod, const uint32_t *pad, void *stream) {
+  if (!t || !m || !dst || !inv_prod || num_limbs < 0 || num_polys < 1 ||
+      num_polys > 4 || (src2 == nullptr && src2_hi > src2_lo))
+    return set_error(CHD_ERR_ARG,
+                     "chd_k_ntt_fwd_moddown_multi: invalid argument");
+  NttArgs a{};
+  for (int p = 0; p < num_polys; p++) {
+    if (!dst[p] || dst[p] == src2)
+      return set_error(CHD_ERR_ARG,
+                       "chd_k_ntt_fwd_moddown_multi: invalid destination");
+    a.dst_list[p] = dst[p];
+  }
+  a.src = dst[0];
+  a.dst = dst[0];
+  a.map = *m;
+  a.map.src_gap = 0;
+  a.tab = *t;
+  a.src2 = src2;
+  a.src2_pstride = src2_pstride;
+  a.src2_lo = src2_lo;
+  a.src2_hi = src2_hi;
+  a.cst2 = inv_prod;
+  a.pad = pad;
+  hipError_t e = launch_ntt_fwd(a, num_limbs, num_polys, false, kEpiModDown,
+                                static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return set_error(CHD_ERR_HIP, std::string("chd_k_ntt_fwd_moddown_multi: ") +
                                       hipGetErrorString(e));
   return 0;
 }

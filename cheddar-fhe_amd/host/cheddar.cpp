@@ -580,46 +580,98 @@ void ModSwitchHandler<uint32_t>::BuildSwitch(
   st.table.Upload(packed.data(), packed.size());
 }
 
+// src/core/ModSwitch.cu:429-485: INTTAndMultConst(centre) of src into intt,
+// then the BConv of every dnum group in one launch, group i into dst[i].
+void ModSwitchHandler<uint32_t>::ModUpBconv(word *const *dst,
+                                            const DvConstView<word> &src,
+                                            word *intt) const {
+  const NPInfo np = param_.LevelToNP(level_, 0);
+  const int num_q = np.GetNumQ();
+  const int n = param_.degree_;
+  AssertTrue(src.QSize() == num_q * n, "ModUp src q size mismatch");
+  AssertTrue(src.AuxSize() == 0, "ModUp src aux size mismatch");
+  AssertTrue(beta_ <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
+  DvView<word> intt_view(intt, num_q * n, 0);
+  ntt_.INTTAndMultConst(intt_view, np, src,
+                        DvConstView<word>(mod_up1_.data(), num_q, 0), true);
+  NPInfo np_aux = np;
+  np_aux.num_aux_ = num_aux_;
+  chd_limb_map m = NoSkipMap(param_, np_aux);
+  chd_bconv_job jobs[CHD_MAX_JOBS] = {};
+  for (int i = 0; i < beta_; i++) {
+    const int s0 = i * num_aux_;
+    const int s1 = std::min((i + 1) * num_aux_, num_q);
+    const SwitchTable &st = mod_up_[i];
+    jobs[i].dst = dst[i];
+    jobs[i].src = reinterpret_cast<const int32_t *>(intt) +
+                  static_cast<size_t>(s0) * n;
+    jobs[i].table = st.table.as<void>();
+    jobs[i].src_len = st.src_len;
+    jobs[i].dst_len = st.dst_len;
+    jobs[i].skip_lo = s0;
+    jobs[i].skip_len = s1 - s0;
+  }
+  K(chd_k_bconv_batch(&ntt_.Tables(), &m, jobs, beta_, CurrentStream()));
+}
+
+// ModUp with every group's column pass (and, with_rows, row pass) batched;
+// group i lives at modup + i * group_stride. Own limbs are not written.
+void ModSwitchHandler<uint32_t>::ModUpGroups(word *modup,
+                                             long long group_stride,
+                                             const DvConstView<word> &src,
+                                             word *intt, bool with_rows) const {
+  const NPInfo np = param_.LevelToNP(level_, 0);
+  const int num_q = np.GetNumQ();
+  word *dst[CHD_MAX_JOBS];
+  AssertTrue(beta_ <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
+  for (int i = 0; i < beta_; i++) dst[i] = modup + i * group_stride;
+  ModUpBconv(dst, src, intt);
+  NPInfo np_aux = np;
+  np_aux.num_aux_ = num_aux_;
+  chd_limb_map m = NoSkipMap(param_, np_aux);
+  K(chd_k_ntt_fwd_groups(&ntt_.Tables(), &m, modup, group_stride, beta_,
+                         num_aux_, num_q + num_aux_, with_rows ? 1 : 0,
+                         CurrentStream()));
+}
+
 // src/core/ModSwitch.cu:429-509
 void ModSwitchHandler<uint32_t>::ModUp(std::vector<DvView<word>> &dst,
                                        const DvConstView<word> &src) const {
   const NPInfo np = param_.LevelToNP(level_, 0);
   const int num_q = np.GetNumQ();
   const int n = param_.degree_;
-  AssertTrue(src.QSize() == num_q * n, "ModUp src q size mismatch");
-  AssertTrue(src.AuxSize() == 0, "ModUp src aux size mismatch");
   AssertTrue(static_cast<int>(dst.size()) == beta_, "ModUp dst size mismatch");
-  Scratch intt(static_cast<size_t>(num_q) * n);
-  DvView<word> intt_view(intt.data(), num_q * n, 0);
-  ntt_.INTTAndMultConst(intt_view, np,
-                        src, DvConstView<word>(mod_up1_.data(), num_q, 0),
-                        true);
-  NPInfo np_aux = np;
-  np_aux.num_aux_ = num_aux_;
+  AssertTrue(beta_ <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
+  const long long gs = static_cast<long long>(num_q + num_aux_) * n;
+  bool strided = true;
   for (int i = 0; i < beta_; i++) {
-    const int s0 = i * num_aux_;
-    const int s1 = std::min((i + 1) * num_aux_, num_q);
     AssertTrue(dst[i].AuxSize() == num_aux_ * n &&
                    dst[i].QSize() == num_q * n,
                "ModUp dst size mismatch");
+    strided = strided && dst[i].data() == dst[0].data() + i * gs;
+  }
+  for (int i = 0; i < beta_; i++) {
+    const int s0 = i * num_aux_;
+    const int s1 = std::min((i + 1) * num_aux_, num_q);
     HipCheck(hipMemcpyAsync(dst[i].data() + static_cast<size_t>(s0) * n,
                             src.data() + static_cast<size_t>(s0) * n,
                             static_cast<size_t>(s1 - s0) * n * sizeof(word),
                             hipMemcpyDeviceToDevice, CurrentStream()),
              "hipMemcpyAsync");
   }
+  Scratch intt(static_cast<size_t>(num_q) * n);
+  if (strided) {  // groups equally spaced: one launch per pass for all
+    ModUpGroups(dst[0].data(), gs, src, intt.data(), true);
+    return;
+  }
+  word *d[CHD_MAX_JOBS];
+  for (int i = 0; i < beta_; i++) d[i] = dst[i].data();
+  ModUpBconv(d, src, intt.data());
+  NPInfo np_aux = np;
+  np_aux.num_aux_ = num_aux_;
   for (int i = 0; i < beta_; i++) {
     const int s0 = i * num_aux_;
     const int s1 = std::min((i + 1) * num_aux_, num_q);
-    const SwitchTable &st = mod_up_[i];
-    chd_limb_map m = NoSkipMap(param_, np_aux);
-    m.skip_lo = s0;
-    m.skip_len = s1 - s0;
-    K(chd_k_bconv(&ntt_.Tables(), &m, dst[i].data(),
-                  reinterpret_cast<const int32_t *>(intt.data()) +
-                      static_cast<size_t>(s0) * n,
-                  st.src_len, st.dst_len, st.table.as<void>(),
-                  CurrentStream()));
     ntt_.NTTForModUp(dst[i], np_aux, s0, s1, DvConstView<word>(dst[i]));
   }
 }
@@ -667,7 +719,21 @@ void ModSwitchHandler<uint32_t>::ModDownAndRescale(
 void ModSwitchHandler<uint32_t>::ModDownWorker(DvView<word> &dst,
                                                const DvConstView<word> &src,
                                                Kind kind) const {
+  ModDownMulti({dst.data()}, src.data(), 0, kind);
+}
+
+// ModDownWorker over num_polys polynomials with one launch per phase:
+// INTTForModDown (centre), BConv, NTTForModDown.
+void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
+                                              const word *src,
+                                              long long src_pstride,
+                                              Kind kind) const {
   const int n = param_.degree_;
+  const int num_polys = static_cast<int>(dst.size());
+  AssertTrue(num_polys >= 1 && num_polys <= 4,
+             "ModDown: 1 to 4 polynomials per call");
+  AssertTrue(kind == Kind::ModDown || level_ > 0,
+             "Not enough q primes to rescale");
   const int num_src_aux = kind == Kind::Rescale ? 0 : num_aux_;
   const NPInfo np_src = param_.LevelToNP(level_, num_src_aux);
   const NPInfo np_dst =
@@ -681,15 +747,39 @@ void ModSwitchHandler<uint32_t>::ModDownWorker(DvView<word> &dst,
                                                   : mod_down_rescale_;
   AssertTrue(st.src_len == src_len && st.dst_len == dst_len,
              "ModDown: constant table mismatch");
-  Scratch intt(static_cast<size_t>(src_len) * n);
-  DvView<word> intt_view(intt.data(), src_len * n, 0);
-  ntt_.INTTForModDown(intt_view, np_src, np_non_intt, src,
-                      DvConstView<word>(st.const1.data(), src_len,
-                                        num_src_aux));
+  AssertTrue(np_src.num_ter_ == np_non_intt.num_ter_,
+             "INTTForModDown: terminal-prime INTT is not supported");
+  const long long ilen = static_cast<long long>(src_len) * n;
+  Scratch intt(static_cast<size_t>(num_polys) * ilen);
+  for (int p = 0; p < num_polys; p++) {
+    AssertTrue(dst[p] != nullptr, "ModDown: null destination");
+    // INTTForModDown requires src != dst per polynomial
+    AssertTrue(dst[p] != src + p * src_pstride,
+               "ModDown: src and dst should be different");
+  }
+  // INTTForModDown (NTT.cu:973-1071 case 1) of all polynomials
+  chd_limb_map mi{};
+  mi.num_q = np_src.num_main_ - np_non_intt.num_main_;
+  mi.skip_lo = INT_MAX;
+  mi.tab_off = param_.GetMaxNumTer() + np_non_intt.num_main_;
+  mi.tab_gap = param_.MainLeft(np_src);
+  const size_t off =
+      static_cast<size_t>(np_src.num_ter_ + np_non_intt.num_main_) * n;
+  K(chd_k_ntt_inv(&ntt_.Tables(), &mi, intt.data(), ilen, src + off,
+                  src_pstride, src_len, num_polys, st.const1.data(), 1,
+                  CurrentStream()));
   chd_limb_map m = NoSkipMap(param_, np_dst);
-  K(chd_k_bconv(&ntt_.Tables(), &m, dst.data(),
-                reinterpret_cast<const int32_t *>(intt.data()), src_len,
-                dst_len, st.table.as<void>(), CurrentStream()));
+  chd_bconv_job jobs[CHD_MAX_JOBS] = {};
+  for (int p = 0; p < num_polys; p++) {
+    jobs[p].dst = dst[p];
+    jobs[p].src = reinterpret_cast<const int32_t *>(intt.data()) + p * ilen;
+    jobs[p].table = st.table.as<void>();
+    jobs[p].src_len = src_len;
+    jobs[p].dst_len = dst_len;
+    jobs[p].skip_lo = INT_MAX;
+    jobs[p].skip_len = 0;
+  }
+  K(chd_k_bconv_batch(&ntt_.Tables(), &m, jobs, num_polys, CurrentStream()));
   const DeviceVector<word> &ipp =
       kind == Kind::ModDown   ? inv_prime_prod_
       : kind == Kind::Rescale ? rescale_inv_prime_prod_
@@ -697,12 +787,14 @@ void ModSwitchHandler<uint32_t>::ModDownWorker(DvView<word> &dst,
   const word *pad = kind == Kind::ModDown   ? nullptr
                     : kind == Kind::Rescale ? rescale_padding_.data()
                                             : mod_down_rescale_padding_.data();
+  // NTTForModDown (NTT.cu:417-604) with src2 = the untouched low limbs
   const int src2_off = std::max(0, np_src.num_ter_ - np_dst.num_ter_);
-  DvConstView<word> src2(src.data() + static_cast<size_t>(src2_off) * n,
-                         dst_len * n, 0);
-  ntt_.NTTForModDown(dst, np_dst, np_non_intt, DvConstView<word>(dst), src2,
-                     DvConstView<word>(ipp.data(), dst_len, 0),
-                     DvConstView<word>(pad, pad ? dst_len : 0, 0));
+  const int s2_lo = np_dst.num_ter_ - np_non_intt.num_ter_;
+  const int s2_hi = s2_lo + np_non_intt.GetNumQ();
+  K(chd_k_ntt_fwd_moddown_multi(&ntt_.Tables(), &m, dst.data(), num_polys,
+                                dst_len, src + static_cast<size_t>(src2_off) * n,
+                                src_pstride, s2_lo, s2_hi, ipp.data(), pad,
+                                CurrentStream()));
 }
 
 // ---------------------------------------------------------------- Context --
@@ -753,7 +845,10 @@ void Context<uint32_t>::TensorV(int level, CtRef res, CtCRef a,
                         DvConstView<word>(b.ax, sz, 0)});
 }
 
-// src/core/Context.cpp:609-712
+// src/core/Context.cpp:609-712: ModUp, PAccum over the dnum groups and
+// CAccum, fused. ModUpGroups leaves every group after its column pass; one
+// kernel then finishes the NTT of each group limb by limb, multiplies by the
+// key and accumulates, so the ModUp output is written and read once.
 void Context<uint32_t>::KeyMultNoModDownV(int level, word *acc_b, word *acc_a,
                                           const word *d, const word *cb,
                                           const word *ca,
@@ -768,40 +863,36 @@ void Context<uint32_t>::KeyMultNoModDownV(int level, word *acc_b, word *acc_a,
   AssertTrue(static_cast<int>(key.bx.size()) >= beta &&
                  key.bx.size() == key.ax.size(),
              "Beta mismatch");
+  AssertTrue(beta <= CHD_MAX_JOBS, "MultKeyNoModDown: dnum too large");
+  const auto &ms = mod_switch_handlers_.at(level);
+  AssertTrue(ms.GetBeta() == beta, "MultKeyNoModDown: beta mismatch");
   const int total = num_q + num_aux;
-  Scratch modup(static_cast<size_t>(beta) * total * n);
-  std::vector<DvView<word>> up_views;
-  for (int g = 0; g < beta; g++)
-    up_views.emplace_back(modup.data() + static_cast<size_t>(g) * total * n,
-                          total * n, num_aux * n);
-  mod_switch_handlers_.at(level).ModUp(up_views,
-                                       DvConstView<word>(d, num_q * n, 0));
-  const NPInfo np(a_np.num_main_, a_np.num_ter_, num_aux);
-  std::vector<DvView<word>> acc{DvView<word>(acc_b, total * n, num_aux * n),
-                                DvView<word>(acc_a, total * n, num_aux * n)};
-  const int key_total = key.np.GetNumTotal() * n - prime_offset * n;
-  std::vector<std::vector<DvConstView<word>>> key_views;
-  std::vector<DvConstView<word>> up_const;
+  const long long gs = static_cast<long long>(total) * n;
+  Scratch buf(static_cast<size_t>(beta) * gs + static_cast<size_t>(num_q) * n);
+  ms.ModUpGroups(buf.data(), gs, DvConstView<word>(d, num_q * n, 0),
+                 buf.data() + beta * gs, false);
+  chd_keyacc_args k{};
+  k.num_q = num_q;
+  k.tab_off = param_.TerLeft(a_np);
+  k.tab_gap = param_.MainLeft(a_np);
+  k.alpha = num_aux;
+  k.beta = beta;
+  k.modup = buf.data();
+  k.group_stride = gs;
+  k.d = d;
   for (int g = 0; g < beta; g++) {
-    key_views.push_back(
-        {DvConstView<word>(key.bx[g] + prime_offset * n, key_total,
-                           num_aux * n),
-         DvConstView<word>(key.ax[g] + prime_offset * n, key_total,
-                           num_aux * n)});
-    up_const.emplace_back(up_views[g]);
+    k.kb[g] = key.bx[g] + static_cast<size_t>(prime_offset) * n;
+    k.ka[g] = key.ax[g] + static_cast<size_t>(prime_offset) * n;
   }
-  elem_handler_.PAccum(acc, np, key_views, up_const);
-  // accum.{b,a} (q part) += p_prod * ct.{b,a}
-  std::vector<DvView<word>> cres{DvView<word>(acc_b, num_q * n, 0)};
-  std::vector<DvConstView<word>> ct_part{DvConstView<word>(cb, num_q * n, 0)};
-  std::vector<DvConstView<word>> acc_part{
-      DvConstView<word>(acc_b, total * n, num_aux * n)};
-  if (ca != nullptr) {
-    cres.emplace_back(acc_a, num_q * n, 0);
-    ct_part.emplace_back(ca, num_q * n, 0);
-    acc_part.emplace_back(acc_a, total * n, num_aux * n);
-  }
-  elem_handler_.CAccum(cres, a_np, {ct_part, acc_part}, {GetPProd(a_np)});
+  // key layout: q limbs of the key's level, then its aux limbs
+  k.key_gap = static_cast<long long>(key.np.GetNumQ() - prime_offset - num_q) * n;
+  AssertTrue(k.key_gap >= 0, "MultKeyNoModDown: key level below input level");
+  k.p_prod = GetPProd(a_np).data();
+  k.cb = cb;
+  k.ca = ca;
+  k.acc_b = acc_b;
+  k.acc_a = acc_a;
+  K(chd_k_modup_keyacc(&ntt_handler_.Tables(), &k, CurrentStream()));
 }
 
 // src/core/Context.cpp:862-871 with 714-737 / 559-607
@@ -819,19 +910,11 @@ void Context<uint32_t>::HMultV(int level, CtRef res, CtCRef a, CtCRef b,
   word *acc_b = acc.data();
   word *acc_a = acc.data() + static_cast<size_t>(total) * n;
   KeyMultNoModDownV(level, acc_b, acc_a, tr.rx, tr.bx, tr.ax, key);
-  const auto &ms = mod_switch_handlers_.at(level);
-  DvConstView<word> sb(acc_b, total * n, param_.alpha_ * n);
-  DvConstView<word> sa(acc_a, total * n, param_.alpha_ * n);
-  if (rescale) {
-    const int nq = param_.LevelToNP(level - 1).GetNumQ();
-    DvView<word> db(res.bx, nq * n, 0), da(res.ax, nq * n, 0);
-    ms.ModDownAndRescale(db, sb);
-    ms.ModDownAndRescale(da, sa);
-  } else {
-    DvView<word> db(res.bx, num_q * n, 0), da(res.ax, num_q * n, 0);
-    ms.ModDown(db, sb);
-    ms.ModDown(da, sa);
-  }
+  AssertTrue(!rescale || level > 0, "Not enough q primes to rescale");
+  mod_switch_handlers_.at(level).ModDownMulti(
+      {res.bx, res.ax}, acc_b, static_cast<long long>(total) * n,
+      rescale ? ModSwitchHandler<word>::Kind::ModDownAndRescale
+              : ModSwitchHandler<word>::Kind::ModDown);
 }
 
 // src/core/Context.cpp:739-774
@@ -860,10 +943,9 @@ void Context<uint32_t>::MultKeyV(int level, CtRef res, CtCRef a,
   word *acc_b = acc.data();
   word *acc_a = acc.data() + static_cast<size_t>(total) * n;
   KeyMultNoModDownV(level, acc_b, acc_a, a.ax, a.bx, nullptr, key);
-  const auto &ms = mod_switch_handlers_.at(level);
-  DvView<word> db(res.bx, num_q * n, 0), da(res.ax, num_q * n, 0);
-  ms.ModDown(db, DvConstView<word>(acc_b, total * n, param_.alpha_ * n));
-  ms.ModDown(da, DvConstView<word>(acc_a, total * n, param_.alpha_ * n));
+  mod_switch_handlers_.at(level).ModDownMulti(
+      {res.bx, res.ax}, acc_b, static_cast<long long>(total) * n,
+      ModSwitchHandler<word>::Kind::ModDown);
 }
 
 void Context<uint32_t>::PermuteV(int level, CtRef res, CtCRef a,
@@ -917,11 +999,9 @@ void Context<uint32_t>::Relinearize(Ct &res, const Ct &a,
   Scratch acc(static_cast<size_t>(2) * total * n);
   KeyMultNoModDownV(level, acc.data(), acc.data() + static_cast<size_t>(total) * n,
                     a.rx_.data(), a.bx_.data(), a.ax_.data(), RefOf(key));
-  const auto &ms = mod_switch_handlers_.at(level);
-  DvView<word> db = out.bx_.View(), da = out.ax_.View();
-  ms.ModDown(db, DvConstView<word>(acc.data(), total * n, param_.alpha_ * n));
-  ms.ModDown(da, DvConstView<word>(acc.data() + static_cast<size_t>(total) * n,
-                                   total * n, param_.alpha_ * n));
+  mod_switch_handlers_.at(level).ModDownMulti(
+      {out.bx_.data(), out.ax_.data()}, acc.data(),
+      static_cast<long long>(total) * n, ModSwitchHandler<word>::Kind::ModDown);
   out.SetScale(a.GetScale());
   out.SetNumSlots(a.GetNumSlots());
   res = std::move(out);
@@ -938,13 +1018,10 @@ void Context<uint32_t>::RelinearizeRescale(Ct &res, const Ct &a,
   Scratch acc(static_cast<size_t>(2) * total * n);
   KeyMultNoModDownV(level, acc.data(), acc.data() + static_cast<size_t>(total) * n,
                     a.rx_.data(), a.bx_.data(), a.ax_.data(), RefOf(key));
-  const auto &ms = mod_switch_handlers_.at(level);
-  DvView<word> db = out.bx_.View(), da = out.ax_.View();
-  ms.ModDownAndRescale(
-      db, DvConstView<word>(acc.data(), total * n, param_.alpha_ * n));
-  ms.ModDownAndRescale(
-      da, DvConstView<word>(acc.data() + static_cast<size_t>(total) * n,
-                            total * n, param_.alpha_ * n));
+  mod_switch_handlers_.at(level).ModDownMulti(
+      {out.bx_.data(), out.ax_.data()}, acc.data(),
+      static_cast<long long>(total) * n,
+      ModSwitchHandler<word>::Kind::ModDownAndRescale);
   out.SetScale(a.GetScale() / param_.GetRescalePrimeProd(level));
   out.SetNumSlots(a.GetNumSlots());
   res = std::move(out);

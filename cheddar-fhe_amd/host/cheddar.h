@@ -299,8 +299,26 @@ class ModSwitchHandler<uint32_t> {
                          const DvConstView<word> &src) const;
   int GetBeta() const { return beta_; }
 
- private:
+  // Batched pieces of ModUp used by the fused key switch (no single
+  // reference counterpart). ModUpBconv: INTTAndMultConst(centre) of src into
+  // intt (num_q limbs) and the BConv of every dnum group i into dst[i].
+  // ModUpGroups: ModUpBconv into modup + i * group_stride, then the column
+  // pass (with_rows: and the row pass) of NTTForModUp for all groups in one
+  // launch each. Own limbs of a group are left unwritten.
+  void ModUpBconv(word *const *dst, const DvConstView<word> &src,
+                  word *intt) const;
+  void ModUpGroups(word *modup, long long group_stride,
+                   const DvConstView<word> &src, word *intt,
+                   bool with_rows) const;
+
   enum class Kind { ModDown, Rescale, ModDownAndRescale };
+  // ModDownWorker for several polynomials at once: polynomial p of the
+  // source starts at src + p * src_pstride (words), its result goes to
+  // dst[p] (separate buffers allowed).
+  void ModDownMulti(const std::vector<word *> &dst, const word *src,
+                    long long src_pstride, Kind kind) const;
+
+ private:
   struct SwitchTable {       // one source set -> destination set
     DeviceVector<word> const1;   // (N prod_{j!=i} s_j)^-1 mod s_i
     DevBuf table;                // packed BConv table (chd_bconv_table_pack)

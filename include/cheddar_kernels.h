@@ -58,6 +58,15 @@ int chd_k_ntt_fwd_moddown(const chd_tables *t, const chd_limb_map *m,
                           int src2_lo, int src2_hi, const uint32_t *inv_prod,
                           const uint32_t *pad, void *stream);
 
+/* Same for num_polys (<= 4) polynomials in separate buffers dst[p] (in
+ * place); src2 of polynomial p is at src2 + p * src2_pstride. */
+int chd_k_ntt_fwd_moddown_multi(const chd_tables *t, const chd_limb_map *m,
+                                uint32_t *const *dst, int num_polys,
+                                int num_limbs, const uint32_t *src2,
+                                long long src2_pstride, int src2_lo,
+                                int src2_hi, const uint32_t *inv_prod,
+                                const uint32_t *pad, void *stream);
+
 /* Inverse NTT with epilogue MontMul(N*intt(x), cst[limb]), centred into
  * [-(q-1)/2, (q-1)/2] when centre (NTT.cu:673-813, 973-1128). */
 int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
@@ -76,6 +85,57 @@ int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
 int chd_k_bconv(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
                 const int32_t *src, int src_len, int dst_len,
                 const void *table, void *stream);
+
+/* Batched BConv: up to CHD_MAX_JOBS independent conversions in one launch
+ * (the beta groups of ModUp, or the two polynomials of ModDown). Each job
+ * has its own source, table, lengths and skip range; all share the prime
+ * mapping of m (dst positions are logical limbs of one level). */
+#define CHD_MAX_JOBS 8
+typedef struct chd_bconv_job {
+  uint32_t *dst;
+  const int32_t *src;
+  const void *table;
+  int src_len, dst_len;
+  int skip_lo, skip_len;
+} chd_bconv_job;
+int chd_k_bconv_batch(const chd_tables *t, const chd_limb_map *m,
+                      const chd_bconv_job *jobs, int num_jobs, void *stream);
+
+/* Column pass (stages 0..7) of NTTForModUp for all dnum groups in one launch:
+ * group g's polynomial sits at modup + g * group_stride (group_limbs limbs,
+ * in place) and its own limbs [g alpha, min((g+1) alpha, m->num_q)) are
+ * skipped (NTT.cu:815-887). with_rows also runs stages 8..15 (the complete
+ * NTTForModUp); without it the data is left for chd_k_modup_keyacc. */
+int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
+                         uint32_t *modup, long long group_stride,
+                         int num_groups, int alpha, int group_limbs,
+                         int with_rows, void *stream);
+
+/* Fused ModUp row pass + evaluation-key inner product + CAccum
+ * (Context.cpp:609-712, ElementWise.cu:225-366):
+ *   acc_{b,a}[l] = sum_g MontMul(u_g[l], key_g.{b,a}[l'])
+ *                  + MontMul(p_prod[l], c{b,a}[l])   (q limbs only)
+ * u_g[l] = d[l] on group g's own limbs, otherwise the forward NTT of the
+ * column-pass data in modup (left by chd_k_ntt_fwd_groups). l' = l for q
+ * limbs and l + key_gap/N for aux limbs. ca may be NULL (MultKey). */
+typedef struct chd_keyacc_args {
+  int num_q;
+  int tab_off, tab_gap;
+  int alpha, beta;
+  const uint32_t *modup;
+  long long group_stride;
+  const uint32_t *d;
+  const uint32_t *kb[CHD_MAX_JOBS];
+  const uint32_t *ka[CHD_MAX_JOBS];
+  long long key_gap;
+  const uint32_t *p_prod;
+  const uint32_t *cb;
+  const uint32_t *ca;
+  uint32_t *acc_b;
+  uint32_t *acc_a;
+} chd_keyacc_args;
+int chd_k_modup_keyacc(const chd_tables *t, const chd_keyacc_args *args,
+                       void *stream);
 
 /* Tensor (ElementWise.cu:504-575, 921-953): Karatsuba product of
  * (b1,a1) x (b2,a2) -> (bx, ax, rx) over num_limbs limbs. src2 == src1

@@ -126,14 +126,24 @@ def _evk(r, main, aux, beta):
     return kb, ka
 
 
-@pytest.mark.parametrize("L", [24, 20, 17])
-def test_mod_up(chd, ks, L):
+@pytest.mark.parametrize("L,layout", [(24, "strided"), (20, "strided"),
+                                      (17, "strided"), (24, "separate"),
+                                      (17, "separate")])
+def test_mod_up(chd, ks, L, layout):
+    """Group outputs equally spaced in one buffer take the batched launch;
+    separately allocated ones take the per-group NTT."""
     param, ctx, main, aux = ks
     level = L - 1
     x = uniform_limbs(rng(100 + L), main[:L])
     beta = ctx.beta(level)
     assert beta == (L + 7) // 8
-    outs = [zeros(L + 8, N) for _ in range(beta)]
+    if layout == "strided":
+        whole = zeros(beta * (L + 8), N)
+        outs = [whole[g * (L + 8):(g + 1) * (L + 8)] for g in range(beta)]
+    else:
+        # a gap between the groups rules out the strided path
+        whole = zeros(beta * (L + 9), N)
+        outs = [whole[g * (L + 9):g * (L + 9) + L + 8] for g in range(beta)]
     ctx.mod_up(level, outs, dev(x))
     want = _orc.mod_up(x, main[:L], aux, 16)
     for g in range(beta):
