@@ -31,6 +31,8 @@ LIMB_BYTES = 4 * N
 # one limb-transform moves one limb in and one limb out (algorithmic bytes)
 LIMB_TRANSFORM_BYTES = 2 * LIMB_BYTES
 MALL_BYTES = 256 << 20
+# calibration copy: 1 GiB each way, far beyond L2 and the 256 MiB MALL
+COPY_BYTES = 1 << 30
 
 
 def parse():
@@ -41,7 +43,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU-baseline leg")
     ap.add_argument("--only", choices=["ntt_fwd", "ntt_inv", "hmult",
-                                       "bconv"],
+                                       "bconv", "copy"],
                     help="run only this workload's timed loop (for "
                          "profiling); prints its average time")
     return ap.parse_args()
@@ -192,6 +194,16 @@ def run_only(chd, what, steps):
         return bench_hmult(chd, steps) * 1e3
     if what == "bconv":
         return bench_bconv(chd, steps) * 1e3
+    if what == "copy":
+        # plain device copy of COPY_BYTES: the reference point that scales
+        # the FETCH_SIZE / WRITE_SIZE counters into HBM bytes
+        src = torch.ones(COPY_BYTES // 4, dtype=torch.int32, device="cuda")
+        dst = torch.empty_like(src)
+        stream = torch.cuda.current_stream()
+        fn = lambda i: dst.copy_(src)  # noqa: E731
+        fn(0)
+        torch.cuda.synchronize()
+        return event_time_ms(fn, steps, stream) / steps * 1e3
     primes = ntt_primes(30, 32)
     plan = chd.NttPlan(primes)
     rng = np.random.default_rng(0xC0FFEE02)

@@ -131,8 +131,8 @@ __device__ __forceinline__ uint32_t *poly_dst(const NttArgs &a, int z) {
   return a.dst_list[0] != nullptr ? a.dst_list[z] : a.dst + z * a.dst_pstride;
 }
 
-// element load/store at a 32-bit byte offset from a wave-uniform base, so the
-// compiler emits the scalar-base + 32-bit-offset addressing form
+// Element load/store at a 32-bit byte offset from a wave-uniform base, so the
+// compiler emits the scalar-base + 32-bit-offset addressing form.
 template <typename T>
 __device__ __forceinline__ T ld_at(const void *base, uint32_t byte_off) {
   return *reinterpret_cast<const T *>(static_cast<const char *>(base) +
@@ -141,6 +141,22 @@ __device__ __forceinline__ T ld_at(const void *base, uint32_t byte_off) {
 template <typename T>
 __device__ __forceinline__ void st_at(void *base, uint32_t byte_off, T v) {
   *reinterpret_cast<T *>(static_cast<char *>(base) + byte_off) = v;
+}
+// Streaming (nontemporal) variants for limb data that a transform touches
+// once: the column passes' loads and stores (whole 128-byte lines per wave
+// instruction) and the row passes' strided dword accesses. Measured 8-11%
+// faster per transform. The fused key-accumulation kernel keeps default
+// loads: with many concurrent streams the hint evicts a half-used line before
+// the next instruction reads its other half (twice the traffic, measured).
+template <typename T>
+__device__ __forceinline__ T ld_nt(const void *base, uint32_t byte_off) {
+  return __builtin_nontemporal_load(reinterpret_cast<const T *>(
+      static_cast<const char *>(base) + byte_off));
+}
+template <typename T>
+__device__ __forceinline__ void st_nt(void *base, uint32_t byte_off, T v) {
+  __builtin_nontemporal_store(
+      v, reinterpret_cast<T *>(static_cast<char *>(base) + byte_off));
 }
 
 // Per-limb arithmetic policy. Values between the two passes of a transform
@@ -262,7 +278,7 @@ __device__ __forceinline__ void fwd_cols_body(const NttArgs &a, const Limb &lb,
   }
 #pragma unroll
   for (int k = 0; k < 16; k++)
-    st_at<T>(dst, ((16 * rg + k) * kCols + col) * 4u, x[k]);
+    st_nt<T>(dst, ((16 * rg + k) * kCols + col) * 4u, x[k]);
 }
 
 template <bool kPre>
@@ -286,7 +302,7 @@ __global__ __launch_bounds__(512) void ntt_fwd_cols(NttArgs a) {
   uint32_t x[16];
 #pragma unroll
   for (int k = 0; k < 16; k++)
-    x[k] = ld_at<uint32_t>(src, ((rg + 16 * k) * kCols + col) * 4u);
+    x[k] = ld_nt<uint32_t>(src, ((rg + 16 * k) * kCols + col) * 4u);
   const uint32_t q = a.tab.q[lb.ti];
   const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
   if (q < (1u << 30))
@@ -413,7 +429,7 @@ __global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
                             kCols) * 4u;
   uint32_t x[16];
 #pragma unroll
-  for (int k = 0; k < 16; k++) x[k] = ld_at<uint32_t>(dst, rbase + (c + 16 * k) * 4u);
+  for (int k = 0; k < 16; k++) x[k] = ld_nt<uint32_t>(dst, rbase + (c + 16 * k) * 4u);
   const uint32_t q = a.tab.q[lb.ti];
   const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
   if (q < (1u << 30))
@@ -479,7 +495,7 @@ __device__ __forceinline__ void inv_rows_body(const NttArgs &a, const Limb &lb,
     }
   }
 #pragma unroll
-  for (int k = 0; k < 16; k++) st_at<T>(dst, rbase + (c + 16 * k) * 4u, x[k]);
+  for (int k = 0; k < 16; k++) st_nt<T>(dst, rbase + (c + 16 * k) * 4u, x[k]);
 }
 
 __global__ __launch_bounds__(256) void ntt_inv_rows(NttArgs a) {
@@ -570,7 +586,7 @@ __device__ __forceinline__ void inv_cols_body(const NttArgs &a, const Limb &lb,
     int32_t v = static_cast<int32_t>(ar.canon_inv(ar.mul(x[k], ce, ceq)));
     if constexpr (kEpi == kEpiConstCentre)
       if (v > (qs >> 1)) v -= qs;
-    st_at<int32_t>(dst, ((rg + 16 * k) * kCols + col) * 4u, v);
+    st_nt<int32_t>(dst, ((rg + 16 * k) * kCols + col) * 4u, v);
   }
 }
 
@@ -585,7 +601,7 @@ __global__ __launch_bounds__(512) void ntt_inv_cols(NttArgs a) {
   uint32_t x[16];
 #pragma unroll
   for (int k = 0; k < 16; k++)
-    x[k] = ld_at<uint32_t>(dst, ((16 * rg + k) * kCols + col) * 4u);
+    x[k] = ld_nt<uint32_t>(dst, ((16 * rg + k) * kCols + col) * 4u);
   const uint32_t q = a.tab.q[lb.ti];
   const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
   if (q < (1u << 30))

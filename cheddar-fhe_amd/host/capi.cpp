@@ -405,7 +405,8 @@ extern "C" int chd_hrot(const chd_context *ctx, int level, uint32_t *res_bx,
              const auto &p = ctx->c->param_;
              const size_t words =
                  static_cast<size_t>(p.LevelToNP(level).GetNumQ()) * p.degree_;
-             cheddar::Scratch t(2 * words);
+             cheddar::Workspace::Use use_ws(ctx->c->GetWorkspace());
+             cheddar::Scratch t(ctx->c->GetWorkspace(), 2 * words);
              ctx->c->MultKeyV(level, {t.data(), t.data() + words, nullptr},
                               {a_bx, a_ax, nullptr},
                               MakeEvk(ctx, evk_bx, evk_ax, evk_beta));

@@ -35,14 +35,85 @@ hipStream_t CurrentStream() { return g_stream; }
 StreamScope::StreamScope(hipStream_t s) : prev_(g_stream) { g_stream = s; }
 StreamScope::~StreamScope() { g_stream = prev_; }
 
-Scratch::Scratch(size_t words) : s_(CurrentStream()) {
+Workspace::Workspace(size_t words) {
+  buf_.Resize(words * sizeof(uint32_t));
+  cap_ = words;
+  HipCheck(hipEventCreateWithFlags(&done_, hipEventDisableTiming),
+           "hipEventCreateWithFlags");
+}
+
+Workspace::~Workspace() {
+  if (done_ != nullptr) (void)hipEventDestroy(done_);
+}
+
+void Workspace::Enter() {
+  mu_.lock();
+  if (depth_++ > 0) return;
+  cur_ = CurrentStream();
+  if (has_last_ && cur_ != last_) {
+    const hipError_t e = hipStreamWaitEvent(cur_, done_, 0);
+    if (e != hipSuccess) {
+      depth_--;
+      mu_.unlock();
+      HipCheck(e, "hipStreamWaitEvent");
+    }
+  }
+}
+
+void Workspace::Leave() noexcept {
+  if (--depth_ == 0) {
+    if (hipEventRecord(done_, cur_) == hipSuccess) {
+      last_ = cur_;
+      has_last_ = true;
+    } else {
+      // no event to order the next stream after this one: finish the work
+      (void)hipStreamSynchronize(cur_);
+      has_last_ = false;
+    }
+  }
+  mu_.unlock();
+}
+
+Workspace::Use::Use(Workspace *ws) : ws_(ws) {
+  if (ws_ != nullptr) ws_->Enter();
+}
+Workspace::Use::~Use() {
+  if (ws_ != nullptr) ws_->Leave();
+}
+
+uint32_t *Workspace::Push(size_t words) {
+  const size_t w = (words + 63) & ~static_cast<size_t>(63);  // 256-byte steps
+  if (w > cap_ - top_) return nullptr;
+  uint32_t *p = buf_.as<uint32_t>() + top_;
+  top_ += w;
+  return p;
+}
+
+void Workspace::Pop(uint32_t *p) {
+  top_ = static_cast<size_t>(p - buf_.as<uint32_t>());
+}
+
+Scratch::Scratch(Workspace *ws, size_t words) {
   if (words == 0) return;
+  if (ws != nullptr) {
+    p_ = ws->Push(words);
+    if (p_ != nullptr) {
+      ws_ = ws;
+      return;
+    }
+  }
+  s_ = CurrentStream();
   HipCheck(hipMallocAsync(reinterpret_cast<void **>(&p_),
                           words * sizeof(uint32_t), s_),
            "hipMallocAsync");
 }
+
 Scratch::~Scratch() {
-  if (p_ != nullptr) (void)hipFreeAsync(p_, s_);
+  if (p_ == nullptr) return;
+  if (ws_ != nullptr)
+    ws_->Pop(p_);
+  else
+    (void)hipFreeAsync(p_, s_);
 }
 
 NPInfo::NPInfo(int num_main, int num_ter, int num_aux)
@@ -472,14 +543,16 @@ void ElementWiseHandler<uint32_t>::Permute(
 // src/core/ModSwitch.cu:175-318, no terminal primes
 ModSwitchHandler<uint32_t>::ModSwitchHandler(
     const Parameter<word> &param, int level,
-    const ElementWiseHandler<word> &elem, const NTTHandler<word> &ntt)
+    const ElementWiseHandler<word> &elem, const NTTHandler<word> &ntt,
+    Workspace *ws)
     : level_(level),
       num_aux_(param.alpha_),
       beta_(DivCeil(param.LevelToNP(level).num_main_ + param.GetMaxNumTer(),
                     param.alpha_)),
       param_(param),
       elem_(elem),
-      ntt_(ntt) {
+      ntt_(ntt),
+      ws_(ws) {
   const NPInfo np = param_.LevelToNP(level_, num_aux_);
   const int num_q = np.GetNumQ();
   const std::vector<word> lp = param_.GetPrimeVector(np);
@@ -659,7 +732,8 @@ void ModSwitchHandler<uint32_t>::ModUp(std::vector<DvView<word>> &dst,
                             hipMemcpyDeviceToDevice, CurrentStream()),
              "hipMemcpyAsync");
   }
-  Scratch intt(static_cast<size_t>(num_q) * n);
+  Workspace::Use use_ws(ws_);
+  Scratch intt(ws_, static_cast<size_t>(num_q) * n);
   if (strided) {  // groups equally spaced: one launch per pass for all
     ModUpGroups(dst[0].data(), gs, src, intt.data(), true);
     return;
@@ -750,7 +824,8 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
   AssertTrue(np_src.num_ter_ == np_non_intt.num_ter_,
              "INTTForModDown: terminal-prime INTT is not supported");
   const long long ilen = static_cast<long long>(src_len) * n;
-  Scratch intt(static_cast<size_t>(num_polys) * ilen);
+  Workspace::Use use_ws(ws_);
+  Scratch intt(ws_, static_cast<size_t>(num_polys) * ilen);
   for (int p = 0; p < num_polys; p++) {
     AssertTrue(dst[p] != nullptr, "ModDown: null destination");
     // INTTForModDown requires src != dst per polynomial
@@ -807,10 +882,24 @@ std::shared_ptr<Context<uint32_t>> Context<uint32_t>::Create(
 Context<uint32_t>::Context(const Parameter<word> &param)
     : param_(param), elem_handler_(param, ntt_handler_), ntt_handler_(param) {
   Ciphertext<word>::SetDegree(param_.degree_);
+  {
+    // arena for the largest call at the top level: HMult holds the tensor
+    // (3 Lq), the accumulator (2 T) and ModUp's groups plus its INTT
+    // (beta T + Lq); ModDown's INTT (at most 2 (alpha + 2) limbs) and HRot's
+    // permute input (2 Lq) fit in what the ModUp part leaves
+    const NPInfo top = param_.LevelToNP(param_.max_level_);
+    const size_t lq = top.GetNumQ();
+    const size_t t = lq + param_.alpha_;
+    const size_t beta = DivCeil(top.num_main_ + param_.GetMaxNumTer(),
+                                param_.alpha_);
+    const size_t limbs = 3 * lq + 2 * t +
+                         std::max(beta * t + lq, 2 * (param_.alpha_ + 2) + 2 * lq);
+    ws_.reset(new Workspace(limbs * param_.degree_));
+  }
   mod_switch_handlers_.reserve(param_.max_level_ + 1);
   for (int level = 0; level <= param_.max_level_; level++)
     mod_switch_handlers_.emplace_back(param_, level, elem_handler_,
-                                      ntt_handler_);
+                                      ntt_handler_, ws_.get());
   const NPInfo np = param_.LevelToNP(param_.max_level_, param_.alpha_);
   const std::vector<word> primes = param_.GetPrimeVector(np);
   const int num_q = np.GetNumQ();
@@ -868,7 +957,9 @@ void Context<uint32_t>::KeyMultNoModDownV(int level, word *acc_b, word *acc_a,
   AssertTrue(ms.GetBeta() == beta, "MultKeyNoModDown: beta mismatch");
   const int total = num_q + num_aux;
   const long long gs = static_cast<long long>(total) * n;
-  Scratch buf(static_cast<size_t>(beta) * gs + static_cast<size_t>(num_q) * n);
+  Workspace::Use use_ws(ws_.get());
+  Scratch buf(ws_.get(),
+              static_cast<size_t>(beta) * gs + static_cast<size_t>(num_q) * n);
   ms.ModUpGroups(buf.data(), gs, DvConstView<word>(d, num_q * n, 0),
                  buf.data() + beta * gs, false);
   chd_keyacc_args k{};
@@ -902,11 +993,12 @@ void Context<uint32_t>::HMultV(int level, CtRef res, CtCRef a, CtCRef b,
   const int n = param_.degree_;
   const int num_q = np.GetNumQ();
   const int total = num_q + param_.alpha_;
-  Scratch t(static_cast<size_t>(3) * num_q * n);
+  Workspace::Use use_ws(ws_.get());
+  Scratch t(ws_.get(), static_cast<size_t>(3) * num_q * n);
   CtRef tr{t.data(), t.data() + static_cast<size_t>(num_q) * n,
            t.data() + static_cast<size_t>(2) * num_q * n};
   TensorV(level, tr, a, b);
-  Scratch acc(static_cast<size_t>(2) * total * n);
+  Scratch acc(ws_.get(), static_cast<size_t>(2) * total * n);
   word *acc_b = acc.data();
   word *acc_a = acc.data() + static_cast<size_t>(total) * n;
   KeyMultNoModDownV(level, acc_b, acc_a, tr.rx, tr.bx, tr.ax, key);
@@ -939,7 +1031,8 @@ void Context<uint32_t>::MultKeyV(int level, CtRef res, CtCRef a,
   const int n = param_.degree_;
   const int num_q = param_.LevelToNP(level).GetNumQ();
   const int total = num_q + param_.alpha_;
-  Scratch acc(static_cast<size_t>(2) * total * n);
+  Workspace::Use use_ws(ws_.get());
+  Scratch acc(ws_.get(), static_cast<size_t>(2) * total * n);
   word *acc_b = acc.data();
   word *acc_a = acc.data() + static_cast<size_t>(total) * n;
   KeyMultNoModDownV(level, acc_b, acc_a, a.ax, a.bx, nullptr, key);
@@ -996,7 +1089,8 @@ void Context<uint32_t>::Relinearize(Ct &res, const Ct &a,
   const int num_q = a.GetNP().GetNumQ();
   const int total = num_q + param_.alpha_;
   Ct out(a.GetNP());
-  Scratch acc(static_cast<size_t>(2) * total * n);
+  Workspace::Use use_ws(ws_.get());
+  Scratch acc(ws_.get(), static_cast<size_t>(2) * total * n);
   KeyMultNoModDownV(level, acc.data(), acc.data() + static_cast<size_t>(total) * n,
                     a.rx_.data(), a.bx_.data(), a.ax_.data(), RefOf(key));
   mod_switch_handlers_.at(level).ModDownMulti(
@@ -1015,7 +1109,8 @@ void Context<uint32_t>::RelinearizeRescale(Ct &res, const Ct &a,
   const int num_q = a.GetNP().GetNumQ();
   const int total = num_q + param_.alpha_;
   Ct out(param_.LevelToNP(level - 1));
-  Scratch acc(static_cast<size_t>(2) * total * n);
+  Workspace::Use use_ws(ws_.get());
+  Scratch acc(ws_.get(), static_cast<size_t>(2) * total * n);
   KeyMultNoModDownV(level, acc.data(), acc.data() + static_cast<size_t>(total) * n,
                     a.rx_.data(), a.bx_.data(), a.ax_.data(), RefOf(key));
   mod_switch_handlers_.at(level).ModDownMulti(

@@ -19,6 +19,7 @@
 
 #include <cstdint>
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -176,6 +177,66 @@ class DeviceVector {
   size_t n_ = 0;
 };
 
+// Device scratch arena of one Context. Key-switch temporaries (the
+// reference's per-call RMM allocations, ModSwitch.cu:442,597;
+// Context.cpp:670-682) are carved from it in LIFO order with a bump pointer:
+// stream-ordered allocation costs tens of microseconds of host time per call
+// on this runtime, more than some of the kernels it feeds. The arena serves
+// one stream at a time: a call on a different stream than the previous call
+// first makes its stream wait for the event recorded at the end of that call.
+// Calls from several host threads are serialised by a mutex.
+class Workspace {
+ public:
+  explicit Workspace(size_t words);
+  ~Workspace();
+  Workspace(const Workspace &) = delete;
+  Workspace &operator=(const Workspace &) = delete;
+  // Guard for one API call that takes scratch from the arena (re-entrant).
+  class Use {
+   public:
+    explicit Use(Workspace *ws);
+    ~Use();
+    Use(const Use &) = delete;
+    Use &operator=(const Use &) = delete;
+
+   private:
+    Workspace *ws_;
+  };
+  // nullptr when the arena has no room left
+  uint32_t *Push(size_t words);
+  void Pop(uint32_t *p);
+  size_t Capacity() const { return cap_; }
+
+ private:
+  void Enter();
+  void Leave() noexcept;
+  DevBuf buf_;
+  size_t cap_ = 0, top_ = 0;
+  int depth_ = 0;
+  hipEvent_t done_ = nullptr;
+  hipStream_t cur_ = nullptr, last_ = nullptr;
+  bool has_last_ = false;
+  std::recursive_mutex mu_;
+};
+
+// A temporary of `words` words: from the arena when one is given and has
+// room, otherwise stream-ordered (hipMallocAsync / hipFreeAsync on the
+// current stream). Must be released in LIFO order (automatic scope).
+class Scratch {
+ public:
+  Scratch(Workspace *ws, size_t words);
+  explicit Scratch(size_t words) : Scratch(nullptr, words) {}
+  ~Scratch();
+  Scratch(const Scratch &) = delete;
+  Scratch &operator=(const Scratch &) = delete;
+  uint32_t *data() const { return p_; }
+
+ private:
+  uint32_t *p_ = nullptr;
+  Workspace *ws_ = nullptr;
+  hipStream_t s_ = nullptr;
+};
+
 template <typename word>
 class Ciphertext;
 template <>
@@ -290,7 +351,7 @@ class ModSwitchHandler<uint32_t> {
   using word = uint32_t;
   ModSwitchHandler(const Parameter<word> &param, int level,
                    const ElementWiseHandler<word> &elem,
-                   const NTTHandler<word> &ntt);
+                   const NTTHandler<word> &ntt, Workspace *ws = nullptr);
   void ModUp(std::vector<DvView<word>> &dst,
              const DvConstView<word> &src) const;
   void ModDown(DvView<word> &dst, const DvConstView<word> &src) const;
@@ -334,6 +395,7 @@ class ModSwitchHandler<uint32_t> {
   const Parameter<word> &param_;
   const ElementWiseHandler<word> &elem_;
   const NTTHandler<word> &ntt_;
+  Workspace *ws_;
   DeviceVector<word> mod_up1_;
   std::vector<SwitchTable> mod_up_;
   SwitchTable mod_down_, rescale_, mod_down_rescale_;
@@ -384,6 +446,8 @@ class Context<uint32_t> {
   void RescaleV(int level, CtRef res, CtCRef a) const;
   void MultKeyV(int level, CtRef res, CtCRef a, const EvkRef &key) const;
   void PermuteV(int level, CtRef res, CtCRef a, int galois_amount) const;
+  // scratch arena of this context (sized for HMult / HRot at the top level)
+  Workspace *GetWorkspace() const { return ws_.get(); }
 
   const Parameter<word> &param_;
   ElementWiseHandler<word> elem_handler_;
@@ -394,22 +458,7 @@ class Context<uint32_t> {
   explicit Context(const Parameter<word> &param);
   DvConstView<word> GetPProd(const NPInfo &np) const;
   DeviceVector<word> p_prod_;
-};
-
-// Stream-ordered scratch allocation (hipMallocAsync / hipFreeAsync on the
-// current stream), the counterpart of the reference's per-call RMM
-// temporaries (ModSwitch.cu:442,597; Context.cpp:670-682).
-class Scratch {
- public:
-  explicit Scratch(size_t words);
-  ~Scratch();
-  Scratch(const Scratch &) = delete;
-  Scratch &operator=(const Scratch &) = delete;
-  uint32_t *data() const { return p_; }
-
- private:
-  uint32_t *p_ = nullptr;
-  hipStream_t s_;
+  std::unique_ptr<Workspace> ws_;
 };
 
 }  // namespace cheddar

@@ -250,3 +250,31 @@ def test_permute_conjugate(chd, ks):
     g = 2 * N - 1
     assert np.array_equal(host(res[0]), _orc.permute(b, 16, g))
     assert np.array_equal(host(res[1]), _orc.permute(a, 16, g))
+
+
+def test_hmult_alternating_streams(chd, ks):
+    """Key switches issued back to back on two streams share the context's
+    scratch arena; the second stream must wait for the first one's use."""
+    import ctypes
+    import torch
+    param, ctx, main, aux = ks
+    L = 24
+    r = rng(470)
+    kb, ka = _evk(r, main, aux, 3)
+    dkb, dka = [dev(k) for k in kb], [dev(k) for k in ka]
+    cases = []
+    for _ in range(2):
+        b1, a1, b2, a2 = (uniform_limbs(r, main) for _ in range(4))
+        cases.append(((b1, a1, b2, a2), (dev(b1), dev(a1)), (dev(b2), dev(a2)),
+                      (zeros(L - 1, N), zeros(L - 1, N))))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for rep in range(3):
+        for i, (_, a, b, res) in enumerate(cases):
+            s = ctypes.c_void_p(streams[i].cuda_stream)
+            ctx.hmult(L - 1, res, a, b, dkb, dka, rescale=True, stream=s)
+    torch.cuda.synchronize()
+    for (b1, a1, b2, a2), _, _, res in cases:
+        wb, wa = _orc.hmult(b1, a1, b2, a2, kb, ka, L, 24, main, aux, 16, 1)
+        assert np.array_equal(host(res[0]), wb)
+        assert np.array_equal(host(res[1]), wa)
