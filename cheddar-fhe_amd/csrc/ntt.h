@@ -26,6 +26,9 @@ struct NttArgs {
   LimbMap map;
   NttTables tab;
   const uint32_t *cst;    // per-limb MontMul constant (prologue or epilogue)
+  // inverse row pass only: when set, the input element is the canonical
+  // MontMul(src, src_mul) (same layout as src)
+  const uint32_t *src_mul;
   // ModDown epilogue (src/core/NTT.cu:456-601)
   const uint32_t *src2;   // kept limbs of the original input
   long long src2_pstride;

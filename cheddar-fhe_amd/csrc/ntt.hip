@@ -520,6 +520,21 @@ __global__ __launch_bounds__(256) void ntt_inv_rows(NttArgs a) {
   }
   const uint32_t q = a.tab.q[lb.ti];
   const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
+  if (a.src_mul != nullptr) {
+    // Tensor's rx = MontMul(a1, a2) (ElementWise.cu:504-546), canonical
+    const uint32_t *sm = a.src_mul + blockIdx.z * a.src_pstride +
+                         (static_cast<size_t>(lb.sl) << kLogN);
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const uint4 u = ld_at<uint4>(sm, rbase + 64u * c + 16u * v);
+      const uint32_t y[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        x[4 * v + j] = mont_mul(static_cast<int32_t>(x[4 * v + j]),
+                                static_cast<int32_t>(y[j]), q,
+                                static_cast<int32_t>(qinv));
+    }
+  }
   if (q < (1u << 30))
     inv_rows_body<true>(a, lb, x, q, qinv, dst, xch);
   else
@@ -654,15 +669,30 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
     const int own_hi = min(own_lo + a.alpha, a.num_q);
     uint32_t u[16];
     if (l >= own_lo && l < own_hi) {
-      // own limb: the input itself (ModSwitch.cu:466-470 copies it)
-      const uint32_t *dl = a.d + loff;
+      // own limb: the input itself (ModSwitch.cu:466-470 copies it); in
+      // tensor mode the input is rx = MontMul(a1, a2)
+      if (a.a1 != nullptr) {
 #pragma unroll
-      for (int v = 0; v < 4; v++) {
-        uint4 t = ld_at<uint4>(dl, cbase + 16u * v);
-        u[4 * v] = t.x;
-        u[4 * v + 1] = t.y;
-        u[4 * v + 2] = t.z;
-        u[4 * v + 3] = t.w;
+        for (int v = 0; v < 4; v++) {
+          const uint4 s = ld_at<uint4>(a.a1 + loff, cbase + 16u * v);
+          const uint4 t = ld_at<uint4>(a.a2 + loff, cbase + 16u * v);
+          const uint32_t sv[4] = {s.x, s.y, s.z, s.w};
+          const uint32_t tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            u[4 * v + j] = mont_mul(static_cast<int32_t>(sv[j]),
+                                    static_cast<int32_t>(tv[j]), q, qi);
+        }
+      } else {
+        const uint32_t *dl = a.d + loff;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+          uint4 t = ld_at<uint4>(dl, cbase + 16u * v);
+          u[4 * v] = t.x;
+          u[4 * v + 1] = t.y;
+          u[4 * v + 2] = t.z;
+          u[4 * v + 3] = t.w;
+        }
       }
     } else {
       const uint32_t *src = a.modup + g * a.group_stride + loff;
@@ -722,7 +752,38 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
       }
     }
   }
-  if (!aux) {
+  if (!aux && a.a1 != nullptr) {
+    // CAccum with the Tensor's bx, ax formed here (ElementWise.cu:504-546)
+    const int32_t pp = static_cast<int32_t>(a.p_prod[l]);
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const uint4 vb1 = ld_at<uint4>(a.b1 + loff, cbase + 16u * v);
+      const uint4 va1 = ld_at<uint4>(a.a1 + loff, cbase + 16u * v);
+      const uint4 vb2 = ld_at<uint4>(a.b2 + loff, cbase + 16u * v);
+      const uint4 va2 = ld_at<uint4>(a.a2 + loff, cbase + 16u * v);
+      const uint32_t x1[4] = {vb1.x, vb1.y, vb1.z, vb1.w};
+      const uint32_t y1[4] = {va1.x, va1.y, va1.z, va1.w};
+      const uint32_t x2[4] = {vb2.x, vb2.y, vb2.z, vb2.w};
+      const uint32_t y2[4] = {va2.x, va2.y, va2.z, va2.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int32_t s1 = (static_cast<int32_t>(x1[j]) - qs) +
+                           static_cast<int32_t>(y1[j]);
+        const int32_t s2 = (static_cast<int32_t>(x2[j]) - qs) +
+                           static_cast<int32_t>(y2[j]);
+        const uint32_t bb = mont_mul(static_cast<int32_t>(x1[j]),
+                                     static_cast<int32_t>(x2[j]), q, qi);
+        const uint32_t rr = mont_mul(static_cast<int32_t>(y1[j]),
+                                     static_cast<int32_t>(y2[j]), q, qi);
+        const uint32_t ax = sub_mod(sub_mod(mont_mul(s1, s2, q, qi), bb, q),
+                                    rr, q);
+        accb[4 * v + j] = add_mod(
+            accb[4 * v + j], mont_mul(pp, static_cast<int32_t>(bb), q, qi), q);
+        acca[4 * v + j] = add_mod(
+            acca[4 * v + j], mont_mul(pp, static_cast<int32_t>(ax), q, qi), q);
+      }
+    }
+  } else if (!aux) {
     // CAccum (Context.cpp:684-699): acc += p_prod * ct (bx, and ax if given)
     const int32_t pp = static_cast<int32_t>(a.p_prod[l]);
 #pragma unroll
@@ -885,15 +946,17 @@ extern "C" int chd_k_ntt_fwd_moddown(const chd_tables *t,
   return 0;
 }
 
-extern "C" int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m,
-                             uint32_t *dst, long long dst_pstride,
-                             const uint32_t *src, long long src_pstride,
-                             int num_limbs, int num_polys, const uint32_t *cst,
-                             int centre, void *stream) {
+static int ntt_inv_common(const char *name, const chd_tables *t,
+                          const chd_limb_map *m, uint32_t *dst,
+                          long long dst_pstride, const uint32_t *src,
+                          const uint32_t *src_mul, long long src_pstride,
+                          int num_limbs, int num_polys, const uint32_t *cst,
+                          int centre, void *stream) {
   if (!t || !m || !dst || !src || !cst || num_limbs < 0 || num_polys < 0)
-    return set_error(CHD_ERR_ARG, "chd_k_ntt_inv: invalid argument");
+    return set_error(CHD_ERR_ARG, std::string(name) + ": invalid argument");
   NttArgs a{};
   a.src = src;
+  a.src_mul = src_mul;
   a.dst = dst;
   a.src_pstride = src_pstride;
   a.dst_pstride = dst_pstride;
@@ -905,9 +968,32 @@ extern "C" int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m,
                      centre ? kEpiConstCentre : kEpiConst,
                      static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
-    return set_error(CHD_ERR_HIP, std::string("chd_k_ntt_inv: ") +
-                                      hipGetErrorString(e));
+    return set_error(CHD_ERR_HIP,
+                     std::string(name) + ": " + hipGetErrorString(e));
   return 0;
+}
+
+extern "C" int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m,
+                             uint32_t *dst, long long dst_pstride,
+                             const uint32_t *src, long long src_pstride,
+                             int num_limbs, int num_polys, const uint32_t *cst,
+                             int centre, void *stream) {
+  return ntt_inv_common("chd_k_ntt_inv", t, m, dst, dst_pstride, src, nullptr,
+                        src_pstride, num_limbs, num_polys, cst, centre,
+                        stream);
+}
+
+extern "C" int chd_k_ntt_inv_mul(const chd_tables *t, const chd_limb_map *m,
+                                 uint32_t *dst, long long dst_pstride,
+                                 const uint32_t *src, const uint32_t *src_mul,
+                                 long long src_pstride, int num_limbs,
+                                 int num_polys, const uint32_t *cst,
+                                 int centre, void *stream) {
+  if (src_mul == nullptr)
+    return set_error(CHD_ERR_ARG, "chd_k_ntt_inv_mul: invalid argument");
+  return ntt_inv_common("chd_k_ntt_inv_mul", t, m, dst, dst_pstride, src,
+                        src_mul, src_pstride, num_limbs, num_polys, cst,
+                        centre, stream);
 }
 
 extern "C" int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
@@ -941,8 +1027,11 @@ extern "C" int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
 
 extern "C" int chd_k_modup_keyacc(const chd_tables *t,
                                   const chd_keyacc_args *args, void *stream) {
-  if (!t || !args || !args->modup || !args->d || !args->p_prod ||
-      !args->cb || !args->acc_b || !args->acc_a || args->alpha < 1 ||
+  const bool tensor = args && args->a1 != nullptr;
+  if (!t || !args || !args->modup || !args->p_prod || !args->acc_b ||
+      !args->acc_a || args->alpha < 1 ||
+      (tensor ? !args->b1 || !args->b2 || !args->a2
+              : !args->d || !args->cb) ||
       args->beta < 1 || args->beta > kMaxGroups ||
       (args->beta - 1) * args->alpha >= args->num_q ||
       args->beta * args->alpha < args->num_q)

@@ -657,16 +657,23 @@ void ModSwitchHandler<uint32_t>::BuildSwitch(
 // then the BConv of every dnum group in one launch, group i into dst[i].
 void ModSwitchHandler<uint32_t>::ModUpBconv(word *const *dst,
                                             const DvConstView<word> &src,
-                                            word *intt) const {
+                                            word *intt,
+                                            const word *src_mul) const {
   const NPInfo np = param_.LevelToNP(level_, 0);
   const int num_q = np.GetNumQ();
   const int n = param_.degree_;
   AssertTrue(src.QSize() == num_q * n, "ModUp src q size mismatch");
   AssertTrue(src.AuxSize() == 0, "ModUp src aux size mismatch");
   AssertTrue(beta_ <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
-  DvView<word> intt_view(intt, num_q * n, 0);
-  ntt_.INTTAndMultConst(intt_view, np, src,
-                        DvConstView<word>(mod_up1_.data(), num_q, 0), true);
+  if (src_mul != nullptr) {
+    const chd_limb_map mi = NoSkipMap(param_, np);
+    K(chd_k_ntt_inv_mul(&ntt_.Tables(), &mi, intt, 0, src.data(), src_mul, 0,
+                        num_q, 1, mod_up1_.data(), 1, CurrentStream()));
+  } else {
+    DvView<word> intt_view(intt, num_q * n, 0);
+    ntt_.INTTAndMultConst(intt_view, np, src,
+                          DvConstView<word>(mod_up1_.data(), num_q, 0), true);
+  }
   NPInfo np_aux = np;
   np_aux.num_aux_ = num_aux_;
   chd_limb_map m = NoSkipMap(param_, np_aux);
@@ -692,13 +699,14 @@ void ModSwitchHandler<uint32_t>::ModUpBconv(word *const *dst,
 void ModSwitchHandler<uint32_t>::ModUpGroups(word *modup,
                                              long long group_stride,
                                              const DvConstView<word> &src,
-                                             word *intt, bool with_rows) const {
+                                             word *intt, bool with_rows,
+                                             const word *src_mul) const {
   const NPInfo np = param_.LevelToNP(level_, 0);
   const int num_q = np.GetNumQ();
   word *dst[CHD_MAX_JOBS];
   AssertTrue(beta_ <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
   for (int i = 0; i < beta_; i++) dst[i] = modup + i * group_stride;
-  ModUpBconv(dst, src, intt);
+  ModUpBconv(dst, src, intt, src_mul);
   NPInfo np_aux = np;
   np_aux.num_aux_ = num_aux_;
   chd_limb_map m = NoSkipMap(param_, np_aux);
@@ -942,6 +950,20 @@ void Context<uint32_t>::KeyMultNoModDownV(int level, word *acc_b, word *acc_a,
                                           const word *d, const word *cb,
                                           const word *ca,
                                           const EvkRef &key) const {
+  KeyAccumulate(level, acc_b, acc_a, d, cb, ca, nullptr, nullptr, key);
+}
+
+void Context<uint32_t>::KeyMultTensorV(int level, word *acc_b, word *acc_a,
+                                       CtCRef a, CtCRef b,
+                                       const EvkRef &key) const {
+  KeyAccumulate(level, acc_b, acc_a, nullptr, nullptr, nullptr, &a, &b, key);
+}
+
+void Context<uint32_t>::KeyAccumulate(int level, word *acc_b, word *acc_a,
+                                      const word *d, const word *cb,
+                                      const word *ca, const CtCRef *ta,
+                                      const CtCRef *tb,
+                                      const EvkRef &key) const {
   const NPInfo a_np = param_.LevelToNP(level);
   const int n = param_.degree_;
   const int num_q = a_np.GetNumQ();
@@ -960,8 +982,10 @@ void Context<uint32_t>::KeyMultNoModDownV(int level, word *acc_b, word *acc_a,
   Workspace::Use use_ws(ws_.get());
   Scratch buf(ws_.get(),
               static_cast<size_t>(beta) * gs + static_cast<size_t>(num_q) * n);
-  ms.ModUpGroups(buf.data(), gs, DvConstView<word>(d, num_q * n, 0),
-                 buf.data() + beta * gs, false);
+  const bool tensor = ta != nullptr;
+  ms.ModUpGroups(buf.data(), gs,
+                 DvConstView<word>(tensor ? ta->ax : d, num_q * n, 0),
+                 buf.data() + beta * gs, false, tensor ? tb->ax : nullptr);
   chd_keyacc_args k{};
   k.num_q = num_q;
   k.tab_off = param_.TerLeft(a_np);
@@ -983,6 +1007,15 @@ void Context<uint32_t>::KeyMultNoModDownV(int level, word *acc_b, word *acc_a,
   k.ca = ca;
   k.acc_b = acc_b;
   k.acc_a = acc_a;
+  if (tensor) {
+    k.d = nullptr;
+    k.cb = nullptr;
+    k.ca = nullptr;
+    k.b1 = ta->bx;
+    k.a1 = ta->ax;
+    k.b2 = tb->bx;
+    k.a2 = tb->ax;
+  }
   K(chd_k_modup_keyacc(&ntt_handler_.Tables(), &k, CurrentStream()));
 }
 
@@ -994,14 +1027,11 @@ void Context<uint32_t>::HMultV(int level, CtRef res, CtCRef a, CtCRef b,
   const int num_q = np.GetNumQ();
   const int total = num_q + param_.alpha_;
   Workspace::Use use_ws(ws_.get());
-  Scratch t(ws_.get(), static_cast<size_t>(3) * num_q * n);
-  CtRef tr{t.data(), t.data() + static_cast<size_t>(num_q) * n,
-           t.data() + static_cast<size_t>(2) * num_q * n};
-  TensorV(level, tr, a, b);
   Scratch acc(ws_.get(), static_cast<size_t>(2) * total * n);
   word *acc_b = acc.data();
   word *acc_a = acc.data() + static_cast<size_t>(total) * n;
-  KeyMultNoModDownV(level, acc_b, acc_a, tr.rx, tr.bx, tr.ax, key);
+  // Tensor fused into ModUp's INTT and the key accumulation
+  KeyMultTensorV(level, acc_b, acc_a, a, b, key);
   AssertTrue(!rescale || level > 0, "Not enough q primes to rescale");
   mod_switch_handlers_.at(level).ModDownMulti(
       {res.bx, res.ax}, acc_b, static_cast<long long>(total) * n,
@@ -1122,13 +1152,23 @@ void Context<uint32_t>::RelinearizeRescale(Ct &res, const Ct &a,
   res = std::move(out);
 }
 
+// src/core/Context.cpp:862-871: Mult, then Relinearize or
+// RelinearizeRescale; here one fused pass (the tensor is never stored)
 void Context<uint32_t>::HMult(Ct &res, const Ct &a, const Ct &b,
                               const Evk &mult_key, bool rescale) const {
-  Mult(res, a, b);
-  if (rescale)
-    RelinearizeRescale(res, res, mult_key);
-  else
-    Relinearize(res, res, mult_key);
+  AssertTrue(a.GetNP() == b.GetNP(), "Mult: NP mismatch");
+  AssertTrue(!a.HasRx() && !b.HasRx(),
+             "Relinearization required before Mult Ct x Ct");
+  const int level = param_.NPToLevel(a.GetNP());
+  AssertTrue(!rescale || level > 0, "Not enough q primes to rescale");
+  Ct out(rescale ? param_.LevelToNP(level - 1) : a.GetNP());
+  HMultV(level, {out.bx_.data(), out.ax_.data(), nullptr},
+         {a.bx_.data(), a.ax_.data(), nullptr},
+         {b.bx_.data(), b.ax_.data(), nullptr}, RefOf(mult_key), rescale);
+  const double scale = a.GetScale() * b.GetScale();
+  out.SetScale(rescale ? scale / param_.GetRescalePrimeProd(level) : scale);
+  out.SetNumSlots(std::max(a.GetNumSlots(), b.GetNumSlots()));
+  res = std::move(out);
 }
 
 void Context<uint32_t>::MultKey(Ct &res, const Ct &a, const Evk &key) const {

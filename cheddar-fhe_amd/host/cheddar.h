@@ -366,11 +366,13 @@ class ModSwitchHandler<uint32_t> {
   // ModUpGroups: ModUpBconv into modup + i * group_stride, then the column
   // pass (with_rows: and the row pass) of NTTForModUp for all groups in one
   // launch each. Own limbs of a group are left unwritten.
+  // With src_mul, the ModUp input is the element-wise MontMul(src, src_mul)
+  // (the Tensor's rx of HMult, formed on the fly).
   void ModUpBconv(word *const *dst, const DvConstView<word> &src,
-                  word *intt) const;
+                  word *intt, const word *src_mul = nullptr) const;
   void ModUpGroups(word *modup, long long group_stride,
                    const DvConstView<word> &src, word *intt,
-                   bool with_rows) const;
+                   bool with_rows, const word *src_mul = nullptr) const;
 
   enum class Kind { ModDown, Rescale, ModDownAndRescale };
   // ModDownWorker for several polynomials at once: polynomial p of the
@@ -441,6 +443,10 @@ class Context<uint32_t> {
   void KeyMultNoModDownV(int level, word *acc_b, word *acc_a, const word *d,
                          const word *cb, const word *ca,
                          const EvkRef &key) const;
+  // the same for HMult with the Tensor fused in: d = rx, (cb, ca) = (bx, ax)
+  // of a x b, formed inside the ModUp and accumulation kernels
+  void KeyMultTensorV(int level, word *acc_b, word *acc_a, CtCRef a, CtCRef b,
+                      const EvkRef &key) const;
   void HMultV(int level, CtRef res, CtCRef a, CtCRef b, const EvkRef &key,
               bool rescale) const;
   void RescaleV(int level, CtRef res, CtCRef a) const;
@@ -457,6 +463,9 @@ class Context<uint32_t> {
  private:
   explicit Context(const Parameter<word> &param);
   DvConstView<word> GetPProd(const NPInfo &np) const;
+  void KeyAccumulate(int level, word *acc_b, word *acc_a, const word *d,
+                     const word *cb, const word *ca, const CtCRef *ta,
+                     const CtCRef *tb, const EvkRef &key) const;
   DeviceVector<word> p_prod_;
   std::unique_ptr<Workspace> ws_;
 };

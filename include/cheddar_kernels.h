@@ -74,6 +74,16 @@ int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
                   long long src_pstride, int num_limbs, int num_polys,
                   const uint32_t *cst, int centre, void *stream);
 
+/* chd_k_ntt_inv of the element-wise Montgomery product MontMul(src, src_mul)
+ * (src_mul laid out like src). With src = a.ax, src_mul = b.ax this is the
+ * Tensor's rx (ElementWise.cu:504-546) fed straight into ModUp's
+ * INTTAndMultConst (ModSwitch.cu:442-447) without storing rx. */
+int chd_k_ntt_inv_mul(const chd_tables *t, const chd_limb_map *m,
+                      uint32_t *dst, long long dst_pstride,
+                      const uint32_t *src, const uint32_t *src_mul,
+                      long long src_pstride, int num_limbs, int num_polys,
+                      const uint32_t *cst, int centre, void *stream);
+
 /* BConv (src/core/ModSwitch.cu:23-171): for dst position k,
  * dst[pos(k)] = sum_i src[i] * T[k][i] * 2^-32 mod p_k with centred int32
  * sources. table = chd_bconv_table_size(src_len, dst_len) bytes made by
@@ -133,6 +143,12 @@ typedef struct chd_keyacc_args {
   const uint32_t *ca;
   uint32_t *acc_b;
   uint32_t *acc_a;
+  /* Tensor mode (HMult), selected by a1 != NULL: d, cb and ca are not read
+   * but formed from the two input ciphertexts (b1, a1) x (b2, a2), q limbs
+   * only, as Tensor computes them (ElementWise.cu:504-546):
+   * d = rx = MontMul(a1, a2), cb = bx = MontMul(b1, b2),
+   * ca = ax = MontMul(b1 - q + a1, b2 - q + a2) - bx - rx. */
+  const uint32_t *b1, *a1, *b2, *a2;
 } chd_keyacc_args;
 int chd_k_modup_keyacc(const chd_tables *t, const chd_keyacc_args *args,
                        void *stream);
