@@ -1,19 +1,38 @@
 // BConv: the base-conversion matrix product of ModUp / ModDown / Rescale
-// (reference kernel ModSwitchMatrixMult, src/core/ModSwitch.cu:23-171).
+// (reference kernel ModSwitchMatrixMult, src/core/ModSwitch.cu:23-171),
+// on the int8 matrix cores.
 //
 //   dst[pos(k)][n] = sum_i c_i[n] * T[k][i] * 2^-32  mod p_k
 //
-// c_i are centred int32 residues (the INTT epilogue's output) and T is the
-// reference's "double Montgomery" table centre(qhat_i R^2 mod p_k). The
-// kernel folds the 2^-32 into the table once on the host:
-// U[k][i] = centre(T[k][i] * 2^-32 mod p_k), split U = Uhi * 2^16 + Ulo with
-// Ulo in [0, 2^16). Then sum_i c_i Uhi and sum_i c_i Ulo are exact fp64
-// FMA chains (|c| < 2^30: partial sums below 2^50 for up to 16 sources), the
-// high part is reduced mod p, recombined as rhi * 2^16 + slo (exact) and
-// reduced to [0, p). All FMAs run at full fp64 VALU rate on gfx950.
+// c_i are centred int32 residues (the INTT epilogue's output, |c| < 2^30) and
+// T is the reference's "double Montgomery" table centre(qhat_i R^2 mod p_k).
 //
-// Layout: one thread per coefficient n, all sources held in registers; the
-// table is wave-uniform (scalar loads). grid (N / 256, dst chunks).
+// Byte-digit decomposition. The host folds the 2^-32 into the table,
+// U[k][i] = centre(T[k][i] 2^-32 mod p_k), and expands it over the four byte
+// positions of a source: V[k][(i,b)] = centre(U[k][i] 256^b mod p_k). A
+// centred source c splits into signed digits d_0..d_3 in [-128, 127] with
+// c = sum_b d_b 256^b; the packed word (c + 0x808080) ^ 0x808080 holds exactly
+// those four int8 digits, so a source costs two VALU ops to decompose. V is
+// split the same way into digit planes v_0..v_3 (packed on the host). Then
+//
+//   acc_c[n][k] = sum_{(i,b)} d_b(c_i[n]) v_c[k][(i,b)]      (int8 MFMA, K=64)
+//   dst[k][n]   = (acc_0 + 2^8 acc_1 + 2^16 acc_2 + 2^24 acc_3) mod p_k
+//
+// which is congruent to sum_i c_i U[k][i]. |acc_c| <= 64 * 128 * 128 = 2^20,
+// so the recombination (< 2^45) is exact in fp64 and one fp64 reduction gives
+// the canonical residue: bit-identical to the reference for every input.
+//
+// One v_mfma_i32_16x16x64_i8 multiplies a 16-coefficient x 64 (sources x
+// bytes, zero-padded beyond 4 * src_len) tile by a 64 x 16-destination tile
+// of one digit plane. Operand lanes (checked on gfx950): A row = lane % 16,
+// k = 16 (lane / 16) + byte; B column = lane % 16, same k; D column =
+// lane % 16, rows 4 (lane / 16) + 0..3. So lane l packs sources
+// 4 (l / 16) .. + 3 of coefficient l % 16, and finishes four consecutive
+// coefficients of destination 16 t + l % 16.
+//
+// Grid (N / kCoefPerBlock, 1, jobs), 256 threads; a wave takes kTilesPerWave
+// 16-coefficient tiles. The packed table (4 KiB per 16 destinations) is read
+// through the caches by every wave.
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -25,54 +44,89 @@
 namespace chd {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kMaxSrc = 16;
-constexpr int kDstChunk = 12;
+typedef int v4i __attribute__((ext_vector_type(4)));
 
-struct BconvTab {   // per (k, i): {Uhi, Ulo} as doubles
-  double hi, lo;
-};
+constexpr int kThreads = 256;
+constexpr int kMaxSrc = 16;            // 4 bytes x 16 sources = K of 64
+constexpr int kTilesPerWave = 2;
+constexpr int kCoefPerBlock = (kThreads / 64) * kTilesPerWave * 16;
+constexpr int kPlaneBytes = 64 * 16;   // one digit plane of a 16-dst tile
 
 struct BconvBatch {
   chd_bconv_job job[CHD_MAX_JOBS];
 };
 
-template <int kSrc>
-__global__ __launch_bounds__(kThreads) void bconv_kernel(chd_tables t,
-                                                         chd_limb_map m,
-                                                         BconvBatch b) {
+// four signed byte digits of a centred value |c| < 2^30, packed as int8 x4
+__device__ __forceinline__ int digits(int32_t c) {
+  return static_cast<int>((static_cast<uint32_t>(c) + 0x808080u) ^ 0x808080u);
+}
+
+__global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
+                                                       chd_limb_map m,
+                                                       BconvBatch b) {
   const chd_bconv_job &jb = b.job[blockIdx.z];
-  const int n = blockIdx.x * kThreads + threadIdx.x;
-  const int k0 = blockIdx.y * kDstChunk;
-  const int k1 = min(jb.dst_len, k0 + kDstChunk);
-  if (k0 >= k1) return;
-  const int ns = kSrc > 0 ? kSrc : jb.src_len;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int wave = threadIdx.x >> 6;
+  const int n_wave = blockIdx.x * kCoefPerBlock + wave * kTilesPerWave * 16;
   const int32_t *__restrict__ src = jb.src;
-  const BconvTab *__restrict__ tab = static_cast<const BconvTab *>(jb.table);
-  double c[kMaxSrc];
+  const v4i *__restrict__ tab = static_cast<const v4i *>(jb.table);
+  // A operands of this wave's coefficient tiles
+  v4i a[kTilesPerWave];
 #pragma unroll
-  for (int i = 0; i < kMaxSrc; i++)
-    if (i < ns) c[i] = static_cast<double>(src[(static_cast<size_t>(i) << kLogN) + n]);
-  for (int k = k0; k < k1; k++) {
+  for (int mt = 0; mt < kTilesPerWave; mt++) {
+    const int n = n_wave + mt * 16 + r;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = 4 * g + j;
+      const int32_t c =
+          i < jb.src_len ? src[(static_cast<size_t>(i) << kLogN) + n] : 0;
+      a[mt][j] = digits(c);
+    }
+  }
+  const int tiles = (jb.dst_len + 15) >> 4;
+  for (int tt = 0; tt < tiles; tt++) {
+    const v4i *tp = tab + (static_cast<size_t>(tt) * 4) * 64 + lane;
+    const v4i b0 = tp[0], b1 = tp[64], b2 = tp[128], b3 = tp[192];
+    const int k = tt * 16 + r;
+    const bool live = k < jb.dst_len;
     const int pos = k + (k >= jb.skip_lo ? jb.skip_len : 0);
     const bool aux = pos >= m.num_q;
     const int ti = m.tab_off + pos + (aux ? m.tab_gap : 0);
-    const double p = t.qd[ti];
-    const double pinv = t.qinvd[ti];
-    const BconvTab *row = tab + static_cast<size_t>(k) * ns;
-    double shi = 0.0, slo = 0.0;
+    const double p = live ? t.qd[ti] : 1.0;
+    const double pinv = live ? t.qinvd[ti] : 1.0;
 #pragma unroll
-    for (int i = 0; i < kMaxSrc; i++) {
-      if (i < ns) {
-        const BconvTab e = row[i];
-        shi = __builtin_fma(c[i], e.hi, shi);
-        slo = __builtin_fma(c[i], e.lo, slo);
+    for (int mt = 0; mt < kTilesPerWave; mt++) {
+      const v4i z = {0, 0, 0, 0};
+      const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mt], b0, z, 0, 0, 0);
+      const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mt], b1, z, 0, 0, 0);
+      const v4i d2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mt], b2, z, 0, 0, 0);
+      const v4i d3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mt], b3, z, 0, 0, 0);
+      if (live) {
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          double y = __builtin_fma(static_cast<double>(d3[i]), 16777216.0,
+                                   static_cast<double>(d2[i]) * 65536.0);
+          y = __builtin_fma(static_cast<double>(d1[i]), 256.0, y);
+          y += static_cast<double>(d0[i]);
+          o[i] = reduce_f64(y, p, pinv);
+        }
+        const int n = n_wave + mt * 16 + 4 * g;
+        *reinterpret_cast<uint4 *>(jb.dst + (static_cast<size_t>(pos) << kLogN) +
+                                   n) = make_uint4(o[0], o[1], o[2], o[3]);
       }
     }
-    const double rhi = __builtin_fma(-__builtin_rint(shi * pinv), p, shi);
-    const double v = __builtin_fma(rhi, 65536.0, slo);
-    jb.dst[(static_cast<size_t>(pos) << kLogN) + n] = reduce_f64(v, p, pinv);
   }
+}
+
+// centred residue of v mod p
+int64_t centre_mod(int64_t v, int64_t p) {
+  v %= p;
+  if (v < 0) v += p;
+  if (v > p / 2) v -= p;
+  return v;
 }
 
 }  // namespace
@@ -81,8 +135,8 @@ __global__ __launch_bounds__(kThreads) void bconv_kernel(chd_tables t,
 using namespace chd;
 
 extern "C" long long chd_bconv_table_size(int src_len, int dst_len) {
-  if (src_len < 1 || dst_len < 1) return 0;
-  return static_cast<long long>(src_len) * dst_len * sizeof(BconvTab);
+  if (src_len < 1 || src_len > kMaxSrc || dst_len < 1) return 0;
+  return static_cast<long long>((dst_len + 15) / 16) * 4 * kPlaneBytes;
 }
 
 extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
@@ -91,11 +145,13 @@ extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
   if (!host_out || !table_ref || !dst_primes || src_len < 1 ||
       src_len > kMaxSrc || dst_len < 1)
     return set_error(CHD_ERR_ARG, "chd_bconv_table_pack: invalid argument");
-  BconvTab *out = static_cast<BconvTab *>(host_out);
+  const int tiles = (dst_len + 15) / 16;
+  int8_t *out = static_cast<int8_t *>(host_out);
+  std::memset(out, 0, static_cast<size_t>(tiles) * 4 * kPlaneBytes);
   for (int k = 0; k < dst_len; k++) {
-    const uint64_t p = dst_primes[k];
-    // 2^-32 mod p by Fermat-free extended Euclid on (2^32 mod p, p)
-    int64_t r0 = static_cast<int64_t>(p), r1 = static_cast<int64_t>((1ull << 32) % p);
+    const int64_t p = dst_primes[k];
+    // 2^-32 mod p by extended Euclid on (p, 2^32 mod p)
+    int64_t r0 = p, r1 = static_cast<int64_t>((1ull << 32) % static_cast<uint64_t>(p));
     int64_t t0 = 0, t1 = 1;
     while (r1 != 0) {
       int64_t qq = r0 / r1, tmp = t0 - qq * t1;
@@ -105,17 +161,30 @@ extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
       r0 = r1;
       r1 = tmp;
     }
-    const uint64_t rinv = static_cast<uint64_t>(t0 < 0 ? t0 + static_cast<int64_t>(p) : t0);
+    const int64_t rinv = t0 < 0 ? t0 + p : t0;
+    const int tt = k / 16, col = k % 16;
     for (int i = 0; i < src_len; i++) {
-      int64_t tv = table_ref[static_cast<size_t>(k) * src_len + i];
-      uint64_t tu = static_cast<uint64_t>(tv < 0 ? tv + static_cast<int64_t>(p) : tv);
-      uint64_t u = tu * rinv % p;
-      int64_t uc = static_cast<int64_t>(u);
-      if (u > (p >> 1)) uc -= static_cast<int64_t>(p);
-      int64_t lo = uc & 0xFFFF;
-      int64_t hi = (uc - lo) / 65536;
-      out[static_cast<size_t>(k) * src_len + i] =
-          BconvTab{static_cast<double>(hi), static_cast<double>(lo)};
+      const int64_t tv = centre_mod(table_ref[static_cast<size_t>(k) * src_len + i], p);
+      const int64_t u = centre_mod((tv < 0 ? tv + p : tv) * rinv, p);
+      int64_t ub = u < 0 ? u + p : u;  // U * 256^b, canonical
+      for (int bb = 0; bb < 4; bb++) {
+        const int64_t v = centre_mod(ub, p);  // |v| < 2^30
+        // signed digits of v: (v + 0x808080) has unsigned low bytes e_0..e_2
+        // and a signed top byte e_3; digit b = e_b - 128 (b < 3), e_3
+        const int64_t w = v + 0x808080;
+        int8_t dig[4];
+        for (int c = 0; c < 3; c++)
+          dig[c] = static_cast<int8_t>(((w >> (8 * c)) & 0xff) - 128);
+        dig[3] = static_cast<int8_t>(w >> 24);
+        // K index of (i, bb) and its lane / byte in the B operand
+        const int kk = 4 * i + bb;
+        const int lane = (kk / 16) * 16 + col;
+        const int byte = kk % 16;
+        for (int c = 0; c < 4; c++)
+          out[((static_cast<size_t>(tt) * 4 + c) * 64 + lane) * 16 + byte] =
+              dig[c];
+        ub = (ub * 256) % p;
+      }
     }
   }
   return 0;
@@ -127,34 +196,16 @@ extern "C" int chd_k_bconv_batch(const chd_tables *t, const chd_limb_map *m,
   if (!t || !m || !jobs || num_jobs < 1 || num_jobs > CHD_MAX_JOBS)
     return set_error(CHD_ERR_ARG, "chd_k_bconv_batch: invalid argument");
   BconvBatch b{};
-  int max_dst = 0, src_len = jobs[0].src_len;
-  bool same_src = true;
   for (int j = 0; j < num_jobs; j++) {
     const chd_bconv_job &jb = jobs[j];
     if (!jb.dst || !jb.src || !jb.table || jb.src_len < 1 ||
         jb.src_len > kMaxSrc || jb.dst_len < 1 || jb.skip_len < 0)
       return set_error(CHD_ERR_ARG, "chd_k_bconv_batch: invalid job");
     b.job[j] = jb;
-    max_dst = std::max(max_dst, jb.dst_len);
-    same_src = same_src && jb.src_len == src_len;
   }
-  dim3 g(kN / kThreads, (max_dst + kDstChunk - 1) / kDstChunk, num_jobs);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int sl = same_src ? src_len : 0;
-  switch (sl) {
-    case 1:
-      hipLaunchKernelGGL(bconv_kernel<1>, g, dim3(kThreads), 0, s, *t, *m, b);
-      break;
-    case 8:
-      hipLaunchKernelGGL(bconv_kernel<8>, g, dim3(kThreads), 0, s, *t, *m, b);
-      break;
-    case 9:
-      hipLaunchKernelGGL(bconv_kernel<9>, g, dim3(kThreads), 0, s, *t, *m, b);
-      break;
-    default:
-      hipLaunchKernelGGL(bconv_kernel<0>, g, dim3(kThreads), 0, s, *t, *m, b);
-      break;
-  }
+  dim3 g(kN / kCoefPerBlock, 1, num_jobs);
+  hipLaunchKernelGGL(bconv_mfma, g, dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), *t, *m, b);
   return check_launch("chd_k_bconv_batch");
 }
 
