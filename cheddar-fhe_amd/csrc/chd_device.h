@@ -1,16 +1,16 @@
 // Device-side modular arithmetic for u32 RNS residues (primes q < 2^31).
 //
 // Two families:
-//  * fp64 exact modular multiply (mulmod_f64): the NTT and BConv hot loops.
-//    gfx950 issues fp64 FMA at full VALU rate while 32-bit integer
-//    multiplies are quarter rate, so a product b*w mod q costs 5 full-rate
-//    ops: h = b*w; l = fma(b,w,-h) (exact low part); t = rint(b*(w/q));
-//    r = fma(-t,q,h) + l. Exactness: |b| < 2^45 and w < 2^31 keep
-//    |h - t*q| < 2^34, an integer, so both the fma and the final add are
-//    exact; the result is congruent to b*w with |r| <= q/2 + small.
-//  * signed Montgomery (R = 2^32) on VALU integers: the element-wise kernels,
-//    with the reference's convention MontMul(a,b) = a*b*2^-32 mod q
-//    (include/common/Basic.cuh:72-137).
+//  * fp64 exact reductions (reduce_f64, centre_f64, mulmod_f64): BConv's
+//    recombination of exact integer sums below 2^50. mulmod_f64 forms b*w
+//    mod q from h = b*w, l = fma(b,w,-h) (exact low part),
+//    t = rint(b*(w/q)), r = fma(-t,q,h) + l: |b| < 2^45 and w < 2^31 keep
+//    |h - t*q| < 2^34, an integer, so the fma and the add are exact.
+//  * signed Montgomery (R = 2^32) on VALU integers, the reference's
+//    convention MontMul(a,b) = a*b*2^-32 mod q
+//    (include/common/Basic.cuh:72-137): the NTT and element-wise kernels.
+//    gfx950 issues 32-bit mul_lo / mul_hi at about the rate of other 32-bit
+//    VALU ops (measured), so three multiplies per product are cheap.
 #pragma once
 
 #include <hip/hip_runtime.h>
