@@ -1,0 +1,249 @@
+// C++ drop-in API test: the reference's own call shapes (Parameter,
+// Context::Create, Ciphertext / EvaluationKey containers, Context::HMult /
+// HRot / MultKey / Rescale / Mult + Relinearize(Rescale), and the public
+// handler members) on config-4 sizes, checked bit-exactly against the CPU
+// oracle (oracle/oracle.h), which this test links as its checker.
+//
+// Mirrors the structure of the reference's unittest/BasicTest.cpp: build a
+// parameter set, run one operation per test, compare. Prints one line per
+// test; exit status 0 only if every test passes. Needs a HIP device.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "cheddar.h"
+#include "oracle.h"
+
+using namespace cheddar;
+using word = uint32_t;
+using Ct = Ciphertext<word>;
+using Evk = EvaluationKey<word>;
+
+namespace {
+
+constexpr int kLogN = 16;
+constexpr size_t kN = size_t{1} << kLogN;
+
+uint64_t g_state = 0xC0FFEE04ull;
+uint64_t next64() {  // splitmix64
+  uint64_t z = (g_state += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+std::vector<word> primes(int bits, int count) {
+  std::vector<word> r;
+  const uint64_t step = 1u << 17;
+  uint64_t q = ((uint64_t{1} << bits) - 1) / step * step + 1;
+  auto is_prime = [](uint64_t n) {
+    for (uint64_t d = 2; d * d <= n; d++)
+      if (n % d == 0) return false;
+    return true;
+  };
+  while (static_cast<int>(r.size()) < count) {
+    if (is_prime(q)) r.push_back(static_cast<word>(q));
+    q -= step;
+  }
+  return r;
+}
+
+// uniform residues, limb i under chain[i]
+std::vector<word> uniform(const std::vector<word> &chain, int limbs) {
+  std::vector<word> v(static_cast<size_t>(limbs) * kN);
+  for (int l = 0; l < limbs; l++)
+    for (size_t n = 0; n < kN; n++) v[l * kN + n] = next64() % chain[l];
+  return v;
+}
+
+void upload(word *dst, const std::vector<word> &h) {
+  HipCheck(hipMemcpy(dst, h.data(), h.size() * sizeof(word),
+                     hipMemcpyHostToDevice),
+           "hipMemcpy");
+}
+std::vector<word> download(const word *src, size_t words) {
+  std::vector<word> h(words);
+  HipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  HipCheck(hipMemcpy(h.data(), src, words * sizeof(word),
+                     hipMemcpyDeviceToHost),
+           "hipMemcpy");
+  return h;
+}
+
+int g_fail = 0;
+void check(const std::string &name, bool ok) {
+  std::printf("%s %s\n", ok ? "PASS" : "FAIL", name.c_str());
+  std::fflush(stdout);
+  if (!ok) g_fail++;
+}
+bool same(const std::vector<word> &a, const std::vector<word> &b) {
+  return a.size() == b.size() &&
+         std::memcmp(a.data(), b.data(), a.size() * sizeof(word)) == 0;
+}
+
+}  // namespace
+
+int main() {
+  const int L = 24, alpha = 8;
+  const std::vector<word> main_p = primes(30, L), aux_p = primes(31, alpha);
+  std::vector<std::pair<int, int>> levels;
+  for (int i = 1; i <= L; i++) levels.emplace_back(i, 0);
+  // Parameter.h:42-47 argument order
+  Parameter<word> param(kLogN, 0x1p30, L - 1, levels, main_p, aux_p);
+  auto ctx = Context<word>::Create(param);
+  orc_set_threads(8);
+
+  const NPInfo np = param.LevelToNP(L - 1);
+  const NPInfo np_key = param.LevelToNP(param.max_level_, alpha);
+  const int beta = param.dnum_;
+  const size_t qw = static_cast<size_t>(L) * kN;
+  const size_t kw = static_cast<size_t>(L + alpha) * kN;
+  std::vector<word> chain_k(main_p);
+  chain_k.insert(chain_k.end(), aux_p.begin(), aux_p.end());
+
+  // two ciphertexts and a key of beta groups (UserInterface.cu:522-541 shape)
+  Ct a(np), b(np);
+  const std::vector<word> hb1 = uniform(main_p, L), ha1 = uniform(main_p, L);
+  const std::vector<word> hb2 = uniform(main_p, L), ha2 = uniform(main_p, L);
+  upload(a.bx_.data(), hb1);
+  upload(a.ax_.data(), ha1);
+  upload(b.bx_.data(), hb2);
+  upload(b.ax_.data(), ha2);
+  a.SetScale(0x1p30);
+  b.SetScale(0x1p30);
+  Evk key(np_key, beta);
+  std::vector<word> kb(beta * kw), ka(beta * kw);
+  for (int g = 0; g < beta; g++) {
+    const std::vector<word> x = uniform(chain_k, L + alpha);
+    const std::vector<word> y = uniform(chain_k, L + alpha);
+    std::copy(x.begin(), x.end(), kb.begin() + g * kw);
+    std::copy(y.begin(), y.end(), ka.begin() + g * kw);
+    upload(key.bx_[g].data(), x);
+    upload(key.ax_[g].data(), y);
+  }
+
+  // oracle results
+  std::vector<word> wb((L) * kN), wa((L) * kN), wbr((L - 1) * kN),
+      war((L - 1) * kN);
+  orc_hmult(wbr.data(), war.data(), hb1.data(), ha1.data(), hb2.data(),
+            ha2.data(), kb.data(), ka.data(), L, L, main_p.data(),
+            aux_p.data(), alpha, kLogN, 1);
+  orc_hmult(wb.data(), wa.data(), hb1.data(), ha1.data(), hb2.data(),
+            ha2.data(), kb.data(), ka.data(), L, L, main_p.data(),
+            aux_p.data(), alpha, kLogN, 0);
+
+  // Context::HMult with merged rescale (Context.cpp:862-871)
+  {
+    Ct res;
+    ctx->HMult(res, a, b, key, true);
+    check("HMult(rescale=true) level and scale",
+          res.GetNP() == param.LevelToNP(L - 2) &&
+              res.GetScale() == 0x1p60 / param.GetRescalePrimeProd(L - 1));
+    check("HMult(rescale=true) bx", same(download(res.bx_.data(), (L - 1) * kN), wbr));
+    check("HMult(rescale=true) ax", same(download(res.ax_.data(), (L - 1) * kN), war));
+  }
+  // HMult without rescale, then Rescale (Context.cpp:739-774)
+  {
+    Ct res, res2;
+    ctx->HMult(res, a, b, key, false);
+    check("HMult(rescale=false) bx", same(download(res.bx_.data(), qw), wb));
+    check("HMult(rescale=false) ax", same(download(res.ax_.data(), qw), wa));
+    ctx->Rescale(res2, res);
+    std::vector<word> rb((L - 1) * kN), ra((L - 1) * kN);
+    orc_rescale(rb.data(), wb.data(), L, main_p.data(), 1, kLogN);
+    orc_rescale(ra.data(), wa.data(), L, main_p.data(), 1, kLogN);
+    check("Rescale bx", same(download(res2.bx_.data(), (L - 1) * kN), rb));
+    check("Rescale ax", same(download(res2.ax_.data(), (L - 1) * kN), ra));
+  }
+  // Mult (tensor with rx) then Relinearize / RelinearizeRescale
+  {
+    Ct t, r1, r2;
+    ctx->Mult(t, a, b);
+    check("Mult keeps rx", t.HasRx());
+    ctx->Relinearize(r1, t, key);
+    check("Mult + Relinearize == HMult(false)",
+          same(download(r1.bx_.data(), qw), wb) &&
+              same(download(r1.ax_.data(), qw), wa));
+    ctx->RelinearizeRescale(r2, t, key);
+    check("Mult + RelinearizeRescale == HMult(true)",
+          same(download(r2.bx_.data(), (L - 1) * kN), wbr) &&
+              same(download(r2.ax_.data(), (L - 1) * kN), war));
+  }
+  // in place: res aliases the first input (Context.cpp:867)
+  {
+    Ct c(np);
+    upload(c.bx_.data(), hb1);
+    upload(c.ax_.data(), ha1);
+    c.SetScale(0x1p30);
+    ctx->HMult(c, c, b, key, true);
+    check("HMult in place",
+          same(download(c.bx_.data(), (L - 1) * kN), wbr) &&
+              same(download(c.ax_.data(), (L - 1) * kN), war));
+  }
+  // MultKey and HRot (Context.cpp:584-607, 776-791)
+  {
+    Ct mk, rot;
+    ctx->MultKey(mk, a, key);
+    std::vector<word> mb(qw), ma(qw);
+    orc_mult_key(mb.data(), ma.data(), hb1.data(), ha1.data(), kb.data(),
+                 ka.data(), L, L, main_p.data(), aux_p.data(), alpha, kLogN);
+    check("MultKey", same(download(mk.bx_.data(), qw), mb) &&
+                         same(download(mk.ax_.data(), qw), ma));
+    ctx->HRot(rot, a, key, 5);
+    std::vector<word> hrb(qw), hra(qw);
+    orc_hrot(hrb.data(), hra.data(), hb1.data(), ha1.data(), kb.data(),
+             ka.data(), L, L, main_p.data(), aux_p.data(), alpha, kLogN, 5);
+    check("HRot(5)", same(download(rot.bx_.data(), qw), hrb) &&
+                         same(download(rot.ax_.data(), qw), hra));
+  }
+  // public handler members (Context.h:83-92), used directly by extensions
+  {
+    DeviceVector<word> y(qw);
+    DvView<word> yv = y.View();
+    ctx->ntt_handler_.NTT(yv, np, a.bx_.ConstView(), false);
+    std::vector<word> want = hb1;
+    orc_ntt_batch(want.data(), L, kLogN, main_p.data(), 0);
+    check("ntt_handler_.NTT", same(download(y.data(), qw), want));
+    DeviceVector<word> z(qw);
+    DvView<word> zv = z.View();
+    ctx->ntt_handler_.INTT(zv, np, y.ConstView(), false);
+    check("ntt_handler_.INTT round trip", same(download(z.data(), qw), hb1));
+
+    const auto &ms = ctx->mod_switch_handlers_[L - 1];
+    std::vector<DeviceVector<word>> up(ms.GetBeta());
+    std::vector<DvView<word>> upv;
+    for (auto &u : up) {
+      u.resize(kw);
+      upv.push_back(u.View(alpha * static_cast<int>(kN)));
+    }
+    ms.ModUp(upv, a.ax_.ConstView());
+    std::vector<word> wup(static_cast<size_t>(ms.GetBeta()) * kw);
+    orc_mod_up(wup.data(), ha1.data(), L, main_p.data(), aux_p.data(), alpha,
+               kLogN);
+    bool ok = true;
+    for (int g = 0; g < ms.GetBeta(); g++)
+      ok = ok && same(download(up[g].data(), kw),
+                      std::vector<word>(wup.begin() + g * kw,
+                                        wup.begin() + (g + 1) * kw));
+    check("mod_switch_handlers_[level].ModUp", ok);
+  }
+  // an invalid call throws cheddar::Error instead of exiting
+  {
+    bool threw = false;
+    try {
+      Ct bad(param.LevelToNP(L - 2));
+      Ct res;
+      ctx->HMult(res, a, bad, key, true);
+    } catch (const Error &) {
+      threw = true;
+    }
+    check("NP mismatch throws cheddar::Error", threw);
+  }
+  std::printf("%s\n", g_fail == 0 ? "ALL PASS" : "FAILURES");
+  return g_fail == 0 ? 0 : 1;
+}
