@@ -148,10 +148,18 @@ __device__ __forceinline__ void st_at(void *base, uint32_t byte_off, T v) {
 // faster per transform. The fused key-accumulation kernel keeps default
 // loads: with many concurrent streams the hint evicts a half-used line before
 // the next instruction reads its other half (twice the traffic, measured).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <typename T>
 __device__ __forceinline__ T ld_nt(const void *base, uint32_t byte_off) {
-  return __builtin_nontemporal_load(reinterpret_cast<const T *>(
-      static_cast<const char *>(base) + byte_off));
+  const char *p = static_cast<const char *>(base) + byte_off;
+  if constexpr (sizeof(T) == 16) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    T r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+  } else {
+    return __builtin_nontemporal_load(reinterpret_cast<const T *>(p));
+  }
 }
 template <typename T>
 __device__ __forceinline__ void st_nt(void *base, uint32_t byte_off, T v) {
@@ -317,7 +325,8 @@ template <int kEpi, bool kLazy>
 __device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
                                               uint32_t (&xin)[16], uint32_t q,
                                               uint32_t qinv, uint32_t *dst,
-                                              int32_t *xch) {
+                                              int32_t *xch,
+                                              const uint32_t (&s2v)[16]) {
   using A = Arith<kLazy>;
   using T = typename A::T;
   const A ar{static_cast<T>(q)};
@@ -370,34 +379,16 @@ __device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
   }
   uint32_t out[16];
   if constexpr (kEpi == kEpiModDown) {
-    // NTTPhase2ForModDown epilogue (NTT.cu:567-600)
+    // NTTPhase2ForModDown epilogue (NTT.cu:567-600); src2 (and its optional
+    // padding product) was loaded and prepared before the butterflies
     const int32_t qs = static_cast<int32_t>(q);
     const int32_t c2 = static_cast<int32_t>(a.cst2[lb.l]);
     const int32_t c2q = static_cast<int32_t>(static_cast<uint32_t>(c2) * qinv);
-    const int s2 = lb.l - a.src2_lo;
-    const bool has2 = lb.l >= a.src2_lo && lb.l < a.src2_hi;
-    if (has2) {
-      const int32_t *s2p = reinterpret_cast<const int32_t *>(a.src2) +
-                           blockIdx.z * a.src2_pstride +
-                           (static_cast<size_t>(s2) << kLogN) + row * kCols +
-                           16 * c;
-      int32_t pe = 0, peq = 0;
-      if (a.pad != nullptr) {
-        pe = static_cast<int32_t>(a.pad[s2]);
-        peq = static_cast<int32_t>(static_cast<uint32_t>(pe) * qinv);
-      }
 #pragma unroll
-      for (int k = 0; k < 16; k++) {
-        int32_t v = s2p[k];
-        if (a.pad != nullptr) v = norm(mont(v, pe, peq, qs), qs);
-        v -= static_cast<int32_t>(ar.canon_fwd(x[k]));
-        out[k] = static_cast<uint32_t>(norm(mont(v, c2, c2q, qs), qs));
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 16; k++)
-        out[k] = static_cast<uint32_t>(norm(
-            mont(-static_cast<int32_t>(ar.canon_fwd(x[k])), c2, c2q, qs), qs));
+    for (int k = 0; k < 16; k++) {
+      const int32_t v = static_cast<int32_t>(s2v[k]) -
+                        static_cast<int32_t>(ar.canon_fwd(x[k]));
+      out[k] = static_cast<uint32_t>(norm(mont(v, c2, c2q, qs), qs));
     }
   } else {
 #pragma unroll
@@ -430,12 +421,42 @@ __global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
   uint32_t x[16];
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = ld_nt<uint32_t>(dst, rbase + (c + 16 * k) * 4u);
+  // ModDown epilogue operand: this thread's 16 output words of src2 (zero
+  // outside [src2_lo, src2_hi)), loaded with the data so their latency hides
+  // behind the butterflies
+  uint32_t s2v[16] = {};
+  if constexpr (kEpi == kEpiModDown) {
+    if (lb.l >= a.src2_lo && lb.l < a.src2_hi) {
+      const uint32_t *s2p = a.src2 + blockIdx.z * a.src2_pstride +
+                            (static_cast<size_t>(lb.l - a.src2_lo) << kLogN);
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const uint4 t = ld_nt<uint4>(s2p, rbase + 64u * c + 16u * v);
+        s2v[4 * v] = t.x;
+        s2v[4 * v + 1] = t.y;
+        s2v[4 * v + 2] = t.z;
+        s2v[4 * v + 3] = t.w;
+      }
+    }
+  }
   const uint32_t q = a.tab.q[lb.ti];
   const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
+  if constexpr (kEpi == kEpiModDown) {
+    if (a.pad != nullptr && lb.l >= a.src2_lo && lb.l < a.src2_hi) {
+      // src2 * padding (BitPacker restore, NTT.cu:579-585)
+      const int32_t qs = static_cast<int32_t>(q);
+      const int32_t pe = static_cast<int32_t>(a.pad[lb.l - a.src2_lo]);
+      const int32_t peq = static_cast<int32_t>(static_cast<uint32_t>(pe) * qinv);
+#pragma unroll
+      for (int k = 0; k < 16; k++)
+        s2v[k] = static_cast<uint32_t>(
+            norm(mont(static_cast<int32_t>(s2v[k]), pe, peq, qs), qs));
+    }
+  }
   if (q < (1u << 30))
-    fwd_rows_body<kEpi, true>(a, lb, x, q, qinv, dst, xch);
+    fwd_rows_body<kEpi, true>(a, lb, x, q, qinv, dst, xch, s2v);
   else
-    fwd_rows_body<kEpi, false>(a, lb, x, q, qinv, dst, xch);
+    fwd_rows_body<kEpi, false>(a, lb, x, q, qinv, dst, xch, s2v);
 }
 
 // inverse, row pass: GS stages 15..8 (src -> dst, dst left unreduced)

@@ -610,11 +610,9 @@ ModSwitchHandler<uint32_t>::ModSwitchHandler(
   BuildSwitch(mod_down_rescale_, mdr_src, rdst);
   upload(rescale_inv_prime_prod_, inv_prod(rsrc, rdst));
   upload(mod_down_rescale_inv_prime_prod_, inv_prod(mdr_src, rdst));
-  // BitPacker padding with an empty restore range: ToMont(1) per limb
-  std::vector<word> pad(rdst.size());
-  for (size_t k = 0; k < rdst.size(); k++) pad[k] = pm::to_mont(1, rdst[k]);
-  upload(rescale_padding_, pad);
-  upload(mod_down_rescale_padding_, pad);
+  // The reference's BitPacker padding (ModSwitch.cu:372-411) is ToMont(1) on
+  // every limb when the restore range is empty (no terminal primes), an
+  // identity in the ModDown epilogue, so no padding table is kept.
 }
 
 // PopulateModSwitchConstants (ModSwitch.cu:320-370), restore range empty
@@ -867,9 +865,11 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
       kind == Kind::ModDown   ? inv_prime_prod_
       : kind == Kind::Rescale ? rescale_inv_prime_prod_
                               : mod_down_rescale_inv_prime_prod_;
-  const word *pad = kind == Kind::ModDown   ? nullptr
-                    : kind == Kind::Rescale ? rescale_padding_.data()
-                                            : mod_down_rescale_padding_.data();
+  // The padding of Rescale / ModDownAndRescale is ToMont(1) on every limb
+  // here (no terminal primes, so the BitPacker restore range is empty), and
+  // MontMul(x, ToMont(1)) = x for the canonical src2 limbs: the epilogue's
+  // padding multiply is the identity and is skipped (nullptr).
+  const word *pad = nullptr;
   // NTTForModDown (NTT.cu:417-604) with src2 = the untouched low limbs
   const int src2_off = std::max(0, np_src.num_ter_ - np_dst.num_ter_);
   const int s2_lo = np_dst.num_ter_ - np_non_intt.num_ter_;

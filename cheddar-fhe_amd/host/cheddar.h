@@ -402,8 +402,7 @@ class ModSwitchHandler<uint32_t> {
   std::vector<SwitchTable> mod_up_;
   SwitchTable mod_down_, rescale_, mod_down_rescale_;
   DeviceVector<word> inv_prime_prod_, rescale_inv_prime_prod_,
-      mod_down_rescale_inv_prime_prod_, rescale_padding_,
-      mod_down_rescale_padding_;
+      mod_down_rescale_inv_prime_prod_;
 };
 
 template <typename word>
