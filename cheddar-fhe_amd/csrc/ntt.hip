@@ -671,14 +671,8 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
   const uint32_t rbase = static_cast<uint32_t>(row * kCols) * 4u;
   const uint32_t cbase = rbase + 64u * c;  // this thread's 16 contiguous words
   T *xr = reinterpret_cast<T *>(xch) + r * kRowPad;
-  uint32_t w1[15], w2[15];
-#pragma unroll
-  for (int s = 0, i = 0; s < 4; s++)
-#pragma unroll
-    for (int g = 0; g < (1 << s); g++, i++) {
-      w1[i] = tw[(256 << s) + (row << s) + g];
-      w2[i] = tw[(4096 << s) + (row << (4 + s)) + (c << s) + g];
-    }
+  // twiddles are (re)loaded inside each group's row pass (cache hits after
+  // the first group) instead of living in 30 registers across the loop
   const size_t loff = static_cast<size_t>(l) << kLogN;
   const size_t koff = loff + (aux ? a.key_gap : 0);
   uint32_t accb[16], acca[16];
@@ -691,18 +685,42 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
     uint32_t u[16];
     if (l >= own_lo && l < own_hi) {
       // own limb: the input itself (ModSwitch.cu:466-470 copies it); in
-      // tensor mode the input is rx = MontMul(a1, a2)
+      // tensor mode the input is rx = MontMul(a1, a2), and the CAccum of
+      // this q limb (Context.cpp:684-699) is done here too, from the same
+      // loads of the two ciphertexts: bx = MontMul(b1, b2),
+      // ax = MontMul(b1 - q + a1, b2 - q + a2) - bx - rx (ElementWise.cu:504-546)
       if (a.a1 != nullptr) {
+        const int32_t pp = static_cast<int32_t>(a.p_prod[l]);
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-          const uint4 s = ld_at<uint4>(a.a1 + loff, cbase + 16u * v);
-          const uint4 t = ld_at<uint4>(a.a2 + loff, cbase + 16u * v);
-          const uint32_t sv[4] = {s.x, s.y, s.z, s.w};
-          const uint32_t tv[4] = {t.x, t.y, t.z, t.w};
+          const uint4 vb1 = ld_at<uint4>(a.b1 + loff, cbase + 16u * v);
+          const uint4 va1 = ld_at<uint4>(a.a1 + loff, cbase + 16u * v);
+          const uint4 vb2 = ld_at<uint4>(a.b2 + loff, cbase + 16u * v);
+          const uint4 va2 = ld_at<uint4>(a.a2 + loff, cbase + 16u * v);
+          const uint32_t x1[4] = {vb1.x, vb1.y, vb1.z, vb1.w};
+          const uint32_t y1[4] = {va1.x, va1.y, va1.z, va1.w};
+          const uint32_t x2[4] = {vb2.x, vb2.y, vb2.z, vb2.w};
+          const uint32_t y2[4] = {va2.x, va2.y, va2.z, va2.w};
 #pragma unroll
-          for (int j = 0; j < 4; j++)
-            u[4 * v + j] = mont_mul(static_cast<int32_t>(sv[j]),
-                                    static_cast<int32_t>(tv[j]), q, qi);
+          for (int j = 0; j < 4; j++) {
+            const int32_t s1 = (static_cast<int32_t>(x1[j]) - qs) +
+                               static_cast<int32_t>(y1[j]);
+            const int32_t s2 = (static_cast<int32_t>(x2[j]) - qs) +
+                               static_cast<int32_t>(y2[j]);
+            const uint32_t bb = mont_mul(static_cast<int32_t>(x1[j]),
+                                         static_cast<int32_t>(x2[j]), q, qi);
+            const uint32_t rr = mont_mul(static_cast<int32_t>(y1[j]),
+                                         static_cast<int32_t>(y2[j]), q, qi);
+            const uint32_t ax = sub_mod(
+                sub_mod(mont_mul(s1, s2, q, qi), bb, q), rr, q);
+            u[4 * v + j] = rr;
+            accb[4 * v + j] = add_mod(
+                accb[4 * v + j], mont_mul(pp, static_cast<int32_t>(bb), q, qi),
+                q);
+            acca[4 * v + j] = add_mod(
+                acca[4 * v + j], mont_mul(pp, static_cast<int32_t>(ax), q, qi),
+                q);
+          }
         }
       } else {
         const uint32_t *dl = a.d + loff;
@@ -716,6 +734,14 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
         }
       }
     } else {
+      uint32_t w1[15], w2[15];
+#pragma unroll
+      for (int s = 0, i = 0; s < 4; s++)
+#pragma unroll
+        for (int gg = 0; gg < (1 << s); gg++, i++) {
+          w1[i] = tw[(256 << s) + (row << s) + gg];
+          w2[i] = tw[(4096 << s) + (row << (4 + s)) + (c << s) + gg];
+        }
       const uint32_t *src = a.modup + g * a.group_stride + loff;
       T x[16];
 #pragma unroll
@@ -773,38 +799,7 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
       }
     }
   }
-  if (!aux && a.a1 != nullptr) {
-    // CAccum with the Tensor's bx, ax formed here (ElementWise.cu:504-546)
-    const int32_t pp = static_cast<int32_t>(a.p_prod[l]);
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      const uint4 vb1 = ld_at<uint4>(a.b1 + loff, cbase + 16u * v);
-      const uint4 va1 = ld_at<uint4>(a.a1 + loff, cbase + 16u * v);
-      const uint4 vb2 = ld_at<uint4>(a.b2 + loff, cbase + 16u * v);
-      const uint4 va2 = ld_at<uint4>(a.a2 + loff, cbase + 16u * v);
-      const uint32_t x1[4] = {vb1.x, vb1.y, vb1.z, vb1.w};
-      const uint32_t y1[4] = {va1.x, va1.y, va1.z, va1.w};
-      const uint32_t x2[4] = {vb2.x, vb2.y, vb2.z, vb2.w};
-      const uint32_t y2[4] = {va2.x, va2.y, va2.z, va2.w};
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int32_t s1 = (static_cast<int32_t>(x1[j]) - qs) +
-                           static_cast<int32_t>(y1[j]);
-        const int32_t s2 = (static_cast<int32_t>(x2[j]) - qs) +
-                           static_cast<int32_t>(y2[j]);
-        const uint32_t bb = mont_mul(static_cast<int32_t>(x1[j]),
-                                     static_cast<int32_t>(x2[j]), q, qi);
-        const uint32_t rr = mont_mul(static_cast<int32_t>(y1[j]),
-                                     static_cast<int32_t>(y2[j]), q, qi);
-        const uint32_t ax = sub_mod(sub_mod(mont_mul(s1, s2, q, qi), bb, q),
-                                    rr, q);
-        accb[4 * v + j] = add_mod(
-            accb[4 * v + j], mont_mul(pp, static_cast<int32_t>(bb), q, qi), q);
-        acca[4 * v + j] = add_mod(
-            acca[4 * v + j], mont_mul(pp, static_cast<int32_t>(ax), q, qi), q);
-      }
-    }
-  } else if (!aux) {
+  if (!aux && a.a1 == nullptr) {
     // CAccum (Context.cpp:684-699): acc += p_prod * ct (bx, and ax if given)
     const int32_t pp = static_cast<int32_t>(a.p_prod[l]);
 #pragma unroll
