@@ -190,6 +190,126 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(chd_limb_map m,
   }
 }
 
+// galois index map of Permute (ElementWise.cu:370-391): dst[x] = src[perm(x)]
+__device__ __forceinline__ uint32_t perm_index(uint32_t x, uint32_t galois) {
+  const uint32_t e = (__brev(x) >> (32 - (kLogN + 1))) + 1;
+  return __brev(e * galois - 1) >> (32 - (kLogN + 1));
+}
+
+__global__ __launch_bounds__(kThreads) void zero_kernel(uint4 *dst,
+                                                      long long n4) {
+  const long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i < n4) dst[i] = make_uint4(0, 0, 0, 0);
+}
+
+struct PermAccArgs {
+  uint32_t *dst[CHD_MAX_POLY];
+  const uint32_t *src0[CHD_MAX_POLY];
+  long long src0_gap;
+  chd_perm_src s[CHD_MAX_ACCUM];
+};
+
+// PermuteAccum / PermuteAccumAdd (ElementWise.cu:395-501)
+template <int kPoly>
+__global__ __launch_bounds__(kThreads) void permute_accum_kernel(
+    chd_tables t, chd_limb_map m, PermAccArgs a, int num_src) {
+  const LimbIdx li = limb_of(t, m);
+  const size_t base = static_cast<size_t>(li.l) << kLogN;
+  const int c0 = blockIdx.x * kCoefPerBlock + threadIdx.x * kPerThread;
+  uint32_t acc[kPoly][4];
+#pragma unroll
+  for (int p = 0; p < kPoly; p++) {
+    if (a.src0[0] != nullptr) {
+      const uint4 v = ld4(a.src0[p] + base + c0 + (li.aux ? a.src0_gap : 0));
+      acc[p][0] = v.x;
+      acc[p][1] = v.y;
+      acc[p][2] = v.z;
+      acc[p][3] = v.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[p][i] = 0;
+    }
+  }
+  for (int j = 0; j < num_src; j++) {
+    const chd_perm_src &s = a.s[j];
+    uint32_t idx[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) idx[i] = perm_index(c0 + i, s.galois);
+    const size_t sb = base + (li.aux ? s.src_gap : 0);
+#pragma unroll
+    for (int p = 0; p < kPoly; p++) {
+      const uint32_t *sp = s.src[p] + sb;
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[p][i] = add_mod(acc[p][i], sp[idx[i]], li.q);
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < kPoly; p++)
+    st4(a.dst[p] + base + c0, make_uint4(acc[p][0], acc[p][1], acc[p][2], acc[p][3]));
+}
+
+// Hoisted baby step (BSFusedKernel, src/extension/Hoist.cu:20-78): the ModUp
+// of a is read once per coefficient and reused by every rotation; the
+// automorphism is applied as a scatter with the inverse galois factor, so the
+// key loads stay coalesced.
+__global__ __launch_bounds__(kThreads) void bs_fused_kernel(chd_tables t,
+                                                          chd_limb_map m,
+                                                          chd_bs_args a) {
+  const LimbIdx li = limb_of(t, m);
+  const size_t loff = static_cast<size_t>(li.l) << kLogN;
+  const int c0 = blockIdx.x * kCoefPerBlock + threadIdx.x * kPerThread;
+  uint32_t u[CHD_MAX_BS_GROUPS][4];
+  for (int g = 0; g < a.beta; g++) {
+    const int own_lo = g * a.alpha;
+    const int own_hi = min(own_lo + a.alpha, a.num_q);
+    const uint32_t *src = (li.l >= own_lo && li.l < own_hi)
+                              ? a.d + loff
+                              : a.modup + g * a.group_stride + loff;
+    const uint4 v = ld4(src + c0);
+    u[g][0] = v.x;
+    u[g][1] = v.y;
+    u[g][2] = v.z;
+    u[g][3] = v.w;
+  }
+  uint32_t pb[4] = {0, 0, 0, 0};
+  if (!li.aux) {
+    // PseudoModUp of b (ModSwitch.cu:414-428): MontMul(b, p_prod)
+    const int32_t pp = static_cast<int32_t>(a.p_prod[li.l]);
+    const uint4 v = ld4(a.ct_b + loff + c0);
+    pb[0] = mont_mul(static_cast<int32_t>(v.x), pp, li.q, li.qinv);
+    pb[1] = mont_mul(static_cast<int32_t>(v.y), pp, li.q, li.qinv);
+    pb[2] = mont_mul(static_cast<int32_t>(v.z), pp, li.q, li.qinv);
+    pb[3] = mont_mul(static_cast<int32_t>(v.w), pp, li.q, li.qinv);
+  }
+  const size_t koff = loff + (li.aux ? a.key_gap : 0);
+  for (int k = 0; k < a.num_rot; k++) {
+    uint32_t tb[4], ta[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      tb[i] = pb[i];
+      ta[i] = 0;
+    }
+    for (int g = 0; g < a.beta; g++) {
+      const uint4 kb = ld4(a.kb[k][g] + koff + c0);
+      const uint4 ka = ld4(a.ka[k][g] + koff + c0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int32_t uv = static_cast<int32_t>(u[g][i]);
+        tb[i] = add_mod(tb[i], mont_mul(uv, static_cast<int32_t>(get(kb, i)),
+                                        li.q, li.qinv), li.q);
+        ta[i] = add_mod(ta[i], mont_mul(uv, static_cast<int32_t>(get(ka, i)),
+                                        li.q, li.qinv), li.q);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t di = perm_index(c0 + i, a.galois[k]);
+      a.dst_b[k][loff + di] = tb[i];
+      a.dst_a[k][loff + di] = ta[i];
+    }
+  }
+}
+
 }  // namespace
 }  // namespace chd
 
@@ -284,4 +404,82 @@ extern "C" int chd_k_permute(const chd_limb_map *m, uint32_t *const *dst,
     hipLaunchKernelGGL(permute_kernel<3>, g, dim3(kThreads), 0, s, *m, a,
                        galois);
   return check_launch("chd_k_permute");
+}
+
+extern "C" int chd_k_permute_accum(const chd_tables *t, const chd_limb_map *m,
+                                   uint32_t *const *dst, int num_polys,
+                                   const uint32_t *const *src0,
+                                   long long src0_gap,
+                                   const chd_perm_src *srcs, int num_src,
+                                   int num_limbs, void *stream) {
+  if (!t || !m || !dst || (num_src > 0 && !srcs) || num_polys < 1 ||
+      num_polys > CHD_MAX_POLY || num_src < 0 || num_src > CHD_MAX_ACCUM ||
+      (num_src == 0 && !src0) || num_limbs < 0)
+    return set_error(CHD_ERR_ARG, "chd_k_permute_accum: invalid argument");
+  if (num_limbs == 0) return 0;
+  PermAccArgs a{};
+  for (int p = 0; p < num_polys; p++) {
+    if (!dst[p] || (src0 && !src0[p]))
+      return set_error(CHD_ERR_ARG, "chd_k_permute_accum: null polynomial");
+    a.dst[p] = dst[p];
+    a.src0[p] = src0 ? src0[p] : nullptr;
+  }
+  a.src0_gap = src0_gap;
+  for (int j = 0; j < num_src; j++) {
+    for (int p = 0; p < num_polys; p++)
+      if (!srcs[j].src[p])
+        return set_error(CHD_ERR_ARG, "chd_k_permute_accum: null source");
+    if ((srcs[j].galois & 1u) == 0 || srcs[j].galois >= 2u * kN)
+      return set_error(CHD_ERR_ARG, "chd_k_permute_accum: invalid galois factor");
+    a.s[j] = srcs[j];
+  }
+  dim3 g(kN / kCoefPerBlock, num_limbs);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (num_polys) {
+    case 1:
+      hipLaunchKernelGGL(permute_accum_kernel<1>, g, dim3(kThreads), 0, s, *t, *m, a, num_src);
+      break;
+    case 2:
+      hipLaunchKernelGGL(permute_accum_kernel<2>, g, dim3(kThreads), 0, s, *t, *m, a, num_src);
+      break;
+    default:
+      hipLaunchKernelGGL(permute_accum_kernel<3>, g, dim3(kThreads), 0, s, *t, *m, a, num_src);
+      break;
+  }
+  return check_launch("chd_k_permute_accum");
+}
+
+extern "C" int chd_k_bs_fused(const chd_tables *t, const chd_limb_map *m,
+                              const chd_bs_args *args, void *stream) {
+  if (!t || !m || !args || args->num_rot < 1 || args->num_rot > CHD_MAX_BS ||
+      args->beta < 1 || args->beta > CHD_MAX_BS_GROUPS || args->alpha < 1 ||
+      (args->beta - 1) * args->alpha >= args->num_q ||
+      args->beta * args->alpha < args->num_q || !args->modup || !args->d ||
+      !args->ct_b || !args->p_prod || args->num_q != m->num_q ||
+      m->skip_len != 0)
+    return set_error(CHD_ERR_ARG, "chd_k_bs_fused: invalid argument");
+  for (int k = 0; k < args->num_rot; k++) {
+    if (!args->dst_b[k] || !args->dst_a[k] || (args->galois[k] & 1u) == 0 ||
+        args->galois[k] >= 2u * kN)
+      return set_error(CHD_ERR_ARG, "chd_k_bs_fused: invalid rotation");
+    for (int g = 0; g < args->beta; g++)
+      if (!args->kb[k][g] || !args->ka[k][g])
+        return set_error(CHD_ERR_ARG, "chd_k_bs_fused: null key pointer");
+  }
+  dim3 g(kN / kCoefPerBlock, args->num_q + args->alpha);
+  hipLaunchKernelGGL(bs_fused_kernel, g, dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), *t, *m, *args);
+  return check_launch("chd_k_bs_fused");
+}
+
+extern "C" int chd_k_zero(uint32_t *dst, long long words, void *stream) {
+  if (!dst || words < 0 || (words & 3) != 0 ||
+      (reinterpret_cast<uintptr_t>(dst) & 15) != 0)
+    return set_error(CHD_ERR_ARG, "chd_k_zero: invalid argument");
+  if (words == 0) return 0;
+  const long long n4 = words / 4;
+  hipLaunchKernelGGL(zero_kernel, dim3((n4 + kThreads - 1) / kThreads),
+                     dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     reinterpret_cast<uint4 *>(dst), n4);
+  return check_launch("chd_k_zero");
 }

@@ -799,7 +799,17 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
       }
     }
   }
-  if (!aux && a.a1 == nullptr) {
+  if (a.add_b != nullptr) {
+    // extended-basis b of a giant-step accumulator, added on every limb
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const uint4 t = ld_at<uint4>(a.add_b + loff, cbase + 16u * v);
+      const uint32_t tv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) accb[4 * v + j] = add_mod(accb[4 * v + j], tv[j], q);
+    }
+  }
+  if (!aux && a.a1 == nullptr && a.cb != nullptr) {
     // CAccum (Context.cpp:684-699): acc += p_prod * ct (bx, and ax if given)
     const int32_t pp = static_cast<int32_t>(a.p_prod[l]);
 #pragma unroll
@@ -1046,8 +1056,7 @@ extern "C" int chd_k_modup_keyacc(const chd_tables *t,
   const bool tensor = args && args->a1 != nullptr;
   if (!t || !args || !args->modup || !args->p_prod || !args->acc_b ||
       !args->acc_a || args->alpha < 1 ||
-      (tensor ? !args->b1 || !args->b2 || !args->a2
-              : !args->d || !args->cb) ||
+      (tensor ? !args->b1 || !args->b2 || !args->a2 : !args->d) ||
       args->beta < 1 || args->beta > kMaxGroups ||
       (args->beta - 1) * args->alpha >= args->num_q ||
       args->beta * args->alpha < args->num_q)

@@ -424,3 +424,130 @@ extern "C" int chd_permute(const chd_context *ctx, int level, uint32_t *res_bx,
            ctx->c->PermuteV(level, {res_bx, res_ax, nullptr},
                             {a_bx, a_ax, nullptr}, rot))
 }
+
+namespace {
+// ciphertext copy of two device polynomials of `limbs` limbs (the C-ABI's
+// inputs are raw pointers; the hoisting engine works on Ciphertext objects)
+cheddar::Ciphertext<word> CtCopy(const cheddar::Parameter<word> &p, int level,
+                                 const uint32_t *bx, const uint32_t *ax) {
+  cheddar::Ciphertext<word> ct(p.LevelToNP(level));
+  const size_t bytes = ct.bx_.size() * sizeof(word);
+  cheddar::HipCheck(hipMemcpyAsync(ct.bx_.data(), bx, bytes,
+                                   hipMemcpyDeviceToDevice,
+                                   cheddar::CurrentStream()),
+                    "hipMemcpyAsync");
+  cheddar::HipCheck(hipMemcpyAsync(ct.ax_.data(), ax, bytes,
+                                   hipMemcpyDeviceToDevice,
+                                   cheddar::CurrentStream()),
+                    "hipMemcpyAsync");
+  return ct;
+}
+
+cheddar::HoistHandler<word>::KeyLookup Keys(const chd_context *ctx,
+                                            int num_keys, const int *key_rot,
+                                            const uint32_t *const *key_bx,
+                                            const uint32_t *const *key_ax,
+                                            int key_beta) {
+  return [=](int r) {
+    for (int i = 0; i < num_keys; i++)
+      if (key_rot[i] == r)
+        return MakeEvk(ctx, key_bx + static_cast<size_t>(i) * key_beta,
+                       key_ax + static_cast<size_t>(i) * key_beta, key_beta);
+    throw cheddar::Error("no rotation key for " + std::to_string(r));
+  };
+}
+}  // namespace
+
+extern "C" int chd_hoist_baby_steps(
+    const chd_context *ctx, int level, const uint32_t *ct_bx,
+    const uint32_t *ct_ax, int num_rot, const int *rots,
+    uint32_t *const *dst_bx, uint32_t *const *dst_ax, int num_keys,
+    const int *key_rot, const uint32_t *const *key_bx,
+    const uint32_t *const *key_ax, int key_beta, void *stream) {
+  CHD_CALL("chd_hoist_baby_steps",
+           LevelOk(ctx, level) && ct_bx && ct_ax && num_rot > 0 && rots &&
+               dst_bx && dst_ax && num_keys >= 0 && key_beta > 0 &&
+               (num_keys == 0 || (key_rot && key_bx && key_ax)),
+           {
+             const auto &p = ctx->c->param_;
+             // one plaintext slot per baby step makes the handler's index set
+             cheddar::HoistHandler<word>::PtMap pts;
+             for (int i = 0; i < num_rot; i++)
+               pts[0].try_emplace(rots[i],
+                                  p.LevelToNP(level, p.alpha_), p.degree_);
+             cheddar::HoistHandler<word> h(ctx->c, std::move(pts), level, 1.0);
+             const cheddar::Ciphertext<word> in = CtCopy(p, level, ct_bx, ct_ax);
+             std::map<int, cheddar::Ciphertext<word>> bs;
+             h.BabyStep(*ctx->c, bs, in,
+                        Keys(ctx, num_keys, key_rot, key_bx, key_ax, key_beta));
+             for (int i = 0; i < num_rot; i++) {
+               const auto &ct = bs.at(rots[i]);
+               const size_t bytes = ct.bx_.size() * sizeof(word);
+               if (!dst_bx[i] || !dst_ax[i])
+                 throw cheddar::Error("null baby-step destination");
+               cheddar::HipCheck(
+                   hipMemcpyAsync(dst_bx[i], ct.bx_.data(), bytes,
+                                  hipMemcpyDeviceToDevice,
+                                  cheddar::CurrentStream()),
+                   "hipMemcpyAsync");
+               cheddar::HipCheck(
+                   hipMemcpyAsync(dst_ax[i], ct.ax_.data(), bytes,
+                                  hipMemcpyDeviceToDevice,
+                                  cheddar::CurrentStream()),
+                   "hipMemcpyAsync");
+             }
+             // the temporaries are freed on return: finish the copies first
+             cheddar::HipCheck(hipStreamSynchronize(cheddar::CurrentStream()),
+                               "hipStreamSynchronize");
+           })
+}
+
+extern "C" int chd_hoist_evaluate(
+    const chd_context *ctx, int level, uint32_t *res_bx, uint32_t *res_ax,
+    const uint32_t *ct_bx, const uint32_t *ct_ax, int num_gs, const int *gs,
+    int num_bs, const int *bs, const uint32_t *const *pt, int num_keys,
+    const int *key_rot, const uint32_t *const *key_bx,
+    const uint32_t *const *key_ax, int key_beta, void *stream) {
+  CHD_CALL("chd_hoist_evaluate",
+           LevelOk(ctx, level) && level > 0 && res_bx && res_ax && ct_bx &&
+               ct_ax && num_gs > 0 && gs && num_bs > 0 && bs && pt &&
+               num_keys >= 0 && key_beta > 0 &&
+               (num_keys == 0 || (key_rot && key_bx && key_ax)),
+           {
+             const auto &p = ctx->c->param_;
+             const cheddar::NPInfo np = p.LevelToNP(level, p.alpha_);
+             cheddar::HoistHandler<word>::PtMap pts;
+             for (int g = 0; g < num_gs; g++)
+               for (int b = 0; b < num_bs; b++) {
+                 const uint32_t *src = pt[static_cast<size_t>(g) * num_bs + b];
+                 if (src == nullptr) continue;
+                 auto &pl = pts[gs[g]].try_emplace(bs[b], np, p.degree_)
+                                .first->second;
+                 cheddar::HipCheck(
+                     hipMemcpyAsync(pl.mx_.data(), src,
+                                    pl.mx_.size() * sizeof(word),
+                                    hipMemcpyDeviceToDevice,
+                                    cheddar::CurrentStream()),
+                     "hipMemcpyAsync");
+               }
+             cheddar::HoistHandler<word> h(ctx->c, std::move(pts), level, 1.0);
+             const cheddar::Ciphertext<word> in = CtCopy(p, level, ct_bx, ct_ax);
+             const auto keys =
+                 Keys(ctx, num_keys, key_rot, key_bx, key_ax, key_beta);
+             std::map<int, cheddar::Ciphertext<word>> babies;
+             h.BabyStep(*ctx->c, babies, in, keys);
+             cheddar::Ciphertext<word> res;
+             h.GiantStep(*ctx->c, res, babies, keys);
+             const size_t bytes = res.bx_.size() * sizeof(word);
+             cheddar::HipCheck(hipMemcpyAsync(res_bx, res.bx_.data(), bytes,
+                                              hipMemcpyDeviceToDevice,
+                                              cheddar::CurrentStream()),
+                               "hipMemcpyAsync");
+             cheddar::HipCheck(hipMemcpyAsync(res_ax, res.ax_.data(), bytes,
+                                              hipMemcpyDeviceToDevice,
+                                              cheddar::CurrentStream()),
+                               "hipMemcpyAsync");
+             cheddar::HipCheck(hipStreamSynchronize(cheddar::CurrentStream()),
+                               "hipStreamSynchronize");
+           })
+}

@@ -284,6 +284,19 @@ EvaluationKey<uint32_t>::EvaluationKey(const NPInfo &np, int beta, int degree)
   }
 }
 
+Plaintext<uint32_t>::Plaintext(const NPInfo &np, int degree) : np_(np) {
+  mx_.resize(static_cast<size_t>(np.GetNumTotal()) * degree);
+}
+
+// EvkMap.cpp: GetRotationKey asserts the key exists
+const EvaluationKey<uint32_t> &EvkMap<uint32_t>::GetRotationKey(
+    int rot_idx) const {
+  auto it = find(rot_idx);
+  AssertTrue(it != end(),
+             "EvkMap: rotation key " + std::to_string(rot_idx) + " not found");
+  return it->second;
+}
+
 // ------------------------------------------------------------ NTTHandler --
 NTTHandler<uint32_t>::NTTHandler(const Parameter<word> &param)
     : param_(param), chain_(param.log_degree_, param.ChainPrimes()) {}
@@ -539,6 +552,63 @@ void ElementWiseHandler<uint32_t>::Permute(
                   CurrentStream()));
 }
 
+// ElementWise.cu:1002-1110 (PermuteAccumWorker): one launch per
+// CHD_MAX_ACCUM sources; later launches add onto dst
+void ElementWiseHandler<uint32_t>::PermuteAccum(
+    std::vector<DvView<word>> &dst, const NPInfo &np,
+    const std::vector<int> &permute_amounts,
+    const std::vector<std::vector<DvConstView<word>>> &srcs) const {
+  const int num_poly = static_cast<int>(dst.size());
+  const int num_accum = static_cast<int>(permute_amounts.size());
+  const bool has_extra_ct = static_cast<int>(srcs.size()) == num_accum + 1;
+  AssertTrue(num_poly > 0 && num_poly <= CHD_MAX_POLY,
+             "PermuteAccum: Invalid number of polynomials");
+  AssertTrue(num_accum == static_cast<int>(srcs.size()) || has_extra_ct,
+             "PermuteAccum: Incompatible srcs/permute_amounts size");
+  AssertTrue(num_accum > 0 || has_extra_ct,
+             "PermuteAccum: nothing to accumulate");
+  const int n = param_.degree_;
+  const int q_size = np.GetNumQ() * n;
+  for (auto &d : dst)
+    AssertTrue(d.TotalSize() == np.GetNumTotal() * n,
+               "PermuteAccum: NP mismatch");
+  for (auto &s : srcs)
+    AssertTrue(static_cast<int>(s.size()) == num_poly,
+               "PermuteAccum: Incompatible dst/src size");
+  chd_limb_map m = NoSkipMap(param_, np);
+  std::vector<uint32_t *> dptr(num_poly);
+  std::vector<const uint32_t *> s0(num_poly);
+  for (int p = 0; p < num_poly; p++) dptr[p] = dst[p].data();
+  bool use_s0 = has_extra_ct;
+  long long s0_gap = 0;
+  if (has_extra_ct) {
+    for (int p = 0; p < num_poly; p++) s0[p] = srcs.back()[p].data();
+    s0_gap = srcs.back()[0].QSize() - q_size;
+  }
+  // a source that aliases dst would be read after other blocks wrote it
+  for (int j = 0; j < num_accum; j++)
+    for (int p = 0; p < num_poly; p++)
+      AssertTrue(srcs[j][p].data() != dptr[p] || permute_amounts[j] == 0,
+                 "PermuteAccum: a permuted source cannot alias dst");
+  int base = 0;
+  do {
+    const int cnt = std::min(CHD_MAX_ACCUM, num_accum - base);
+    chd_perm_src s[CHD_MAX_ACCUM] = {};
+    for (int j = 0; j < cnt; j++) {
+      for (int p = 0; p < num_poly; p++) s[j].src[p] = srcs[base + j][p].data();
+      s[j].src_gap = srcs[base + j][0].QSize() - q_size;
+      s[j].galois = PermuteAmountToGaloisFactor(permute_amounts[base + j]);
+    }
+    K(chd_k_permute_accum(&ntt_.Tables(), &m, dptr.data(), num_poly,
+                          use_s0 ? s0.data() : nullptr, s0_gap, s, cnt,
+                          np.GetNumTotal(), CurrentStream()));
+    for (int p = 0; p < num_poly; p++) s0[p] = dptr[p];
+    s0_gap = 0;
+    use_s0 = true;
+    base += cnt;
+  } while (base < num_accum);
+}
+
 // ----------------------------------------------------- ModSwitchHandler --
 // src/core/ModSwitch.cu:175-318, no terminal primes
 ModSwitchHandler<uint32_t>::ModSwitchHandler(
@@ -756,6 +826,25 @@ void ModSwitchHandler<uint32_t>::ModUp(std::vector<DvView<word>> &dst,
   }
 }
 
+// src/core/ModSwitch.cu:414-428 (MultConst by p_prod)
+void ModSwitchHandler<uint32_t>::PseudoModUp(
+    DvView<word> &dst, const DvConstView<word> &src,
+    const DvConstView<word> &p_prod) const {
+  const NPInfo np = param_.LevelToNP(level_, 0);
+  const int num_q = np.GetNumQ();
+  const int n = param_.degree_;
+  AssertTrue(src.TotalSize() == num_q * n, "PseudoModUp src size mismatch");
+  AssertTrue(dst.TotalSize() == num_q * n, "PseudoModUp dst size mismatch");
+  AssertTrue(p_prod.TotalSize() == num_q, "PseudoModUp p_prod size mismatch");
+  chd_limb_map m = NoSkipMap(param_, np);
+  chd_accum_src s = {};
+  s.src[0] = src.data();
+  s.common = p_prod.data();
+  word *d = dst.data();
+  K(chd_k_cpaccum(&ntt_.Tables(), &m, &d, 1, nullptr, 0, &s, 1, 1, num_q,
+                  CurrentStream()));
+}
+
 void ModSwitchHandler<uint32_t>::ModDown(DvView<word> &dst,
                                          const DvConstView<word> &src) const {
   const int n = param_.degree_;
@@ -900,8 +989,12 @@ Context<uint32_t>::Context(const Parameter<word> &param)
     const size_t t = lq + param_.alpha_;
     const size_t beta = DivCeil(top.num_main_ + param_.GetMaxNumTer(),
                                 param_.alpha_);
-    const size_t limbs = 3 * lq + 2 * t +
+    const size_t hmult = 3 * lq + 2 * t +
                          std::max(beta * t + lq, 2 * (param_.alpha_ + 2) + 2 * lq);
+    // the hoisted giant step holds three extended pairs and a ModDown
+    // output while a key switch runs (Hoist.cu:939-957)
+    const size_t hoist = 6 * t + lq + beta * t + lq + 2 * (param_.alpha_ + 2);
+    const size_t limbs = std::max(hmult, hoist);
     ws_.reset(new Workspace(limbs * param_.degree_));
   }
   mod_switch_handlers_.reserve(param_.max_level_ + 1);
@@ -959,11 +1052,18 @@ void Context<uint32_t>::KeyMultTensorV(int level, word *acc_b, word *acc_a,
   KeyAccumulate(level, acc_b, acc_a, nullptr, nullptr, nullptr, &a, &b, key);
 }
 
+void Context<uint32_t>::KeyMultExtV(int level, word *acc_b, word *acc_a,
+                                    const word *d, const word *add_b,
+                                    const EvkRef &key) const {
+  KeyAccumulate(level, acc_b, acc_a, d, nullptr, nullptr, nullptr, nullptr,
+                key, add_b);
+}
+
 void Context<uint32_t>::KeyAccumulate(int level, word *acc_b, word *acc_a,
                                       const word *d, const word *cb,
                                       const word *ca, const CtCRef *ta,
-                                      const CtCRef *tb,
-                                      const EvkRef &key) const {
+                                      const CtCRef *tb, const EvkRef &key,
+                                      const word *add_b) const {
   const NPInfo a_np = param_.LevelToNP(level);
   const int n = param_.degree_;
   const int num_q = a_np.GetNumQ();
@@ -1007,6 +1107,7 @@ void Context<uint32_t>::KeyAccumulate(int level, word *acc_b, word *acc_a,
   k.ca = ca;
   k.acc_b = acc_b;
   k.acc_a = acc_a;
+  k.add_b = add_b;
   if (tensor) {
     k.d = nullptr;
     k.cb = nullptr;
@@ -1231,6 +1332,253 @@ void Context<uint32_t>::HRot(Ct &res, const Ct &a, const Evk &rot_key,
   }
   MultKey(tmp, a, rot_key);
   Permute(res, tmp, r);
+}
+
+Context<uint32_t>::EvkRef Context<uint32_t>::RefOfKey(const Evk &k) {
+  return RefOf(k);
+}
+
+// ---------------------------------------------------------- HoistHandler --
+// src/extension/Hoist.cu:131-177 (CompilePlaintexts / ExtractBSIndices on
+// already encoded plaintexts)
+HoistHandler<uint32_t>::HoistHandler(ConstContextPtr<word> context,
+                                     PtMap &&encoded, int pt_level,
+                                     double pt_scale)
+    : pt_level_(pt_level), pt_scale_(pt_scale), pt_map_(std::move(encoded)) {
+  AssertTrue(!pt_map_.empty(), "Hoist: hoist_map should not be empty");
+  const Parameter<word> &param = context->param_;
+  const NPInfo np = param.LevelToNP(pt_level_, param.alpha_);
+  for (const auto &[gs, bs_map] : pt_map_) {
+    AssertTrue(!bs_map.empty(), "Hoist: empty baby-step map");
+    AssertTrue(gs >= 0 && gs < param.degree_ / 2, "Hoist: invalid giant step");
+    gs_indices_.push_back(gs);
+    for (const auto &[bs, pt] : bs_map) {
+      AssertTrue(bs >= 0 && bs < param.degree_ / 2,
+                 "Hoist: invalid baby step");
+      AssertTrue(pt.GetNP() == np && pt.mx_.size() ==
+                     static_cast<size_t>(np.GetNumTotal()) * param.degree_,
+                 "Hoist: plaintexts must hold pt_level's q primes and alpha "
+                 "aux primes");
+      bs_indices_.insert(bs);
+    }
+  }
+  AssertTrue(gs_indices_.size() == 1 || gs_indices_.front() == 0,
+             "Hoist: a giant step 0 is required with several giant steps");
+  AssertTrue(!(bs_indices_.size() == 1 && *bs_indices_.begin() == 0),
+             "Hoist: maps with only baby step 0 (the reference's bs == 1 "
+             "path) are not supported by this build");
+  AssertTrue(bs_indices_.size() <= 64, "Hoist: too many baby steps");
+}
+
+std::set<int> HoistHandler<uint32_t>::RequiredRotations() const {
+  std::set<int> r;
+  for (int b : bs_indices_)
+    if (b != 0) r.insert(b);
+  for (int g : gs_indices_)
+    if (g != 0) r.insert(g);
+  return r;
+}
+
+void HoistHandler<uint32_t>::Evaluate(ConstContextPtr<word> context, Ct &res,
+                                      const Ct &input,
+                                      const EvkMap<word> &evk_map) const {
+  std::map<int, Ct> bs;
+  EvaluateBabyStep(context, bs, input, evk_map);
+  EvaluateGiantStep(context, res, bs, evk_map);
+}
+
+// src/extension/Hoist.cu:578-691 (hoisted path with BSFusedKeyMult): one
+// ModUp of a, then every baby step's key multiply, the PseudoModUp of b and
+// the automorphism in one fused launch per CHD_MAX_BS rotations. Results stay
+// in the extended basis (q and alpha aux limbs), not divided by P.
+void HoistHandler<uint32_t>::EvaluateBabyStep(
+    ConstContextPtr<word> context, std::map<int, Ct> &bs, const Ct &input,
+    const EvkMap<word> &evk_map) const {
+  BabyStep(*context, bs, input, [&](int r) {
+    return Context<word>::RefOfKey(evk_map.GetRotationKey(r));
+  });
+}
+
+void HoistHandler<uint32_t>::EvaluateGiantStep(
+    ConstContextPtr<word> context, Ct &res, const std::map<int, Ct> &bs,
+    const EvkMap<word> &evk_map) const {
+  GiantStep(*context, res, bs, [&](int r) {
+    return Context<word>::RefOfKey(evk_map.GetRotationKey(r));
+  });
+}
+
+void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
+                                      std::map<int, Ct> &bs, const Ct &input,
+                                      const KeyLookup &key_of) const {
+  const Parameter<word> &param = ctx.param_;
+  const int n = param.degree_;
+  const NPInfo in_np = input.GetNP();
+  AssertTrue(in_np == param.LevelToNP(pt_level_),
+             "Hoist: input level mismatch");
+  AssertTrue(!input.HasRx(), "Hoist: input should be relinearized");
+  AssertTrue(bs.empty(), "Hoist: bs should be empty");
+  const int num_q = in_np.GetNumQ();
+  const int alpha = param.alpha_;
+  const int total = num_q + alpha;
+  const NPInfo ext_np(in_np.num_main_, in_np.num_ter_, alpha);
+  const auto &ms = ctx.mod_switch_handlers_.at(pt_level_);
+  const int beta = ms.GetBeta();
+  AssertTrue(beta <= CHD_MAX_BS_GROUPS, "Hoist: dnum too large");
+  const DvConstView<word> p_prod = ctx.PProd(in_np);
+  Workspace *ws = ctx.GetWorkspace();
+  Workspace::Use use_ws(ws);
+  // 1. ModUp of a, all groups (own limbs are read from a by the kernel)
+  const long long gs = static_cast<long long>(total) * n;
+  Scratch buf(ws, static_cast<size_t>(beta) * gs + static_cast<size_t>(num_q) * n);
+  ms.ModUpGroups(buf.data(), gs, input.ax_.ConstView(), buf.data() + beta * gs,
+                 true);
+  // 2. baby step 0: the PseudoModUp of (b, a), zero on the aux limbs
+  if (bs_indices_.count(0) != 0) {
+    Ct &b0 = bs.try_emplace(0, ext_np).first->second;
+    b0.SetScale(input.GetScale());
+    b0.SetNumSlots(input.GetNumSlots());
+    for (DeviceVector<word> *v : {&b0.bx_, &b0.ax_}) {
+      DvView<word> q_part(v->data(), num_q * n, 0);
+      const DeviceVector<word> &src = v == &b0.bx_ ? input.bx_ : input.ax_;
+      ms.PseudoModUp(q_part, src.ConstView(), p_prod);
+      K(chd_k_zero(v->data() + static_cast<size_t>(num_q) * n,
+                   static_cast<long long>(alpha) * n, CurrentStream()));
+    }
+  }
+  // 3. the other baby steps, CHD_MAX_BS per fused launch
+  std::vector<int> rots;
+  for (int b : bs_indices_)
+    if (b != 0) rots.push_back(b);
+  const int prime_offset = param.GetMaxNumTer() - in_np.num_ter_;
+  chd_limb_map m{};
+  m.num_q = num_q;
+  m.skip_lo = INT_MAX;
+  m.tab_off = param.TerLeft(ext_np);
+  m.tab_gap = param.MainLeft(ext_np);
+  for (size_t base = 0; base < rots.size(); base += CHD_MAX_BS) {
+    chd_bs_args a{};
+    a.num_q = num_q;
+    a.alpha = alpha;
+    a.beta = beta;
+    a.modup = buf.data();
+    a.group_stride = gs;
+    a.d = input.ax_.data();
+    a.ct_b = input.bx_.data();
+    a.p_prod = p_prod.data();
+    const int cnt = static_cast<int>(std::min<size_t>(CHD_MAX_BS, rots.size() - base));
+    a.num_rot = cnt;
+    for (int k = 0; k < cnt; k++) {
+      const int r = rots[base + k];
+      const Context<word>::EvkRef key = key_of(r);
+      AssertTrue(static_cast<int>(key.bx.size()) >= beta &&
+                     key.bx.size() == key.ax.size() &&
+                     key.np.num_aux_ == alpha,
+                 "Hoist: rotation key shape mismatch");
+      const long long key_gap =
+          static_cast<long long>(key.np.GetNumQ() - prime_offset - num_q) * n;
+      AssertTrue(key_gap >= 0, "Hoist: key level below the input level");
+      if (k == 0)
+        a.key_gap = key_gap;
+      else
+        AssertTrue(a.key_gap == key_gap, "Hoist: keys of different levels");
+      for (int g = 0; g < beta; g++) {
+        a.kb[k][g] = key.bx[g] + static_cast<size_t>(prime_offset) * n;
+        a.ka[k][g] = key.ax[g] + static_cast<size_t>(prime_offset) * n;
+      }
+      // scatter with the inverse automorphism (Hoist.cu:290-300)
+      a.galois[k] = static_cast<uint32_t>(param.GetGaloisFactor(n / 2 - r));
+      Ct &out = bs.try_emplace(r, ext_np).first->second;
+      out.SetScale(input.GetScale());
+      out.SetNumSlots(input.GetNumSlots());
+      a.dst_b[k] = out.bx_.data();
+      a.dst_a[k] = out.ax_.data();
+    }
+    K(chd_k_bs_fused(&ctx.ntt_handler_.Tables(), &m, &a, CurrentStream()));
+  }
+}
+
+// src/extension/Hoist.cu:840-975 (EvaluateGiantStepOptimized) and 487-515
+// (EvaluateFinalModDown). For every giant step g != 0 the accumulator's a is
+// brought down to Q, re-raised and key-multiplied, its b added, and the
+// result permuted into the running sum; the b-parts of Hoist.cu's final
+// PermuteAccum are folded into the same permuted sum (Permute is linear).
+void HoistHandler<uint32_t>::GiantStep(const Context<word> &ctx, Ct &res,
+                                       const std::map<int, Ct> &bs,
+                                       const KeyLookup &key_of) const {
+  const Parameter<word> &param = ctx.param_;
+  const int n = param.degree_;
+  AssertTrue(!bs.empty(), "Hoist: bs should not be empty");
+  const Ct &ref = bs.begin()->second;
+  const NPInfo ext_np = ref.GetNP();
+  const int alpha = param.alpha_;
+  AssertTrue(ext_np.num_aux_ == alpha, "Hoist: baby steps must be extended");
+  AssertTrue(param.NPToLevel(NPInfo(ext_np.num_main_, ext_np.num_ter_, 0)) ==
+                 pt_level_,
+             "Hoist: baby-step level mismatch");
+  const int num_q = ext_np.GetNumQ();
+  const int total = num_q + alpha;
+  const size_t tw = static_cast<size_t>(total) * n;
+  const double input_scale = ref.GetScale();
+  int num_slots = ref.GetNumSlots();
+  for (const auto &[g, pmap] : pt_map_)
+    for (const auto &[b, pt] : pmap) {
+      AssertTrue(bs.count(b) != 0, "Hoist: missing baby step");
+      num_slots = std::max({num_slots, pt.GetNumSlots(),
+                            bs.at(b).GetNumSlots()});
+    }
+  const auto &ms = ctx.mod_switch_handlers_.at(pt_level_);
+  Workspace *ws = ctx.GetWorkspace();
+  Workspace::Use use_ws(ws);
+  // final accumulator (giant step 0's plaintext products) and one temporary
+  Scratch fin(ws, 2 * tw), acc(ws, 2 * tw), tmp(ws, 2 * tw), down(ws, static_cast<size_t>(num_q) * n);
+  auto pt_accum = [&](word *dst, const std::map<int, Pt> &pmap) {
+    // PAccum of Hoist.cu:448-485 over q + alpha limbs
+    std::vector<DvView<word>> d{DvView<word>(dst, static_cast<int>(tw), alpha * n),
+                                DvView<word>(dst + tw, static_cast<int>(tw), alpha * n)};
+    std::vector<std::vector<DvConstView<word>>> cts;
+    std::vector<DvConstView<word>> pts;
+    for (const auto &[b, pt] : pmap) {
+      const Ct &ct = bs.at(b);
+      cts.push_back({DvConstView<word>(ct.bx_.data(), static_cast<int>(tw), alpha * n),
+                     DvConstView<word>(ct.ax_.data(), static_cast<int>(tw), alpha * n)});
+      pts.push_back(DvConstView<word>(pt.mx_.data(), static_cast<int>(tw), alpha * n));
+    }
+    ctx.elem_handler_.PAccum(d, ext_np, cts, pts);
+  };
+  chd_limb_map m = NoSkipMap(param, ext_np);
+  bool first = true;
+  for (const auto &[g, pmap] : pt_map_) {
+    if (g == 0) {
+      pt_accum(fin.data(), pmap);
+      first = false;
+      continue;
+    }
+    // accumulator of this giant step, then its key switch without ModDown
+    pt_accum(acc.data(), pmap);
+    ms.ModDownMulti({down.data()}, acc.data() + tw, 0,
+                    ModSwitchHandler<word>::Kind::ModDown);
+    ctx.KeyMultExtV(pt_level_, tmp.data(), tmp.data() + tw, down.data(),
+                    acc.data(), key_of(g));
+    // fin (+)= Permute(tmp, g)
+    chd_perm_src s = {};
+    s.src[0] = tmp.data();
+    s.src[1] = tmp.data() + tw;
+    s.galois = ctx.elem_handler_.PermuteAmountToGaloisFactor(g);
+    word *dp[2] = {fin.data(), fin.data() + tw};
+    const word *s0[2] = {fin.data(), fin.data() + tw};
+    K(chd_k_permute_accum(&ctx.ntt_handler_.Tables(), &m, dp, 2,
+                          first ? nullptr : s0, 0, &s, 1, total,
+                          CurrentStream()));
+    first = false;
+  }
+  // EvaluateFinalModDown: merged ModDown and rescale of both polynomials
+  Ct out(param.LevelToNP(pt_level_ - 1));
+  ms.ModDownMulti({out.bx_.data(), out.ax_.data()}, fin.data(),
+                  static_cast<long long>(tw),
+                  ModSwitchHandler<word>::Kind::ModDownAndRescale);
+  out.SetNumSlots(num_slots);
+  out.SetScale(pt_scale_ * input_scale / param.GetRescalePrimeProd(pt_level_));
+  res = std::move(out);
 }
 
 }  // namespace cheddar

@@ -19,7 +19,11 @@
 
 #include <cstdint>
 #include <memory>
+#include <functional>
+#include <map>
 #include <mutex>
+#include <set>
+#include <unordered_map>
 #include <stdexcept>
 #include <string>
 #include <utility>
@@ -278,6 +282,44 @@ class EvaluationKey<uint32_t> {
   NPInfo np_;
 };
 
+// Plaintext (include/core/Container.h:226-270): one polynomial mx_ in the
+// NTT domain (Montgomery form), with its primes, scale and slot count.
+template <typename word>
+class Plaintext;
+template <>
+class Plaintext<uint32_t> {
+ public:
+  using word = uint32_t;
+  explicit Plaintext(const NPInfo &np = NPInfo{}, int degree = 1 << 16);
+  DeviceVector<word> mx_;
+  NPInfo GetNP() const { return np_; }
+  int GetNumSlots() const { return num_slots_; }
+  void SetNumSlots(int n) { num_slots_ = n; }
+  double GetScale() const { return scale_; }
+  void SetScale(double s) { scale_ = s; }
+
+ private:
+  NPInfo np_;
+  int num_slots_ = (1 << 16) / 2;
+  double scale_ = 1.0;
+};
+
+// Rotation-key container (include/core/EvkMap.h): evaluation keys by index.
+template <typename word>
+class EvkMap;
+template <>
+class EvkMap<uint32_t>
+    : public std::unordered_map<int, EvaluationKey<uint32_t>> {
+ public:
+  using Base = std::unordered_map<int, EvaluationKey<uint32_t>>;
+  using Base::Base;
+  EvkMap() = default;
+  EvkMap(const EvkMap &) = delete;
+  EvkMap &operator=(const EvkMap &) = delete;
+  EvkMap(EvkMap &&) = default;
+  const EvaluationKey<uint32_t> &GetRotationKey(int rot_idx) const;
+};
+
 template <typename word>
 class NTTHandler;
 template <>
@@ -333,6 +375,12 @@ class ElementWiseHandler<uint32_t> {
                int permute_amount,
                const std::vector<DvConstView<word>> &src1) const;
   uint32_t PermuteAmountToGaloisFactor(int permute_amount) const;
+  // ElementWise.cu:1002-1110: dst = sum_i Permute(srcs[i], amounts[i]), plus
+  // srcs.back() unpermuted when srcs has one entry more than amounts
+  void PermuteAccum(std::vector<DvView<word>> &dst, const NPInfo &np,
+                    const std::vector<int> &permute_amounts,
+                    const std::vector<std::vector<DvConstView<word>>> &srcs)
+      const;
 
  private:
   void CPAccumWorker(bool const_accum, std::vector<DvView<word>> &dst,
@@ -359,6 +407,9 @@ class ModSwitchHandler<uint32_t> {
   void ModDownAndRescale(DvView<word> &dst,
                          const DvConstView<word> &src) const;
   int GetBeta() const { return beta_; }
+  // ModSwitch.cu:414-428: dst = MontMul(src, p_prod) on the q limbs
+  void PseudoModUp(DvView<word> &dst, const DvConstView<word> &src,
+                   const DvConstView<word> &p_prod) const;
 
   // Batched pieces of ModUp used by the fused key switch (no single
   // reference counterpart). ModUpBconv: INTTAndMultConst(centre) of src into
@@ -453,6 +504,14 @@ class Context<uint32_t> {
   void PermuteV(int level, CtRef res, CtCRef a, int galois_amount) const;
   // scratch arena of this context (sized for HMult / HRot at the top level)
   Workspace *GetWorkspace() const { return ws_.get(); }
+  // MultKeyNoModDown of an extended-basis accumulator (Context.cpp:609-643,
+  // as the giant step of Hoist.cu:939-957 uses it): the ModUp of d (q limbs,
+  // level's prime count), multiplied by the key and summed over the dnum
+  // groups, plus add_b (q + alpha limbs) on the b part.
+  void KeyMultExtV(int level, word *acc_b, word *acc_a, const word *d,
+                   const word *add_b, const EvkRef &key) const;
+  static EvkRef RefOfKey(const Evk &k);
+  DvConstView<word> PProd(const NPInfo &np) const { return GetPProd(np); }
 
   const Parameter<word> &param_;
   ElementWiseHandler<word> elem_handler_;
@@ -464,9 +523,66 @@ class Context<uint32_t> {
   DvConstView<word> GetPProd(const NPInfo &np) const;
   void KeyAccumulate(int level, word *acc_b, word *acc_a, const word *d,
                      const word *cb, const word *ca, const CtCRef *ta,
-                     const CtCRef *tb, const EvkRef &key) const;
+                     const CtCRef *tb, const EvkRef &key,
+                     const word *add_b = nullptr) const;
   DeviceVector<word> p_prod_;
   std::unique_ptr<Workspace> ws_;
+};
+
+template <typename word>
+using ConstContextPtr = std::shared_ptr<const Context<word>>;
+
+// Baby-step / giant-step evaluation with double hoisting
+// (include/extension/Hoist.h, src/extension/Hoist.cu), the non-min_ks
+// optimized path: res = Rescale(sum_g Rot_g(sum_b pt[g][b] * Rot_b(input))).
+//
+// The reference's constructor takes complex messages and encodes them at
+// (pt_level, alpha aux primes) (Hoist.cu:131-177). The encoder is not part
+// of this build, so this constructor takes the plaintexts already encoded in
+// that form: mx_ holds num_q(pt_level) + alpha limbs in the NTT domain. The
+// reference's encode-time bs/gs swap for single-giant-step maps therefore
+// does not apply; the map is evaluated as given. A giant step 0 must be
+// present when there are other giant steps (the reference's optimized path
+// reads its accumulator unconditionally).
+template <typename word>
+class HoistHandler;
+template <>
+class HoistHandler<uint32_t> {
+ public:
+  using word = uint32_t;
+  using Ct = Ciphertext<word>;
+  using Pt = Plaintext<word>;
+  using PtMap = std::map<int, std::map<int, Pt>>;  // gs -> bs -> plaintext
+  HoistHandler(ConstContextPtr<word> context, PtMap &&encoded, int pt_level,
+               double pt_scale);
+  HoistHandler(const HoistHandler &) = delete;
+  HoistHandler &operator=(const HoistHandler &) = delete;
+  HoistHandler(HoistHandler &&) = default;
+
+  // rotation keys Evaluate needs (AddRequiredRotations, Hoist.cu:978-995)
+  std::set<int> RequiredRotations() const;
+  void Evaluate(ConstContextPtr<word> context, Ct &res, const Ct &input,
+                const EvkMap<word> &evk_map) const;
+  void EvaluateBabyStep(ConstContextPtr<word> context, std::map<int, Ct> &bs,
+                        const Ct &input, const EvkMap<word> &evk_map) const;
+  void EvaluateGiantStep(ConstContextPtr<word> context, Ct &res,
+                         const std::map<int, Ct> &bs,
+                         const EvkMap<word> &evk_map) const;
+
+  // the same with keys looked up by rotation index through a callback
+  // (used by the C-ABI, whose keys are raw device pointers)
+  using KeyLookup = std::function<Context<word>::EvkRef(int)>;
+  void BabyStep(const Context<word> &ctx, std::map<int, Ct> &bs,
+                const Ct &input, const KeyLookup &key) const;
+  void GiantStep(const Context<word> &ctx, Ct &res,
+                 const std::map<int, Ct> &bs, const KeyLookup &key) const;
+
+ private:
+  int pt_level_;
+  double pt_scale_;
+  PtMap pt_map_;
+  std::set<int> bs_indices_;
+  std::vector<int> gs_indices_;
 };
 
 }  // namespace cheddar

@@ -27,6 +27,7 @@ _c_i32p = ctypes.POINTER(ctypes.c_int32)
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _pp = ctypes.POINTER(ctypes.c_void_p)
+_ip = ctypes.POINTER(ctypes.c_int)
 
 lib = ctypes.CDLL(LIB_PATH)
 _SIGS = {
@@ -62,6 +63,10 @@ _SIGS = {
     "chd_mult_key": (_i, [_vp, _i] + [_vp] * 4 + [_pp, _pp, _i, _vp]),
     "chd_hrot": (_i, [_vp, _i] + [_vp] * 4 + [_pp, _pp, _i, _i, _i, _vp]),
     "chd_permute": (_i, [_vp, _i] + [_vp] * 4 + [_i, _vp]),
+    "chd_hoist_baby_steps": (_i, [_vp, _i, _vp, _vp, _i, _ip, _pp, _pp, _i,
+                                  _ip, _pp, _pp, _i, _vp]),
+    "chd_hoist_evaluate": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _ip, _i, _ip,
+                                _pp, _i, _ip, _pp, _pp, _i, _vp]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
@@ -245,6 +250,37 @@ class Context:
                             ptr(a[0]), ptr(a[1]), ptr_array(evk_b),
                             ptr_array(evk_a), len(evk_b), rot, num_slots,
                             self._s(stream)))
+
+    @staticmethod
+    def _keys(keys):
+        """{rot: (bx groups, ax groups)} -> key_rot, key_bx, key_ax, beta"""
+        rots = sorted(keys)
+        beta = len(keys[rots[0]][0]) if rots else 1
+        kb = [t for r in rots for t in keys[r][0]]
+        ka = [t for r in rots for t in keys[r][1]]
+        return ((ctypes.c_int * max(1, len(rots)))(*rots), ptr_array(kb),
+                ptr_array(ka), len(rots), beta)
+
+    def hoist_baby_steps(self, level, ct, rots, dst, keys, stream=None):
+        """dst[i] = (bx, ax) tensors of num_q(level) + alpha limbs"""
+        kr, kb, ka, nk, beta = self._keys(keys)
+        _check(lib.chd_hoist_baby_steps(
+            self.h, level, ptr(ct[0]), ptr(ct[1]), len(rots),
+            (ctypes.c_int * len(rots))(*rots), ptr_array([d[0] for d in dst]),
+            ptr_array([d[1] for d in dst]), nk, kr, kb, ka, beta,
+            self._s(stream)))
+
+    def hoist_evaluate(self, level, res, ct, gs, bs, pts, keys, stream=None):
+        """pts: {(g, b): tensor of num_q(level) + alpha limbs}"""
+        kr, kb, ka, nk, beta = self._keys(keys)
+        parr = (ctypes.c_void_p * (len(gs) * len(bs)))(*[
+            pts[(g, b)].data_ptr() if (g, b) in pts else None
+            for g in gs for b in bs])
+        _check(lib.chd_hoist_evaluate(
+            self.h, level, ptr(res[0]), ptr(res[1]), ptr(ct[0]), ptr(ct[1]),
+            len(gs), (ctypes.c_int * len(gs))(*gs), len(bs),
+            (ctypes.c_int * len(bs))(*bs), parr, nk, kr, kb, ka, beta,
+            self._s(stream)))
 
     def permute(self, level, res, a, rot, stream=None):
         _check(lib.chd_permute(self.h, level, ptr(res[0]), ptr(res[1]),

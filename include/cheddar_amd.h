@@ -159,6 +159,40 @@ int chd_permute(const chd_context *ctx, int level, uint32_t *res_bx,
                 uint32_t *res_ax, const uint32_t *a_bx, const uint32_t *a_ax,
                 int rot, void *stream);
 
+/* ---------------------------------------------------------------------- */
+/* Hoisted rotations (src/extension/Hoist.cu; include/extension/Hoist.h)   */
+/* ---------------------------------------------------------------------- */
+/* Rotation keys are passed as num_keys entries: key_rot[i] is the rotation
+ * index, key_bx/key_ax[i * key_beta + g] its dnum group g (max-level limbs,
+ * as for chd_hrot). Both calls synchronise the stream before returning.
+ *
+ * HoistHandler::EvaluateBabyStep (Hoist.cu:578-691), hoisted path: for
+ * rotation rots[i] (0 <= r < N/2), (dst_bx[i], dst_ax[i]) gets the baby step
+ * in the extended basis (num_q(level) + alpha limbs, not divided by P):
+ * Permute(KeySwitchNoModDown(ct.ax) + PseudoModUp(ct.bx), r); r = 0 gives
+ * (PseudoModUp(bx), PseudoModUp(ax)) with zero aux limbs. */
+int chd_hoist_baby_steps(const chd_context *ctx, int level,
+                         const uint32_t *ct_bx, const uint32_t *ct_ax,
+                         int num_rot, const int *rots, uint32_t *const *dst_bx,
+                         uint32_t *const *dst_ax, int num_keys,
+                         const int *key_rot, const uint32_t *const *key_bx,
+                         const uint32_t *const *key_ax, int key_beta,
+                         void *stream);
+/* HoistHandler::Evaluate (Hoist.cu:569-576, 840-975, 487-515): baby steps
+ * bs[0..num_bs), giant steps gs[0..num_gs) (gs must contain 0 when
+ * num_gs > 1), plaintexts pt[g * num_bs + b] (num_q(level) + alpha limbs in
+ * the NTT domain, Montgomery form, or NULL when absent);
+ * res (num_q(level - 1) limbs) = ModDownAndRescale(
+ *     sum_g Rot_g(sum_b pt[g][b] * Rot_b(ct))) with double hoisting. */
+int chd_hoist_evaluate(const chd_context *ctx, int level, uint32_t *res_bx,
+                       uint32_t *res_ax, const uint32_t *ct_bx,
+                       const uint32_t *ct_ax, int num_gs, const int *gs,
+                       int num_bs, const int *bs, const uint32_t *const *pt,
+                       int num_keys, const int *key_rot,
+                       const uint32_t *const *key_bx,
+                       const uint32_t *const *key_ax, int key_beta,
+                       void *stream);
+
 #ifdef __cplusplus
 }
 #endif

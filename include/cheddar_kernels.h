@@ -127,7 +127,8 @@ int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
  *                  + MontMul(p_prod[l], c{b,a}[l])   (q limbs only)
  * u_g[l] = d[l] on group g's own limbs, otherwise the forward NTT of the
  * column-pass data in modup (left by chd_k_ntt_fwd_groups). l' = l for q
- * limbs and l + key_gap/N for aux limbs. ca may be NULL (MultKey). */
+ * limbs and l + key_gap/N for aux limbs. ca may be NULL (MultKey); cb NULL
+ * skips the CAccum (a plain PAccum, MultKeyNoModDown of Context.cpp:609-643). */
 typedef struct chd_keyacc_args {
   int num_q;
   int tab_off, tab_gap;
@@ -149,6 +150,9 @@ typedef struct chd_keyacc_args {
    * d = rx = MontMul(a1, a2), cb = bx = MontMul(b1, b2),
    * ca = ax = MontMul(b1 - q + a1, b2 - q + a2) - bx - rx. */
   const uint32_t *b1, *a1, *b2, *a2;
+  /* when set, added to acc_b on every limb (q and aux), unscaled: the
+   * extended-basis b of a giant-step accumulator (Hoist.cu:940-957) */
+  const uint32_t *add_b;
 } chd_keyacc_args;
 int chd_k_modup_keyacc(const chd_tables *t, const chd_keyacc_args *args,
                        void *stream);
@@ -182,6 +186,53 @@ int chd_k_cpaccum(const chd_tables *t, const chd_limb_map *m,
 int chd_k_permute(const chd_limb_map *m, uint32_t *const *dst,
                   const uint32_t *const *src, int num_polys, int num_limbs,
                   uint32_t galois, void *stream);
+
+/* PermuteAccum / PermuteAccumAdd (ElementWise.cu:395-501, 1002-1110):
+ * dst[p] = src0[p] (if given) + sum_j Permute(srcs[j].src[p], galois_j),
+ * modular sums. Aux limbs of src0 / src_j are read src0_gap / src_gap words
+ * further on. galois 1 adds a source unpermuted. dst may alias src0. */
+typedef struct chd_perm_src {
+  const uint32_t *src[CHD_MAX_POLY];
+  uint32_t galois;
+  long long src_gap;
+} chd_perm_src;
+int chd_k_permute_accum(const chd_tables *t, const chd_limb_map *m,
+                        uint32_t *const *dst, int num_polys,
+                        const uint32_t *const *src0, long long src0_gap,
+                        const chd_perm_src *srcs, int num_src, int num_limbs,
+                        void *stream);
+
+/* Hoisted baby step, key multiply + automorphism fused (BSFusedKernel,
+ * src/extension/Hoist.cu:20-78, 207-327). For every rotation k:
+ *   t_b = sum_g u_g * key_k,g.b,  t_a = sum_g u_g * key_k,g.a  (q + alpha
+ *   limbs), t_b += MontMul(ct_b, p_prod) on q limbs (PseudoModUp of b),
+ *   dst_k = Permute((t_b, t_a), galois_k)
+ * where u_g is dnum group g of ModUp(a): modup + g * group_stride, except on
+ * the group's own limbs [g alpha, min((g+1) alpha, num_q)), where it is the
+ * input limb d itself. Keys hold key_gap/N extra q limbs before their aux
+ * limbs. Up to CHD_MAX_BS rotations and CHD_MAX_BS_GROUPS groups. */
+/* dst[0..words) = 0 (words a multiple of 4, dst 16-byte aligned); a kernel,
+ * not a memset node, so the call is safe inside captured graphs */
+int chd_k_zero(uint32_t *dst, long long words, void *stream);
+
+#define CHD_MAX_BS 8
+#define CHD_MAX_BS_GROUPS 4
+typedef struct chd_bs_args {
+  int num_q, alpha, beta, num_rot;
+  const uint32_t *modup;
+  long long group_stride;
+  const uint32_t *d;
+  const uint32_t *ct_b;
+  const uint32_t *p_prod;
+  const uint32_t *kb[CHD_MAX_BS][CHD_MAX_BS_GROUPS];
+  const uint32_t *ka[CHD_MAX_BS][CHD_MAX_BS_GROUPS];
+  long long key_gap;
+  uint32_t galois[CHD_MAX_BS];
+  uint32_t *dst_b[CHD_MAX_BS];
+  uint32_t *dst_a[CHD_MAX_BS];
+} chd_bs_args;
+int chd_k_bs_fused(const chd_tables *t, const chd_limb_map *m,
+                   const chd_bs_args *args, void *stream);
 
 #ifdef __cplusplus
 }

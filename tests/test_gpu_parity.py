@@ -278,3 +278,51 @@ def test_hmult_alternating_streams(chd, ks):
         wb, wa = _orc.hmult(b1, a1, b2, a2, kb, ka, L, 24, main, aux, 16, 1)
         assert np.array_equal(host(res[0]), wb)
         assert np.array_equal(host(res[1]), wa)
+
+
+# ------------------------------------------------------- hoisted rotations ----
+def _rot_keys(r, main, aux, rots, beta=3):
+    return {rot: _evk(r, main, aux, beta) for rot in rots}
+
+
+def test_hoist_baby_steps_config5_level(chd, ks):
+    """config-5 level (L = 20 of a 24-prime chain; keys skip 4 q limbs via
+    the extra gap): every baby step bit-exact against the restatement"""
+    import hoist_ref
+    param, ctx, main, aux = ks
+    L = 20
+    r = rng(500)
+    b, a = uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L])
+    rots = [0, 1, 2, 5, 27, 28, 29, 30, 31, 32]  # 9 non-zero: two launches
+    keys = _rot_keys(r, main, aux, [x for x in rots if x])
+    dkeys = {k: ([dev(x) for x in v[0]], [dev(x) for x in v[1]])
+             for k, v in keys.items()}
+    dst = [(zeros(L + 8, N), zeros(L + 8, N)) for _ in rots]
+    ctx.hoist_baby_steps(L - 1, (dev(b), dev(a)), rots, dst, dkeys)
+    modup = _orc.mod_up(a, main[:L], aux, 16)
+    for rot, (db, da) in zip(rots, dst):
+        wb, wa = hoist_ref.baby_step(b, a, keys.get(rot), rot, L, 24, main,
+                                     aux, 16, modup)
+        assert np.array_equal(host(db), wb), "rot %d b" % rot
+        assert np.array_equal(host(da), wa), "rot %d a" % rot
+
+
+def test_hoist_evaluate_config5_level(chd, ks):
+    """double-hoisted BSGS with 4 baby and 3 giant steps at L = 20"""
+    import hoist_ref
+    param, ctx, main, aux = ks
+    L = 20
+    r = rng(510)
+    b, a = uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L])
+    bsi, gsi = [0, 1, 2, 3], [0, 4, 8]
+    pts = {(g, s): uniform_limbs(r, main[:L] + aux) for g in gsi for s in bsi
+           if (g, s) != (8, 3)}  # one absent plaintext
+    keys = _rot_keys(r, main, aux, [1, 2, 3, 4, 8])
+    dkeys = {k: ([dev(x) for x in v[0]], [dev(x) for x in v[1]])
+             for k, v in keys.items()}
+    res = (zeros(L - 1, N), zeros(L - 1, N))
+    ctx.hoist_evaluate(L - 1, res, (dev(b), dev(a)), gsi, bsi,
+                       {k: dev(v) for k, v in pts.items()}, dkeys)
+    wb, wa = hoist_ref.evaluate(b, a, pts, keys, L, 24, main, aux, 16)
+    assert np.array_equal(host(res[0]), wb)
+    assert np.array_equal(host(res[1]), wa)

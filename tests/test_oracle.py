@@ -453,3 +453,73 @@ def test_hrot_decrypts(sem):
     dec = keys.decrypt(rb, ra, L)
     want = ck.automorphism(m, g)
     assert max(abs(d - int(w)) for d, w in zip(dec, want)) < 1 << 12
+
+
+# --------------------------------------------------------------------------
+# hoisted rotations (src/extension/Hoist.cu), restated in tests/hoist_ref.py
+# --------------------------------------------------------------------------
+def test_hoisted_baby_step_moddown_is_hrot(sem):
+    """ModDown of an extended-basis baby step is exactly HRot: the key
+    switch is the same, PseudoModUp(b) = P b contributes b after the
+    division by P, and the automorphism commutes with ModDown."""
+    import hoist_ref
+    keys, _, _, max_q = sem
+    L = 5
+    r = rng(95)
+    b, a = keys.uniform(keys.q[:L]), keys.uniform(keys.q[:L])
+    primes = keys.q[:L] + keys.p
+    for rot in (1, 7):
+        g = _orc.lib.orc_galois_factor(rot, LOG_N_SEM)
+        kb, ka = keys.rot_key(g, max_q)
+        sb, sa = hoist_ref.baby_step(b, a, (kb, ka), rot, L, max_q, keys.q,
+                                     keys.p, LOG_N_SEM)
+        hb, ha = _orc.hrot(b, a, kb, ka, L, max_q, keys.q, keys.p, LOG_N_SEM,
+                           rot)
+        assert np.array_equal(_orc.mod_down(sb, primes, L, LOG_N_SEM), hb)
+        assert np.array_equal(_orc.mod_down(sa, primes, L, LOG_N_SEM), ha)
+    # rotation 0: PseudoModUp of both parts, divided by P gives the input
+    sb, sa = hoist_ref.baby_step(b, a, None, 0, L, max_q, keys.q, keys.p,
+                                 LOG_N_SEM)
+    assert np.array_equal(_orc.mod_down(sb, primes, L, LOG_N_SEM), b)
+    assert np.array_equal(_orc.mod_down(sa, primes, L, LOG_N_SEM), a)
+    assert not sb[L:].any() and not sa[L:].any()
+
+
+def test_hoisted_bsgs_decrypts(sem):
+    """sum_g Rot_g(sum_b pt[g,b] * Rot_b(m)), rescaled, decrypts to the
+    plaintext-domain result under the known secret."""
+    import hoist_ref
+    keys, _, _, max_q = sem
+    L = 6
+    n = keys.n
+    r = rng(96)
+    m = [int(v) for v in r.integers(-4, 5, n) * (1 << 30)]
+    b, a = keys.encrypt(m, L)
+    primes = keys.q[:L] + keys.p
+    bsi, gsi = (0, 1, 2), (0, 3)
+    pts, pt_coef = {}, {}
+    for g in gsi:
+        for s in bsi:
+            c = [int(v) for v in r.integers(-2, 3, n)]
+            pt_coef[(g, s)] = c
+            pts[(g, s)] = keys.ntt_of(c, primes)
+    rot_keys = {}
+    for rot in (1, 2, 3):
+        rot_keys[rot] = keys.rot_key(_orc.lib.orc_galois_factor(rot, LOG_N_SEM),
+                                     max_q)
+    rb, ra = hoist_ref.evaluate(b, a, pts, rot_keys, L, max_q, keys.q, keys.p,
+                                LOG_N_SEM)
+    dec = keys.decrypt(rb, ra, L - 1)
+    want = np.zeros(n, dtype=object)
+    for g in gsi:
+        inner = np.zeros(n, dtype=object)
+        for s in bsi:
+            gs_ = _orc.lib.orc_galois_factor(s, LOG_N_SEM)
+            inner = inner + ck.negacyclic_mul(pt_coef[(g, s)],
+                                              ck.automorphism(m, gs_))
+        want = want + ck.automorphism(list(inner),
+                                      _orc.lib.orc_galois_factor(g, LOG_N_SEM))
+    qt = keys.q[L - 1]
+    err = max(abs(d - int(w) / qt) for d, w in zip(dec, want))
+    assert max(abs(int(w)) for w in want) / qt > 1 << 6  # the check is not vacuous
+    assert err < 64
