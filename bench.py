@@ -10,8 +10,9 @@ larger than the 256 MB MALL so the timed traffic comes from HBM.
 The same JSON line carries the other two parts of the metric: the HMult
 key-switch time at config 4 (L = 24, dnum = 3, alpha = 8, merged
 ModDown+Rescale) and the config-3 BConv time, both measured with HIP events,
-plus the roofline of the NTT and the CPU baseline (the oracle's scalar
-Montgomery NTT on this host, bounded sample).
+the time of a config-5-shaped hoisted BSGS linear transform, plus the
+roofline of the NTT and the CPU baseline (the oracle's scalar Montgomery NTT
+on this host, bounded sample).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -43,7 +44,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU-baseline leg")
     ap.add_argument("--only", choices=["ntt_fwd", "ntt_inv", "hmult",
-                                       "bconv", "copy"],
+                                       "bconv", "copy", "hoist"],
                     help="run only this workload's timed loop (for "
                          "profiling); prints its average time")
     return ap.parse_args()
@@ -134,6 +135,43 @@ def bench_hmult(chd, iters=20):
     return event_time_ms(run, iters, stream) / iters
 
 
+def bench_hoist(chd, iters=5):
+    """config 5's shape: a 768 x 768 BSGS linear transform (28 baby steps,
+    28 giant steps, 768 diagonal plaintexts) on one ciphertext at L = 20 of
+    the config-4 chain, double hoisting. Residues are synthetic uniform
+    values below every prime (the plaintexts are not encoder output)."""
+    import torch
+    from chd_primes import ntt_primes
+    main, aux = ntt_primes(30, 24), ntt_primes(31, 8)
+    param = chd.Param(main, aux, [(i, 0) for i in range(1, 25)])
+    ctx = chd.Context(param)
+    L, level = 20, 19
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0xC0FFEE05)
+
+    def limbs(n):
+        return torch.randint(0, 1 << 29, (n, N), dtype=torch.int32,
+                             device="cuda", generator=gen)
+    bs = list(range(28))
+    gs = [28 * k for k in range(28)]
+    pts = {(g, b): limbs(L + 8) for g in gs for b in bs if g + b < 768}
+    rots = sorted(set(bs[1:] + gs[1:]))
+    keys = {r: ([limbs(32) for _ in range(3)], [limbs(32) for _ in range(3)])
+            for r in rots}
+    h = chd.Hoist(ctx, level, gs, bs, pts)
+    del pts
+    ct = (limbs(L), limbs(L))
+    res = (torch.empty(L - 1, N, dtype=torch.int32, device="cuda"),
+           torch.empty(L - 1, N, dtype=torch.int32, device="cuda"))
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    for _ in range(2):
+        h.run(res, ct, keys, stream=sp)
+    torch.cuda.synchronize()
+    return event_time_ms(lambda i: h.run(res, ct, keys, stream=sp), iters,
+                         stream) / iters
+
+
 def bench_bconv(chd, iters=50):
     import numpy as np
     import torch
@@ -194,6 +232,8 @@ def run_only(chd, what, steps):
         return bench_hmult(chd, steps) * 1e3
     if what == "bconv":
         return bench_bconv(chd, steps) * 1e3
+    if what == "hoist":
+        return bench_hoist(chd, steps) * 1e3
     if what == "copy":
         # plain device copy of COPY_BYTES: the reference point that scales
         # the FETCH_SIZE / WRITE_SIZE counters into HBM bytes
@@ -255,6 +295,7 @@ def main():
     lt = 128 * args.steps / (ms / 1e3)
     hmult_us = bench_hmult(chd) * 1e3
     bconv_us = bench_bconv(chd) * 1e3
+    hoist_ms = bench_hoist(chd)
     fwd_bytes = 64 * LIMB_TRANSFORM_BYTES
     achieved = fwd_bytes / (fwd_ms / 1e3) / 1e9
     line = {
@@ -291,7 +332,12 @@ def main():
             "ntt_inverse_us": inv_ms * 1e3,
             "ntt_forward_warm_mall_us": warm_ms * 1e3,
             "hmult_keyswitch_us_config4": hmult_us,
-            "bconv_us_config3": bconv_us,
+            "bconv_us_config3_warm": bconv_us,
+            "hoist_bsgs_ms_config5_shape": hoist_ms,
+            "notes": "hmult: warm (same key and inputs each step), host "
+                     "enqueue included; hoist: 768x768 BSGS (28 baby, 28 "
+                     "giant steps, 54 rotation keys, 768 plaintexts) at "
+                     "L=20, synthetic plaintexts",
         },
     }
     nsets = max(4, (2 * MALL_BYTES) // (2 * 32 * LIMB_BYTES) + 1)

@@ -310,6 +310,59 @@ __global__ __launch_bounds__(kThreads) void bs_fused_kernel(chd_tables t,
   }
 }
 
+// Hoisted giant step (GSFusedKernel, src/extension/Hoist.cu:80-118): a
+// thread owns 4 coefficients of one limb and the accumulators of every giant
+// step of the launch; each baby step is loaded once and multiplied into all
+// of them (baby steps outer, giant steps inner).
+__global__ __launch_bounds__(kThreads) void gs_fused_kernel(chd_tables t,
+                                                          chd_limb_map m,
+                                                          chd_gs_args a) {
+  const LimbIdx li = limb_of(t, m);
+  const size_t o = (static_cast<size_t>(li.l) << kLogN) +
+                   blockIdx.x * kCoefPerBlock + threadIdx.x * kPerThread;
+  uint32_t rb[CHD_GS_MAX_GS][4], ra[CHD_GS_MAX_GS][4];
+#pragma unroll
+  for (int g = 0; g < CHD_GS_MAX_GS; g++) {
+    if (g < a.num_gs && a.add_to_dst) {
+      const uint4 vb = ld4(a.dst_b[g] + o), va = ld4(a.dst_a[g] + o);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        rb[g][i] = get(vb, i);
+        ra[g][i] = get(va, i);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) rb[g][i] = ra[g][i] = 0;
+    }
+  }
+  for (int b = 0; b < a.num_bs; b++) {
+    const uint4 xb = ld4(a.bs_b[b] + o), xa = ld4(a.bs_a[b] + o);
+#pragma unroll
+    for (int g = 0; g < CHD_GS_MAX_GS; g++) {
+      if (g < a.num_gs && a.pt[g][b] != nullptr) {
+        const uint4 mv = ld4(a.pt[g][b] + o);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int32_t mm = static_cast<int32_t>(get(mv, i));
+          rb[g][i] = add_mod(rb[g][i],
+                             mont_mul(mm, static_cast<int32_t>(get(xb, i)),
+                                      li.q, li.qinv), li.q);
+          ra[g][i] = add_mod(ra[g][i],
+                             mont_mul(mm, static_cast<int32_t>(get(xa, i)),
+                                      li.q, li.qinv), li.q);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < CHD_GS_MAX_GS; g++) {
+    if (g < a.num_gs) {
+      st4(a.dst_b[g] + o, make_uint4(rb[g][0], rb[g][1], rb[g][2], rb[g][3]));
+      st4(a.dst_a[g] + o, make_uint4(ra[g][0], ra[g][1], ra[g][2], ra[g][3]));
+    }
+  }
+}
+
 }  // namespace
 }  // namespace chd
 
@@ -482,4 +535,24 @@ extern "C" int chd_k_zero(uint32_t *dst, long long words, void *stream) {
                      dim3(kThreads), 0, static_cast<hipStream_t>(stream),
                      reinterpret_cast<uint4 *>(dst), n4);
   return check_launch("chd_k_zero");
+}
+
+extern "C" int chd_k_gs_fused(const chd_tables *t, const chd_limb_map *m,
+                              const chd_gs_args *args, int num_limbs,
+                              void *stream) {
+  if (!t || !m || !args || args->num_bs < 1 ||
+      args->num_bs > CHD_GS_MAX_BS || args->num_gs < 1 ||
+      args->num_gs > CHD_GS_MAX_GS || num_limbs < 0 || m->skip_len != 0)
+    return set_error(CHD_ERR_ARG, "chd_k_gs_fused: invalid argument");
+  for (int b = 0; b < args->num_bs; b++)
+    if (!args->bs_b[b] || !args->bs_a[b])
+      return set_error(CHD_ERR_ARG, "chd_k_gs_fused: null baby step");
+  for (int g = 0; g < args->num_gs; g++)
+    if (!args->dst_b[g] || !args->dst_a[g])
+      return set_error(CHD_ERR_ARG, "chd_k_gs_fused: null destination");
+  if (num_limbs == 0) return 0;
+  dim3 g(kN / kCoefPerBlock, num_limbs);
+  hipLaunchKernelGGL(gs_fused_kernel, g, dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), *t, *m, *args);
+  return check_launch("chd_k_gs_fused");
 }

@@ -502,6 +502,91 @@ extern "C" int chd_hoist_baby_steps(
            })
 }
 
+struct chd_hoist {
+  std::shared_ptr<cheddar::Context<word>> c;
+  std::unique_ptr<cheddar::HoistHandler<word>> h;
+  int level;
+  // buffers kept across runs: the input copy, the baby steps, the result
+  cheddar::Ciphertext<word> in, res;
+  std::map<int, cheddar::Ciphertext<word>> babies;
+};
+
+extern "C" int chd_hoist_create(chd_hoist **out, const chd_context *ctx,
+                                int level, int num_gs, const int *gs,
+                                int num_bs, const int *bs,
+                                const uint32_t *const *pt, void *stream) {
+  if (!out || !LevelOk(ctx, level) || level < 1 || num_gs < 1 || !gs ||
+      num_bs < 1 || !bs || !pt)
+    return set_error(CHD_ERR_ARG, "chd_hoist_create: invalid argument");
+  CHD_TRY cheddar::StreamScope scope(static_cast<hipStream_t>(stream));
+  const auto &p = ctx->c->param_;
+  const cheddar::NPInfo np = p.LevelToNP(level, p.alpha_);
+  cheddar::HoistHandler<word>::PtMap pts;
+  for (int g = 0; g < num_gs; g++)
+    for (int b = 0; b < num_bs; b++) {
+      const uint32_t *src = pt[static_cast<size_t>(g) * num_bs + b];
+      if (src == nullptr) continue;
+      auto &pl = pts[gs[g]].try_emplace(bs[b], np, p.degree_).first->second;
+      cheddar::HipCheck(hipMemcpyAsync(pl.mx_.data(), src,
+                                       pl.mx_.size() * sizeof(word),
+                                       hipMemcpyDeviceToDevice,
+                                       cheddar::CurrentStream()),
+                        "hipMemcpyAsync");
+    }
+  std::unique_ptr<chd_hoist> h(new chd_hoist);
+  h->c = ctx->c;
+  h->level = level;
+  h->h.reset(new cheddar::HoistHandler<word>(ctx->c, std::move(pts), level,
+                                             1.0));
+  cheddar::HipCheck(hipStreamSynchronize(cheddar::CurrentStream()),
+                    "hipStreamSynchronize");
+  *out = h.release();
+  return 0;
+  CHD_CATCH("chd_hoist_create")
+}
+
+extern "C" void chd_hoist_destroy(chd_hoist *h) { delete h; }
+
+extern "C" int chd_hoist_run(const chd_hoist *h, uint32_t *res_bx,
+                             uint32_t *res_ax, const uint32_t *ct_bx,
+                             const uint32_t *ct_ax, int num_keys,
+                             const int *key_rot, const uint32_t *const *key_bx,
+                             const uint32_t *const *key_ax, int key_beta,
+                             void *stream) {
+  if (!h || !res_bx || !res_ax || !ct_bx || !ct_ax || num_keys < 0 ||
+      key_beta < 1 || (num_keys > 0 && (!key_rot || !key_bx || !key_ax)))
+    return set_error(CHD_ERR_ARG, "chd_hoist_run: invalid argument");
+  CHD_TRY cheddar::StreamScope scope(static_cast<hipStream_t>(stream));
+  const auto &p = h->c->param_;
+  chd_context view{h->c};
+  const auto keys = Keys(&view, num_keys, key_rot, key_bx, key_ax, key_beta);
+  chd_hoist *m = const_cast<chd_hoist *>(h);  // buffers, not the handler
+  if (!(m->in.GetNP() == p.LevelToNP(h->level)) || m->in.bx_.size() == 0)
+    m->in = cheddar::Ciphertext<word>(p.LevelToNP(h->level));
+  const size_t in_bytes = m->in.bx_.size() * sizeof(word);
+  cheddar::HipCheck(hipMemcpyAsync(m->in.bx_.data(), ct_bx, in_bytes,
+                                   hipMemcpyDeviceToDevice,
+                                   cheddar::CurrentStream()),
+                    "hipMemcpyAsync");
+  cheddar::HipCheck(hipMemcpyAsync(m->in.ax_.data(), ct_ax, in_bytes,
+                                   hipMemcpyDeviceToDevice,
+                                   cheddar::CurrentStream()),
+                    "hipMemcpyAsync");
+  h->h->BabyStep(*h->c, m->babies, m->in, keys);
+  h->h->GiantStep(*h->c, m->res, m->babies, keys);
+  const size_t bytes = m->res.bx_.size() * sizeof(word);
+  cheddar::HipCheck(hipMemcpyAsync(res_bx, m->res.bx_.data(), bytes,
+                                   hipMemcpyDeviceToDevice,
+                                   cheddar::CurrentStream()),
+                    "hipMemcpyAsync");
+  cheddar::HipCheck(hipMemcpyAsync(res_ax, m->res.ax_.data(), bytes,
+                                   hipMemcpyDeviceToDevice,
+                                   cheddar::CurrentStream()),
+                    "hipMemcpyAsync");
+  return chd::check_launch("chd_hoist_run");
+  CHD_CATCH("chd_hoist_run")
+}
+
 extern "C" int chd_hoist_evaluate(
     const chd_context *ctx, int level, uint32_t *res_bx, uint32_t *res_ax,
     const uint32_t *ct_bx, const uint32_t *ct_ax, int num_gs, const int *gs,

@@ -1416,7 +1416,12 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
   AssertTrue(in_np == param.LevelToNP(pt_level_),
              "Hoist: input level mismatch");
   AssertTrue(!input.HasRx(), "Hoist: input should be relinearized");
-  AssertTrue(bs.empty(), "Hoist: bs should be empty");
+  // the reference requires an empty bs; here bs may also hold the baby
+  // steps of an earlier call, whose buffers are reused when their primes
+  // match (no allocation in repeated evaluations)
+  for (const auto &[idx, ct] : bs)
+    AssertTrue(bs_indices_.count(idx) != 0,
+               "Hoist: bs holds a baby step this handler does not use");
   const int num_q = in_np.GetNumQ();
   const int alpha = param.alpha_;
   const int total = num_q + alpha;
@@ -1433,8 +1438,15 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
   ms.ModUpGroups(buf.data(), gs, input.ax_.ConstView(), buf.data() + beta * gs,
                  true);
   // 2. baby step 0: the PseudoModUp of (b, a), zero on the aux limbs
+  auto slot = [&](int idx) -> Ct & {
+    Ct &ct = bs.try_emplace(idx, ext_np).first->second;
+    if (!(ct.GetNP() == ext_np) ||
+        ct.bx_.size() != static_cast<size_t>(total) * n || ct.HasRx())
+      ct = Ct(ext_np);
+    return ct;
+  };
   if (bs_indices_.count(0) != 0) {
-    Ct &b0 = bs.try_emplace(0, ext_np).first->second;
+    Ct &b0 = slot(0);
     b0.SetScale(input.GetScale());
     b0.SetNumSlots(input.GetNumSlots());
     for (DeviceVector<word> *v : {&b0.bx_, &b0.ax_}) {
@@ -1487,7 +1499,7 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
       }
       // scatter with the inverse automorphism (Hoist.cu:290-300)
       a.galois[k] = static_cast<uint32_t>(param.GetGaloisFactor(n / 2 - r));
-      Ct &out = bs.try_emplace(r, ext_np).first->second;
+      Ct &out = slot(r);
       out.SetScale(input.GetScale());
       out.SetNumSlots(input.GetNumSlots());
       a.dst_b[k] = out.bx_.data();
@@ -1529,56 +1541,79 @@ void HoistHandler<uint32_t>::GiantStep(const Context<word> &ctx, Ct &res,
   const auto &ms = ctx.mod_switch_handlers_.at(pt_level_);
   Workspace *ws = ctx.GetWorkspace();
   Workspace::Use use_ws(ws);
-  // final accumulator (giant step 0's plaintext products) and one temporary
-  Scratch fin(ws, 2 * tw), acc(ws, 2 * tw), tmp(ws, 2 * tw), down(ws, static_cast<size_t>(num_q) * n);
-  auto pt_accum = [&](word *dst, const std::map<int, Pt> &pmap) {
-    // PAccum of Hoist.cu:448-485 over q + alpha limbs
-    std::vector<DvView<word>> d{DvView<word>(dst, static_cast<int>(tw), alpha * n),
-                                DvView<word>(dst + tw, static_cast<int>(tw), alpha * n)};
-    std::vector<std::vector<DvConstView<word>>> cts;
-    std::vector<DvConstView<word>> pts;
-    for (const auto &[b, pt] : pmap) {
-      const Ct &ct = bs.at(b);
-      cts.push_back({DvConstView<word>(ct.bx_.data(), static_cast<int>(tw), alpha * n),
-                     DvConstView<word>(ct.ax_.data(), static_cast<int>(tw), alpha * n)});
-      pts.push_back(DvConstView<word>(pt.mx_.data(), static_cast<int>(tw), alpha * n));
-    }
-    ctx.elem_handler_.PAccum(d, ext_np, cts, pts);
-  };
   chd_limb_map m = NoSkipMap(param, ext_np);
-  bool first = true;
-  for (const auto &[g, pmap] : pt_map_) {
-    if (g == 0) {
-      pt_accum(fin.data(), pmap);
-      first = false;
-      continue;
+  // 1. every giant step's plaintext accumulation (GSFusedPAccum,
+  //    Hoist.cu:334-445): one fused launch per CHD_GS_MAX_GS giant steps and
+  //    CHD_GS_MAX_BS baby steps, each baby step read once per launch
+  const int num_gs = static_cast<int>(gs_indices_.size());
+  const std::vector<int> bsv(bs_indices_.begin(), bs_indices_.end());
+  Scratch accs(ws, static_cast<size_t>(num_gs) * 2 * tw);
+  auto acc_b = [&](int gi) { return accs.data() + static_cast<size_t>(gi) * 2 * tw; };
+  for (int g0 = 0; g0 < num_gs; g0 += CHD_GS_MAX_GS) {
+    const int gcnt = std::min(CHD_GS_MAX_GS, num_gs - g0);
+    for (size_t b0 = 0; b0 < bsv.size(); b0 += CHD_GS_MAX_BS) {
+      const int bcnt = static_cast<int>(
+          std::min<size_t>(CHD_GS_MAX_BS, bsv.size() - b0));
+      chd_gs_args a{};
+      a.num_bs = bcnt;
+      a.num_gs = gcnt;
+      a.add_to_dst = b0 > 0 ? 1 : 0;
+      for (int j = 0; j < bcnt; j++) {
+        const Ct &ct = bs.at(bsv[b0 + j]);
+        a.bs_b[j] = ct.bx_.data();
+        a.bs_a[j] = ct.ax_.data();
+      }
+      for (int k = 0; k < gcnt; k++) {
+        const std::map<int, Pt> &pmap = pt_map_.at(gs_indices_[g0 + k]);
+        for (int j = 0; j < bcnt; j++) {
+          auto it = pmap.find(bsv[b0 + j]);
+          a.pt[k][j] = it == pmap.end() ? nullptr : it->second.mx_.data();
+        }
+        a.dst_b[k] = acc_b(g0 + k);
+        a.dst_a[k] = acc_b(g0 + k) + tw;
+      }
+      K(chd_k_gs_fused(&ctx.ntt_handler_.Tables(), &m, &a, total,
+                       CurrentStream()));
     }
-    // accumulator of this giant step, then its key switch without ModDown
-    pt_accum(acc.data(), pmap);
-    ms.ModDownMulti({down.data()}, acc.data() + tw, 0,
+  }
+  // 2. giant-step rotations (EvaluateGiantStepOptimized, Hoist.cu:895-957):
+  //    fin = acc_0 + sum_{g != 0} Permute(KS(ModUp(ModDown(acc_g.a))) with
+  //    acc_g.b added, g)
+  // giant step 0 (the first, indices ascend) accumulates in place
+  const bool has0 = gs_indices_.front() == 0;
+  Scratch fin_buf(ws, has0 ? 0 : 2 * tw), tmp(ws, 2 * tw),
+      down(ws, static_cast<size_t>(num_q) * n);
+  word *const finp = has0 ? acc_b(0) : fin_buf.data();
+  bool first = !has0;
+  for (int gi = has0 ? 1 : 0; gi < num_gs; gi++) {
+    const int g = gs_indices_[gi];
+    ms.ModDownMulti({down.data()}, acc_b(gi) + tw, 0,
                     ModSwitchHandler<word>::Kind::ModDown);
     ctx.KeyMultExtV(pt_level_, tmp.data(), tmp.data() + tw, down.data(),
-                    acc.data(), key_of(g));
-    // fin (+)= Permute(tmp, g)
+                    acc_b(gi), key_of(g));
     chd_perm_src s = {};
     s.src[0] = tmp.data();
     s.src[1] = tmp.data() + tw;
     s.galois = ctx.elem_handler_.PermuteAmountToGaloisFactor(g);
-    word *dp[2] = {fin.data(), fin.data() + tw};
-    const word *s0[2] = {fin.data(), fin.data() + tw};
+    word *dp[2] = {finp, finp + tw};
+    const word *s0[2] = {finp, finp + tw};
     K(chd_k_permute_accum(&ctx.ntt_handler_.Tables(), &m, dp, 2,
                           first ? nullptr : s0, 0, &s, 1, total,
                           CurrentStream()));
     first = false;
   }
-  // EvaluateFinalModDown: merged ModDown and rescale of both polynomials
-  Ct out(param.LevelToNP(pt_level_ - 1));
-  ms.ModDownMulti({out.bx_.data(), out.ax_.data()}, fin.data(),
+  // EvaluateFinalModDown: merged ModDown and rescale of both polynomials,
+  // into res's own buffers when they already have the output's primes
+  const NPInfo out_np = param.LevelToNP(pt_level_ - 1);
+  if (!(res.GetNP() == out_np) ||
+      res.bx_.size() != static_cast<size_t>(out_np.GetNumTotal()) * n ||
+      res.HasRx())
+    res = Ct(out_np);
+  ms.ModDownMulti({res.bx_.data(), res.ax_.data()}, finp,
                   static_cast<long long>(tw),
                   ModSwitchHandler<word>::Kind::ModDownAndRescale);
-  out.SetNumSlots(num_slots);
-  out.SetScale(pt_scale_ * input_scale / param.GetRescalePrimeProd(pt_level_));
-  res = std::move(out);
+  res.SetNumSlots(num_slots);
+  res.SetScale(pt_scale_ * input_scale / param.GetRescalePrimeProd(pt_level_));
 }
 
 }  // namespace cheddar

@@ -67,6 +67,10 @@ _SIGS = {
                                   _ip, _pp, _pp, _i, _vp]),
     "chd_hoist_evaluate": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _ip, _i, _ip,
                                 _pp, _i, _ip, _pp, _pp, _i, _vp]),
+    "chd_hoist_create": (_i, [_pp, _vp, _i, _i, _ip, _i, _ip, _pp, _vp]),
+    "chd_hoist_destroy": (None, [_vp]),
+    "chd_hoist_run": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _ip, _pp, _pp, _i,
+                           _vp]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
@@ -285,3 +289,31 @@ class Context:
     def permute(self, level, res, a, rot, stream=None):
         _check(lib.chd_permute(self.h, level, ptr(res[0]), ptr(res[1]),
                                ptr(a[0]), ptr(a[1]), rot, self._s(stream)))
+
+
+class Hoist:
+    """HoistHandler built once from encoded plaintexts {(g, b): tensor}"""
+
+    def __init__(self, ctx, level, gs, bs, pts, stream=None):
+        self.ctx = ctx
+        h = ctypes.c_void_p()
+        parr = (ctypes.c_void_p * (len(gs) * len(bs)))(*[
+            pts[(g, b)].data_ptr() if (g, b) in pts else None
+            for g in gs for b in bs])
+        _check(lib.chd_hoist_create(
+            ctypes.byref(h), ctx.h, level, len(gs),
+            (ctypes.c_int * len(gs))(*gs), len(bs),
+            (ctypes.c_int * len(bs))(*bs), parr,
+            stream if stream is not None else current_stream()))
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib.chd_hoist_destroy(self.h)
+            self.h = None
+
+    def run(self, res, ct, keys, stream=None):
+        kr, kb, ka, nk, beta = Context._keys(keys)
+        _check(lib.chd_hoist_run(
+            self.h, ptr(res[0]), ptr(res[1]), ptr(ct[0]), ptr(ct[1]), nk, kr,
+            kb, ka, beta, stream if stream is not None else current_stream()))

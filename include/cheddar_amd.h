@@ -178,6 +178,21 @@ int chd_hoist_baby_steps(const chd_context *ctx, int level,
                          const int *key_rot, const uint32_t *const *key_bx,
                          const uint32_t *const *key_ax, int key_beta,
                          void *stream);
+/* A HoistHandler kept across calls (Hoist.h: the handler is built once
+ * from its plaintexts, then evaluated many times): chd_hoist_create copies
+ * the plaintexts (layout as for chd_hoist_evaluate) and synchronises the
+ * stream; chd_hoist_run evaluates one ciphertext at the handler's level,
+ * reusing the handler's baby-step and result buffers (no allocation after
+ * the first run; runs of one handler must not overlap). */
+typedef struct chd_hoist chd_hoist;
+int chd_hoist_create(chd_hoist **out, const chd_context *ctx, int level,
+                     int num_gs, const int *gs, int num_bs, const int *bs,
+                     const uint32_t *const *pt, void *stream);
+void chd_hoist_destroy(chd_hoist *h);
+int chd_hoist_run(const chd_hoist *h, uint32_t *res_bx, uint32_t *res_ax,
+                  const uint32_t *ct_bx, const uint32_t *ct_ax, int num_keys,
+                  const int *key_rot, const uint32_t *const *key_bx,
+                  const uint32_t *const *key_ax, int key_beta, void *stream);
 /* HoistHandler::Evaluate (Hoist.cu:569-576, 840-975, 487-515): baby steps
  * bs[0..num_bs), giant steps gs[0..num_gs) (gs must contain 0 when
  * num_gs > 1), plaintexts pt[g * num_bs + b] (num_q(level) + alpha limbs in

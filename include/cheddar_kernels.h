@@ -215,6 +215,22 @@ int chd_k_permute_accum(const chd_tables *t, const chd_limb_map *m,
  * not a memset node, so the call is safe inside captured graphs */
 int chd_k_zero(uint32_t *dst, long long words, void *stream);
 
+/* Hoisted giant-step plaintext accumulation (GSFusedKernel,
+ * src/extension/Hoist.cu:80-118, 334-445): for every giant step g of the
+ * launch, dst_g = [dst_g +] sum_b MontMul(pt[g][b], bs_b) for both parts,
+ * over num_limbs extended-basis limbs. Each baby step is read once per
+ * launch. pt[g][b] NULL skips the pair. */
+#define CHD_GS_MAX_BS 32
+#define CHD_GS_MAX_GS 8
+typedef struct chd_gs_args {
+  int num_bs, num_gs, add_to_dst;
+  const uint32_t *bs_b[CHD_GS_MAX_BS], *bs_a[CHD_GS_MAX_BS];
+  const uint32_t *pt[CHD_GS_MAX_GS][CHD_GS_MAX_BS];
+  uint32_t *dst_b[CHD_GS_MAX_GS], *dst_a[CHD_GS_MAX_GS];
+} chd_gs_args;
+int chd_k_gs_fused(const chd_tables *t, const chd_limb_map *m,
+                   const chd_gs_args *args, int num_limbs, void *stream);
+
 #define CHD_MAX_BS 8
 #define CHD_MAX_BS_GROUPS 4
 typedef struct chd_bs_args {

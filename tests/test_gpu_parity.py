@@ -308,21 +308,32 @@ def test_hoist_baby_steps_config5_level(chd, ks):
 
 
 def test_hoist_evaluate_config5_level(chd, ks):
-    """double-hoisted BSGS with 4 baby and 3 giant steps at L = 20"""
+    """double-hoisted BSGS at L = 20: 10 baby steps (two fused launches, two
+    accumulation chunks) and 3 giant steps; the one-shot entry point and a
+    handler run twice (buffer reuse) on different ciphertexts"""
     import hoist_ref
     param, ctx, main, aux = ks
     L = 20
     r = rng(510)
-    b, a = uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L])
-    bsi, gsi = [0, 1, 2, 3], [0, 4, 8]
+    bsi, gsi = list(range(10)), [0, 10, 20]
     pts = {(g, s): uniform_limbs(r, main[:L] + aux) for g in gsi for s in bsi
-           if (g, s) != (8, 3)}  # one absent plaintext
-    keys = _rot_keys(r, main, aux, [1, 2, 3, 4, 8])
+           if (g, s) != (20, 9)}  # one absent plaintext
+    keys = _rot_keys(r, main, aux, sorted(set(bsi[1:] + gsi[1:])))
     dkeys = {k: ([dev(x) for x in v[0]], [dev(x) for x in v[1]])
              for k, v in keys.items()}
+    dpts = {k: dev(v) for k, v in pts.items()}
+    cts = [(uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L]))
+           for _ in range(2)]
+    wants = [hoist_ref.evaluate(b, a, pts, keys, L, 24, main, aux, 16)
+             for b, a in cts]
     res = (zeros(L - 1, N), zeros(L - 1, N))
-    ctx.hoist_evaluate(L - 1, res, (dev(b), dev(a)), gsi, bsi,
-                       {k: dev(v) for k, v in pts.items()}, dkeys)
-    wb, wa = hoist_ref.evaluate(b, a, pts, keys, L, 24, main, aux, 16)
-    assert np.array_equal(host(res[0]), wb)
-    assert np.array_equal(host(res[1]), wa)
+    ctx.hoist_evaluate(L - 1, res, (dev(cts[0][0]), dev(cts[0][1])), gsi, bsi,
+                       dpts, dkeys)
+    assert np.array_equal(host(res[0]), wants[0][0])
+    assert np.array_equal(host(res[1]), wants[0][1])
+    h = chd.Hoist(ctx, L - 1, gsi, bsi, dpts)
+    for (b, a), (wb, wa) in zip(cts, wants):
+        out = (zeros(L - 1, N), zeros(L - 1, N))
+        h.run(out, (dev(b), dev(a)), dkeys)
+        assert np.array_equal(host(out[0]), wb)
+        assert np.array_equal(host(out[1]), wa)
