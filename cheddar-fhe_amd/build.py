@@ -34,6 +34,7 @@ SOURCES = [
     ("csrc/elementwise.hip", True),
     ("host/device_tables.cpp", False),
     ("host/cheddar.cpp", False),
+    ("host/encoder.cpp", False),
     ("host/capi.cpp", False),
 ]
 

@@ -636,3 +636,108 @@ extern "C" int chd_hoist_evaluate(
                                "hipStreamSynchronize");
            })
 }
+
+// ------------------------------------------------------------- encoder --
+namespace {
+std::vector<cheddar::Complex> Message(const double *re, const double *im,
+                                      int len) {
+  std::vector<cheddar::Complex> m(len);
+  for (int i = 0; i < len; i++) m[i] = cheddar::Complex(re[i], im[i]);
+  return m;
+}
+bool AuxOk(const Parameter<word> &p, int num_aux) {
+  return num_aux == 0 || num_aux == p.alpha_;
+}
+int PaddedSlots(int len) {
+  int s = 1;
+  while (s < len) s <<= 1;
+  return s;
+}
+}  // namespace
+
+extern "C" int chd_encode(const chd_context *ctx, int level, int num_aux,
+                          double scale, const double *msg_re,
+                          const double *msg_im, int msg_len, uint32_t *dst,
+                          void *stream) {
+  if (!LevelOk(ctx, level) || !AuxOk(ctx->c->param_, num_aux) || !msg_re ||
+      !msg_im || msg_len < 1 || msg_len > ctx->c->param_.degree_ / 2 || !dst)
+    return set_error(CHD_ERR_ARG, "chd_encode: invalid argument");
+  CHD_TRY cheddar::StreamScope scope(static_cast<hipStream_t>(stream));
+  cheddar::Plaintext<word> pt;
+  ctx->c->encoder_.Encode(pt, level, scale, Message(msg_re, msg_im, msg_len),
+                          num_aux);
+  cheddar::HipCheck(hipMemcpyAsync(dst, pt.mx_.data(),
+                                   pt.mx_.size() * sizeof(word),
+                                   hipMemcpyDeviceToDevice,
+                                   cheddar::CurrentStream()),
+                    "hipMemcpyAsync");
+  cheddar::HipCheck(hipStreamSynchronize(cheddar::CurrentStream()),
+                    "hipStreamSynchronize");
+  return pt.GetNumSlots();
+  CHD_CATCH("chd_encode")
+}
+
+extern "C" int chd_encode_constant(const chd_context *ctx, int level,
+                                   int num_aux, double scale, double number,
+                                   uint32_t *dst, void *stream) {
+  CHD_CALL("chd_encode_constant",
+           LevelOk(ctx, level) && AuxOk(ctx->c->param_, num_aux) && dst, {
+             cheddar::Constant<word> c;
+             ctx->c->encoder_.EncodeConstant(c, level, scale, number, num_aux);
+             cheddar::HipCheck(hipMemcpyAsync(dst, c.cx_.data(),
+                                              c.cx_.size() * sizeof(word),
+                                              hipMemcpyDeviceToDevice,
+                                              cheddar::CurrentStream()),
+                               "hipMemcpyAsync");
+             cheddar::HipCheck(
+                 hipStreamSynchronize(cheddar::CurrentStream()),
+                 "hipStreamSynchronize");
+           })
+}
+
+extern "C" int chd_decode(const chd_context *ctx, int level, double scale,
+                          int num_slots, const uint32_t *src, double *out_re,
+                          double *out_im, void *stream) {
+  CHD_CALL("chd_decode",
+           LevelOk(ctx, level) && src && out_re && out_im && num_slots >= 1 &&
+               num_slots <= ctx->c->param_.degree_ / 2 &&
+               PaddedSlots(num_slots) == num_slots,
+           {
+             const auto &p = ctx->c->param_;
+             cheddar::Plaintext<word> pt(p.LevelToNP(level), p.degree_);
+             cheddar::HipCheck(hipMemcpyAsync(pt.mx_.data(), src,
+                                              pt.mx_.size() * sizeof(word),
+                                              hipMemcpyDeviceToDevice,
+                                              cheddar::CurrentStream()),
+                               "hipMemcpyAsync");
+             pt.SetNumSlots(num_slots);
+             pt.SetScale(scale);
+             std::vector<cheddar::Complex> m;
+             ctx->c->encoder_.Decode(m, pt);
+             for (int i = 0; i < num_slots; i++) {
+               out_re[i] = m[i].real();
+               out_im[i] = m[i].imag();
+             }
+           })
+}
+
+extern "C" int chd_encode_coefficients(const chd_param *param, int level,
+                                       int num_aux, double scale,
+                                       const double *msg_re,
+                                       const double *msg_im, int msg_len,
+                                       uint32_t *host_out) {
+  if (!param || level < 0 || level > param->p->max_level_ ||
+      !AuxOk(*param->p, num_aux) || !msg_re || !msg_im || msg_len < 1 ||
+      msg_len > param->p->degree_ / 2 || !host_out)
+    return set_error(CHD_ERR_ARG, "chd_encode_coefficients: invalid argument");
+  CHD_TRY
+  const cheddar::Encoder<word> enc(*param->p);
+  const int slots = PaddedSlots(msg_len);
+  std::vector<cheddar::Complex> m = Message(msg_re, msg_im, msg_len);
+  m.resize(slots);
+  const std::vector<word> r =
+      enc.CoefficientResidues(level, scale, std::move(m), num_aux);
+  std::memcpy(host_out, r.data(), r.size() * sizeof(word));
+  return slots;
+  CHD_CATCH("chd_encode_coefficients")
+}

@@ -288,6 +288,10 @@ Plaintext<uint32_t>::Plaintext(const NPInfo &np, int degree) : np_(np) {
   mx_.resize(static_cast<size_t>(np.GetNumTotal()) * degree);
 }
 
+Constant<uint32_t>::Constant(const NPInfo &np) : np_(np) {
+  cx_.resize(static_cast<size_t>(np.GetNumTotal()));
+}
+
 // EvkMap.cpp: GetRotationKey asserts the key exists
 const EvaluationKey<uint32_t> &EvkMap<uint32_t>::GetRotationKey(
     int rot_idx) const {
@@ -305,6 +309,18 @@ chd_limb_map NTTHandler<uint32_t>::Map(const NPInfo &np) const {
   return NoSkipMap(param_, np);
 }
 
+namespace {
+// Limb gap between src's q and aux parts, checked against src's size: the
+// kernels read num_q limbs from src and num_aux limbs from src + QSize().
+int SrcGap(const DvConstView<uint32_t> &src, const NPInfo &np, int n,
+           const char *who) {
+  AssertTrue(src.QSize() >= np.GetNumQ() * n && src.QSize() % n == 0 &&
+                 src.TotalSize() >= src.QSize() + np.num_aux_ * n,
+             std::string(who) + ": src too small for its limbs");
+  return (src.QSize() - np.GetNumQ() * n) / n;
+}
+}  // namespace
+
 // src/core/NTT.cu:606-671
 void NTTHandler<uint32_t>::NTT(DvView<word> &dst, const NPInfo &np,
                                const DvConstView<word> &src,
@@ -312,7 +328,7 @@ void NTTHandler<uint32_t>::NTT(DvView<word> &dst, const NPInfo &np,
   const int n = param_.degree_;
   AssertTrue(dst.TotalSize() == np.GetNumTotal() * n, "NTT: Invalid dst size");
   chd_limb_map m = Map(np);
-  m.src_gap = (src.QSize() - np.GetNumQ() * n) / n;
+  m.src_gap = SrcGap(src, np, n, "NTT");
   m.cst_gap = param_.MainLeft(np);
   const word *pre = montgomery_conversion
                         ? chain_.mont_converter() + param_.TerLeft(np)
@@ -329,7 +345,7 @@ void NTTHandler<uint32_t>::INTT(DvView<word> &dst, const NPInfo &np,
   AssertTrue(dst.TotalSize() == np.GetNumTotal() * n,
              "INTT: Invalid dst size");
   chd_limb_map m = Map(np);
-  m.src_gap = (src.QSize() - np.GetNumQ() * n) / n;
+  m.src_gap = SrcGap(src, np, n, "INTT");
   m.cst_gap = param_.MainLeft(np);
   const word *cst =
       (montgomery_conversion ? chain_.inv_degree() : chain_.inv_degree_mont()) +
@@ -347,8 +363,11 @@ void NTTHandler<uint32_t>::INTTAndMultConst(DvView<word> &dst,
   const int n = param_.degree_;
   AssertTrue(dst.TotalSize() == np.GetNumTotal() * n,
              "INTTAndMultConst: Invalid dst size");
+  AssertTrue(src_const.QSize() >= np.GetNumQ() &&
+                 src_const.TotalSize() >= src_const.QSize() + np.num_aux_,
+             "INTTAndMultConst: src_const too small for its limbs");
   chd_limb_map m = Map(np);
-  m.src_gap = (src.QSize() - np.GetNumQ() * n) / n;
+  m.src_gap = SrcGap(src, np, n, "INTTAndMultConst");
   m.cst_gap = src_const.QSize() - np.GetNumQ();
   K(chd_k_ntt_inv(&chain_.tables(), &m, dst.data(), 0, src.data(), 0,
                   np.GetNumTotal(), 1, src_const.data(), normalize ? 1 : 0,
@@ -369,7 +388,7 @@ void NTTHandler<uint32_t>::NTTForModUp(DvView<word> &dst, const NPInfo &np,
   chd_limb_map m = Map(np);
   m.skip_lo = skip_start;
   m.skip_len = skip_end - skip_start;
-  m.src_gap = (src.QSize() - num_q * n) / n;
+  m.src_gap = SrcGap(src, np, n, "NTTForModUp");
   K(chd_k_ntt_fwd(&chain_.tables(), &m, dst.data(), 0, src.data(), 0,
                   np.GetNumTotal() - m.skip_len, 1, nullptr, CurrentStream()));
 }
@@ -977,7 +996,10 @@ std::shared_ptr<Context<uint32_t>> Context<uint32_t>::Create(
 
 // src/core/Context.cpp:68-124
 Context<uint32_t>::Context(const Parameter<word> &param)
-    : param_(param), elem_handler_(param, ntt_handler_), ntt_handler_(param) {
+    : param_(param),
+      elem_handler_(param, ntt_handler_),
+      ntt_handler_(param),
+      encoder_(param, ntt_handler_) {
   Ciphertext<word>::SetDegree(param_.degree_);
   {
     // arena for the largest call at the top level: HMult holds the tensor

@@ -17,6 +17,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <complex>
 #include <cstdint>
 #include <memory>
 #include <functional>
@@ -304,6 +305,25 @@ class Plaintext<uint32_t> {
   double scale_ = 1.0;
 };
 
+// Constant (include/core/Container.h:72-130): one residue per prime, in
+// Montgomery form, with its scale.
+template <typename word>
+class Constant;
+template <>
+class Constant<uint32_t> {
+ public:
+  using word = uint32_t;
+  explicit Constant(const NPInfo &np = NPInfo{});
+  DeviceVector<word> cx_;
+  NPInfo GetNP() const { return np_; }
+  double GetScale() const { return scale_; }
+  void SetScale(double s) { scale_ = s; }
+
+ private:
+  NPInfo np_;
+  double scale_ = 1.0;
+};
+
 // Rotation-key container (include/core/EvkMap.h): evaluation keys by index.
 template <typename word>
 class EvkMap;
@@ -456,6 +476,50 @@ class ModSwitchHandler<uint32_t> {
       mod_down_rescale_inv_prime_prod_;
 };
 
+// CKKS encoder (include/core/Encode.h, src/core/Encode.cpp). Host arithmetic
+// in IEEE double in the reference's operation order: the special IFFT with
+// its twiddle indexing, division by the slot count, scaling, truncation
+// toward zero and non-negative residues, then the device NTT with Montgomery
+// conversion. The host part is compiled with -ffp-contract=off so no product
+// and sum fuse: the residues are bit-identical to the reference's for every
+// message it accepts. Decode inverts it through INTTAndMultConst, an exact
+// CRT with a normalisation to (-Q/2, Q/2] and libtommath's conversion to
+// double (the reference's default big-integer backend).
+using Complex = std::complex<double>;
+template <typename word>
+class Encoder;
+template <>
+class Encoder<uint32_t> {
+ public:
+  using word = uint32_t;
+  Encoder(const Parameter<word> &param, const NTTHandler<word> &ntt_handler);
+  // host half only (SpecialIFFT / SpecialFFT / CoefficientResidues): no
+  // device tables are needed, Encode / Decode / EncodeConstant throw
+  explicit Encoder(const Parameter<word> &param);
+  // Encode.cpp:23-43: the message is zero-padded to a power of two slots
+  void Encode(Plaintext<word> &ptxt, int level, double scale,
+              const std::vector<Complex> &message, int num_aux = 0) const;
+  // Encode.cpp:45-82: aux primes are not supported, as in the reference
+  void Decode(std::vector<Complex> &message, const Plaintext<word> &ptxt) const;
+  // Encode.cpp:248-273: round(number * scale) truncated, per-prime Montgomery
+  void EncodeConstant(Constant<word> &constant, int level, double scale,
+                      double number, int num_aux = 0) const;
+  Complex GetTwiddleFactor(int index) const { return twiddle_.at(index); }
+  // ComplexVectorToPlaintext's host residues (before the NTT), [limb][N];
+  // the message must already hold a power-of-two slot count
+  std::vector<word> CoefficientResidues(int level, double scale,
+                                        std::vector<Complex> data,
+                                        int num_aux = 0) const;
+  void SpecialIFFT(std::vector<Complex> &data) const;
+  void SpecialFFT(std::vector<Complex> &data) const;
+
+ private:
+  const Parameter<word> &param_;
+  const NTTHandler<word> *ntt_handler_;
+  const int m_;  // 2N
+  std::vector<Complex> twiddle_;
+};
+
 template <typename word>
 class Context;
 template <>
@@ -517,6 +581,7 @@ class Context<uint32_t> {
   ElementWiseHandler<word> elem_handler_;
   NTTHandler<word> ntt_handler_;
   std::vector<ModSwitchHandler<word>> mod_switch_handlers_;
+  Encoder<word> encoder_;
 
  private:
   explicit Context(const Parameter<word> &param);

@@ -8,6 +8,8 @@ loudly if the HIP library has not been built.
 import ctypes
 import os
 
+import numpy as np
+
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG, "lib", "libcheddar_amd.so")
 LOG_N = 16
@@ -28,6 +30,8 @@ _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _pp = ctypes.POINTER(ctypes.c_void_p)
 _ip = ctypes.POINTER(ctypes.c_int)
+_dp = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
 
 lib = ctypes.CDLL(LIB_PATH)
 _SIGS = {
@@ -69,6 +73,13 @@ _SIGS = {
                                 _pp, _i, _ip, _pp, _pp, _i, _vp]),
     "chd_hoist_create": (_i, [_pp, _vp, _i, _i, _ip, _i, _ip, _pp, _vp]),
     "chd_hoist_destroy": (None, [_vp]),
+    "chd_encode": (_i, [_vp, _i, _i, ctypes.c_double, _dp, _dp, _i, _vp,
+                        _vp]),
+    "chd_encode_constant": (_i, [_vp, _i, _i, ctypes.c_double,
+                                 ctypes.c_double, _vp, _vp]),
+    "chd_decode": (_i, [_vp, _i, ctypes.c_double, _i, _vp, _dp, _dp, _vp]),
+    "chd_encode_coefficients": (_i, [_vp, _i, _i, ctypes.c_double, _dp, _dp,
+                                     _i, _u32p]),
     "chd_hoist_run": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _ip, _pp, _pp, _i,
                            _vp]),
 }
@@ -76,6 +87,12 @@ for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
     _f.restype = _res
     _f.argtypes = _args
+
+
+def _split(msg):
+    m = np.asarray(msg, np.complex128).reshape(-1)
+    return (np.ascontiguousarray(m.real, np.float64),
+            np.ascontiguousarray(m.imag, np.float64))
 
 
 def _check(status):
@@ -186,6 +203,17 @@ class Param:
     def num_q(self, level):
         return lib.chd_param_num_q(self.h, level)
 
+    def encode_coefficients(self, level, num_aux, scale, msg, log_n=LOG_N):
+        """host half of the encoder: (residues [limbs][N] before the NTT,
+        padded slot count)"""
+        re, im = _split(msg)
+        out = np.zeros((self.num_q(level) + num_aux) << log_n, np.uint32)
+        slots = lib.chd_encode_coefficients(self.h, level, num_aux, scale, re,
+                                            im, re.size, out)
+        if slots < 0:
+            _check(slots)
+        return out.reshape(-1, 1 << log_n), slots
+
     def __del__(self):
         if getattr(self, "h", None):
             lib.chd_param_destroy(self.h)
@@ -285,6 +313,29 @@ class Context:
             len(gs), (ctypes.c_int * len(gs))(*gs), len(bs),
             (ctypes.c_int * len(bs))(*bs), parr, nk, kr, kb, ka, beta,
             self._s(stream)))
+
+    def encode(self, level, num_aux, scale, msg, dst, stream=None):
+        """message (complex array) -> plaintext limbs in dst (device);
+        returns the padded slot count"""
+        re, im = _split(msg)
+        slots = lib.chd_encode(self.h, level, num_aux, scale, re, im, re.size,
+                               ptr(dst), self._s(stream))
+        if slots < 0:
+            _check(slots)
+        return slots
+
+    def encode_constant(self, level, num_aux, scale, number, dst,
+                        stream=None):
+        _check(lib.chd_encode_constant(self.h, level, num_aux, scale,
+                                       float(number), ptr(dst),
+                                       self._s(stream)))
+
+    def decode(self, level, scale, num_slots, src, stream=None):
+        re = np.zeros(num_slots, np.float64)
+        im = np.zeros(num_slots, np.float64)
+        _check(lib.chd_decode(self.h, level, scale, num_slots, ptr(src), re,
+                              im, self._s(stream)))
+        return re + 1j * im
 
     def permute(self, level, res, a, rot, stream=None):
         _check(lib.chd_permute(self.h, level, ptr(res[0]), ptr(res[1]),

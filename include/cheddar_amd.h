@@ -208,6 +208,37 @@ int chd_hoist_evaluate(const chd_context *ctx, int level, uint32_t *res_bx,
                        const uint32_t *const *key_ax, int key_beta,
                        void *stream);
 
+/* ------------------------------------------------------------ encoder --
+ * Encoder::Encode (src/core/Encode.cpp:23-43, 84-109, 135-190): the message
+ * (msg_re[i], msg_im[i], i < msg_len, zero-padded to the next power of two
+ * slots) -> dst (device, (num_q(level) + num_aux) * N words, the plaintext
+ * in the NTT domain, Montgomery form). num_aux is 0 or alpha (a plaintext
+ * for the extended basis, Hoist.cu:131-145). Returns the padded slot count
+ * (> 0) or a negative error code. Synchronises the stream. */
+int chd_encode(const chd_context *ctx, int level, int num_aux, double scale,
+               const double *msg_re, const double *msg_im, int msg_len,
+               uint32_t *dst, void *stream);
+/* Encoder::EncodeConstant (Encode.cpp:248-273): trunc(number * scale) mod
+ * each prime, Montgomery form, into dst (device, num_q(level) + num_aux
+ * words). Synchronises the stream. */
+int chd_encode_constant(const chd_context *ctx, int level, int num_aux,
+                        double scale, double number, uint32_t *dst,
+                        void *stream);
+/* Encoder::Decode (Encode.cpp:45-82, 192-246): src (device, num_q(level)
+ * limbs in the NTT domain, Montgomery form) with num_slots slots (a power of
+ * two <= N/2) at scale -> out_re / out_im (host, num_slots each).
+ * Synchronises the stream. */
+int chd_decode(const chd_context *ctx, int level, double scale, int num_slots,
+               const uint32_t *src, double *out_re, double *out_im,
+               void *stream);
+/* The host half of chd_encode alone (no device): the coefficient residues
+ * ComplexVectorToPlaintext writes before the NTT, [num_q(level) +
+ * num_aux][N] words into host_out. Returns the padded slot count. */
+int chd_encode_coefficients(const chd_param *param, int level, int num_aux,
+                            double scale, const double *msg_re,
+                            const double *msg_im, int msg_len,
+                            uint32_t *host_out);
+
 #ifdef __cplusplus
 }
 #endif
