@@ -545,6 +545,41 @@ extern "C" int chd_hoist_create(chd_hoist **out, const chd_context *ctx,
   CHD_CATCH("chd_hoist_create")
 }
 
+extern "C" int chd_hoist_create_from_messages(
+    chd_hoist **out, const chd_context *ctx, int level, double pt_scale,
+    int num_gs, const int *gs, int num_bs, const int *bs,
+    const double *const *msg_re, const double *const *msg_im,
+    const int *msg_len, int suppress_bs_swap, void *stream) {
+  if (!out || !LevelOk(ctx, level) || level < 1 || num_gs < 1 || !gs ||
+      num_bs < 1 || !bs || !msg_re || !msg_im || !msg_len)
+    return set_error(CHD_ERR_ARG,
+                     "chd_hoist_create_from_messages: invalid argument");
+  CHD_TRY cheddar::StreamScope scope(static_cast<hipStream_t>(stream));
+  cheddar::HoistHandler<word>::PlainHoistMap map;
+  for (int g = 0; g < num_gs; g++)
+    for (int b = 0; b < num_bs; b++) {
+      const size_t k = static_cast<size_t>(g) * num_bs + b;
+      if (msg_re[k] == nullptr) continue;
+      if (msg_im[k] == nullptr || msg_len[k] < 1 ||
+          msg_len[k] > ctx->c->param_.degree_ / 2)
+        throw cheddar::Error("invalid message");
+      cheddar::HoistHandler<word>::Message m(msg_len[k]);
+      for (int i = 0; i < msg_len[k]; i++)
+        m[i] = cheddar::Complex(msg_re[k][i], msg_im[k][i]);
+      map[gs[g]][bs[b]] = std::move(m);
+    }
+  std::unique_ptr<chd_hoist> h(new chd_hoist);
+  h->c = ctx->c;
+  h->level = level;
+  h->h.reset(new cheddar::HoistHandler<word>(ctx->c, map, level, pt_scale,
+                                             suppress_bs_swap != 0));
+  cheddar::HipCheck(hipStreamSynchronize(cheddar::CurrentStream()),
+                    "hipStreamSynchronize");
+  *out = h.release();
+  return 0;
+  CHD_CATCH("chd_hoist_create_from_messages")
+}
+
 extern "C" void chd_hoist_destroy(chd_hoist *h) { delete h; }
 
 extern "C" int chd_hoist_run(const chd_hoist *h, uint32_t *res_bx,

@@ -1363,32 +1363,93 @@ Context<uint32_t>::EvkRef Context<uint32_t>::RefOfKey(const Evk &k) {
 // ---------------------------------------------------------- HoistHandler --
 // src/extension/Hoist.cu:131-177 (CompilePlaintexts / ExtractBSIndices on
 // already encoded plaintexts)
+// Hoist.cu:131-145 (CompilePlaintexts) and 146-173 (the bs/gs swap)
+HoistHandler<uint32_t>::PtMap HoistHandler<uint32_t>::EncodeMap(
+    const Context<word> &context, const PlainHoistMap &hoist_map,
+    int pt_level, double pt_scale, bool suppress_bs_swap) {
+  AssertTrue(!hoist_map.empty(), "Hoist: hoist_map should not be empty");
+  const int alpha = context.param_.alpha_;
+  PtMap out;
+  auto encode = [&](int g, int b, const Message &msg) {
+    Pt &pt = out[g].try_emplace(b, NPInfo(0, 0, 0)).first->second;
+    context.encoder_.Encode(pt, pt_level, pt_scale, msg, alpha);
+  };
+  if (hoist_map.size() == 1 && hoist_map.begin()->first == 0 &&
+      !suppress_bs_swap) {
+    // single giant step: baby step b becomes giant step b with baby step 0,
+    // its message rotated right by b
+    for (const auto &[b, msg] : hoist_map.begin()->second) {
+      const size_t sz = msg.size();
+      AssertTrue(sz > 0, "Hoist: empty message");
+      Message rot(sz);
+      for (size_t i = 0; i < sz; i++) rot[(i + b) % sz] = msg[i];
+      encode(b, 0, rot);
+    }
+  } else {
+    for (const auto &[g, bs_map] : hoist_map)
+      for (const auto &[b, msg] : bs_map) encode(g, b, msg);
+  }
+  return out;
+}
+
+HoistHandler<uint32_t>::HoistHandler(ConstContextPtr<word> context,
+                                     const PlainHoistMap &hoist_map,
+                                     int pt_level, double pt_scale,
+                                     bool suppress_bs_swap)
+    : HoistHandler(context,
+                   EncodeMap(*context, hoist_map, pt_level, pt_scale,
+                             suppress_bs_swap),
+                   pt_level, pt_scale) {}
+
 HoistHandler<uint32_t>::HoistHandler(ConstContextPtr<word> context,
                                      PtMap &&encoded, int pt_level,
                                      double pt_scale)
     : pt_level_(pt_level), pt_scale_(pt_scale), pt_map_(std::move(encoded)) {
   AssertTrue(!pt_map_.empty(), "Hoist: hoist_map should not be empty");
   const Parameter<word> &param = context->param_;
+  const int n = param.degree_;
   const NPInfo np = param.LevelToNP(pt_level_, param.alpha_);
+  bool only_bs0 = true;
   for (const auto &[gs, bs_map] : pt_map_) {
     AssertTrue(!bs_map.empty(), "Hoist: empty baby-step map");
-    AssertTrue(gs >= 0 && gs < param.degree_ / 2, "Hoist: invalid giant step");
-    gs_indices_.push_back(gs);
+    AssertTrue(gs >= 0 && gs < n / 2, "Hoist: invalid giant step");
     for (const auto &[bs, pt] : bs_map) {
-      AssertTrue(bs >= 0 && bs < param.degree_ / 2,
-                 "Hoist: invalid baby step");
+      AssertTrue(bs >= 0 && bs < n / 2, "Hoist: invalid baby step");
       AssertTrue(pt.GetNP() == np && pt.mx_.size() ==
-                     static_cast<size_t>(np.GetNumTotal()) * param.degree_,
+                     static_cast<size_t>(np.GetNumTotal()) * n,
                  "Hoist: plaintexts must hold pt_level's q primes and alpha "
                  "aux primes");
-      bs_indices_.insert(bs);
+      only_bs0 = only_bs0 && bs == 0;
     }
+  }
+  if (only_bs0) {
+    // giant steps with baby step 0 only: one giant step 0 whose baby steps
+    // are the rotations, plaintexts permuted ahead (see the class comment)
+    PtMap conv;
+    std::map<int, Pt> &row = conv[0];
+    const int aux_words = param.alpha_ * n;
+    for (auto &[g, bs_map] : pt_map_) {
+      Pt &src = bs_map.begin()->second;
+      if (g == 0) {
+        row.emplace(0, std::move(src));
+        continue;
+      }
+      Pt dst(np, n);
+      dst.SetScale(src.GetScale());
+      dst.SetNumSlots(src.GetNumSlots());
+      std::vector<DvView<word>> d = {dst.mx_.View(aux_words)};
+      context->elem_handler_.Permute(d, np, g, {src.mx_.ConstView(aux_words)});
+      row.emplace(g, std::move(dst));
+    }
+    HipCheck(hipStreamSynchronize(CurrentStream()), "hipStreamSynchronize");
+    pt_map_ = std::move(conv);
+  }
+  for (const auto &[gs, bs_map] : pt_map_) {
+    gs_indices_.push_back(gs);
+    for (const auto &[bs, pt] : bs_map) bs_indices_.insert(bs);
   }
   AssertTrue(gs_indices_.size() == 1 || gs_indices_.front() == 0,
              "Hoist: a giant step 0 is required with several giant steps");
-  AssertTrue(!(bs_indices_.size() == 1 && *bs_indices_.begin() == 0),
-             "Hoist: maps with only baby step 0 (the reference's bs == 1 "
-             "path) are not supported by this build");
   AssertTrue(bs_indices_.size() <= 64, "Hoist: too many baby steps");
 }
 
@@ -1454,11 +1515,17 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
   const DvConstView<word> p_prod = ctx.PProd(in_np);
   Workspace *ws = ctx.GetWorkspace();
   Workspace::Use use_ws(ws);
+  std::vector<int> rots;
+  for (int b : bs_indices_)
+    if (b != 0) rots.push_back(b);
   // 1. ModUp of a, all groups (own limbs are read from a by the kernel)
   const long long gs = static_cast<long long>(total) * n;
-  Scratch buf(ws, static_cast<size_t>(beta) * gs + static_cast<size_t>(num_q) * n);
-  ms.ModUpGroups(buf.data(), gs, input.ax_.ConstView(), buf.data() + beta * gs,
-                 true);
+  Scratch buf(ws, rots.empty() ? 0
+                               : static_cast<size_t>(beta) * gs +
+                                     static_cast<size_t>(num_q) * n);
+  if (!rots.empty())
+    ms.ModUpGroups(buf.data(), gs, input.ax_.ConstView(),
+                   buf.data() + beta * gs, true);
   // 2. baby step 0: the PseudoModUp of (b, a), zero on the aux limbs
   auto slot = [&](int idx) -> Ct & {
     Ct &ct = bs.try_emplace(idx, ext_np).first->second;
@@ -1480,9 +1547,6 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
     }
   }
   // 3. the other baby steps, CHD_MAX_BS per fused launch
-  std::vector<int> rots;
-  for (int b : bs_indices_)
-    if (b != 0) rots.push_back(b);
   const int prime_offset = param.GetMaxNumTer() - in_np.num_ter_;
   chd_limb_map m{};
   m.num_q = num_q;

@@ -601,14 +601,21 @@ using ConstContextPtr = std::shared_ptr<const Context<word>>;
 // (include/extension/Hoist.h, src/extension/Hoist.cu), the non-min_ks
 // optimized path: res = Rescale(sum_g Rot_g(sum_b pt[g][b] * Rot_b(input))).
 //
-// The reference's constructor takes complex messages and encodes them at
-// (pt_level, alpha aux primes) (Hoist.cu:131-177). The encoder is not part
-// of this build, so this constructor takes the plaintexts already encoded in
-// that form: mx_ holds num_q(pt_level) + alpha limbs in the NTT domain. The
-// reference's encode-time bs/gs swap for single-giant-step maps therefore
-// does not apply; the map is evaluated as given. A giant step 0 must be
-// present when there are other giant steps (the reference's optimized path
-// reads its accumulator unconditionally).
+// Two constructors, as in the reference: from complex messages, which are
+// encoded at (pt_level, alpha aux primes) with pt_scale (Hoist.cu:131-177,
+// including the bs/gs swap of single-giant-step maps), or from plaintexts
+// already encoded in that form (mx_ holds num_q(pt_level) + alpha limbs in
+// the NTT domain). A giant step 0 must be present when there are other giant
+// steps and more than one baby step (the reference's optimized path reads
+// its accumulator unconditionally).
+//
+// Maps whose giant steps all hold only baby step 0 (the swapped maps; the
+// reference's bs == 1 path, Hoist.cu:715-797) multiply the key-switched
+// input by pt_g before the automorphism g. Permute only moves NTT-domain
+// residues, so Permute_g(x pt_g) = Permute_g(x) Permute_g(pt_g) exactly; such
+// a map is evaluated as the single giant step 0 with baby steps g and
+// plaintexts Permute_g(pt_g), prepared once here: the same residues, the
+// same rotation keys.
 template <typename word>
 class HoistHandler;
 template <>
@@ -618,6 +625,10 @@ class HoistHandler<uint32_t> {
   using Ct = Ciphertext<word>;
   using Pt = Plaintext<word>;
   using PtMap = std::map<int, std::map<int, Pt>>;  // gs -> bs -> plaintext
+  using Message = std::vector<Complex>;
+  using PlainHoistMap = std::map<int, std::map<int, Message>>;
+  HoistHandler(ConstContextPtr<word> context, const PlainHoistMap &hoist_map,
+               int pt_level, double pt_scale, bool suppress_bs_swap = false);
   HoistHandler(ConstContextPtr<word> context, PtMap &&encoded, int pt_level,
                double pt_scale);
   HoistHandler(const HoistHandler &) = delete;
@@ -645,6 +656,9 @@ class HoistHandler<uint32_t> {
  private:
   int pt_level_;
   double pt_scale_;
+  static PtMap EncodeMap(const Context<word> &context,
+                         const PlainHoistMap &hoist_map, int pt_level,
+                         double pt_scale, bool suppress_bs_swap);
   PtMap pt_map_;
   std::set<int> bs_indices_;
   std::vector<int> gs_indices_;

@@ -73,6 +73,9 @@ _SIGS = {
                                 _pp, _i, _ip, _pp, _pp, _i, _vp]),
     "chd_hoist_create": (_i, [_pp, _vp, _i, _i, _ip, _i, _ip, _pp, _vp]),
     "chd_hoist_destroy": (None, [_vp]),
+    "chd_hoist_create_from_messages": (_i, [_pp, _vp, _i, ctypes.c_double,
+                                            _i, _ip, _i, _ip, _pp, _pp, _ip,
+                                            _i, _vp]),
     "chd_encode": (_i, [_vp, _i, _i, ctypes.c_double, _dp, _dp, _i, _vp,
                         _vp]),
     "chd_encode_constant": (_i, [_vp, _i, _i, ctypes.c_double,
@@ -357,6 +360,32 @@ class Hoist:
             (ctypes.c_int * len(bs))(*bs), parr,
             stream if stream is not None else current_stream()))
         self.h = h
+
+    @classmethod
+    def from_messages(cls, ctx, level, pt_scale, gs, bs, msgs,
+                      suppress_bs_swap=False, stream=None):
+        """the reference's message constructor: msgs {(g, b): complex
+        array}, encoded by the library"""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        keys = [(g, b) for g in gs for b in bs]
+        parts = {k: _split(msgs[k]) for k in keys if k in msgs}
+        self._keep = parts
+        re = (ctypes.c_void_p * len(keys))(*[
+            parts[k][0].ctypes.data if k in parts else None for k in keys])
+        im = (ctypes.c_void_p * len(keys))(*[
+            parts[k][1].ctypes.data if k in parts else None for k in keys])
+        ln = (ctypes.c_int * len(keys))(*[
+            parts[k][0].size if k in parts else 0 for k in keys])
+        h = ctypes.c_void_p()
+        _check(lib.chd_hoist_create_from_messages(
+            ctypes.byref(h), ctx.h, level, pt_scale, len(gs),
+            (ctypes.c_int * len(gs))(*gs), len(bs),
+            (ctypes.c_int * len(bs))(*bs), re, im, ln,
+            1 if suppress_bs_swap else 0,
+            stream if stream is not None else current_stream()))
+        self.h = h
+        return self
 
     def __del__(self):
         if getattr(self, "h", None):

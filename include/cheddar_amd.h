@@ -188,6 +188,19 @@ typedef struct chd_hoist chd_hoist;
 int chd_hoist_create(chd_hoist **out, const chd_context *ctx, int level,
                      int num_gs, const int *gs, int num_bs, const int *bs,
                      const uint32_t *const *pt, void *stream);
+/* The reference's message constructor (Hoist.cu:131-177): messages
+ * msg_re / msg_im [g * num_bs + b] of msg_len[g * num_bs + b] complex values
+ * (NULL when absent) are encoded at (level, alpha aux primes) with pt_scale;
+ * a map with the single giant step 0 is evaluated with baby and giant steps
+ * swapped (messages rotated right by their baby step) unless
+ * suppress_bs_swap is non-zero. Synchronises the stream. */
+int chd_hoist_create_from_messages(chd_hoist **out, const chd_context *ctx,
+                                   int level, double pt_scale, int num_gs,
+                                   const int *gs, int num_bs, const int *bs,
+                                   const double *const *msg_re,
+                                   const double *const *msg_im,
+                                   const int *msg_len, int suppress_bs_swap,
+                                   void *stream);
 void chd_hoist_destroy(chd_hoist *h);
 int chd_hoist_run(const chd_hoist *h, uint32_t *res_bx, uint32_t *res_ax,
                   const uint32_t *ct_bx, const uint32_t *ct_ax, int num_keys,

@@ -107,3 +107,35 @@ def evaluate(ct_b, ct_a, pts, keys, L, max_q, q_primes, p_primes, log_n):
     rb = _orc.mod_down(fb, primes, L - 1, log_n)
     ra = _orc.mod_down(fa, primes, L - 1, log_n)
     return rb, ra
+
+
+def evaluate_gs_only(ct_b, ct_a, pts, keys, L, max_q, q_primes, p_primes,
+                     log_n):
+    """maps whose giant steps hold only baby step 0 (Hoist.cu:715-797), in
+    the reference's order: for g != 0 the key switch of ct with key g plus
+    P * ct_b, multiplied by pt_g, then permuted by g; for g == 0 the P-raised
+    ct times pt_0; the sum brought down by ModDownAndRescale.
+    pts: {g: L + alpha limbs}."""
+    q = list(q_primes[:L])
+    p = list(p_primes)
+    primes = q + p
+    n = 1 << log_n
+    modup = _orc.mod_up(ct_a, q, p, log_n)
+    pb = pseudo_mod_up(ct_b, q, p)
+    fb = np.zeros((L + len(p), n), np.uint32)
+    fa = np.zeros_like(fb)
+    for g, pt in sorted(pts.items()):
+        if g == 0:
+            tb, ta = pb, pseudo_mod_up(ct_a, q, p)
+        else:
+            tb, ta = paccum(modup, keys[g][0], keys[g][1], L, max_q, q, p,
+                            log_n)
+            tb = _add(tb, pb, primes)
+        tb, ta = _mul(tb, pt, primes), _mul(ta, pt, primes)
+        if g != 0:
+            gal = _orc.lib.orc_galois_factor(g, log_n)
+            tb, ta = _orc.permute(tb, log_n, gal), _orc.permute(ta, log_n, gal)
+        fb, fa = _add(fb, tb, primes), _add(fa, ta, primes)
+    rb = _orc.mod_down(fb, primes, L - 1, log_n)
+    ra = _orc.mod_down(fa, primes, L - 1, log_n)
+    return rb, ra
