@@ -504,7 +504,9 @@ extern "C" int chd_hoist_baby_steps(
 
 struct chd_hoist {
   std::shared_ptr<cheddar::Context<word>> c;
-  std::unique_ptr<cheddar::HoistHandler<word>> h;
+  std::unique_ptr<cheddar::HoistHandler<word>> own;
+  std::unique_ptr<cheddar::LinearTransform<word>> lt;
+  const cheddar::HoistHandler<word> *h = nullptr;  // own's or lt's
   int level;
   // buffers kept across runs: the input copy, the baby steps, the result
   cheddar::Ciphertext<word> in, res;
@@ -536,8 +538,9 @@ extern "C" int chd_hoist_create(chd_hoist **out, const chd_context *ctx,
   std::unique_ptr<chd_hoist> h(new chd_hoist);
   h->c = ctx->c;
   h->level = level;
-  h->h.reset(new cheddar::HoistHandler<word>(ctx->c, std::move(pts), level,
-                                             1.0));
+  h->own.reset(new cheddar::HoistHandler<word>(ctx->c, std::move(pts), level,
+                                               1.0));
+  h->h = h->own.get();
   cheddar::HipCheck(hipStreamSynchronize(cheddar::CurrentStream()),
                     "hipStreamSynchronize");
   *out = h.release();
@@ -571,8 +574,9 @@ extern "C" int chd_hoist_create_from_messages(
   std::unique_ptr<chd_hoist> h(new chd_hoist);
   h->c = ctx->c;
   h->level = level;
-  h->h.reset(new cheddar::HoistHandler<word>(ctx->c, map, level, pt_scale,
-                                             suppress_bs_swap != 0));
+  h->own.reset(new cheddar::HoistHandler<word>(ctx->c, map, level, pt_scale,
+                                               suppress_bs_swap != 0));
+  h->h = h->own.get();
   cheddar::HipCheck(hipStreamSynchronize(cheddar::CurrentStream()),
                     "hipStreamSynchronize");
   *out = h.release();
@@ -582,15 +586,15 @@ extern "C" int chd_hoist_create_from_messages(
 
 extern "C" void chd_hoist_destroy(chd_hoist *h) { delete h; }
 
-extern "C" int chd_hoist_run(const chd_hoist *h, uint32_t *res_bx,
-                             uint32_t *res_ax, const uint32_t *ct_bx,
-                             const uint32_t *ct_ax, int num_keys,
-                             const int *key_rot, const uint32_t *const *key_bx,
-                             const uint32_t *const *key_ax, int key_beta,
-                             void *stream) {
+namespace {
+int HoistRun(const char *name, const chd_hoist *h, uint32_t *res_bx,
+             uint32_t *res_ax, const uint32_t *ct_bx, const uint32_t *ct_ax,
+             int num_keys, const int *key_rot, const uint32_t *const *key_bx,
+             const uint32_t *const *key_ax, int key_beta, bool min_ks,
+             void *stream) {
   if (!h || !res_bx || !res_ax || !ct_bx || !ct_ax || num_keys < 0 ||
       key_beta < 1 || (num_keys > 0 && (!key_rot || !key_bx || !key_ax)))
-    return set_error(CHD_ERR_ARG, "chd_hoist_run: invalid argument");
+    return set_error(CHD_ERR_ARG, std::string(name) + ": invalid argument");
   CHD_TRY cheddar::StreamScope scope(static_cast<hipStream_t>(stream));
   const auto &p = h->c->param_;
   chd_context view{h->c};
@@ -607,8 +611,8 @@ extern "C" int chd_hoist_run(const chd_hoist *h, uint32_t *res_bx,
                                    hipMemcpyDeviceToDevice,
                                    cheddar::CurrentStream()),
                     "hipMemcpyAsync");
-  h->h->BabyStep(*h->c, m->babies, m->in, keys);
-  h->h->GiantStep(*h->c, m->res, m->babies, keys);
+  h->h->BabyStep(*h->c, m->babies, m->in, keys, min_ks);
+  h->h->GiantStep(*h->c, m->res, m->babies, keys, min_ks);
   const size_t bytes = m->res.bx_.size() * sizeof(word);
   cheddar::HipCheck(hipMemcpyAsync(res_bx, m->res.bx_.data(), bytes,
                                    hipMemcpyDeviceToDevice,
@@ -618,9 +622,85 @@ extern "C" int chd_hoist_run(const chd_hoist *h, uint32_t *res_bx,
                                    hipMemcpyDeviceToDevice,
                                    cheddar::CurrentStream()),
                     "hipMemcpyAsync");
-  return chd::check_launch("chd_hoist_run");
-  CHD_CATCH("chd_hoist_run")
+  return chd::check_launch(name);
+  }
+  catch (const std::exception &e) {
+    return set_error(CHD_ERR_STATE, std::string(name) + ": " + e.what());
+  }
 }
+}  // namespace
+
+extern "C" int chd_hoist_run(const chd_hoist *h, uint32_t *res_bx,
+                             uint32_t *res_ax, const uint32_t *ct_bx,
+                             const uint32_t *ct_ax, int num_keys,
+                             const int *key_rot, const uint32_t *const *key_bx,
+                             const uint32_t *const *key_ax, int key_beta,
+                             void *stream) {
+  return HoistRun("chd_hoist_run", h, res_bx, res_ax, ct_bx, ct_ax, num_keys,
+                  key_rot, key_bx, key_ax, key_beta, false, stream);
+}
+
+extern "C" int chd_hoist_run_min_ks(const chd_hoist *h, uint32_t *res_bx,
+                                    uint32_t *res_ax, const uint32_t *ct_bx,
+                                    const uint32_t *ct_ax, int num_keys,
+                                    const int *key_rot,
+                                    const uint32_t *const *key_bx,
+                                    const uint32_t *const *key_ax,
+                                    int key_beta, void *stream) {
+  return HoistRun("chd_hoist_run_min_ks", h, res_bx, res_ax, ct_bx, ct_ax,
+                  num_keys, key_rot, key_bx, key_ax, key_beta, true, stream);
+}
+
+extern "C" int chd_hoist_required_rotations(const chd_hoist *h, int min_ks,
+                                            int *out, int capacity) {
+  if (!h || capacity < 0 || (capacity > 0 && !out))
+    return set_error(CHD_ERR_ARG,
+                     "chd_hoist_required_rotations: invalid argument");
+  CHD_TRY
+  const std::set<int> r = h->h->RequiredRotations(min_ks != 0);
+  int i = 0;
+  for (int v : r) {
+    if (i >= capacity) break;
+    out[i++] = v;
+  }
+  return static_cast<int>(r.size());
+  CHD_CATCH("chd_hoist_required_rotations")
+}
+
+extern "C" int chd_linear_transform_create(
+    chd_hoist **out, const chd_context *ctx, int level, double pt_scale,
+    int dim, int num_diag, const int *diag_idx, const double *const *diag_re,
+    const double *const *diag_im, int bs, int gs, int pre_rotation,
+    int additional_pt_rot, void *stream) {
+  if (!out || !LevelOk(ctx, level) || level < 1 || dim < 1 ||
+      dim > ctx->c->param_.degree_ / 2 || num_diag < 1 || !diag_idx ||
+      !diag_re || !diag_im || bs < 1 || gs < 1)
+    return set_error(CHD_ERR_ARG,
+                     "chd_linear_transform_create: invalid argument");
+  CHD_TRY cheddar::StreamScope scope(static_cast<hipStream_t>(stream));
+  cheddar::StripedMatrix mat(dim, dim);
+  for (int k = 0; k < num_diag; k++) {
+    if (!diag_re[k] || !diag_im[k])
+      throw cheddar::Error("null diagonal pointer");
+    std::vector<cheddar::Complex> d(dim);
+    for (int j = 0; j < dim; j++)
+      d[j] = cheddar::Complex(diag_re[k][j], diag_im[k][j]);
+    mat[diag_idx[k]] = std::move(d);
+  }
+  std::unique_ptr<chd_hoist> h(new chd_hoist);
+  h->c = ctx->c;
+  h->level = level;
+  h->lt.reset(new cheddar::LinearTransform<word>(
+      ctx->c, mat, level, pt_scale, bs, gs, pre_rotation, additional_pt_rot));
+  h->h = &h->lt->GetHoistHandler();
+  cheddar::HipCheck(hipStreamSynchronize(cheddar::CurrentStream()),
+                    "hipStreamSynchronize");
+  *out = h.release();
+  return 0;
+  CHD_CATCH("chd_linear_transform_create")
+}
+
+
 
 extern "C" int chd_hoist_evaluate(
     const chd_context *ctx, int level, uint32_t *res_bx, uint32_t *res_ax,

@@ -3,6 +3,7 @@
 #include "cheddar.h"
 
 #include <algorithm>
+#include <numeric>
 #include <climits>
 #include <cmath>
 
@@ -1361,8 +1362,17 @@ Context<uint32_t>::EvkRef Context<uint32_t>::RefOfKey(const Evk &k) {
 }
 
 // ---------------------------------------------------------- HoistHandler --
-// src/extension/Hoist.cu:131-177 (CompilePlaintexts / ExtractBSIndices on
-// already encoded plaintexts)
+// src/core/EvkRequest.cpp:7-17
+void EvkRequest::AddRequest(int rot_idx, int level) {
+  AssertTrue(rot_idx >= 0, "Invalid rotation index");
+  AssertTrue(level >= 0, "Invalid level");
+  auto it = find(rot_idx);
+  if (it == end())
+    emplace(rot_idx, level);
+  else if (it->second < level)
+    it->second = level;
+}
+
 // Hoist.cu:131-145 (CompilePlaintexts) and 146-173 (the bs/gs swap)
 HoistHandler<uint32_t>::PtMap HoistHandler<uint32_t>::EncodeMap(
     const Context<word> &context, const PlainHoistMap &hoist_map,
@@ -1443,6 +1453,7 @@ HoistHandler<uint32_t>::HoistHandler(ConstContextPtr<word> context,
     }
     HipCheck(hipStreamSynchronize(CurrentStream()), "hipStreamSynchronize");
     pt_map_ = std::move(conv);
+    gs_only_ = pt_map_.at(0).size() > 1 || pt_map_.at(0).count(0) == 0;
   }
   for (const auto &[gs, bs_map] : pt_map_) {
     gs_indices_.push_back(gs);
@@ -1453,8 +1464,42 @@ HoistHandler<uint32_t>::HoistHandler(ConstContextPtr<word> context,
   AssertTrue(bs_indices_.size() <= 64, "Hoist: too many baby steps");
 }
 
-std::set<int> HoistHandler<uint32_t>::RequiredRotations() const {
+// Hoist.cu:178-204: the baby and giant steps must be 0, s, 2s, ..., ks
+std::pair<int, int> HoistHandler<uint32_t>::CheckStrideMinKS() const {
+  AssertTrue(!gs_only_, "Hoist: min_ks should be false for bs == 1 case");
+  auto stride = [](auto begin, auto end, const char *what) {
+    int count = 0, g = 0, mx = 0;
+    for (auto it = begin; it != end; ++it) {
+      if (*it == 0) continue;
+      g = std::gcd(g, *it);
+      count++;
+      mx = std::max(mx, *it);
+    }
+    AssertTrue(count * g == mx, std::string("MinKS does not apply to the "
+                                            "given hoist map ") + what);
+    return g;
+  };
+  return {stride(bs_indices_.begin(), bs_indices_.end(), "baby-step sequence"),
+          stride(gs_indices_.begin(), gs_indices_.end(),
+                 "giant-step sequence")};
+}
+
+// Hoist.cu:978-1004
+void HoistHandler<uint32_t>::AddRequiredRotations(EvkRequest &req,
+                                                  bool min_ks) const {
+  for (int r : RequiredRotations(min_ks)) req.AddRequest(r, pt_level_);
+}
+
+std::set<int> HoistHandler<uint32_t>::RequiredRotations(bool min_ks) const {
   std::set<int> r;
+  if (min_ks) {
+    const auto [bs_stride, gs_stride] = CheckStrideMinKS();
+    r.insert(bs_stride);
+    r.insert(gs_stride);
+    return r;
+  }
+  // a giant-step-only map asks for its giant steps, which here are the
+  // baby steps of the converted map: the same set
   for (int b : bs_indices_)
     if (b != 0) r.insert(b);
   for (int g : gs_indices_)
@@ -1464,10 +1509,11 @@ std::set<int> HoistHandler<uint32_t>::RequiredRotations() const {
 
 void HoistHandler<uint32_t>::Evaluate(ConstContextPtr<word> context, Ct &res,
                                       const Ct &input,
-                                      const EvkMap<word> &evk_map) const {
+                                      const EvkMap<word> &evk_map,
+                                      bool min_ks) const {
   std::map<int, Ct> bs;
-  EvaluateBabyStep(context, bs, input, evk_map);
-  EvaluateGiantStep(context, res, bs, evk_map);
+  EvaluateBabyStep(context, bs, input, evk_map, min_ks);
+  EvaluateGiantStep(context, res, bs, evk_map, min_ks);
 }
 
 // src/extension/Hoist.cu:578-691 (hoisted path with BSFusedKeyMult): one
@@ -1476,23 +1522,162 @@ void HoistHandler<uint32_t>::Evaluate(ConstContextPtr<word> context, Ct &res,
 // in the extended basis (q and alpha aux limbs), not divided by P.
 void HoistHandler<uint32_t>::EvaluateBabyStep(
     ConstContextPtr<word> context, std::map<int, Ct> &bs, const Ct &input,
-    const EvkMap<word> &evk_map) const {
-  BabyStep(*context, bs, input, [&](int r) {
-    return Context<word>::RefOfKey(evk_map.GetRotationKey(r));
-  });
+    const EvkMap<word> &evk_map, bool min_ks) const {
+  BabyStep(
+      *context, bs, input,
+      [&](int r) { return Context<word>::RefOfKey(evk_map.GetRotationKey(r)); },
+      min_ks);
 }
 
 void HoistHandler<uint32_t>::EvaluateGiantStep(
     ConstContextPtr<word> context, Ct &res, const std::map<int, Ct> &bs,
-    const EvkMap<word> &evk_map) const {
-  GiantStep(*context, res, bs, [&](int r) {
-    return Context<word>::RefOfKey(evk_map.GetRotationKey(r));
-  });
+    const EvkMap<word> &evk_map, bool min_ks) const {
+  GiantStep(
+      *context, res, bs,
+      [&](int r) { return Context<word>::RefOfKey(evk_map.GetRotationKey(r)); },
+      min_ks);
+}
+
+namespace {
+// HRot at the view level (Context.cpp:776-791): MultKey, then Permute by the
+// amount reduced modulo the slot count
+void HRotV(const Context<uint32_t> &ctx, int level, uint32_t *res_b,
+           uint32_t *res_a, const uint32_t *b, const uint32_t *a,
+           const Context<uint32_t>::EvkRef &key, int amount, int slots) {
+  const size_t words =
+      static_cast<size_t>(ctx.param_.LevelToNP(level).GetNumQ()) *
+      ctx.param_.degree_;
+  int r = amount % slots;
+  if (r < 0) r += slots;
+  Workspace::Use use_ws(ctx.GetWorkspace());
+  Scratch t(ctx.GetWorkspace(), 2 * words);
+  if (r == 0) {
+    ctx.PermuteV(level, {res_b, res_a, nullptr}, {b, a, nullptr}, 0);
+    return;
+  }
+  ctx.MultKeyV(level, {t.data(), t.data() + words, nullptr},
+               {b, a, nullptr}, key);
+  ctx.PermuteV(level, {res_b, res_a, nullptr},
+               {t.data(), t.data() + words, nullptr}, r);
+}
+}  // namespace
+
+// Hoist.cu:517-537: bs[0] = input, bs[k s] = HRot(bs[(k - 1) s], s)
+void HoistHandler<uint32_t>::MinKSBabyStep(const Context<word> &ctx,
+                                           std::map<int, Ct> &bs,
+                                           const Ct &input,
+                                           const KeyLookup &key_of) const {
+  const int bs_stride = CheckStrideMinKS().first;
+  const NPInfo np = input.GetNP();
+  const size_t bytes = static_cast<size_t>(np.GetNumQ()) *
+                       ctx.param_.degree_ * sizeof(word);
+  auto slot = [&](int idx) -> Ct & {
+    Ct &ct = bs.try_emplace(idx, np).first->second;
+    if (!(ct.GetNP() == np) || ct.HasRx()) ct = Ct(np);
+    ct.SetScale(input.GetScale());
+    ct.SetNumSlots(input.GetNumSlots());
+    return ct;
+  };
+  for (int b : bs_indices_) {
+    Ct &out = slot(b);
+    if (b == 0) {
+      HipCheck(hipMemcpyAsync(out.bx_.data(), input.bx_.data(), bytes,
+                              hipMemcpyDeviceToDevice, CurrentStream()),
+               "hipMemcpyAsync");
+      HipCheck(hipMemcpyAsync(out.ax_.data(), input.ax_.data(), bytes,
+                              hipMemcpyDeviceToDevice, CurrentStream()),
+               "hipMemcpyAsync");
+      continue;
+    }
+    auto prev = bs.find(b - bs_stride);
+    AssertTrue(prev != bs.end(),
+               "Hoist: MinKS baby-step sequence is not complete");
+    HRotV(ctx, pt_level_, out.bx_.data(), out.ax_.data(),
+          prev->second.bx_.data(), prev->second.ax_.data(), key_of(bs_stride),
+          bs_stride, prev->second.GetNumSlots());
+  }
+}
+
+// Hoist.cu:539-566: giant steps from the last down, each accumulation added
+// to the rotated running sum (PAccum with inplace), HRot by the giant-step
+// stride unless at giant step 0, then Rescale
+void HoistHandler<uint32_t>::MinKSGiantStep(const Context<word> &ctx, Ct &res,
+                                            const std::map<int, Ct> &bs,
+                                            const KeyLookup &key_of) const {
+  const int gs_stride = CheckStrideMinKS().second;
+  const Parameter<word> &param = ctx.param_;
+  const int n = param.degree_;
+  const NPInfo np = param.LevelToNP(pt_level_);
+  const size_t qw = static_cast<size_t>(np.GetNumQ()) * n;
+  const Ct &ref = bs.begin()->second;
+  AssertTrue(ref.GetNP() == np, "Hoist: baby-step level mismatch");
+  int num_slots = ref.GetNumSlots();
+  for (const auto &[g, pmap] : pt_map_)
+    for (const auto &[b, pt] : pmap) {
+      AssertTrue(bs.count(b) != 0, "Hoist: missing baby step");
+      AssertTrue(bs.at(b).GetNP() == np, "Hoist: baby-step level mismatch");
+      num_slots = std::max({num_slots, pt.GetNumSlots(),
+                            bs.at(b).GetNumSlots()});
+    }
+  Workspace *ws = ctx.GetWorkspace();
+  Workspace::Use use_ws(ws);
+  Scratch acc(ws, 2 * qw);
+  const chd_limb_map m = NoSkipMap(param, np);
+  bool first = true;
+  int prev = 0;
+  for (auto it = pt_map_.rbegin(); it != pt_map_.rend(); ++it) {
+    const int g = it->first;
+    const std::map<int, Pt> &pmap = it->second;
+    // accumulation over this giant step's baby steps (q limbs of each
+    // plaintext), onto the rotated running sum after the first
+    std::vector<int> bsv;
+    for (const auto &[b, pt] : pmap) bsv.push_back(b);
+    for (size_t b0 = 0; b0 < bsv.size(); b0 += CHD_GS_MAX_BS) {
+      const int bcnt =
+          static_cast<int>(std::min<size_t>(CHD_GS_MAX_BS, bsv.size() - b0));
+      chd_gs_args a{};
+      a.num_bs = bcnt;
+      a.num_gs = 1;
+      a.add_to_dst = (!first || b0 > 0) ? 1 : 0;
+      for (int j = 0; j < bcnt; j++) {
+        const Ct &ct = bs.at(bsv[b0 + j]);
+        a.bs_b[j] = ct.bx_.data();
+        a.bs_a[j] = ct.ax_.data();
+        a.pt[0][j] = pmap.at(bsv[b0 + j]).mx_.data();
+      }
+      a.dst_b[0] = acc.data();
+      a.dst_a[0] = acc.data() + qw;
+      K(chd_k_gs_fused(&ctx.ntt_handler_.Tables(), &m, &a, np.GetNumQ(),
+                       CurrentStream()));
+    }
+    if (!first)
+      AssertTrue(prev == g + gs_stride,
+                 "Hoist: MinKS giant-step sequence is not complete");
+    if (g != 0)
+      HRotV(ctx, pt_level_, acc.data(), acc.data() + qw, acc.data(),
+            acc.data() + qw, key_of(gs_stride), gs_stride, num_slots);
+    else
+      AssertTrue(first || prev == gs_stride,
+                 "Hoist: MinKS giant-step sequence is not complete");
+    first = false;
+    prev = g;
+  }
+  const NPInfo out_np = param.LevelToNP(pt_level_ - 1);
+  if (!(res.GetNP() == out_np) ||
+      res.bx_.size() != static_cast<size_t>(out_np.GetNumTotal()) * n ||
+      res.HasRx())
+    res = Ct(out_np);
+  ctx.RescaleV(pt_level_, {res.bx_.data(), res.ax_.data(), nullptr},
+               {acc.data(), acc.data() + qw, nullptr});
+  res.SetNumSlots(num_slots);
+  res.SetScale(pt_scale_ * ref.GetScale() /
+               param.GetRescalePrimeProd(pt_level_));
 }
 
 void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
                                       std::map<int, Ct> &bs, const Ct &input,
-                                      const KeyLookup &key_of) const {
+                                      const KeyLookup &key_of,
+                                      bool min_ks) const {
   const Parameter<word> &param = ctx.param_;
   const int n = param.degree_;
   const NPInfo in_np = input.GetNP();
@@ -1505,6 +1690,10 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
   for (const auto &[idx, ct] : bs)
     AssertTrue(bs_indices_.count(idx) != 0,
                "Hoist: bs holds a baby step this handler does not use");
+  if (min_ks) {
+    MinKSBabyStep(ctx, bs, input, key_of);
+    return;
+  }
   const int num_q = in_np.GetNumQ();
   const int alpha = param.alpha_;
   const int total = num_q + alpha;
@@ -1602,10 +1791,15 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
 // PermuteAccum are folded into the same permuted sum (Permute is linear).
 void HoistHandler<uint32_t>::GiantStep(const Context<word> &ctx, Ct &res,
                                        const std::map<int, Ct> &bs,
-                                       const KeyLookup &key_of) const {
+                                       const KeyLookup &key_of,
+                                       bool min_ks) const {
   const Parameter<word> &param = ctx.param_;
   const int n = param.degree_;
   AssertTrue(!bs.empty(), "Hoist: bs should not be empty");
+  if (min_ks) {
+    MinKSGiantStep(ctx, res, bs, key_of);
+    return;
+  }
   const Ct &ref = bs.begin()->second;
   const NPInfo ext_np = ref.GetNP();
   const int alpha = param.alpha_;
@@ -1701,5 +1895,109 @@ void HoistHandler<uint32_t>::GiantStep(const Context<word> &ctx, Ct &res,
   res.SetNumSlots(num_slots);
   res.SetScale(pt_scale_ * input_scale / param.GetRescalePrimeProd(pt_level_));
 }
+
+// ------------------------------------------------------- StripedMatrix --
+// src/extension/StripedMatrix.cpp:17-47
+StripedMatrix StripedMatrix::Mult(const StripedMatrix &a,
+                                  const StripedMatrix &b) {
+  AssertTrue(a.width_ == a.height_ && b.width_ == b.height_,
+             "StripedMatrix must be square to perform multiplication");
+  AssertTrue(a.GetHeight() == b.GetWidth(), "StripedMatrix dimension mismatch");
+  const int w = a.width_;
+  StripedMatrix c(w, w);
+  for (const auto &[i, da] : a)
+    for (const auto &[j, db] : b) {
+      std::vector<Complex> &dc =
+          c.try_emplace((i + j) % w, std::vector<Complex>(w)).first->second;
+      for (int k = 0; k < w; k++) dc[k] += da[k] * db[(k + i) % w];
+    }
+  return c;
+}
+
+StripedMatrix StripedMatrix::Mult(const StripedMatrix &a, const Complex b) {
+  StripedMatrix c(a.GetHeight(), a.GetWidth());
+  for (const auto &[i, d] : a) {
+    std::vector<Complex> &dc = c.try_emplace(i, d.size()).first->second;
+    for (size_t j = 0; j < d.size(); j++) dc[j] = d[j] * b;
+  }
+  return c;
+}
+
+// ----------------------------------------------------- LinearTransform --
+// src/extension/LinearTransform.cpp:9-38: the gcd of the diagonals' rotation
+// amounts after the pre-rotation
+int LinearTransform<uint32_t>::DetermineStride(const StripedMatrix &matrix,
+                                               int bs, int gs,
+                                               int pre_rotation) {
+  const int width = matrix.GetWidth();
+  AssertTrue(width > 0, "LinearTransform requires a positive width");
+  int gcd_rot = 0, max_rot = 0, num_pt = 0;
+  for (const auto &[i, diag] : matrix) {
+    num_pt++;
+    int rot = (i - pre_rotation) % width;
+    if (rot < 0) rot += width;
+    gcd_rot = std::gcd(gcd_rot, rot);
+    max_rot = std::max(max_rot, rot);
+  }
+  AssertTrue(num_pt > 1, "LinearTransform requires at least 2 plaintexts");
+  AssertTrue(gcd_rot > 0, "Something went wrong during LinearTransform setup");
+  AssertTrue(max_rot <= (bs * gs - 1) * gcd_rot,
+             "Incompatible matrix and LinearTransform parameters: bs (" +
+                 std::to_string(bs) + "), gs (" + std::to_string(gs) +
+                 "), pre_rotation (" + std::to_string(pre_rotation) + ")");
+  return gcd_rot;
+}
+
+// LinearTransform.cpp:40-72: diagonal rot = gs_rot + bs_rot with bs_rot below
+// stride * bs; its message is the diagonal rotated right by
+// gs_rot - additional_pt_rot (the giant step's rotation undone ahead)
+HoistHandler<uint32_t>::PlainHoistMap
+LinearTransform<uint32_t>::ConstructPlainHoistMap(const StripedMatrix &matrix,
+                                                  int bs, int gs,
+                                                  int pre_rotation,
+                                                  int additional_pt_rot) {
+  const int height = matrix.GetHeight();
+  const int width = matrix.GetWidth();
+  auto pow2 = [](int v) {
+    AssertTrue(v > 0, "IsPowOfTwo only accepts positive values");
+    return (v & (v - 1)) == 0;
+  };
+  AssertTrue(pow2(height), "LinearTransform requires power-of-two height");
+  AssertTrue(pow2(width), "LinearTransform requires power-of-two width");
+  AssertTrue(height == width, "LinearTransform requires square matrix");
+  const int gs_stride = DetermineStride(matrix, bs, gs, pre_rotation) * bs;
+  HoistHandler<word>::PlainHoistMap map;
+  for (const auto &[i, diag] : matrix) {
+    AssertTrue(static_cast<int>(diag.size()) >= height,
+               "LinearTransform: diagonal shorter than the matrix");
+    int rot = (i - pre_rotation) % width;
+    if (rot < 0) rot += width;
+    const int bs_rot = rot % gs_stride;
+    const int gs_rot = rot - bs_rot;
+    std::vector<Complex> &msg =
+        map[gs_rot].try_emplace(bs_rot, height, Complex(0)).first->second;
+    int offset = (gs_rot - additional_pt_rot) % height;
+    if (offset < 0) offset += height;
+    for (int j = 0; j < height; j++) msg[(j + offset) % height] = diag[j];
+  }
+  return map;
+}
+
+// LinearTransform.cpp:74-88
+LinearTransform<uint32_t>::LinearTransform(ConstContextPtr<word> context,
+                                           const StripedMatrix &matrix,
+                                           int pt_level, double pt_scale,
+                                           int bs, int gs, int pre_rotation,
+                                           int additional_pt_rot)
+    : pt_level_(pt_level),
+      pt_scale_(pt_scale),
+      bs_(bs),
+      gs_(gs),
+      pre_rotation_(pre_rotation),
+      additional_pt_rot_(additional_pt_rot),
+      hoist_(context,
+             ConstructPlainHoistMap(matrix, bs, gs, pre_rotation,
+                                    additional_pt_rot),
+             pt_level, pt_scale) {}
 
 }  // namespace cheddar

@@ -340,6 +340,15 @@ class EvkMap<uint32_t>
   const EvaluationKey<uint32_t> &GetRotationKey(int rot_idx) const;
 };
 
+// Rotation-key request (include/core/EvkRequest.h, src/core/EvkRequest.cpp):
+// rotation index -> the highest level a key is needed at.
+class EvkRequest : public std::map<int, int> {
+ public:
+  using Base = std::map<int, int>;
+  using Base::Base;
+  void AddRequest(int rot_idx, int level);
+};
+
 template <typename word>
 class NTTHandler;
 template <>
@@ -635,33 +644,105 @@ class HoistHandler<uint32_t> {
   HoistHandler &operator=(const HoistHandler &) = delete;
   HoistHandler(HoistHandler &&) = default;
 
-  // rotation keys Evaluate needs (AddRequiredRotations, Hoist.cu:978-995)
-  std::set<int> RequiredRotations() const;
+  // rotation keys Evaluate needs (Hoist.cu:978-1004); with min_ks the two
+  // strides of the baby- and giant-step sequences
+  void AddRequiredRotations(EvkRequest &req, bool min_ks = false) const;
+  std::set<int> RequiredRotations(bool min_ks = false) const;
+  // min_ks (Hoist.cu:517-566): baby steps by repeated HRot with the
+  // baby-step stride, giant steps Horner-style with the giant-step stride,
+  // so only two rotation keys are needed
   void Evaluate(ConstContextPtr<word> context, Ct &res, const Ct &input,
-                const EvkMap<word> &evk_map) const;
+                const EvkMap<word> &evk_map, bool min_ks = false) const;
   void EvaluateBabyStep(ConstContextPtr<word> context, std::map<int, Ct> &bs,
-                        const Ct &input, const EvkMap<word> &evk_map) const;
+                        const Ct &input, const EvkMap<word> &evk_map,
+                        bool min_ks = false) const;
   void EvaluateGiantStep(ConstContextPtr<word> context, Ct &res,
                          const std::map<int, Ct> &bs,
-                         const EvkMap<word> &evk_map) const;
+                         const EvkMap<word> &evk_map,
+                         bool min_ks = false) const;
 
   // the same with keys looked up by rotation index through a callback
   // (used by the C-ABI, whose keys are raw device pointers)
   using KeyLookup = std::function<Context<word>::EvkRef(int)>;
   void BabyStep(const Context<word> &ctx, std::map<int, Ct> &bs,
-                const Ct &input, const KeyLookup &key) const;
+                const Ct &input, const KeyLookup &key,
+                bool min_ks = false) const;
   void GiantStep(const Context<word> &ctx, Ct &res,
-                 const std::map<int, Ct> &bs, const KeyLookup &key) const;
+                 const std::map<int, Ct> &bs, const KeyLookup &key,
+                 bool min_ks = false) const;
 
  private:
   int pt_level_;
   double pt_scale_;
+  std::pair<int, int> CheckStrideMinKS() const;
+  void MinKSBabyStep(const Context<word> &ctx, std::map<int, Ct> &bs,
+                     const Ct &input, const KeyLookup &key_of) const;
+  void MinKSGiantStep(const Context<word> &ctx, Ct &res,
+                      const std::map<int, Ct> &bs,
+                      const KeyLookup &key_of) const;
   static PtMap EncodeMap(const Context<word> &context,
                          const PlainHoistMap &hoist_map, int pt_level,
                          double pt_scale, bool suppress_bs_swap);
   PtMap pt_map_;
   std::set<int> bs_indices_;
   std::vector<int> gs_indices_;
+  bool gs_only_ = false;  // a giant-step-only map, evaluated converted
+};
+
+// Square matrix by its generalised diagonals (include/extension/
+// StripedMatrix.h, src/extension/StripedMatrix.cpp): diagonal i holds
+// M[j][(j + i) % width] at j.
+class StripedMatrix : public std::map<int, std::vector<Complex>> {
+ public:
+  using Base = std::map<int, std::vector<Complex>>;
+  explicit StripedMatrix(int height = 0, int width = 0)
+      : height_(height), width_(width) {}
+  int GetHeight() const { return height_; }
+  int GetWidth() const { return width_; }
+  int GetNumDiag() const { return static_cast<int>(size()); }
+  static StripedMatrix Mult(const StripedMatrix &a, const StripedMatrix &b);
+  static StripedMatrix Mult(const StripedMatrix &a, const Complex b);
+
+ private:
+  int height_, width_;
+};
+
+// Matrix-vector product by BSGS over a HoistHandler
+// (include/extension/LinearTransform.h, src/extension/LinearTransform.cpp).
+template <typename word>
+class LinearTransform;
+template <>
+class LinearTransform<uint32_t> {
+ public:
+  using word = uint32_t;
+  using Ct = Ciphertext<word>;
+  LinearTransform(ConstContextPtr<word> context, const StripedMatrix &matrix,
+                  int pt_level, double pt_scale, int bs, int gs = 1,
+                  int pre_rotation = 0, int additional_pt_rot = 0);
+  bool IsUsingBSGS() const { return bs_ > 1 && gs_ > 1; }
+  int GetBS() const { return bs_; }
+  int GetGS() const { return gs_; }
+  int GetPreRotationAmount() const { return pre_rotation_; }
+  void AddRequiredRotations(EvkRequest &req, bool min_ks = false) const {
+    hoist_.AddRequiredRotations(req, min_ks);
+  }
+  void Evaluate(ConstContextPtr<word> context, Ct &res, const Ct &input,
+                const EvkMap<word> &evk_map, bool min_ks = false) const {
+    hoist_.Evaluate(context, res, input, evk_map, min_ks);
+  }
+  const HoistHandler<word> &GetHoistHandler() const { return hoist_; }
+  // the reference's hoist map for a matrix (LinearTransform.cpp:40-72)
+  static HoistHandler<word>::PlainHoistMap ConstructPlainHoistMap(
+      const StripedMatrix &matrix, int bs, int gs, int pre_rotation,
+      int additional_pt_rot);
+
+ private:
+  static int DetermineStride(const StripedMatrix &matrix, int bs, int gs,
+                             int pre_rotation);
+  int pt_level_;
+  double pt_scale_;
+  int bs_, gs_, pre_rotation_, additional_pt_rot_;
+  HoistHandler<word> hoist_;
 };
 
 }  // namespace cheddar

@@ -73,6 +73,12 @@ _SIGS = {
                                 _pp, _i, _ip, _pp, _pp, _i, _vp]),
     "chd_hoist_create": (_i, [_pp, _vp, _i, _i, _ip, _i, _ip, _pp, _vp]),
     "chd_hoist_destroy": (None, [_vp]),
+    "chd_hoist_run_min_ks": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _ip, _pp, _pp,
+                                  _i, _vp]),
+    "chd_hoist_required_rotations": (_i, [_vp, _i, _ip, _i]),
+    "chd_linear_transform_create": (_i, [_pp, _vp, _i, ctypes.c_double, _i,
+                                         _i, _ip, _pp, _pp, _i, _i, _i, _i,
+                                         _vp]),
     "chd_hoist_create_from_messages": (_i, [_pp, _vp, _i, ctypes.c_double,
                                             _i, _ip, _i, _ip, _pp, _pp, _ip,
                                             _i, _vp]),
@@ -392,8 +398,38 @@ class Hoist:
             lib.chd_hoist_destroy(self.h)
             self.h = None
 
-    def run(self, res, ct, keys, stream=None):
+    @classmethod
+    def linear_transform(cls, ctx, level, pt_scale, dim, diags, bs, gs=1,
+                         pre_rotation=0, additional_pt_rot=0, stream=None):
+        """LinearTransform of a dim x dim matrix given by its generalised
+        diagonals {i: complex array of dim values}"""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        idx = sorted(diags)
+        parts = [_split(diags[i]) for i in idx]
+        self._keep = parts
+        re = (ctypes.c_void_p * len(idx))(*[p[0].ctypes.data for p in parts])
+        im = (ctypes.c_void_p * len(idx))(*[p[1].ctypes.data for p in parts])
+        h = ctypes.c_void_p()
+        _check(lib.chd_linear_transform_create(
+            ctypes.byref(h), ctx.h, level, pt_scale, dim, len(idx),
+            (ctypes.c_int * len(idx))(*idx), re, im, bs, gs, pre_rotation,
+            additional_pt_rot,
+            stream if stream is not None else current_stream()))
+        self.h = h
+        return self
+
+    def required_rotations(self, min_ks=False):
+        n = lib.chd_hoist_required_rotations(self.h, int(min_ks), None, 0)
+        if n < 0:
+            _check(n)
+        out = (ctypes.c_int * max(n, 1))()
+        lib.chd_hoist_required_rotations(self.h, int(min_ks), out, n)
+        return list(out[:n])
+
+    def run(self, res, ct, keys, min_ks=False, stream=None):
         kr, kb, ka, nk, beta = Context._keys(keys)
-        _check(lib.chd_hoist_run(
+        fn = lib.chd_hoist_run_min_ks if min_ks else lib.chd_hoist_run
+        _check(fn(
             self.h, ptr(res[0]), ptr(res[1]), ptr(ct[0]), ptr(ct[1]), nk, kr,
             kb, ka, beta, stream if stream is not None else current_stream()))

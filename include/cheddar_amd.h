@@ -206,6 +206,34 @@ int chd_hoist_run(const chd_hoist *h, uint32_t *res_bx, uint32_t *res_ax,
                   const uint32_t *ct_bx, const uint32_t *ct_ax, int num_keys,
                   const int *key_rot, const uint32_t *const *key_bx,
                   const uint32_t *const *key_ax, int key_beta, void *stream);
+/* HoistHandler::Evaluate with min_ks (Hoist.cu:517-566): baby steps by
+ * repeated HRot with the baby-step stride, giant steps Horner-style with the
+ * giant-step stride, then Rescale; only the two stride keys are needed.
+ * Same arguments as chd_hoist_run. */
+int chd_hoist_run_min_ks(const chd_hoist *h, uint32_t *res_bx,
+                         uint32_t *res_ax, const uint32_t *ct_bx,
+                         const uint32_t *ct_ax, int num_keys,
+                         const int *key_rot, const uint32_t *const *key_bx,
+                         const uint32_t *const *key_ax, int key_beta,
+                         void *stream);
+/* HoistHandler::AddRequiredRotations (Hoist.cu:978-1004): writes up to
+ * capacity rotation indices (ascending) into out and returns how many the
+ * handler needs. */
+int chd_hoist_required_rotations(const chd_hoist *h, int min_ks, int *out,
+                                 int capacity);
+/* LinearTransform (src/extension/LinearTransform.cpp:40-88): a dim x dim
+ * matrix (dim a power of two) given by num_diag generalised diagonals,
+ * diagonal diag_idx[k] = (diag_re[k][j], diag_im[k][j]) = M[j][(j + i) % dim],
+ * as a hoisting handle (run with chd_hoist_run / chd_hoist_run_min_ks,
+ * destroy with chd_hoist_destroy). bs, gs, pre_rotation and
+ * additional_pt_rot have the reference's meaning. Synchronises the stream. */
+int chd_linear_transform_create(chd_hoist **out, const chd_context *ctx,
+                                int level, double pt_scale, int dim,
+                                int num_diag, const int *diag_idx,
+                                const double *const *diag_re,
+                                const double *const *diag_im, int bs, int gs,
+                                int pre_rotation, int additional_pt_rot,
+                                void *stream);
 /* HoistHandler::Evaluate (Hoist.cu:569-576, 840-975, 487-515): baby steps
  * bs[0..num_bs), giant steps gs[0..num_gs) (gs must contain 0 when
  * num_gs > 1), plaintexts pt[g * num_bs + b] (num_q(level) + alpha limbs in

@@ -232,6 +232,89 @@ int main() {
                                         wup.begin() + (g + 1) * kw));
     check("mod_switch_handlers_[level].ModUp", ok);
   }
+  // encoder member (Context.h:88): Encode / Decode round trip within the
+  // reference's EncodeDecode tolerance (Testbed.h:93), EncodeConstant
+  {
+    std::vector<Complex> msg(1 << 12);
+    for (auto &m : msg)
+      m = Complex((next64() % 2001) / 1000.0 - 1.0,
+                  (next64() % 2001) / 1000.0 - 1.0);
+    Plaintext<word> pt;
+    ctx->encoder_.Encode(pt, L - 1, 0x1p30, msg);
+    std::vector<Complex> back;
+    ctx->encoder_.Decode(back, pt);
+    double err = 0;
+    for (size_t i = 0; i < msg.size(); i++)
+      err = std::max(err, std::abs(back[i] - msg[i]));
+    check("Encoder Encode/Decode round trip",
+          pt.GetNumSlots() == (1 << 12) && pt.GetNP() == np && err < 1e-3);
+    Constant<word> c;
+    ctx->encoder_.EncodeConstant(c, 3, 0x1p20, -1.5);
+    std::vector<word> cx = download(c.cx_.data(), c.cx_.size());
+    bool ok = cx.size() == 4;
+    for (int i = 0; i < 4 && ok; i++) {
+      const uint64_t p = main_p[i];
+      const uint64_t v = (p - (uint64_t{3} << 19) % p) % p;  // -1.5 * 2^20
+      ok = cx[i] == (v << 32) % p;
+    }
+    check("Encoder EncodeConstant", ok);
+  }
+  // EvkRequest keeps the highest level per rotation (EvkRequest.cpp:7-17)
+  {
+    EvkRequest req;
+    req.AddRequest(3, 5);
+    req.AddRequest(3, 2);
+    req.AddRequest(7, 1);
+    req.AddRequest(3, 9);
+    check("EvkRequest", req.size() == 2 && req.at(3) == 9 && req.at(7) == 1);
+  }
+  // StripedMatrix::Mult against the dense product (StripedMatrix.cpp:17-36)
+  {
+    const int w = 8;
+    StripedMatrix a(w, w), b(w, w);
+    for (int i : {0, 1, 5}) {
+      a[i].resize(w);
+      for (auto &v : a[i]) v = Complex(int(next64() % 7) - 3, int(next64() % 5) - 2);
+    }
+    for (int i : {2, 3}) {
+      b[i].resize(w);
+      for (auto &v : b[i]) v = Complex(int(next64() % 7) - 3, int(next64() % 5) - 2);
+    }
+    auto dense = [](const StripedMatrix &m) {
+      std::vector<Complex> d(w * w);
+      for (const auto &[i, diag] : m)
+        for (int j = 0; j < w; j++) d[j * w + (j + i) % w] += diag[j];
+      return d;
+    };
+    const std::vector<Complex> da = dense(a), db = dense(b);
+    const std::vector<Complex> dc = dense(StripedMatrix::Mult(a, b));
+    bool ok = true;
+    for (int r = 0; r < w; r++)
+      for (int c2 = 0; c2 < w; c2++) {
+        Complex s = 0;
+        for (int k = 0; k < w; k++) s += da[r * w + k] * db[k * w + c2];
+        ok = ok && std::abs(s - dc[r * w + c2]) < 1e-12;
+      }
+    const std::vector<Complex> ds =
+        dense(StripedMatrix::Mult(a, Complex(0.0, 2.0)));
+    for (int k = 0; k < w * w; k++)
+      ok = ok && std::abs(ds[k] - da[k] * Complex(0.0, 2.0)) < 1e-12;
+    check("StripedMatrix::Mult", ok);
+    // LinearTransform's hoist map (LinearTransform.cpp:40-72): diagonal 5 of
+    // a bs = 2 transform lands at giant step 4, baby step 1, rotated right
+    // by 4
+    StripedMatrix m(w, w);
+    for (int i : {0, 1, 2, 5}) {
+      m[i].resize(w);
+      for (int j = 0; j < w; j++) m[i][j] = Complex(10 * i + j, 0);
+    }
+    const auto map = LinearTransform<word>::ConstructPlainHoistMap(m, 2, 3, 0, 0);
+    ok = map.size() == 3 && map.at(0).size() == 2 && map.at(2).size() == 1 &&
+         map.at(4).size() == 1 && map.at(4).count(1) == 1;
+    for (int j = 0; ok && j < w; j++)
+      ok = map.at(4).at(1)[(j + 4) % w] == Complex(50 + j, 0);
+    check("LinearTransform::ConstructPlainHoistMap", ok);
+  }
   // an invalid call throws cheddar::Error instead of exiting
   {
     bool threw = false;

@@ -139,3 +139,41 @@ def evaluate_gs_only(ct_b, ct_a, pts, keys, L, max_q, q_primes, p_primes,
     rb = _orc.mod_down(fb, primes, L - 1, log_n)
     ra = _orc.mod_down(fa, primes, L - 1, log_n)
     return rb, ra
+
+
+def evaluate_min_ks(ct_b, ct_a, pts, keys, L, max_q, q_primes, p_primes,
+                    log_n):
+    """min_ks (Hoist.cu:517-566): bs[0] = ct, bs[k s] = HRot(bs[(k-1) s], s);
+    giant steps from the last down: acc = sum_b pt[g, b] * bs[b] (q limbs of
+    each plaintext) plus the running sum, HRot by the giant-step stride
+    unless g == 0; then Rescale. keys: {stride: (key_b, key_a)}."""
+    import math
+    q = list(q_primes[:L])
+    bs_idx = sorted({b for (_, b) in pts})
+    gs_idx = sorted({g for (g, _) in pts})
+    bs_stride = math.gcd(*[b for b in bs_idx if b] or [0])
+    gs_stride = math.gcd(*[g for g in gs_idx if g] or [0])
+    bs = {0: (ct_b, ct_a)}
+    for b in bs_idx:
+        if b == 0:
+            continue
+        pb, pa = bs[b - bs_stride]
+        bs[b] = _orc.hrot(pb, pa, keys[bs_stride][0], keys[bs_stride][1], L,
+                          max_q, q_primes, p_primes, log_n, bs_stride)
+    acc = None
+    for g in reversed(gs_idx):
+        ab = np.zeros_like(ct_b) if acc is None else acc[0]
+        aa = np.zeros_like(ct_a) if acc is None else acc[1]
+        for b in bs_idx:
+            if (g, b) not in pts:
+                continue
+            pt = pts[(g, b)][:L]
+            ab = _add(ab, _mul(pt, bs[b][0], q), q)
+            aa = _add(aa, _mul(pt, bs[b][1], q), q)
+        if g != 0:
+            ab, aa = _orc.hrot(ab, aa, keys[gs_stride][0], keys[gs_stride][1],
+                               L, max_q, q_primes, p_primes, log_n, gs_stride)
+        acc = (ab, aa)
+    rb = _orc.rescale(acc[0], q_primes, L, 1, log_n)
+    ra = _orc.rescale(acc[1], q_primes, L, 1, log_n)
+    return rb, ra
