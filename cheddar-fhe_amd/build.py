@@ -35,6 +35,7 @@ SOURCES = [
     ("host/device_tables.cpp", False),
     ("host/cheddar.cpp", False),
     ("host/encoder.cpp", False),
+    ("host/param_json.cpp", False),
     ("host/capi.cpp", False),
 ]
 

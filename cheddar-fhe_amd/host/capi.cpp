@@ -216,6 +216,17 @@ extern "C" int chd_param_create(chd_param **out, int log_degree,
   CHD_CATCH("chd_param_create")
 }
 
+extern "C" int chd_param_create_json(chd_param **out, const char *json_text) {
+  if (!out || !json_text)
+    return set_error(CHD_ERR_ARG, "chd_param_create_json: invalid argument");
+  CHD_TRY
+  auto p = std::make_unique<chd_param>();
+  p->p = cheddar::ParameterFromJson(json_text);
+  *out = p.release();
+  return 0;
+  CHD_CATCH("chd_param_create_json")
+}
+
 extern "C" void chd_param_destroy(chd_param *param) { delete param; }
 
 extern "C" int chd_param_num_q(const chd_param *param, int level) {

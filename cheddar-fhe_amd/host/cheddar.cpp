@@ -150,8 +150,6 @@ Parameter<uint32_t>::Parameter(
       aux_primes_(aux_primes),
       level_config_(std::move(level_config)) {
   AssertTrue(log_degree == 16, "Parameter: only log_degree 16 is supported");
-  AssertTrue(ter_primes.empty(),
-             "Parameter: terminal primes are not supported by this build");
   AssertTrue(additional_base.first == 0 && additional_base.second == 0,
              "Parameter: additional base (sparse-secret encapsulation) is not "
              "supported by this build");
@@ -165,21 +163,36 @@ Parameter<uint32_t>::Parameter(
   };
   for (word p : main_primes_) check(p);
   for (word p : aux_primes_) check(p);
+  for (word p : ter_primes_) check(p);
+  // Parameter.cu:64-91: every level but the last has at most the available
+  // primes and more primes than the one below it (or as many, with more
+  // main primes); the last holds all of them
+  auto below = [](const std::pair<int, int> &a, const std::pair<int, int> &b) {
+    const int ta = a.first + a.second, tb = b.first + b.second;
+    return ta < tb || (ta == tb && a.first < b.first);
+  };
   std::pair<int, int> prev{0, 0};
-  for (size_t i = 0; i < level_config_.size(); i++) {
+  for (size_t i = 0; i + 1 < level_config_.size(); i++) {
     const auto &c = level_config_[i];
     AssertTrue(c.first >= 0 && c.first <= GetMaxNumMain(),
-               "Invalid number of main primes at level " + std::to_string(i));
+               "Invalid number of main primes (" + std::to_string(c.first) +
+                   ") at level " + std::to_string(i));
     AssertTrue(c.second >= 0 && c.second <= GetMaxNumTer(),
-               "Invalid number of terminal primes at level " +
+               "Invalid number of terminal primes (" +
+                   std::to_string(c.second) + ") at level " +
                    std::to_string(i));
-    AssertTrue(c.first + c.second > prev.first + prev.second &&
-                   c.first >= prev.first,
+    AssertTrue(below(prev, c),
                "Invalid level configuration at level " + std::to_string(i));
     prev = c;
   }
   AssertTrue(level_config_.back().first == GetMaxNumMain(),
-             "Invalid number of main primes at the last level");
+             "Invalid number of main primes (" +
+                 std::to_string(level_config_.back().first) +
+                 ") at the last level");
+  AssertTrue(level_config_.back().second == GetMaxNumTer(),
+             "Invalid number of terminal primes (" +
+                 std::to_string(level_config_.back().second) +
+                 ") at the last level");
   AssertTrue(default_encryption_level_ >= 0 &&
                  default_encryption_level_ <= max_level_,
              "Invalid default encryption level");
@@ -194,14 +207,19 @@ Parameter<uint32_t>::Parameter(
   chain_.insert(chain_.end(), ter_primes_.rbegin(), ter_primes_.rend());
   chain_.insert(chain_.end(), main_primes_.begin(), main_primes_.end());
   chain_.insert(chain_.end(), aux_primes_.begin(), aux_primes_.end());
-  // scales (Parameter.cu:149-193), no terminal primes
+  // scales (Parameter.cu:149-193): going down from level i to i - 1 divides
+  // by the primes that leave and multiplies by the primes that come back
   rescale_prime_prod_.assign(max_level_ + 1, 0.0);
   scale_.assign(default_encryption_level_ + 1, base_scale_);
   double s = base_scale_;
   for (int i = 1; i <= max_level_; i++) {
-    double prod = 1.0;
-    for (int j = level_config_[i - 1].first; j < level_config_[i].first; j++)
-      prod *= main_primes_[j];
+    const auto &up = level_config_[i], &lo = level_config_[i - 1];
+    double num = 1.0, den = 1.0;
+    for (int j = lo.second; j < up.second; j++) num *= ter_primes_[j];
+    for (int j = up.second; j < lo.second; j++) den *= ter_primes_[j];
+    for (int j = lo.first; j < up.first; j++) num *= main_primes_[j];
+    for (int j = up.first; j < lo.first; j++) den *= main_primes_[j];
+    const double prod = num / den;
     rescale_prime_prod_[i] = prod;
     if (i <= default_encryption_level_) {
       s = std::sqrt(s * prod);
@@ -217,6 +235,8 @@ NPInfo Parameter<uint32_t>::LevelToNP(int level, int num_aux) const {
   return NPInfo(c.first, c.second, num_aux);
 }
 
+// Parameter.cu:297-313 (the levels are ordered, so the first match is the
+// one its binary search finds)
 int Parameter<uint32_t>::NPToLevel(const NPInfo &np) const {
   for (size_t i = 0; i < level_config_.size(); i++)
     if (level_config_[i].first == np.num_main_ &&

@@ -123,6 +123,12 @@ class Parameter<uint32_t> {
   std::vector<double> scale_, rescale_prime_prod_;
 };
 
+// A parameter set from the reference's JSON layout (parameters/*.json as
+// unittest/Testbed.h:95-179 reads it); throws Error on a malformed file or
+// an unsupported set.
+std::unique_ptr<Parameter<uint32_t>> ParameterFromJson(
+    const std::string &text);
+
 // Non-owning views: (pointer, total words, aux words) (DeviceVector.h:27-72)
 template <typename word>
 class DvView {

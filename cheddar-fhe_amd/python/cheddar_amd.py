@@ -49,6 +49,7 @@ _SIGS = {
     "chd_param_create": (_i, [_pp, _i, ctypes.c_double, _i,
                               ctypes.POINTER(ctypes.c_int), _i, _c_u32p, _i,
                               _c_u32p, _i, _c_u32p, _i]),
+    "chd_param_create_json": (_i, [_pp, ctypes.c_char_p]),
     "chd_param_destroy": (None, [_vp]),
     "chd_param_num_q": (_i, [_vp, _i]),
     "chd_param_alpha": (_i, [_vp]),
@@ -208,6 +209,24 @@ class Param:
         self.alpha = lib.chd_param_alpha(h)
         self.max_level = lib.chd_param_max_level(h)
         self.evk_limbs = lib.chd_param_evk_limbs(h)
+
+    @classmethod
+    def from_json(cls, text):
+        """a parameter set in the reference's JSON layout (parameters/*.json)"""
+        import json
+        self = cls.__new__(cls)
+        h = ctypes.c_void_p()
+        _check(lib.chd_param_create_json(ctypes.byref(h), text.encode()))
+        self.h = h
+        d = json.loads(text)
+        self.main = [int(p) for p in d["main_primes"]]
+        self.ter = [int(p) for p in d.get("terminal_primes", [])]
+        self.aux = [int(p) for p in d["auxiliary_primes"]]
+        self.level_config = [tuple(c) for c in d["level_config"]]
+        self.alpha = lib.chd_param_alpha(h)
+        self.max_level = lib.chd_param_max_level(h)
+        self.evk_limbs = lib.chd_param_evk_limbs(h)
+        return self
 
     def num_q(self, level):
         return lib.chd_param_num_q(self.h, level)

@@ -93,6 +93,11 @@ int chd_param_create(chd_param **out, int log_degree, double base_scale,
                      int num_levels, const uint32_t *main_primes, int num_main,
                      const uint32_t *aux_primes, int num_aux,
                      const uint32_t *ter_primes, int num_ter);
+/* A parameter set from the reference's JSON layout (parameters/*.json:
+ * log_degree, log_default_scale, default_encryption_level, main_primes,
+ * terminal_primes, auxiliary_primes, level_config, additional_base), the
+ * file's text in json_text (unittest/Testbed.h:95-179). */
+int chd_param_create_json(chd_param **out, const char *json_text);
 void chd_param_destroy(chd_param *param);
 /* number of q limbs (main + ter) at a level; -1 on error */
 int chd_param_num_q(const chd_param *param, int level);

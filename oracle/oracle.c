@@ -454,9 +454,20 @@ void orc_moddown_epilogue_consts(const uint32_t *src_primes, int src_len,
 int orc_mod_up(uint32_t *dst, const uint32_t *src, int L,
                const uint32_t *q_primes, const uint32_t *p_primes, int alpha,
                int log_n) {
+  return orc_mod_up_ex(dst, src, L, q_primes, p_primes, alpha, 0, log_n);
+}
+
+/* Groups sit on the full chain's positions (ModSwitch.cu:200-235, 429-509):
+ * with prime_offset = max_ter - num_ter missing terminal primes in front,
+ * group g covers the level's limbs [max(0, g alpha - off),
+ * min((g+1) alpha, L + off) - off); groups that end at or before off are
+ * empty and left untouched in dst. */
+int orc_mod_up_ex(uint32_t *dst, const uint32_t *src, int L,
+                  const uint32_t *q_primes, const uint32_t *p_primes,
+                  int alpha, int prime_offset, int log_n) {
   size_t n = (size_t)1 << log_n;
   int total = L + alpha;
-  int beta = (L + alpha - 1) / alpha;
+  int beta = (L + prime_offset + alpha - 1) / alpha;
   uint32_t *primes = (uint32_t *)malloc(sizeof(uint32_t) * total);
   memcpy(primes, q_primes, sizeof(uint32_t) * L);
   memcpy(primes + L, p_primes, sizeof(uint32_t) * alpha);
@@ -466,8 +477,11 @@ int orc_mod_up(uint32_t *dst, const uint32_t *src, int L,
   uint32_t *dprimes = (uint32_t *)malloc(sizeof(uint32_t) * total);
   uint32_t *z = (uint32_t *)malloc(sizeof(uint32_t) * n * total);
   for (int g = 0; g < beta; g++) {
-    int start = g * alpha;
-    int end = (g + 1) * alpha < L ? (g + 1) * alpha : L;
+    int abs_end = (g + 1) * alpha < L + prime_offset ? (g + 1) * alpha
+                                                     : L + prime_offset;
+    if (abs_end <= prime_offset) continue;
+    int start = g * alpha - prime_offset > 0 ? g * alpha - prime_offset : 0;
+    int end = abs_end - prime_offset;
     int slen = end - start;
     int dlen = total - slen;
     for (int k = 0; k < start; k++) dprimes[k] = primes[k];
@@ -501,38 +515,81 @@ int orc_mod_up(uint32_t *dst, const uint32_t *src, int L,
 /* ------------------------------------------------------------------------ */
 void orc_mod_down(uint32_t *dst, const uint32_t *src, int src_total,
                   const uint32_t *src_primes, int dst_len, int log_n) {
-  size_t n = (size_t)1 << log_n;
   int slen = src_total - dst_len;
-  const uint32_t *sp = src_primes + dst_len;
-  uint32_t *const1 = (uint32_t *)malloc(sizeof(uint32_t) * slen);
-  int32_t *const2 = (int32_t *)malloc(sizeof(int32_t) * slen * dst_len);
-  uint32_t *inv_pp = (uint32_t *)malloc(sizeof(uint32_t) * dst_len);
-  uint32_t *pad = (uint32_t *)malloc(sizeof(uint32_t) * dst_len);
-  int32_t *centred = (int32_t *)malloc(sizeof(int32_t) * n * slen);
+  int *drop = (int *)malloc(sizeof(int) * (slen > 0 ? slen : 1));
+  int *dsrc = (int *)malloc(sizeof(int) * (dst_len > 0 ? dst_len : 1));
+  for (int i = 0; i < slen; i++) drop[i] = dst_len + i;
+  for (int k = 0; k < dst_len; k++) dsrc[k] = k;
+  orc_mod_down_ex(dst, src, src_primes, drop, slen, src_primes, dst_len, dsrc,
+                  log_n);
+  free(drop); free(dsrc);
+}
+
+/* The general form with the BitPacker restore (ModSwitch.cu:258-411, 566-684;
+ * NTT.cu:456-601, 1073-1127): the source limbs drop[0..num_drop) are divided
+ * out; destination limb k has primes dst_primes[k] and takes its kept value
+ * from source limb dst_src[k], or, when dst_src[k] < 0, is a restored prime
+ * with no source limb. With R the product of the restored primes:
+ *   c_i  = centre(INTT(src_i) (N prod_{j != i} q_j)^-1 R)        (i in drop)
+ *   z_k  = R sum_i c_i prod_{j != i} q_j mod p_k  (BConv, double Montgomery)
+ *   dst_k = MontMul(MontMul(src[dst_src[k]], ToMont(R)) - NTT(z_k),
+ *                   ToMont((prod_{i in drop} q_i)^-1))
+ * and for restored limbs the src term is 0. */
+void orc_mod_down_ex(uint32_t *dst, const uint32_t *src,
+                     const uint32_t *src_primes, const int *drop, int num_drop,
+                     const uint32_t *dst_primes, int dst_len,
+                     const int *dst_src, int log_n) {
+  size_t n = (size_t)1 << log_n;
+  int slen = num_drop;
+  uint32_t *sp = (uint32_t *)malloc(sizeof(uint32_t) * (slen > 0 ? slen : 1));
+  for (int i = 0; i < slen; i++) sp[i] = src_primes[drop[i]];
+  uint32_t *const1 = (uint32_t *)malloc(sizeof(uint32_t) * (slen > 0 ? slen : 1));
+  int32_t *const2 = (int32_t *)malloc(sizeof(int32_t) * (slen > 0 ? slen : 1) * dst_len);
+  int32_t *centred = (int32_t *)malloc(sizeof(int32_t) * n * (slen > 0 ? slen : 1));
   uint32_t *z = (uint32_t *)malloc(sizeof(uint32_t) * n * dst_len);
-  orc_modswitch_consts(sp, slen, src_primes, dst_len, log_n, 0, 0, const1,
-                       const2);
-  orc_moddown_epilogue_consts(sp, slen, src_primes, dst_len, 0, 0, inv_pp,
-                              pad);
-  for (int i = 0; i < slen; i++)
-    orc_intt_mult_const(centred + (size_t)i * n,
-                        src + (size_t)(dst_len + i) * n, log_n, sp[i],
-                        const1[i], 1);
-  orc_bconv(z, centred, slen, dst_len, const2, src_primes, log_n);
+  for (int i = 0; i < slen; i++) {
+    uint32_t m = sp[i], v = 1;
+    for (int j = 0; j < slen; j++)
+      if (j != i) v = orc_mulmod(v, sp[j], m);
+    v = orc_mulmod(v, (uint32_t)n, m);
+    v = orc_invmod(v, m);
+    for (int k = 0; k < dst_len; k++)
+      if (dst_src[k] < 0) v = orc_mulmod(v, dst_primes[k], m);
+    const1[i] = v;
+  }
   for (int k = 0; k < dst_len; k++) {
-    uint32_t q = src_primes[k];
-    uint32_t *zl = z + (size_t)k * n;
-    orc_ntt(zl, log_n, q, 0);
-    const uint32_t *s = src + (size_t)k * n;
-    uint32_t *o = dst + (size_t)k * n;
-    for (size_t c = 0; c < n; c++) {
-      uint32_t v = orc_mont_mul(s[c] % q, pad[k], q);
-      uint32_t d = v >= zl[c] ? v - zl[c] : v + q - zl[c];
-      o[c] = orc_mont_mul(d, inv_pp[k], q);
+    uint32_t m = dst_primes[k];
+    for (int i = 0; i < slen; i++) {
+      uint32_t acc = 1;
+      for (int j = 0; j < slen; j++)
+        if (j != i) acc = orc_mulmod(acc, sp[j], m);
+      acc = orc_to_mont(orc_to_mont(acc, m), m);
+      const2[(size_t)k * slen + i] = normalize(acc, m);
     }
   }
-  free(const1); free(const2); free(inv_pp); free(pad); free(centred);
-  free(z);
+  for (int i = 0; i < slen; i++)
+    orc_intt_mult_const(centred + (size_t)i * n, src + (size_t)drop[i] * n,
+                        log_n, sp[i], const1[i], 1);
+  orc_bconv(z, centred, slen, dst_len, const2, dst_primes, log_n);
+  for (int k = 0; k < dst_len; k++) {
+    uint32_t q = dst_primes[k];
+    uint32_t inv = 1, pad = 1;
+    for (int i = 0; i < slen; i++) inv = orc_mulmod(inv, sp[i] % q, q);
+    inv = orc_to_mont(orc_invmod(inv, q), q);
+    for (int j = 0; j < dst_len; j++)
+      if (dst_src[j] < 0) pad = orc_mulmod(pad, dst_primes[j] % q, q);
+    pad = orc_to_mont(pad, q);
+    uint32_t *zl = z + (size_t)k * n;
+    orc_ntt(zl, log_n, q, 0);
+    uint32_t *o = dst + (size_t)k * n;
+    const uint32_t *s = dst_src[k] >= 0 ? src + (size_t)dst_src[k] * n : NULL;
+    for (size_t c = 0; c < n; c++) {
+      uint32_t v = s ? orc_mont_mul(s[c] % q, pad, q) : 0;
+      uint32_t d = v >= zl[c] ? v - zl[c] : v + q - zl[c];
+      o[c] = orc_mont_mul(d, inv, q);
+    }
+  }
+  free(sp); free(const1); free(const2); free(centred); free(z);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -579,6 +636,34 @@ void orc_paccum(uint32_t *acc_b, uint32_t *acc_a, const uint32_t *modup,
         uint64_t m = modup[(size_t)g * total * n + (size_t)l * n + c];
         sb += m * key_b[g * key_stride + (size_t)kl * n + c] % q;
         sa += m * key_a[g * key_stride + (size_t)kl * n + c] % q;
+      }
+      acc_b[(size_t)l * n + c] = (uint32_t)((sb % q) * ri % q);
+      acc_a[(size_t)l * n + c] = (uint32_t)((sa % q) * ri % q);
+    }
+  }
+}
+
+/* PAccum over the non-empty groups of a ModUp with a prime offset
+ * (Context.cpp:609-647): modup group j is paired with key group key_group[j];
+ * q limb l reads key limb key_off + l, aux limb L + k reads max_q + k. */
+void orc_paccum_ex(uint32_t *acc_b, uint32_t *acc_a, const uint32_t *modup,
+                   int num_groups, const int *key_group, const uint32_t *key_b,
+                   const uint32_t *key_a, int L, int alpha, int max_q,
+                   int key_off, const uint32_t *primes, int log_n) {
+  size_t n = (size_t)1 << log_n;
+  int total = L + alpha;
+  size_t key_stride = (size_t)(max_q + alpha) * n;
+  for (int l = 0; l < total; l++) {
+    uint32_t q = primes[l];
+    uint64_t ri = r_inv(q);
+    int kl = l < L ? key_off + l : max_q + (l - L);
+    for (size_t c = 0; c < n; c++) {
+      uint64_t sb = 0, sa = 0;
+      for (int j = 0; j < num_groups; j++) {
+        size_t ko = (size_t)key_group[j] * key_stride + (size_t)kl * n + c;
+        uint64_t m = modup[(size_t)j * total * n + (size_t)l * n + c];
+        sb += m * key_b[ko] % q;
+        sa += m * key_a[ko] % q;
       }
       acc_b[(size_t)l * n + c] = (uint32_t)((sb % q) * ri % q);
       acc_a[(size_t)l * n + c] = (uint32_t)((sa % q) * ri % q);

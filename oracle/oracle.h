@@ -84,6 +84,14 @@ void orc_moddown_epilogue_consts(const uint32_t *src_primes, int src_len,
 int orc_mod_up(uint32_t *dst, const uint32_t *src, int L,
                const uint32_t *q_primes, const uint32_t *p_primes, int alpha,
                int log_n);
+/* ModUp of a level with prime_offset = max_ter - num_ter terminal primes
+ * missing in front: group g covers the level's limbs
+ * [max(0, g alpha - off), min((g+1) alpha, L + off) - off); empty groups
+ * (ending at or before off) are left untouched. Returns beta =
+ * ceil((L + off) / alpha), the number of group slots in dst. */
+int orc_mod_up_ex(uint32_t *dst, const uint32_t *src, int L,
+                  const uint32_t *q_primes, const uint32_t *p_primes,
+                  int alpha, int prime_offset, int log_n);
 
 /* ---- ModDown family (ModSwitch.cu:566-684), no terminal primes ----
  * src holds src_total limbs with primes src_primes; the first dst_len limbs
@@ -93,6 +101,15 @@ int orc_mod_up(uint32_t *dst, const uint32_t *src, int L,
  *   Rescale:           src_total = L,       dst_len = L-k            */
 void orc_mod_down(uint32_t *dst, const uint32_t *src, int src_total,
                   const uint32_t *src_primes, int dst_len, int log_n);
+/* The general ModDown with terminal primes and the BitPacker restore: source
+ * limbs drop[0..num_drop) (indices into src) are divided out; destination
+ * limb k (prime dst_primes[k]) keeps source limb dst_src[k], or is a
+ * restored prime when dst_src[k] < 0 (its value is then -BConv / D).
+ * The result is scaled by R = prod of the restored primes. */
+void orc_mod_down_ex(uint32_t *dst, const uint32_t *src,
+                     const uint32_t *src_primes, const int *drop, int num_drop,
+                     const uint32_t *dst_primes, int dst_len,
+                     const int *dst_src, int log_n);
 
 /* ---- element-wise (ElementWise.cu:225-391, 504-575) ---- */
 void orc_tensor(uint32_t *bx, uint32_t *ax, uint32_t *rx, const uint32_t *b1,
@@ -103,6 +120,13 @@ void orc_tensor(uint32_t *bx, uint32_t *ax, uint32_t *rx, const uint32_t *b1,
 void orc_paccum(uint32_t *acc_b, uint32_t *acc_a, const uint32_t *modup,
                 int beta, const uint32_t *key_b, const uint32_t *key_a, int L,
                 int alpha, int max_q, const uint32_t *primes, int log_n);
+/* PAccum over the non-empty ModUp groups of a level with a prime offset:
+ * modup group j pairs with key group key_group[j]; q limb l reads key limb
+ * key_off + l, aux limb L + k reads max_q + k. */
+void orc_paccum_ex(uint32_t *acc_b, uint32_t *acc_a, const uint32_t *modup,
+                   int num_groups, const int *key_group, const uint32_t *key_b,
+                   const uint32_t *key_a, int L, int alpha, int max_q,
+                   int key_off, const uint32_t *primes, int log_n);
 /* acc[l] += MontMul(p_prod[l], ct[l]) for l < L */
 void orc_caccum(uint32_t *acc, const uint32_t *ct, const uint32_t *p_prod,
                 int L, const uint32_t *primes, int log_n);

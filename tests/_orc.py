@@ -49,6 +49,12 @@ def _load():
                                                _int, _u32p, _u32p]),
         "orc_mod_up": (_int, [_u32p, _u32p, _int, _u32p, _u32p, _int, _int]),
         "orc_mod_down": (None, [_u32p, _u32p, _int, _u32p, _int, _int]),
+        "orc_mod_up_ex": (_int, [_u32p, _u32p, _int, _u32p, _u32p, _int, _int,
+                                 _int]),
+        "orc_mod_down_ex": (None, [_u32p, _u32p, _u32p, _i32p, _int, _u32p,
+                                   _int, _i32p, _int]),
+        "orc_paccum_ex": (None, [_u32p, _u32p, _u32p, _int, _i32p, _u32p,
+                                 _u32p, _int, _int, _int, _int, _u32p, _int]),
         "orc_tensor": (None, [_u32p] * 7 + [_int, _u32p, _int]),
         "orc_paccum": (None, [_u32p, _u32p, _u32p, _int, _u32p, _u32p, _int,
                               _int, _int, _u32p, _int]),
@@ -149,6 +155,39 @@ def mod_up(src, q_primes, p_primes, log_n):
     lib.orc_mod_up(dst, u32(src), L, u32(q_primes), u32(p_primes), alpha,
                    log_n)
     return dst
+
+
+def mod_up_ex(src, q_primes, p_primes, prime_offset, log_n):
+    """ModUp with the chain's group layout: (beta, L + alpha, N) array, the
+    empty groups (ending at or before prime_offset) zero"""
+    L, alpha = len(q_primes), len(p_primes)
+    beta = (L + prime_offset + alpha - 1) // alpha
+    dst = np.zeros((beta, L + alpha, 1 << log_n), np.uint32)
+    lib.orc_mod_up_ex(dst, u32(src), L, u32(q_primes), u32(p_primes), alpha,
+                      prime_offset, log_n)
+    return dst
+
+
+def mod_down_ex(src, src_primes, drop, dst_primes, dst_src, log_n):
+    """general ModDown: drop = source limb indices divided out; dst_src[k] =
+    source limb kept in destination limb k, or -1 for a restored prime"""
+    dst = np.zeros((len(dst_primes), 1 << log_n), np.uint32)
+    lib.orc_mod_down_ex(dst, u32(src), u32(src_primes),
+                        np.ascontiguousarray(drop, np.int32), len(drop),
+                        u32(dst_primes), len(dst_primes),
+                        np.ascontiguousarray(dst_src, np.int32), log_n)
+    return dst
+
+
+def paccum_ex(modup, key_group, key_b, key_a, L, alpha, max_q, key_off,
+              primes, log_n):
+    n = 1 << log_n
+    acc_b = np.zeros((L + alpha, n), np.uint32)
+    acc_a = np.zeros((L + alpha, n), np.uint32)
+    lib.orc_paccum_ex(acc_b, acc_a, u32(modup), len(key_group),
+                      np.ascontiguousarray(key_group, np.int32), u32(key_b),
+                      u32(key_a), L, alpha, max_q, key_off, u32(primes), log_n)
+    return acc_b, acc_a
 
 
 def mod_down(src, src_primes, dst_len, log_n):
