@@ -1021,6 +1021,9 @@ Context<uint32_t>::Context(const Parameter<word> &param)
       elem_handler_(param, ntt_handler_),
       ntt_handler_(param),
       encoder_(param, ntt_handler_) {
+  AssertTrue(param_.GetMaxNumTer() == 0,
+             "Context: terminal primes are not supported by the key-switch "
+             "path of this build yet");
   Ciphertext<word>::SetDegree(param_.degree_);
   {
     // arena for the largest call at the top level: HMult holds the tensor
