@@ -24,15 +24,16 @@
 //
 // One v_mfma_i32_16x16x64_i8 multiplies a 16-coefficient x 64 (sources x
 // bytes, zero-padded beyond 4 * src_len) tile by a 64 x 16-destination tile
-// of one digit plane. Operand lanes (checked on gfx950): A row = lane % 16,
+// of one digit plane; more than 16 sources take a second K chunk of 64
+// accumulated into the same tile (|acc| <= 2^21, still exact). Operand lanes (checked on gfx950): A row = lane % 16,
 // k = 16 (lane / 16) + byte; B column = lane % 16, same k; D column =
 // lane % 16, rows 4 (lane / 16) + 0..3. So lane l packs sources
 // 4 (l / 16) .. + 3 of coefficient l % 16, and finishes four consecutive
 // coefficients of destination 16 t + l % 16.
 //
 // Grid (N / kCoefPerBlock, 1, jobs), 256 threads; a wave takes kTilesPerWave
-// 16-coefficient tiles. The packed table (4 KiB per 16 destinations) is read
-// through the caches by every wave.
+// 16-coefficient tiles. The packed table (4 KiB per 16 destinations and K
+// chunk) is read through the caches by every wave.
 #include <algorithm>
 #include <cstring>
 #include <vector>
@@ -47,7 +48,9 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
-constexpr int kMaxSrc = 16;            // 4 bytes x 16 sources = K of 64
+constexpr int kChunkSrc = 16;          // 4 bytes x 16 sources = K of 64
+constexpr int kMaxChunks = 2;
+constexpr int kMaxSrc = kChunkSrc * kMaxChunks;
 constexpr int kTilesPerWave = 2;
 constexpr int kCoefPerBlock = (kThreads / 64) * kTilesPerWave * 16;
 constexpr int kPlaneBytes = 64 * 16;   // one digit plane of a 16-dst tile
@@ -61,6 +64,7 @@ __device__ __forceinline__ int digits(int32_t c) {
   return static_cast<int>((static_cast<uint32_t>(c) + 0x808080u) ^ 0x808080u);
 }
 
+template <int kChunks>
 __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
                                                        chd_limb_map m,
                                                        BconvBatch b) {
@@ -72,23 +76,40 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
   const int n_wave = blockIdx.x * kCoefPerBlock + wave * kTilesPerWave * 16;
   const int32_t *__restrict__ src = jb.src;
   const v4i *__restrict__ tab = static_cast<const v4i *>(jb.table);
-  // A operands of this wave's coefficient tiles
-  v4i a[kTilesPerWave];
+  // this job's K chunks (its table holds exactly that many per tile)
+  const int nk = kChunks == 1 ? 1 : (jb.src_len + kChunkSrc - 1) / kChunkSrc;
+  // A operands of this wave's coefficient tiles, per K chunk
+  v4i a[kChunks][kTilesPerWave];
 #pragma unroll
-  for (int mt = 0; mt < kTilesPerWave; mt++) {
-    const int n = n_wave + mt * 16 + r;
+  for (int ch = 0; ch < kChunks; ch++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int i = 4 * g + j;
-      const int32_t c =
-          i < jb.src_len ? src[(static_cast<size_t>(i) << kLogN) + n] : 0;
-      a[mt][j] = digits(c);
+    for (int mt = 0; mt < kTilesPerWave; mt++) {
+      const int n = n_wave + mt * 16 + r;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int i = kChunkSrc * ch + 4 * g + j;
+        const int32_t c =
+            i < jb.src_len ? src[(static_cast<size_t>(i) << kLogN) + n] : 0;
+        a[ch][mt][j] = digits(c);
+      }
     }
-  }
   const int tiles = (jb.dst_len + 15) >> 4;
   for (int tt = 0; tt < tiles; tt++) {
-    const v4i *tp = tab + (static_cast<size_t>(tt) * 4) * 64 + lane;
-    const v4i b0 = tp[0], b1 = tp[64], b2 = tp[128], b3 = tp[192];
+    v4i bp[kChunks][4];
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ch++) {
+      if (ch < nk) {
+        const v4i *tp =
+            tab + (static_cast<size_t>(tt * nk + ch) * 4) * 64 + lane;
+        bp[ch][0] = tp[0];
+        bp[ch][1] = tp[64];
+        bp[ch][2] = tp[128];
+        bp[ch][3] = tp[192];
+      } else {
+        const v4i z = {0, 0, 0, 0};
+        bp[ch][0] = bp[ch][1] = bp[ch][2] = bp[ch][3] = z;
+      }
+    }
     const int k = tt * 16 + r;
     const bool live = k < jb.dst_len;
     const int pos = k + (k >= jb.skip_lo ? jb.skip_len : 0);
@@ -98,19 +119,25 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
     const double pinv = live ? t.qinvd[ti] : 1.0;
 #pragma unroll
     for (int mt = 0; mt < kTilesPerWave; mt++) {
-      const v4i z = {0, 0, 0, 0};
-      const v4i d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mt], b0, z, 0, 0, 0);
-      const v4i d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mt], b1, z, 0, 0, 0);
-      const v4i d2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mt], b2, z, 0, 0, 0);
-      const v4i d3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mt], b3, z, 0, 0, 0);
+      v4i d[4];
+#pragma unroll
+      for (int pl = 0; pl < 4; pl++) {
+        const v4i z = {0, 0, 0, 0};
+        d[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0][mt], bp[0][pl], z,
+                                                      0, 0, 0);
+#pragma unroll
+        for (int ch = 1; ch < kChunks; ch++)
+          d[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[ch][mt], bp[ch][pl],
+                                                        d[pl], 0, 0, 0);
+      }
       if (live) {
         uint32_t o[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          double y = __builtin_fma(static_cast<double>(d3[i]), 16777216.0,
-                                   static_cast<double>(d2[i]) * 65536.0);
-          y = __builtin_fma(static_cast<double>(d1[i]), 256.0, y);
-          y += static_cast<double>(d0[i]);
+          double y = __builtin_fma(static_cast<double>(d[3][i]), 16777216.0,
+                                   static_cast<double>(d[2][i]) * 65536.0);
+          y = __builtin_fma(static_cast<double>(d[1][i]), 256.0, y);
+          y += static_cast<double>(d[0][i]);
           o[i] = reduce_f64(y, p, pinv);
         }
         const int n = n_wave + mt * 16 + 4 * g;
@@ -136,7 +163,8 @@ using namespace chd;
 
 extern "C" long long chd_bconv_table_size(int src_len, int dst_len) {
   if (src_len < 1 || src_len > kMaxSrc || dst_len < 1) return 0;
-  return static_cast<long long>((dst_len + 15) / 16) * 4 * kPlaneBytes;
+  const int nk = (src_len + kChunkSrc - 1) / kChunkSrc;
+  return static_cast<long long>((dst_len + 15) / 16) * nk * 4 * kPlaneBytes;
 }
 
 extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
@@ -146,8 +174,9 @@ extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
       src_len > kMaxSrc || dst_len < 1)
     return set_error(CHD_ERR_ARG, "chd_bconv_table_pack: invalid argument");
   const int tiles = (dst_len + 15) / 16;
+  const int nk = (src_len + kChunkSrc - 1) / kChunkSrc;
   int8_t *out = static_cast<int8_t *>(host_out);
-  std::memset(out, 0, static_cast<size_t>(tiles) * 4 * kPlaneBytes);
+  std::memset(out, 0, static_cast<size_t>(tiles) * nk * 4 * kPlaneBytes);
   for (int k = 0; k < dst_len; k++) {
     const int64_t p = dst_primes[k];
     // 2^-32 mod p by extended Euclid on (p, 2^32 mod p)
@@ -176,13 +205,16 @@ extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
         for (int c = 0; c < 3; c++)
           dig[c] = static_cast<int8_t>(((w >> (8 * c)) & 0xff) - 128);
         dig[3] = static_cast<int8_t>(w >> 24);
-        // K index of (i, bb) and its lane / byte in the B operand
+        // K index of (i, bb): its chunk, and its lane / byte in that
+        // chunk's B operand
         const int kk = 4 * i + bb;
-        const int lane = (kk / 16) * 16 + col;
+        const int ch = kk / 64;
+        const int lane = ((kk % 64) / 16) * 16 + col;
         const int byte = kk % 16;
         for (int c = 0; c < 4; c++)
-          out[((static_cast<size_t>(tt) * 4 + c) * 64 + lane) * 16 + byte] =
-              dig[c];
+          out[(((static_cast<size_t>(tt) * nk + ch) * 4 + c) * 64 + lane) *
+                  16 +
+              byte] = dig[c];
         ub = (ub * 256) % p;
       }
     }
@@ -203,9 +235,15 @@ extern "C" int chd_k_bconv_batch(const chd_tables *t, const chd_limb_map *m,
       return set_error(CHD_ERR_ARG, "chd_k_bconv_batch: invalid job");
     b.job[j] = jb;
   }
+  int max_src = 0;
+  for (int j = 0; j < num_jobs; j++) max_src = std::max(max_src, jobs[j].src_len);
   dim3 g(kN / kCoefPerBlock, 1, num_jobs);
-  hipLaunchKernelGGL(bconv_mfma, g, dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), *t, *m, b);
+  if (max_src <= kChunkSrc)
+    hipLaunchKernelGGL(bconv_mfma<1>, g, dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), *t, *m, b);
+  else
+    hipLaunchKernelGGL(bconv_mfma<2>, g, dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), *t, *m, b);
   return check_launch("chd_k_bconv_batch");
 }
 

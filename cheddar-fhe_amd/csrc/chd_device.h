@@ -84,6 +84,24 @@ __device__ __forceinline__ uint32_t sub_mod(uint32_t a, uint32_t b,
   return d < e ? d : e;
 }
 
+// ModUp dnum groups sit on the chain's positions: a level missing `shift`
+// limbs of its first group owns limbs [lo, hi) in group g
+// (ModSwitch.cu:440-470 with prime_offset mod alpha)
+__host__ __device__ __forceinline__ int group_lo(int g, int alpha, int shift) {
+  const int v = g * alpha - shift;
+  return v > 0 ? v : 0;
+}
+__host__ __device__ __forceinline__ int group_hi(int g, int alpha, int shift,
+                                                 int num_q) {
+  const int v = (g + 1) * alpha - shift;
+  return v < num_q ? v : num_q;
+}
+// groups 0..beta-1 cover [0, num_q) and none is empty
+inline bool groups_valid(int beta, int alpha, int shift, int num_q) {
+  return alpha >= 1 && shift >= 0 && shift < alpha && beta >= 1 &&
+         (beta - 1) * alpha - shift < num_q && beta * alpha - shift >= num_q;
+}
+
 // wave-uniform value into an SGPR
 __device__ __forceinline__ int uniform(int v) {
   return __builtin_amdgcn_readfirstlane(v);

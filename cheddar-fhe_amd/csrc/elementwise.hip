@@ -260,8 +260,8 @@ __global__ __launch_bounds__(kThreads) void bs_fused_kernel(chd_tables t,
   const int c0 = blockIdx.x * kCoefPerBlock + threadIdx.x * kPerThread;
   uint32_t u[CHD_MAX_BS_GROUPS][4];
   for (int g = 0; g < a.beta; g++) {
-    const int own_lo = g * a.alpha;
-    const int own_hi = min(own_lo + a.alpha, a.num_q);
+    const int own_lo = group_lo(g, a.alpha, a.group_shift);
+    const int own_hi = group_hi(g, a.alpha, a.group_shift, a.num_q);
     const uint32_t *src = (li.l >= own_lo && li.l < own_hi)
                               ? a.d + loff
                               : a.modup + g * a.group_stride + loff;
@@ -505,9 +505,10 @@ extern "C" int chd_k_permute_accum(const chd_tables *t, const chd_limb_map *m,
 extern "C" int chd_k_bs_fused(const chd_tables *t, const chd_limb_map *m,
                               const chd_bs_args *args, void *stream) {
   if (!t || !m || !args || args->num_rot < 1 || args->num_rot > CHD_MAX_BS ||
-      args->beta < 1 || args->beta > CHD_MAX_BS_GROUPS || args->alpha < 1 ||
-      (args->beta - 1) * args->alpha >= args->num_q ||
-      args->beta * args->alpha < args->num_q || !args->modup || !args->d ||
+      args->beta > CHD_MAX_BS_GROUPS ||
+      !groups_valid(args->beta, args->alpha, args->group_shift,
+                    args->num_q) ||
+      !args->modup || !args->d ||
       !args->ct_b || !args->p_prod || args->num_q != m->num_q ||
       m->skip_len != 0)
     return set_error(CHD_ERR_ARG, "chd_k_bs_fused: invalid argument");

@@ -36,9 +36,10 @@ struct NttArgs {
   const uint32_t *cst2;   // inv prime product per logical limb
   const uint32_t *pad;    // optional padding per src2 limb (nullptr: none)
   // ModUp group mode (group_alpha > 0): grid.z = dnum group g, whose own
-  // limbs [g alpha, min((g+1) alpha, num_q)) are skipped; every group holds
+  // limbs [group_lo(g), group_hi(g)) are skipped; every group holds
   // group_limbs logical limbs (NTTForModUp for all groups in one launch)
   int group_alpha;
+  int group_shift;
   int group_limbs;
   // optional per-polynomial base pointers (used instead of base + z*stride
   // when dst_list[0] is set): polynomials in separate allocations

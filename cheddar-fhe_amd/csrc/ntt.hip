@@ -294,8 +294,10 @@ __global__ __launch_bounds__(512) void ntt_fwd_cols(NttArgs a) {
   __shared__ int32_t xch[kRows * kTileCols];
   LimbMap m = a.map;
   if (a.group_alpha > 0) {
-    m.skip_lo = blockIdx.z * a.group_alpha;
-    m.skip_len = min(a.group_alpha, m.num_q - m.skip_lo);
+    const int g = blockIdx.z;
+    m.skip_lo = group_lo(g, a.group_alpha, a.group_shift);
+    m.skip_len =
+        group_hi(g, a.group_alpha, a.group_shift, m.num_q) - m.skip_lo;
     if (static_cast<int>(blockIdx.y) >= a.group_limbs - m.skip_len) return;
   }
   const Limb lb = decode(m, blockIdx.y);
@@ -407,8 +409,10 @@ __global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
   __shared__ int32_t xch[kTileRows * kRowPad];
   LimbMap m = a.map;
   if (a.group_alpha > 0) {
-    m.skip_lo = blockIdx.z * a.group_alpha;
-    m.skip_len = min(a.group_alpha, m.num_q - m.skip_lo);
+    const int g = blockIdx.z;
+    m.skip_lo = group_lo(g, a.group_alpha, a.group_shift);
+    m.skip_len =
+        group_hi(g, a.group_alpha, a.group_shift, m.num_q) - m.skip_lo;
     if (static_cast<int>(blockIdx.y) >= a.group_limbs - m.skip_len) return;
   }
   const Limb lb = decode(m, blockIdx.y);
@@ -680,8 +684,8 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
   for (int k = 0; k < 16; k++) accb[k] = acca[k] = 0;
   bool synced = false;
   for (int g = 0; g < a.beta; g++) {
-    const int own_lo = g * a.alpha;
-    const int own_hi = min(own_lo + a.alpha, a.num_q);
+    const int own_lo = group_lo(g, a.alpha, a.group_shift);
+    const int own_hi = group_hi(g, a.alpha, a.group_shift, a.num_q);
     uint32_t u[16];
     if (l >= own_lo && l < own_hi) {
       // own limb: the input itself (ModSwitch.cu:466-470 copies it); in
@@ -1024,10 +1028,11 @@ extern "C" int chd_k_ntt_inv_mul(const chd_tables *t, const chd_limb_map *m,
 
 extern "C" int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
                                     uint32_t *modup, long long group_stride,
-                                    int num_groups, int alpha, int group_limbs,
-                                    int with_rows, void *stream) {
-  if (!t || !m || !modup || num_groups < 1 || alpha < 1 ||
-      group_limbs < m->num_q || (num_groups - 1) * alpha >= m->num_q)
+                                    int num_groups, int alpha, int group_shift,
+                                    int group_limbs, int with_rows,
+                                    void *stream) {
+  if (!t || !m || !modup || group_limbs < m->num_q ||
+      !groups_valid(num_groups, alpha, group_shift, m->num_q))
     return set_error(CHD_ERR_ARG, "chd_k_ntt_fwd_groups: invalid argument");
   NttArgs a{};
   a.src = modup;
@@ -1038,9 +1043,13 @@ extern "C" int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
   a.map.src_gap = 0;
   a.tab = *t;
   a.group_alpha = alpha;
+  a.group_shift = group_shift;
   a.group_limbs = group_limbs;
   // grid.y covers the largest group (the smallest skip range)
-  const int min_skip = std::min(alpha, m->num_q - (num_groups - 1) * alpha);
+  int min_skip = alpha;
+  for (int g = 0; g < num_groups; g++)
+    min_skip = std::min(min_skip, group_hi(g, alpha, group_shift, m->num_q) -
+                                      group_lo(g, alpha, group_shift));
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = launch_ntt_fwd_cols(a, group_limbs - min_skip, num_groups, s);
   if (e == hipSuccess && with_rows)
@@ -1057,9 +1066,8 @@ extern "C" int chd_k_modup_keyacc(const chd_tables *t,
   if (!t || !args || !args->modup || !args->p_prod || !args->acc_b ||
       !args->acc_a || args->alpha < 1 ||
       (tensor ? !args->b1 || !args->b2 || !args->a2 : !args->d) ||
-      args->beta < 1 || args->beta > kMaxGroups ||
-      (args->beta - 1) * args->alpha >= args->num_q ||
-      args->beta * args->alpha < args->num_q)
+      args->beta > kMaxGroups ||
+      !groups_valid(args->beta, args->alpha, args->group_shift, args->num_q))
     return set_error(CHD_ERR_ARG, "chd_k_modup_keyacc: invalid argument");
   for (int g = 0; g < args->beta; g++)
     if (!args->kb[g] || !args->ka[g])

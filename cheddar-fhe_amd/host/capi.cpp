@@ -126,7 +126,7 @@ extern "C" int chd_bconv_plan_create(chd_bconv_plan **out, int log_degree,
                                      const uint32_t *src_primes, int src_len,
                                      const uint32_t *dst_primes,
                                      int dst_len) {
-  if (!out || !src_primes || !dst_primes || src_len < 1 || src_len > 16 ||
+  if (!out || !src_primes || !dst_primes || src_len < 1 || src_len > 32 ||
       dst_len < 1)
     return set_error(CHD_ERR_ARG, "chd_bconv_plan_create: invalid argument");
   CHD_TRY
@@ -314,7 +314,9 @@ extern "C" int chd_mod_up(const chd_context *ctx, int level,
     const auto &ms = ctx->c->mod_switch_handlers_.at(level);
     std::vector<cheddar::DvView<word>> v;
     for (int g = 0; g < ms.GetBeta(); g++) {
-      if (!dst[g]) throw cheddar::Error("null ModUp destination");
+      // groups before FirstGroup() hold no limb of this level: unused
+      if (!dst[g] && g >= ms.FirstGroup())
+        throw cheddar::Error("null ModUp destination");
       v.emplace_back(dst[g], (nq + p.alpha_) * n, p.alpha_ * n);
     }
     ms.ModUp(v, cheddar::DvConstView<word>(src, nq * n, 0));

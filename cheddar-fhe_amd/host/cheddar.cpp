@@ -8,6 +8,7 @@
 #include <cmath>
 
 #include "cheddar_amd.h"
+#include "chd_device.h"
 #include "prime_math.h"
 
 namespace cheddar {
@@ -650,7 +651,7 @@ void ElementWiseHandler<uint32_t>::PermuteAccum(
 }
 
 // ----------------------------------------------------- ModSwitchHandler --
-// src/core/ModSwitch.cu:175-318, no terminal primes
+// src/core/ModSwitch.cu:175-318
 ModSwitchHandler<uint32_t>::ModSwitchHandler(
     const Parameter<word> &param, int level,
     const ElementWiseHandler<word> &elem, const NTTHandler<word> &ntt,
@@ -659,6 +660,9 @@ ModSwitchHandler<uint32_t>::ModSwitchHandler(
       num_aux_(param.alpha_),
       beta_(DivCeil(param.LevelToNP(level).num_main_ + param.GetMaxNumTer(),
                     param.alpha_)),
+      prime_offset_(param.GetMaxNumTer() - param.LevelToNP(level).num_ter_),
+      first_group_(prime_offset_ / param.alpha_),
+      group_shift_(prime_offset_ % param.alpha_),
       param_(param),
       elem_(elem),
       ntt_(ntt),
@@ -666,17 +670,17 @@ ModSwitchHandler<uint32_t>::ModSwitchHandler(
   const NPInfo np = param_.LevelToNP(level_, num_aux_);
   const int num_q = np.GetNumQ();
   const std::vector<word> lp = param_.GetPrimeVector(np);
+  // ModUp constants per non-empty group (ModSwitch.cu:200-235)
   std::vector<word> up1(num_q);
-  mod_up_.resize(beta_);
-  for (int i = 0; i < beta_; i++) {
-    const int s0 = i * num_aux_;
-    const int s1 = std::min((i + 1) * num_aux_, num_q);
+  mod_up_.resize(NumGroups());
+  for (int z = 0; z < NumGroups(); z++) {
+    const int s0 = GroupLo(z), s1 = GroupHi(z);
     std::vector<word> src(lp.begin() + s0, lp.begin() + s1);
     std::vector<word> dst(lp.begin(), lp.begin() + s0);
     dst.insert(dst.end(), lp.begin() + s1, lp.end());
-    BuildSwitch(mod_up_[i], src, dst);
+    BuildSwitch(mod_up_[z], src, dst);
     std::vector<word> c1(s1 - s0);
-    HipCheck(hipMemcpy(c1.data(), mod_up_[i].const1.data(),
+    HipCheck(hipMemcpy(c1.data(), mod_up_[z].const1.data(),
                        c1.size() * sizeof(word), hipMemcpyDeviceToHost),
              "hipMemcpy");
     std::copy(c1.begin(), c1.end(), up1.begin() + s0);
@@ -694,7 +698,7 @@ ModSwitchHandler<uint32_t>::ModSwitchHandler(
     std::vector<word> r(dst.size());
     for (size_t k = 0; k < dst.size(); k++) {
       word v = 1;
-      for (word s : src) v = pm::mulmod(v, s, dst[k]);
+      for (word s : src) v = pm::mulmod(v, s % dst[k], dst[k]);
       r[k] = pm::to_mont(pm::invmod(v, dst[k]), dst[k]);
     }
     return r;
@@ -708,27 +712,63 @@ ModSwitchHandler<uint32_t>::ModSwitchHandler(
   upload(inv_prime_prod_, inv_prod(pp, qp));
   if (level_ == 0) return;
 
-  const NPInfo next = param_.LevelToNP(level_ - 1, num_aux_);
+  // Rescale constants (ModSwitch.cu:252-318): the primes that leave, and
+  // the BitPacker restore range of the primes that come back
+  const NPInfo next = param_.LevelToNP(level_ - 1);
+  const std::vector<word> rdst = param_.GetPrimeVector(next);
+  const int next_q = next.GetNumQ();
   const int main_diff = np.num_main_ - next.num_main_;
-  AssertTrue(main_diff > 0, "Invalid rescale amount");
-  const std::vector<word> rdst(lp.begin(), lp.begin() + num_q - main_diff);
-  const std::vector<word> rsrc(lp.begin() + num_q - main_diff,
-                               lp.begin() + num_q);
+  const int ter_diff = np.num_ter_ - next.num_ter_;
+  std::vector<word> rsrc;
+  int rlo = 0, rhi = 0;
+  if (ter_diff > 0) {  // terminal primes leave, main primes may come back
+    AssertTrue(main_diff <= 0, "Invalid rescale amount");
+    rsrc.assign(lp.begin(), lp.begin() + ter_diff);
+    rlo = next_q + main_diff;
+    rhi = next_q;
+  } else if (main_diff > 0) {  // main primes leave, terminal may come back
+    AssertTrue(ter_diff <= 0, "Invalid rescale amount");
+    rsrc.assign(lp.begin() + num_q - main_diff, lp.begin() + num_q);
+    rlo = 0;
+    rhi = -ter_diff;
+  } else {
+    Fail("Invalid rescale amount");
+  }
   std::vector<word> mdr_src = rsrc;
   mdr_src.insert(mdr_src.end(), pp.begin(), pp.end());
-  BuildSwitch(rescale_, rsrc, rdst);
-  BuildSwitch(mod_down_rescale_, mdr_src, rdst);
+  BuildSwitch(rescale_, rsrc, rdst, rlo, rhi);
+  BuildSwitch(mod_down_rescale_, mdr_src, rdst, rlo, rhi);
   upload(rescale_inv_prime_prod_, inv_prod(rsrc, rdst));
   upload(mod_down_rescale_inv_prime_prod_, inv_prod(mdr_src, rdst));
-  // The reference's BitPacker padding (ModSwitch.cu:372-411) is ToMont(1) on
-  // every limb when the restore range is empty (no terminal primes), an
-  // identity in the ModDown epilogue, so no padding table is kept.
+  if (rhi > rlo) {
+    // padding of the kept limbs, indexed as src2 (ModSwitch.cu:388-411):
+    // ToMont(prod of the restored primes)
+    const int rlen = rhi - rlo;
+    std::vector<word> pad(next_q - rlen);
+    for (int i = 0; i < next_q - rlen; i++) {
+      const word m = rdst[i >= rlo ? i + rlen : i];
+      word v = 1;
+      for (int j = rlo; j < rhi; j++) v = pm::mulmod(v, rdst[j] % m, m);
+      pad[i] = pm::to_mont(v, m);
+    }
+    upload(rescale_padding_, pad);
+    upload(mod_down_rescale_padding_, pad);
+  }
 }
 
-// PopulateModSwitchConstants (ModSwitch.cu:320-370), restore range empty
+int ModSwitchHandler<uint32_t>::GroupLo(int z) const {
+  return chd::group_lo(z, num_aux_, group_shift_);
+}
+
+int ModSwitchHandler<uint32_t>::GroupHi(int z) const {
+  return chd::group_hi(z, num_aux_, group_shift_,
+                       param_.LevelToNP(level_).GetNumQ());
+}
+
+// PopulateModSwitchConstants (ModSwitch.cu:320-370)
 void ModSwitchHandler<uint32_t>::BuildSwitch(
     SwitchTable &st, const std::vector<word> &src,
-    const std::vector<word> &dst) const {
+    const std::vector<word> &dst, int restore_lo, int restore_hi) const {
   const int sl = static_cast<int>(src.size());
   const int dl = static_cast<int>(dst.size());
   std::vector<word> c1(sl, 1);
@@ -736,15 +776,19 @@ void ModSwitchHandler<uint32_t>::BuildSwitch(
   for (int i = 0; i < sl; i++) {
     word v = 1;
     for (int j = 0; j < sl; j++)
-      if (j != i) v = pm::mulmod(v, src[j], src[i]);
-    v = pm::mulmod(v, static_cast<word>(param_.degree_), src[i]);
+      if (j != i) v = pm::mulmod(v, src[j] % src[i], src[i]);
+    v = pm::mulmod(v, static_cast<word>(param_.degree_) % src[i], src[i]);
     c1[i] = pm::invmod(v, src[i]);
+    // BitPacker: the restored primes' product folded in (kept as a plain
+    // residue, as the reference does)
+    for (int j = restore_lo; j < restore_hi; j++)
+      c1[i] = pm::mulmod(c1[i], dst[j] % src[i], src[i]);
   }
   for (int k = 0; k < dl; k++)
     for (int i = 0; i < sl; i++) {
       word acc = 1;
       for (int j = 0; j < sl; j++)
-        if (j != i) acc = pm::mulmod(acc, src[j], dst[k]);
+        if (j != i) acc = pm::mulmod(acc, src[j] % dst[k], dst[k]);
       acc = pm::to_mont(pm::to_mont(acc, dst[k]), dst[k]);
       c2[static_cast<size_t>(k) * sl + i] = pm::normalize(acc, dst[k]);
     }
@@ -772,7 +816,7 @@ void ModSwitchHandler<uint32_t>::ModUpBconv(word *const *dst,
   const int n = param_.degree_;
   AssertTrue(src.QSize() == num_q * n, "ModUp src q size mismatch");
   AssertTrue(src.AuxSize() == 0, "ModUp src aux size mismatch");
-  AssertTrue(beta_ <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
+  AssertTrue(NumGroups() <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
   if (src_mul != nullptr) {
     const chd_limb_map mi = NoSkipMap(param_, np);
     K(chd_k_ntt_inv_mul(&ntt_.Tables(), &mi, intt, 0, src.data(), src_mul, 0,
@@ -786,20 +830,19 @@ void ModSwitchHandler<uint32_t>::ModUpBconv(word *const *dst,
   np_aux.num_aux_ = num_aux_;
   chd_limb_map m = NoSkipMap(param_, np_aux);
   chd_bconv_job jobs[CHD_MAX_JOBS] = {};
-  for (int i = 0; i < beta_; i++) {
-    const int s0 = i * num_aux_;
-    const int s1 = std::min((i + 1) * num_aux_, num_q);
-    const SwitchTable &st = mod_up_[i];
-    jobs[i].dst = dst[i];
-    jobs[i].src = reinterpret_cast<const int32_t *>(intt) +
+  for (int z = 0; z < NumGroups(); z++) {
+    const int s0 = GroupLo(z), s1 = GroupHi(z);
+    const SwitchTable &st = mod_up_[z];
+    jobs[z].dst = dst[z];
+    jobs[z].src = reinterpret_cast<const int32_t *>(intt) +
                   static_cast<size_t>(s0) * n;
-    jobs[i].table = st.table.as<void>();
-    jobs[i].src_len = st.src_len;
-    jobs[i].dst_len = st.dst_len;
-    jobs[i].skip_lo = s0;
-    jobs[i].skip_len = s1 - s0;
+    jobs[z].table = st.table.as<void>();
+    jobs[z].src_len = st.src_len;
+    jobs[z].dst_len = st.dst_len;
+    jobs[z].skip_lo = s0;
+    jobs[z].skip_len = s1 - s0;
   }
-  K(chd_k_bconv_batch(&ntt_.Tables(), &m, jobs, beta_, CurrentStream()));
+  K(chd_k_bconv_batch(&ntt_.Tables(), &m, jobs, NumGroups(), CurrentStream()));
 }
 
 // ModUp with every group's column pass (and, with_rows, row pass) batched;
@@ -812,15 +855,15 @@ void ModSwitchHandler<uint32_t>::ModUpGroups(word *modup,
   const NPInfo np = param_.LevelToNP(level_, 0);
   const int num_q = np.GetNumQ();
   word *dst[CHD_MAX_JOBS];
-  AssertTrue(beta_ <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
-  for (int i = 0; i < beta_; i++) dst[i] = modup + i * group_stride;
+  AssertTrue(NumGroups() <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
+  for (int z = 0; z < NumGroups(); z++) dst[z] = modup + z * group_stride;
   ModUpBconv(dst, src, intt, src_mul);
   NPInfo np_aux = np;
   np_aux.num_aux_ = num_aux_;
   chd_limb_map m = NoSkipMap(param_, np_aux);
-  K(chd_k_ntt_fwd_groups(&ntt_.Tables(), &m, modup, group_stride, beta_,
-                         num_aux_, num_q + num_aux_, with_rows ? 1 : 0,
-                         CurrentStream()));
+  K(chd_k_ntt_fwd_groups(&ntt_.Tables(), &m, modup, group_stride, NumGroups(),
+                         num_aux_, group_shift_, num_q + num_aux_,
+                         with_rows ? 1 : 0, CurrentStream()));
 }
 
 // src/core/ModSwitch.cu:429-509
@@ -830,19 +873,21 @@ void ModSwitchHandler<uint32_t>::ModUp(std::vector<DvView<word>> &dst,
   const int num_q = np.GetNumQ();
   const int n = param_.degree_;
   AssertTrue(static_cast<int>(dst.size()) == beta_, "ModUp dst size mismatch");
-  AssertTrue(beta_ <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
+  AssertTrue(NumGroups() <= CHD_MAX_JOBS, "ModUp: dnum larger than supported");
   const long long gs = static_cast<long long>(num_q + num_aux_) * n;
+  const int first = first_group_;
   bool strided = true;
-  for (int i = 0; i < beta_; i++) {
-    AssertTrue(dst[i].AuxSize() == num_aux_ * n &&
-                   dst[i].QSize() == num_q * n,
+  for (int z = 0; z < NumGroups(); z++) {
+    const DvView<word> &d = dst[first + z];
+    AssertTrue(d.AuxSize() == num_aux_ * n && d.QSize() == num_q * n,
                "ModUp dst size mismatch");
-    strided = strided && dst[i].data() == dst[0].data() + i * gs;
+    strided = strided && d.data() == dst[first].data() + z * gs;
   }
-  for (int i = 0; i < beta_; i++) {
-    const int s0 = i * num_aux_;
-    const int s1 = std::min((i + 1) * num_aux_, num_q);
-    HipCheck(hipMemcpyAsync(dst[i].data() + static_cast<size_t>(s0) * n,
+  // own limbs are the input's (ModSwitch.cu:449-470); groups before
+  // FirstGroup() hold no limb of this level and are not written
+  for (int z = 0; z < NumGroups(); z++) {
+    const int s0 = GroupLo(z), s1 = GroupHi(z);
+    HipCheck(hipMemcpyAsync(dst[first + z].data() + static_cast<size_t>(s0) * n,
                             src.data() + static_cast<size_t>(s0) * n,
                             static_cast<size_t>(s1 - s0) * n * sizeof(word),
                             hipMemcpyDeviceToDevice, CurrentStream()),
@@ -851,19 +896,17 @@ void ModSwitchHandler<uint32_t>::ModUp(std::vector<DvView<word>> &dst,
   Workspace::Use use_ws(ws_);
   Scratch intt(ws_, static_cast<size_t>(num_q) * n);
   if (strided) {  // groups equally spaced: one launch per pass for all
-    ModUpGroups(dst[0].data(), gs, src, intt.data(), true);
+    ModUpGroups(dst[first].data(), gs, src, intt.data(), true);
     return;
   }
   word *d[CHD_MAX_JOBS];
-  for (int i = 0; i < beta_; i++) d[i] = dst[i].data();
+  for (int z = 0; z < NumGroups(); z++) d[z] = dst[first + z].data();
   ModUpBconv(d, src, intt.data());
   NPInfo np_aux = np;
   np_aux.num_aux_ = num_aux_;
-  for (int i = 0; i < beta_; i++) {
-    const int s0 = i * num_aux_;
-    const int s1 = std::min((i + 1) * num_aux_, num_q);
-    ntt_.NTTForModUp(dst[i], np_aux, s0, s1, DvConstView<word>(dst[i]));
-  }
+  for (int z = 0; z < NumGroups(); z++)
+    ntt_.NTTForModUp(dst[first + z], np_aux, GroupLo(z), GroupHi(z),
+                     DvConstView<word>(dst[first + z]));
 }
 
 // src/core/ModSwitch.cu:414-428 (MultConst by p_prod)
@@ -956,8 +999,6 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
                                                   : mod_down_rescale_;
   AssertTrue(st.src_len == src_len && st.dst_len == dst_len,
              "ModDown: constant table mismatch");
-  AssertTrue(np_src.num_ter_ == np_non_intt.num_ter_,
-             "INTTForModDown: terminal-prime INTT is not supported");
   const long long ilen = static_cast<long long>(src_len) * n;
   Workspace::Use use_ws(ws_);
   Scratch intt(ws_, static_cast<size_t>(num_polys) * ilen);
@@ -967,14 +1008,27 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
     AssertTrue(dst[p] != src + p * src_pstride,
                "ModDown: src and dst should be different");
   }
-  // INTTForModDown (NTT.cu:973-1071 case 1) of all polynomials
+  // INTTForModDown (NTT.cu:973-1128) of all polynomials: either the top
+  // main limbs (case 1) or the leading terminal limbs (case 2), then the
+  // aux limbs when the source has them
+  const bool intt_on_main = np_src.num_main_ > np_non_intt.num_main_;
+  const bool intt_on_ter = np_src.num_ter_ > np_non_intt.num_ter_;
+  AssertTrue(!intt_on_main || !intt_on_ter,
+             "INTTForModDown: Invalid np combination");
   chd_limb_map mi{};
-  mi.num_q = np_src.num_main_ - np_non_intt.num_main_;
   mi.skip_lo = INT_MAX;
-  mi.tab_off = param_.GetMaxNumTer() + np_non_intt.num_main_;
-  mi.tab_gap = param_.MainLeft(np_src);
-  const size_t off =
-      static_cast<size_t>(np_src.num_ter_ + np_non_intt.num_main_) * n;
+  size_t off = 0;
+  if (!intt_on_ter) {
+    mi.num_q = np_src.num_main_ - np_non_intt.num_main_;
+    mi.tab_off = param_.GetMaxNumTer() + np_non_intt.num_main_;
+    mi.tab_gap = param_.MainLeft(np_src);
+    off = static_cast<size_t>(np_src.num_ter_ + np_non_intt.num_main_) * n;
+  } else {
+    mi.num_q = np_src.num_ter_ - np_non_intt.num_ter_;
+    mi.tab_off = param_.TerLeft(np_src);
+    mi.tab_gap = param_.GetMaxNumMain() + np_non_intt.num_ter_;
+    mi.src_gap = np_src.GetNumQ() - mi.num_q;
+  }
   K(chd_k_ntt_inv(&ntt_.Tables(), &mi, intt.data(), ilen, src + off,
                   src_pstride, src_len, num_polys, st.const1.data(), 1,
                   CurrentStream()));
@@ -994,11 +1048,14 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
       kind == Kind::ModDown   ? inv_prime_prod_
       : kind == Kind::Rescale ? rescale_inv_prime_prod_
                               : mod_down_rescale_inv_prime_prod_;
-  // The padding of Rescale / ModDownAndRescale is ToMont(1) on every limb
-  // here (no terminal primes, so the BitPacker restore range is empty), and
-  // MontMul(x, ToMont(1)) = x for the canonical src2 limbs: the epilogue's
-  // padding multiply is the identity and is skipped (nullptr).
-  const word *pad = nullptr;
+  // BitPacker padding of the kept limbs when primes are restored; with an
+  // empty restore range it is ToMont(1), the identity on the canonical src2
+  // limbs, and the multiply is skipped (nullptr)
+  const DeviceVector<word> &padv = kind == Kind::Rescale
+                                       ? rescale_padding_
+                                       : mod_down_rescale_padding_;
+  const word *pad =
+      kind != Kind::ModDown && padv.size() != 0 ? padv.data() : nullptr;
   // NTTForModDown (NTT.cu:417-604) with src2 = the untouched low limbs
   const int src2_off = std::max(0, np_src.num_ter_ - np_dst.num_ter_);
   const int s2_lo = np_dst.num_ter_ - np_non_intt.num_ter_;
@@ -1021,9 +1078,6 @@ Context<uint32_t>::Context(const Parameter<word> &param)
       elem_handler_(param, ntt_handler_),
       ntt_handler_(param),
       encoder_(param, ntt_handler_) {
-  AssertTrue(param_.GetMaxNumTer() == 0,
-             "Context: terminal primes are not supported by the key-switch "
-             "path of this build yet");
   Ciphertext<word>::SetDegree(param_.degree_);
   {
     // arena for the largest call at the top level: HMult holds the tensor
@@ -1120,30 +1174,35 @@ void Context<uint32_t>::KeyAccumulate(int level, word *acc_b, word *acc_a,
   AssertTrue(static_cast<int>(key.bx.size()) >= beta &&
                  key.bx.size() == key.ax.size(),
              "Beta mismatch");
-  AssertTrue(beta <= CHD_MAX_JOBS, "MultKeyNoModDown: dnum too large");
   const auto &ms = mod_switch_handlers_.at(level);
   AssertTrue(ms.GetBeta() == beta, "MultKeyNoModDown: beta mismatch");
+  // the groups before ms.FirstGroup() hold no limb of this level and are
+  // skipped with their keys (Context.cpp:637-642)
+  const int groups = ms.NumGroups();
+  const int first = ms.FirstGroup();
+  AssertTrue(groups <= CHD_MAX_JOBS, "MultKeyNoModDown: dnum too large");
   const int total = num_q + num_aux;
   const long long gs = static_cast<long long>(total) * n;
   Workspace::Use use_ws(ws_.get());
   Scratch buf(ws_.get(),
-              static_cast<size_t>(beta) * gs + static_cast<size_t>(num_q) * n);
+              static_cast<size_t>(groups) * gs + static_cast<size_t>(num_q) * n);
   const bool tensor = ta != nullptr;
   ms.ModUpGroups(buf.data(), gs,
                  DvConstView<word>(tensor ? ta->ax : d, num_q * n, 0),
-                 buf.data() + beta * gs, false, tensor ? tb->ax : nullptr);
+                 buf.data() + groups * gs, false, tensor ? tb->ax : nullptr);
   chd_keyacc_args k{};
   k.num_q = num_q;
   k.tab_off = param_.TerLeft(a_np);
   k.tab_gap = param_.MainLeft(a_np);
   k.alpha = num_aux;
-  k.beta = beta;
+  k.beta = groups;
+  k.group_shift = ms.GroupShift();
   k.modup = buf.data();
   k.group_stride = gs;
   k.d = d;
-  for (int g = 0; g < beta; g++) {
-    k.kb[g] = key.bx[g] + static_cast<size_t>(prime_offset) * n;
-    k.ka[g] = key.ax[g] + static_cast<size_t>(prime_offset) * n;
+  for (int z = 0; z < groups; z++) {
+    k.kb[z] = key.bx[first + z] + static_cast<size_t>(prime_offset) * n;
+    k.ka[z] = key.ax[first + z] + static_cast<size_t>(prime_offset) * n;
   }
   // key layout: q limbs of the key's level, then its aux limbs
   k.key_gap = static_cast<long long>(key.np.GetNumQ() - prime_offset - num_q) * n;
@@ -1722,7 +1781,10 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
   const int total = num_q + alpha;
   const NPInfo ext_np(in_np.num_main_, in_np.num_ter_, alpha);
   const auto &ms = ctx.mod_switch_handlers_.at(pt_level_);
-  const int beta = ms.GetBeta();
+  // non-empty dnum groups of this level (the first ms.FirstGroup() are
+  // skipped with their keys, Context.cpp:637-642)
+  const int beta = ms.NumGroups();
+  const int first = ms.FirstGroup();
   AssertTrue(beta <= CHD_MAX_BS_GROUPS, "Hoist: dnum too large");
   const DvConstView<word> p_prod = ctx.PProd(in_np);
   Workspace *ws = ctx.GetWorkspace();
@@ -1770,6 +1832,7 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
     a.num_q = num_q;
     a.alpha = alpha;
     a.beta = beta;
+    a.group_shift = ms.GroupShift();
     a.modup = buf.data();
     a.group_stride = gs;
     a.d = input.ax_.data();
@@ -1780,7 +1843,7 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
     for (int k = 0; k < cnt; k++) {
       const int r = rots[base + k];
       const Context<word>::EvkRef key = key_of(r);
-      AssertTrue(static_cast<int>(key.bx.size()) >= beta &&
+      AssertTrue(static_cast<int>(key.bx.size()) >= first + beta &&
                      key.bx.size() == key.ax.size() &&
                      key.np.num_aux_ == alpha,
                  "Hoist: rotation key shape mismatch");
@@ -1792,8 +1855,8 @@ void HoistHandler<uint32_t>::BabyStep(const Context<word> &ctx,
       else
         AssertTrue(a.key_gap == key_gap, "Hoist: keys of different levels");
       for (int g = 0; g < beta; g++) {
-        a.kb[k][g] = key.bx[g] + static_cast<size_t>(prime_offset) * n;
-        a.ka[k][g] = key.ax[g] + static_cast<size_t>(prime_offset) * n;
+        a.kb[k][g] = key.bx[first + g] + static_cast<size_t>(prime_offset) * n;
+        a.ka[k][g] = key.ax[first + g] + static_cast<size_t>(prime_offset) * n;
       }
       // scatter with the inverse automorphism (Hoist.cu:290-300)
       a.galois[k] = static_cast<uint32_t>(param.GetGaloisFactor(n / 2 - r));

@@ -442,6 +442,15 @@ class ModSwitchHandler<uint32_t> {
   void ModDownAndRescale(DvView<word> &dst,
                          const DvConstView<word> &src) const;
   int GetBeta() const { return beta_; }
+  // dnum groups sit on the chain's positions (ModSwitch.cu:200-235): with
+  // terminal primes missing at this level, the first FirstGroup() groups are
+  // empty; non-empty group z (0 <= z < NumGroups(), chain group
+  // FirstGroup() + z) owns the level's limbs [GroupLo(z), GroupHi(z)).
+  int FirstGroup() const { return first_group_; }
+  int NumGroups() const { return beta_ - first_group_; }
+  int GroupShift() const { return group_shift_; }
+  int GroupLo(int z) const;
+  int GroupHi(int z) const;
   // ModSwitch.cu:414-428: dst = MontMul(src, p_prod) on the q limbs
   void PseudoModUp(DvView<word> &dst, const DvConstView<word> &src,
                    const DvConstView<word> &p_prod) const;
@@ -473,13 +482,17 @@ class ModSwitchHandler<uint32_t> {
     DevBuf table;                // packed BConv table (chd_bconv_table_pack)
     int src_len = 0, dst_len = 0;
   };
+  // restore: destination primes [restore_lo, restore_hi) come back without
+  // a source limb (BitPacker, ModSwitch.cu:320-370)
   void BuildSwitch(SwitchTable &st, const std::vector<word> &src,
-                   const std::vector<word> &dst) const;
+                   const std::vector<word> &dst, int restore_lo = 0,
+                   int restore_hi = 0) const;
   void ModDownWorker(DvView<word> &dst, const DvConstView<word> &src,
                      Kind kind) const;
   const int level_;
   const int num_aux_;
   const int beta_;
+  const int prime_offset_, first_group_, group_shift_;
   const Parameter<word> &param_;
   const ElementWiseHandler<word> &elem_;
   const NTTHandler<word> &ntt_;
@@ -489,6 +502,9 @@ class ModSwitchHandler<uint32_t> {
   SwitchTable mod_down_, rescale_, mod_down_rescale_;
   DeviceVector<word> inv_prime_prod_, rescale_inv_prime_prod_,
       mod_down_rescale_inv_prime_prod_;
+  // BitPacker padding of the kept limbs (ModSwitch.cu:372-411); empty when
+  // the rescale restores no prime (the padding is then the identity)
+  DeviceVector<word> rescale_padding_, mod_down_rescale_padding_;
 };
 
 // CKKS encoder (include/core/Encode.h, src/core/Encode.cpp). Host arithmetic

@@ -120,7 +120,10 @@ int chd_tensor(const chd_context *ctx, int level, uint32_t *res_bx,
                const uint32_t *a_ax, const uint32_t *b_bx,
                const uint32_t *b_ax, void *stream);
 /* ModSwitchHandler::ModUp (ModSwitch.cu:429-509): dst[beta] each
- * num_q + alpha limbs */
+ * num_q + alpha limbs, beta = chd_context_beta(level). Dnum groups sit on
+ * the chain's positions: at a level missing terminal primes the leading
+ * groups that hold none of its limbs are not written (their pointers may be
+ * NULL). */
 int chd_mod_up(const chd_context *ctx, int level, uint32_t *const *dst,
                const uint32_t *src, void *stream);
 /* ModDown: (num_q + alpha) -> num_q limbs (ModSwitch.cu:511-527) */

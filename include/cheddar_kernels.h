@@ -86,8 +86,9 @@ int chd_k_ntt_inv_mul(const chd_tables *t, const chd_limb_map *m,
 
 /* BConv (src/core/ModSwitch.cu:23-171): for dst position k,
  * dst[pos(k)] = sum_i src[i] * T[k][i] * 2^-32 mod p_k with centred int32
- * sources. table = chd_bconv_table_size(src_len, dst_len) bytes made by
- * chd_bconv_table_pack from the reference-form table T (dst-major).
+ * sources, 1 <= src_len <= 32. table = chd_bconv_table_size(src_len,
+ * dst_len) bytes made by chd_bconv_table_pack from the reference-form
+ * table T (dst-major).
  * pos(k) = k + (k >= skip_lo ? skip_len : 0); prime of pos via m->tab_*. */
 long long chd_bconv_table_size(int src_len, int dst_len);
 int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
@@ -113,13 +114,15 @@ int chd_k_bconv_batch(const chd_tables *t, const chd_limb_map *m,
 
 /* Column pass (stages 0..7) of NTTForModUp for all dnum groups in one launch:
  * group g's polynomial sits at modup + g * group_stride (group_limbs limbs,
- * in place) and its own limbs [g alpha, min((g+1) alpha, m->num_q)) are
- * skipped (NTT.cu:815-887). with_rows also runs stages 8..15 (the complete
- * NTTForModUp); without it the data is left for chd_k_modup_keyacc. */
+ * in place) and its own limbs [max(0, g alpha - group_shift),
+ * min((g+1) alpha - group_shift, m->num_q)) are skipped (NTT.cu:815-887;
+ * group_shift as in chd_keyacc_args). with_rows also runs stages 8..15 (the
+ * complete NTTForModUp); without it the data is left for
+ * chd_k_modup_keyacc. */
 int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
                          uint32_t *modup, long long group_stride,
-                         int num_groups, int alpha, int group_limbs,
-                         int with_rows, void *stream);
+                         int num_groups, int alpha, int group_shift,
+                         int group_limbs, int with_rows, void *stream);
 
 /* Fused ModUp row pass + evaluation-key inner product + CAccum
  * (Context.cpp:609-712, ElementWise.cu:225-366):
@@ -132,7 +135,10 @@ int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
 typedef struct chd_keyacc_args {
   int num_q;
   int tab_off, tab_gap;
-  int alpha, beta;
+  /* beta non-empty ModUp groups; group g owns the level's limbs
+   * [max(0, g alpha - group_shift), min((g+1) alpha - group_shift, num_q)),
+   * group_shift = (max_ter - num_ter) mod alpha (ModSwitch.cu:440-470) */
+  int alpha, beta, group_shift;
   const uint32_t *modup;
   long long group_stride;
   const uint32_t *d;
@@ -234,7 +240,8 @@ int chd_k_gs_fused(const chd_tables *t, const chd_limb_map *m,
 #define CHD_MAX_BS 8
 #define CHD_MAX_BS_GROUPS 4
 typedef struct chd_bs_args {
-  int num_q, alpha, beta, num_rot;
+  /* groups as in chd_keyacc_args */
+  int num_q, alpha, beta, group_shift, num_rot;
   const uint32_t *modup;
   long long group_stride;
   const uint32_t *d;

@@ -374,6 +374,7 @@ void orc_intt_exact(uint32_t *x, int log_n, uint32_t q, int mont_conv) {
 void orc_bconv(uint32_t *dst, const int32_t *src, int src_len, int dst_len,
                const int32_t *table, const uint32_t *dst_primes, int log_n) {
   size_t n = (size_t)1 << log_n;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
   for (int k = 0; k < dst_len; k++) {
     uint32_t p = dst_primes[k];
     uint64_t ri = r_inv(p);
@@ -489,6 +490,7 @@ int orc_mod_up_ex(uint32_t *dst, const uint32_t *src, int L,
     orc_modswitch_consts(primes + start, slen, dprimes, dlen, log_n, 0, 0,
                          const1, const2);
     /* INTTAndMultConst(normalize) over the group's own limbs */
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int i = 0; i < slen; i++)
       orc_intt_mult_const(centred + (size_t)(start + i) * n,
                           src + (size_t)(start + i) * n, log_n,
@@ -498,6 +500,7 @@ int orc_mod_up_ex(uint32_t *dst, const uint32_t *src, int L,
     uint32_t *out = dst + (size_t)g * total * n;
     memcpy(out + (size_t)start * n, src + (size_t)start * n,
            sizeof(uint32_t) * n * slen);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int k = 0; k < dlen; k++) {
       int pos = k < start ? k : k + slen;
       uint32_t *limb = out + (size_t)pos * n;
@@ -567,10 +570,12 @@ void orc_mod_down_ex(uint32_t *dst, const uint32_t *src,
       const2[(size_t)k * slen + i] = normalize(acc, m);
     }
   }
+#pragma omp parallel for num_threads(g_threads) schedule(static)
   for (int i = 0; i < slen; i++)
     orc_intt_mult_const(centred + (size_t)i * n, src + (size_t)drop[i] * n,
                         log_n, sp[i], const1[i], 1);
   orc_bconv(z, centred, slen, dst_len, const2, dst_primes, log_n);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
   for (int k = 0; k < dst_len; k++) {
     uint32_t q = dst_primes[k];
     uint32_t inv = 1, pad = 1;
@@ -653,6 +658,7 @@ void orc_paccum_ex(uint32_t *acc_b, uint32_t *acc_a, const uint32_t *modup,
   size_t n = (size_t)1 << log_n;
   int total = L + alpha;
   size_t key_stride = (size_t)(max_q + alpha) * n;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
   for (int l = 0; l < total; l++) {
     uint32_t q = primes[l];
     uint64_t ri = r_inv(q);

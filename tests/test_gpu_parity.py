@@ -110,6 +110,20 @@ def test_bconv_extreme_centred_values(chd):
     assert np.array_equal(host(out), _orc.bconv(x, o2, dst_p, 16))
 
 
+@pytest.mark.parametrize("src_len", [17, 24, 32])
+def test_bconv_two_k_chunks(chd, src_len):
+    """more than 16 sources take a second MFMA K chunk (ModDownAndRescale of
+    five terminal primes plus twelve aux primes needs 17)"""
+    src_p, dst_p = (Q30 + Q31)[:src_len], Q31[16:40]
+    plan = chd.BconvPlan(src_p, dst_p)
+    _, o2 = _orc.modswitch_consts(src_p, dst_p, 16)
+    x = centred_limbs(rng(40 + src_len), src_p)
+    x[:, :64] = np.array([(p - 1) // 2 for p in src_p], np.int32)[:, None]
+    out = zeros(len(dst_p), N)
+    plan.apply(out, dev(x.view(np.uint32)))
+    assert np.array_equal(host(out), _orc.bconv(x, o2, dst_p, 16))
+
+
 # --------------------------------------------------- key-switch pipeline ----
 @pytest.fixture(scope="module")
 def ks(chd):
