@@ -36,6 +36,7 @@ SOURCES = [
     ("host/cheddar.cpp", False),
     ("host/encoder.cpp", False),
     ("host/param_json.cpp", False),
+    ("host/context_ops.cpp", False),
     ("host/capi.cpp", False),
 ]
 

@@ -363,6 +363,68 @@ __global__ __launch_bounds__(kThreads) void gs_fused_kernel(chd_tables t,
   }
 }
 
+
+// Element-wise arithmetic (ElementWise.cu:33-220 Sum / Sub / Neg / Mult /
+// AddConst / SubConst / SubOppositeConst / MultConst, 600-660
+// MultImaginaryUnit; Basic.cuh:169-260 for the canonical forms).
+__device__ __forceinline__ uint32_t ew_neg(uint32_t a, uint32_t q) {
+  return a == 0 ? 0u : q - a;
+}
+
+__global__ __launch_bounds__(kThreads) void elementwise_kernel(chd_tables t,
+                                                             chd_limb_map m,
+                                                             chd_ew_args a) {
+  const LimbIdx li = limb_of(t, m);
+  const size_t loff = static_cast<size_t>(li.l) << kLogN;
+  const int c0 = blockIdx.x * kCoefPerBlock + threadIdx.x * kPerThread;
+  const size_t aoff = loff + (li.aux ? static_cast<size_t>(a.a_gap) << kLogN : 0);
+  const size_t boff = loff + (li.aux ? static_cast<size_t>(a.b_gap) << kLogN : 0);
+  const uint32_t q = li.q;
+  const int32_t qi = li.qinv;
+  uint32_t cv = 0;
+  const int op = a.op;
+  if (op >= CHD_EW_ADD_CONST && op <= CHD_EW_MULT_CONST)
+    cv = a.cst[li.l + (li.aux ? a.cst_gap : 0)];
+  if (op == CHD_EW_MULT_I) {
+    const int ti = m.tab_off + li.l + (li.aux ? m.tab_gap : 0);
+    cv = t.tw[(static_cast<size_t>(ti) << kLogN) + 1];  // ToMont(psi^(N/2))
+    if (c0 >= kN / 2) cv = ew_neg(cv, q);
+  }
+  for (int p = 0; p < a.num_poly; p++) {
+    const uint4 x = ld4(a.a[p] + aoff + c0);
+    uint4 y = make_uint4(0, 0, 0, 0);
+    if (op == CHD_EW_ADD || op == CHD_EW_SUB || op == CHD_EW_MULT)
+      y = ld4(a.b[p] + boff + c0);
+    else if (op == CHD_EW_PMULT)
+      y = ld4(a.b[0] + boff + c0);
+    uint32_t xv[4] = {x.x, x.y, x.z, x.w};
+    const uint32_t yv[4] = {y.x, y.y, y.z, y.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      switch (op) {
+        case CHD_EW_ADD: o[i] = add_mod(xv[i], yv[i], q); break;
+        case CHD_EW_SUB: o[i] = sub_mod(xv[i], yv[i], q); break;
+        case CHD_EW_NEG: o[i] = ew_neg(xv[i], q); break;
+        case CHD_EW_MULT:
+        case CHD_EW_PMULT:
+          o[i] = mont_mul(static_cast<int32_t>(xv[i]),
+                          static_cast<int32_t>(yv[i]), q, qi);
+          break;
+        case CHD_EW_ADD_CONST: o[i] = add_mod(xv[i], cv, q); break;
+        case CHD_EW_SUB_CONST: o[i] = sub_mod(xv[i], cv, q); break;
+        case CHD_EW_SUB_OPP_CONST: o[i] = sub_mod(cv, xv[i], q); break;
+        case CHD_EW_MULT_CONST:
+        case CHD_EW_MULT_I:
+          o[i] = mont_mul(static_cast<int32_t>(xv[i]),
+                          static_cast<int32_t>(cv), q, qi);
+          break;
+        default: o[i] = xv[i]; break;
+      }
+    }
+    st4(a.dst[p] + loff + c0, make_uint4(o[0], o[1], o[2], o[3]));
+  }
+}
 }  // namespace
 }  // namespace chd
 
@@ -556,4 +618,26 @@ extern "C" int chd_k_gs_fused(const chd_tables *t, const chd_limb_map *m,
   hipLaunchKernelGGL(gs_fused_kernel, g, dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), *t, *m, *args);
   return check_launch("chd_k_gs_fused");
+}
+
+extern "C" int chd_k_elementwise(const chd_tables *t, const chd_limb_map *m,
+                                 const chd_ew_args *args, int num_limbs,
+                                 void *stream) {
+  if (!t || !m || !args || num_limbs < 1 || args->num_poly < 1 ||
+      args->num_poly > CHD_MAX_POLY || args->op < CHD_EW_ADD ||
+      args->op > CHD_EW_COPY || m->skip_len != 0)
+    return set_error(CHD_ERR_ARG, "chd_k_elementwise: invalid argument");
+  const int op = args->op;
+  const bool need_b =
+      op == CHD_EW_ADD || op == CHD_EW_SUB || op == CHD_EW_MULT;
+  const bool need_c = op >= CHD_EW_ADD_CONST && op <= CHD_EW_MULT_CONST;
+  if ((need_c && !args->cst) || (op == CHD_EW_PMULT && !args->b[0]))
+    return set_error(CHD_ERR_ARG, "chd_k_elementwise: missing operand");
+  for (int p = 0; p < args->num_poly; p++)
+    if (!args->dst[p] || !args->a[p] || (need_b && !args->b[p]))
+      return set_error(CHD_ERR_ARG, "chd_k_elementwise: null polynomial");
+  dim3 g(kN / kCoefPerBlock, num_limbs);
+  hipLaunchKernelGGL(elementwise_kernel, g, dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), *t, *m, *args);
+  return check_launch("chd_k_elementwise");
 }

@@ -765,6 +765,66 @@ extern "C" int chd_hoist_evaluate(
            })
 }
 
+// --------------------------------------------------------- element-wise --
+extern "C" int chd_elementwise(const chd_context *ctx, int level, int num_aux,
+                               int op, int num_poly, uint32_t *const *dst,
+                               const uint32_t *const *a,
+                               const uint32_t *const *b, const uint32_t *cst,
+                               void *stream) {
+  CHD_CALL("chd_elementwise",
+           LevelOk(ctx, level) && num_aux >= 0 &&
+               num_aux <= ctx->c->param_.alpha_ && num_poly >= 1 &&
+               num_poly <= CHD_MAX_POLY && dst && a && op >= CHD_EW_ADD &&
+               op <= CHD_EW_COPY,
+           {
+             const auto &p = ctx->c->param_;
+             const auto &eh = ctx->c->elem_handler_;
+             const cheddar::NPInfo np = p.LevelToNP(level, num_aux);
+             const int words = np.GetNumTotal() * p.degree_;
+             const int aux = num_aux * p.degree_;
+             std::vector<cheddar::DvView<word>> d;
+             std::vector<cheddar::DvConstView<word>> x, y;
+             for (int i = 0; i < num_poly; i++) {
+               if (!dst[i] || !a[i]) throw cheddar::Error("null polynomial");
+               d.emplace_back(dst[i], words, aux);
+               x.emplace_back(a[i], words, aux);
+             }
+             const bool two = op == CHD_EW_ADD || op == CHD_EW_SUB ||
+                              op == CHD_EW_MULT;
+             if (two) {
+               if (!b) throw cheddar::Error("missing second operand");
+               for (int i = 0; i < num_poly; i++) {
+                 if (!b[i]) throw cheddar::Error("null polynomial");
+                 y.emplace_back(b[i], words, aux);
+               }
+             }
+             const bool konst = op >= CHD_EW_ADD_CONST &&
+                                op <= CHD_EW_MULT_CONST;
+             if (konst && !cst) throw cheddar::Error("missing constant");
+             const cheddar::DvConstView<word> c(cst, np.GetNumTotal(),
+                                                num_aux);
+             switch (op) {
+               case CHD_EW_ADD: eh.Add(d, np, x, y); break;
+               case CHD_EW_SUB: eh.Sub(d, np, x, y); break;
+               case CHD_EW_NEG: eh.Neg(d, np, x); break;
+               case CHD_EW_MULT: eh.Mult(d, np, x, y); break;
+               case CHD_EW_PMULT:
+                 if (!b || !b[0]) throw cheddar::Error("missing plaintext");
+                 eh.PMult(d, np, x,
+                          cheddar::DvConstView<word>(b[0], words, aux));
+                 break;
+               case CHD_EW_ADD_CONST: eh.AddConst(d, np, x, c); break;
+               case CHD_EW_SUB_CONST: eh.SubConst(d, np, x, c); break;
+               case CHD_EW_SUB_OPP_CONST:
+                 eh.SubOppositeConst(d, np, x, c);
+                 break;
+               case CHD_EW_MULT_CONST: eh.MultConst(d, np, x, c); break;
+               case CHD_EW_MULT_I: eh.MultImaginaryUnit(d, np, x); break;
+               default: eh.Copy(d, np, x); break;
+             }
+           })
+}
+
 // ------------------------------------------------------------- encoder --
 namespace {
 std::vector<cheddar::Complex> Message(const double *re, const double *im,

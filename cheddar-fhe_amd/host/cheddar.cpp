@@ -486,7 +486,8 @@ void ElementWiseHandler<uint32_t>::Tensor(
     AssertTrue(d.TotalSize() == np.GetNumTotal() * n, "Tensor: NP mismatch");
   chd_limb_map m = NoSkipMap(param_, np);
   m.src_gap = (src1[0].QSize() - q_size) / n;
-  AssertTrue(src2[0].QSize() - q_size == src1[0].QSize() - q_size,
+  AssertTrue(np.num_aux_ == 0 ||
+                 src2[0].QSize() - q_size == src1[0].QSize() - q_size,
              "Tensor: source gap mismatch");
   K(chd_k_tensor(&ntt_.Tables(), &m, dst[0].data(), dst[1].data(),
                  dst[2].data(), src1[0].data(), src1[1].data(), src2[0].data(),
@@ -1114,6 +1115,12 @@ Context<uint32_t>::Context(const Parameter<word> &param)
   HipCheck(hipMemcpy(p_prod_.data(), h.data(), num_q * sizeof(word),
                      hipMemcpyHostToDevice),
            "hipMemcpy");
+  // level-down constants: EncodeConstant(1.0) at each level's default scale
+  // (Context.cpp:102-107; there only built with sparse-secret
+  // encapsulation, here always, so LevelDown works for every parameter set)
+  level_down_consts_.resize(param_.default_encryption_level_ + 1);
+  for (int i = param_.default_encryption_level_; i > 0; i--)
+    encoder_.EncodeConstant(level_down_consts_[i], i, param_.GetScale(i), 1.0);
 }
 
 DvConstView<uint32_t> Context<uint32_t>::GetPProd(const NPInfo &np) const {

@@ -416,8 +416,35 @@ class ElementWiseHandler<uint32_t> {
                     const std::vector<int> &permute_amounts,
                     const std::vector<std::vector<DvConstView<word>>> &srcs)
       const;
+  // ElementWise.cu:687-920, 1673-1706 (canonical residues in and out)
+  using Views = std::vector<DvView<word>>;
+  using CViews = std::vector<DvConstView<word>>;
+  void Add(Views &dst, const NPInfo &np, const CViews &src1,
+           const CViews &src2) const;
+  void Sub(Views &dst, const NPInfo &np, const CViews &src1,
+           const CViews &src2) const;
+  void Neg(Views &dst, const NPInfo &np, const CViews &src1) const;
+  void Mult(Views &dst, const NPInfo &np, const CViews &src1,
+            const CViews &src2) const;
+  void PMult(Views &dst, const NPInfo &np, const CViews &src1,
+             const DvConstView<word> &src2) const;
+  void AddConst(Views &dst, const NPInfo &np, const CViews &src1,
+                const DvConstView<word> &src_const) const;
+  void SubConst(Views &dst, const NPInfo &np, const CViews &src1,
+                const DvConstView<word> &src_const) const;
+  // dst = const - src1
+  void SubOppositeConst(Views &dst, const NPInfo &np, const CViews &src1,
+                        const DvConstView<word> &src_const) const;
+  void MultConst(Views &dst, const NPInfo &np, const CViews &src1,
+                 const DvConstView<word> &src_const) const;
+  // multiplication by X^(N/2), the imaginary unit of the slots
+  void MultImaginaryUnit(Views &dst, const NPInfo &np,
+                         const CViews &src1) const;
+  void Copy(Views &dst, const NPInfo &np, const CViews &src1) const;
 
  private:
+  void Elementwise(int op, Views &dst, const NPInfo &np, const CViews &src1,
+                   const CViews *src2, const DvConstView<word> *cst) const;
   void CPAccumWorker(bool const_accum, std::vector<DvView<word>> &dst,
                      const NPInfo &np,
                      const std::vector<std::vector<DvConstView<word>>> &ct_srcs,
@@ -572,6 +599,38 @@ class Context<uint32_t> {
   void HRot(Ct &res, const Ct &a, const Evk &rot_key, int rot_dist) const;
   void Permute(Ct &res, const Ct &a, int rot_dist) const;
 
+  // element-wise entry points (Context.h:95-300, Context.cpp:132-560,
+  // 794-929); operands share the primes (and scale, where added)
+  using Pt = Plaintext<word>;
+  using Const = Constant<word>;
+  void Copy(Ct &res, const Ct &a) const;
+  void Add(Ct &res, const Ct &a, const Ct &b) const;
+  void Add(Ct &res, const Ct &a, const Pt &b) const;
+  void Add(Ct &res, const Ct &a, const Const &b) const;
+  void Sub(Ct &res, const Ct &a, const Ct &b) const;
+  void Sub(Ct &res, const Ct &a, const Pt &b) const;
+  void Sub(Ct &res, const Ct &a, const Const &b) const;
+  void Sub(Ct &res, const Pt &a, const Ct &b) const;
+  void Sub(Ct &res, const Const &a, const Ct &b) const;
+  void Neg(Ct &res, const Ct &a) const;
+  void Mult(Ct &res, const Ct &a, const Pt &b) const;
+  void Mult(Ct &res, const Ct &a, const Const &b) const;
+  bool IsMultUnsafeCompatible(int level1, int level2) const;
+  void MultUnsafe(Ct &res, const Ct &a, const Ct &b, int level = -1) const;
+  void MultUnsafe(Ct &res, const Ct &a, const Pt &b, int level = -1) const;
+  void MultUnsafe(Ct &res, const Ct &a, const Const &b, int level = -1) const;
+  void PermuteConjugate(Ct &res, const Ct &a) const;
+  void MultImaginaryUnit(Ct &res, const Ct &a) const;
+  void HConj(Ct &res, const Ct &a, const Evk &conj_key) const;
+  void HRotAdd(Ct &res, const Ct &a, const Ct &b, const Evk &rot_key,
+               int rot_dist) const;
+  void HConjAdd(Ct &res, const Ct &a, const Ct &b, const Evk &conj_key) const;
+  // res += a * b on res's primes (Context.cpp:873-915)
+  void MadUnsafe(Ct &res, const Ct &a, const Const &b) const;
+  // multiplication by the encoded constant 1 at the level's scale, then
+  // Rescale, down to target_level (Context.cpp:917-929)
+  void LevelDown(Ct &res, const Ct &a, int target_level) const;
+
   // view-level core used by the C++ API above and by the C-ABI
   struct CtRef {           // polynomials of num_q limbs (rx optional)
     word *bx = nullptr, *ax = nullptr, *rx = nullptr;
@@ -623,6 +682,8 @@ class Context<uint32_t> {
                      const word *add_b = nullptr) const;
   DeviceVector<word> p_prod_;
   std::unique_ptr<Workspace> ws_;
+  // EncodeConstant(1.0) at each level's default scale, for LevelDown
+  std::vector<Constant<word>> level_down_consts_;
 };
 
 template <typename word>

@@ -83,6 +83,7 @@ _SIGS = {
     "chd_hoist_create_from_messages": (_i, [_pp, _vp, _i, ctypes.c_double,
                                             _i, _ip, _i, _ip, _pp, _pp, _ip,
                                             _i, _vp]),
+    "chd_elementwise": (_i, [_vp, _i, _i, _i, _i, _pp, _pp, _pp, _vp, _vp]),
     "chd_encode": (_i, [_vp, _i, _i, ctypes.c_double, _dp, _dp, _i, _vp,
                         _vp]),
     "chd_encode_constant": (_i, [_vp, _i, _i, ctypes.c_double,
@@ -340,6 +341,19 @@ class Context:
             self.h, level, ptr(res[0]), ptr(res[1]), ptr(ct[0]), ptr(ct[1]),
             len(gs), (ctypes.c_int * len(gs))(*gs), len(bs),
             (ctypes.c_int * len(bs))(*bs), parr, nk, kr, kb, ka, beta,
+            self._s(stream)))
+
+    EW_OPS = {"add": 0, "sub": 1, "neg": 2, "mult": 3, "pmult": 4,
+              "add_const": 5, "sub_const": 6, "sub_opp_const": 7,
+              "mult_const": 8, "mult_i": 9, "copy": 10}
+
+    def elementwise(self, level, num_aux, op, dst, a, b=None, cst=None,
+                    stream=None):
+        """ElementWiseHandler op on lists of polynomials (device tensors)"""
+        _check(lib.chd_elementwise(
+            self.h, level, num_aux, self.EW_OPS[op], len(dst),
+            ptr_array(dst), ptr_array(a),
+            ptr_array(b) if b is not None else None, ptr(cst),
             self._s(stream)))
 
     def encode(self, level, num_aux, scale, msg, dst, stream=None):

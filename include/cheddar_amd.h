@@ -257,6 +257,17 @@ int chd_hoist_evaluate(const chd_context *ctx, int level, uint32_t *res_bx,
                        const uint32_t *const *key_ax, int key_beta,
                        void *stream);
 
+/* ElementWiseHandler ops (src/core/ElementWise.cu:687-920, 1673-1706) on
+ * num_poly (1..3) polynomials of num_q(level) + num_aux limbs, canonical in
+ * and out: op is one of CHD_EW_* (include/cheddar_kernels.h); b[p] is read
+ * by ADD / SUB / MULT, b[0] by PMULT (one plaintext for every polynomial);
+ * cst (one Montgomery-form value per limb, a Constant's cx_) by the *_CONST
+ * ops. dst may alias a or b. */
+int chd_elementwise(const chd_context *ctx, int level, int num_aux, int op,
+                    int num_poly, uint32_t *const *dst,
+                    const uint32_t *const *a, const uint32_t *const *b,
+                    const uint32_t *cst, void *stream);
+
 /* ------------------------------------------------------------ encoder --
  * Encoder::Encode (src/core/Encode.cpp:23-43, 84-109, 135-190): the message
  * (msg_re[i], msg_im[i], i < msg_len, zero-padded to the next power of two

@@ -257,6 +257,38 @@ typedef struct chd_bs_args {
 int chd_k_bs_fused(const chd_tables *t, const chd_limb_map *m,
                    const chd_bs_args *args, void *stream);
 
+/* Element-wise ops over num_poly polynomials of m->num_q q limbs plus aux
+ * limbs (ElementWise.cu:33-220, 600-660, Basic.cuh:169-260), canonical in
+ * and out. b: per polynomial (ADD, SUB, MULT) or b[0] for every polynomial
+ * (PMULT). cst: one value per limb (the *_CONST ops). MULT_I multiplies by
+ * the imaginary unit X^(N/2), i.e. by +-ToMont(psi^(N/2)) of each limb (the
+ * second entry of its twiddle table), negated in the upper half of the
+ * evaluation points. a_gap / b_gap / cst_gap: aux-limb gaps as in
+ * chd_limb_map.src_gap (in limbs, or entries for cst). */
+#define CHD_EW_ADD 0
+#define CHD_EW_SUB 1
+#define CHD_EW_NEG 2
+#define CHD_EW_MULT 3
+#define CHD_EW_PMULT 4
+#define CHD_EW_ADD_CONST 5
+#define CHD_EW_SUB_CONST 6
+#define CHD_EW_SUB_OPP_CONST 7
+#define CHD_EW_MULT_CONST 8
+#define CHD_EW_MULT_I 9
+#define CHD_EW_COPY 10
+typedef struct chd_ew_args {
+  int op;
+  int num_poly;
+  uint32_t *dst[CHD_MAX_POLY];
+  const uint32_t *a[CHD_MAX_POLY];
+  const uint32_t *b[CHD_MAX_POLY];
+  int a_gap, b_gap;
+  const uint32_t *cst;
+  int cst_gap;
+} chd_ew_args;
+int chd_k_elementwise(const chd_tables *t, const chd_limb_map *m,
+                      const chd_ew_args *args, int num_limbs, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

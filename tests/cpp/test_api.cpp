@@ -315,6 +315,224 @@ int main() {
       ok = map.at(4).at(1)[(j + 4) % w] == Complex(50 + j, 0);
     check("LinearTransform::ConstructPlainHoistMap", ok);
   }
+  // element-wise Context ops (Context.cpp:132-315, 333-412, 530-560,
+  // 794-929) against host modular arithmetic, the oracle's key switch and
+  // permutation, and the encoder (decode of the b polynomial of a
+  // ciphertext whose a polynomial is zero)
+  {
+    auto lanes = [&](const std::vector<word> &x, const std::vector<word> &y,
+                     int limbs, auto f) {
+      std::vector<word> r(static_cast<size_t>(limbs) * kN);
+      for (int l = 0; l < limbs; l++)
+        for (size_t n = 0; n < kN; n++)
+          r[l * kN + n] = f(x[l * kN + n], y.empty() ? 0 : y[l * kN + n],
+                            static_cast<uint64_t>(main_p[l]), l);
+      return r;
+    };
+    auto add = [](uint64_t x, uint64_t y, uint64_t p, int) {
+      return static_cast<word>((x + y) % p);
+    };
+    auto sub = [](uint64_t x, uint64_t y, uint64_t p, int) {
+      return static_cast<word>((x + p - y) % p);
+    };
+    auto neg = [](uint64_t x, uint64_t, uint64_t p, int) {
+      return static_cast<word>((p - x) % p);
+    };
+    auto mul = [](uint64_t x, uint64_t y, uint64_t p, int) {
+      return orc_mont_mul(static_cast<word>(x), static_cast<word>(y),
+                          static_cast<word>(p));
+    };
+    const std::vector<word> none;
+    auto bx_of = [&](const Ct &c) {
+      return download(c.bx_.data(), static_cast<size_t>(c.GetNP().GetNumQ()) * kN);
+    };
+    auto ax_of = [&](const Ct &c) {
+      return download(c.ax_.data(), static_cast<size_t>(c.GetNP().GetNumQ()) * kN);
+    };
+    Ct r;
+    ctx->Add(r, a, b);
+    check("Context::Add(ct, ct)", same(bx_of(r), lanes(hb1, hb2, L, add)) &&
+                                      same(ax_of(r), lanes(ha1, ha2, L, add)) &&
+                                      r.GetScale() == 0x1p30 && !r.HasRx());
+    ctx->Sub(r, a, b);
+    check("Context::Sub(ct, ct)", same(bx_of(r), lanes(hb1, hb2, L, sub)) &&
+                                      same(ax_of(r), lanes(ha1, ha2, L, sub)));
+    ctx->Neg(r, a);
+    check("Context::Neg", same(bx_of(r), lanes(hb1, none, L, neg)) &&
+                              same(ax_of(r), lanes(ha1, none, L, neg)));
+    {  // in place, res aliasing the second operand
+      Ct c2;
+      ctx->Copy(c2, b);
+      ctx->Sub(c2, a, c2);
+      check("Context::Sub in place", same(bx_of(c2), lanes(hb1, hb2, L, sub)) &&
+                                         same(ax_of(c2), lanes(ha1, ha2, L, sub)));
+    }
+    // plaintext and constant operands
+    std::vector<Complex> msg(1 << 10);
+    for (auto &m : msg)
+      m = Complex((next64() % 2001) / 1000.0 - 1.0,
+                  (next64() % 2001) / 1000.0 - 1.0);
+    Plaintext<word> pt;
+    ctx->encoder_.Encode(pt, L - 1, 0x1p30, msg);
+    const std::vector<word> hm = download(pt.mx_.data(), qw);
+    Constant<word> cst;
+    ctx->encoder_.EncodeConstant(cst, L - 1, 0x1p30, 0.75);
+    const std::vector<word> hc = download(cst.cx_.data(), L);
+    std::vector<word> hcb(qw);
+    for (int l = 0; l < L; l++)
+      for (size_t n = 0; n < kN; n++) hcb[l * kN + n] = hc[l];
+    ctx->Add(r, a, pt);
+    check("Context::Add(ct, pt)", same(bx_of(r), lanes(hb1, hm, L, add)) &&
+                                      same(ax_of(r), ha1));
+    ctx->Sub(r, pt, a);
+    check("Context::Sub(pt, ct)", same(bx_of(r), lanes(hm, hb1, L, sub)) &&
+                                      same(ax_of(r), lanes(ha1, none, L, neg)));
+    ctx->Add(r, a, cst);
+    check("Context::Add(ct, const)", same(bx_of(r), lanes(hb1, hcb, L, add)) &&
+                                         same(ax_of(r), ha1));
+    ctx->Sub(r, a, cst);
+    check("Context::Sub(ct, const)", same(bx_of(r), lanes(hb1, hcb, L, sub)));
+    ctx->Sub(r, cst, a);
+    check("Context::Sub(const, ct)", same(bx_of(r), lanes(hcb, hb1, L, sub)) &&
+                                         same(ax_of(r), lanes(ha1, none, L, neg)));
+    ctx->Mult(r, a, pt);
+    check("Context::Mult(ct, pt)", same(bx_of(r), lanes(hb1, hm, L, mul)) &&
+                                       same(ax_of(r), lanes(ha1, hm, L, mul)) &&
+                                       r.GetScale() == 0x1p60);
+    ctx->Mult(r, a, cst);
+    check("Context::Mult(ct, const)", same(bx_of(r), lanes(hb1, hcb, L, mul)) &&
+                                          same(ax_of(r), lanes(ha1, hcb, L, mul)));
+    {  // MultUnsafe at a lower level reads the operands' leading limbs
+      const int lo = L - 4;
+      ctx->MultUnsafe(r, a, pt, lo - 1);
+      const std::vector<word> sb(hb1.begin(), hb1.begin() + lo * kN),
+          sm(hm.begin(), hm.begin() + lo * kN);
+      check("Context::MultUnsafe(ct, pt, level)",
+            r.GetNP() == param.LevelToNP(lo - 1) &&
+                same(bx_of(r), lanes(sb, sm, lo, mul)));
+      Ct t;
+      ctx->MultUnsafe(t, a, b, lo - 1);
+      std::vector<word> tb(lo * kN), ta(lo * kN), tr(lo * kN);
+      const std::vector<word> a1(hb1.begin(), hb1.begin() + lo * kN),
+          a2(ha1.begin(), ha1.begin() + lo * kN),
+          b1(hb2.begin(), hb2.begin() + lo * kN),
+          b2(ha2.begin(), ha2.begin() + lo * kN);
+      orc_tensor(tb.data(), ta.data(), tr.data(), a1.data(), a2.data(),
+                 b1.data(), b2.data(), lo, main_p.data(), kLogN);
+      check("Context::MultUnsafe(ct, ct, level)",
+            t.HasRx() && same(bx_of(t), tb) && same(ax_of(t), ta) &&
+                same(download(t.rx_.data(), lo * kN), tr));
+    }
+    // MadUnsafe: res += a * const, rx started from zero
+    {
+      Ct acc;
+      ctx->Copy(acc, b);
+      acc.SetScale(0x1p60);
+      ctx->MadUnsafe(acc, a, cst);
+      check("Context::MadUnsafe",
+            same(bx_of(acc), lanes(hb2, lanes(hb1, hcb, L, mul), L, add)) &&
+                same(ax_of(acc), lanes(ha2, lanes(ha1, hcb, L, mul), L, add)));
+    }
+    // MultImaginaryUnit: twice is Neg exactly; on an encoding, decode gives
+    // i * m
+    {
+      Ct t, u;
+      ctx->MultImaginaryUnit(t, a);
+      ctx->MultImaginaryUnit(u, t);
+      bool ok = same(bx_of(u), lanes(hb1, none, L, neg)) &&
+                same(ax_of(u), lanes(ha1, none, L, neg));
+      Ct e(np);
+      upload(e.bx_.data(), hm);
+      upload(e.ax_.data(), std::vector<word>(qw, 0));
+      e.SetScale(0x1p30);
+      e.SetNumSlots(1 << 10);
+      ctx->MultImaginaryUnit(t, e);
+      Plaintext<word> back(np);
+      back.SetScale(0x1p30);
+      back.SetNumSlots(1 << 10);
+      upload(back.mx_.data(), bx_of(t));
+      std::vector<Complex> dec;
+      ctx->encoder_.Decode(dec, back);
+      double err = 0;
+      for (size_t i = 0; i < msg.size(); i++)
+        err = std::max(err, std::abs(dec[i] - Complex(0, 1) * msg[i]));
+      check("Context::MultImaginaryUnit (i*i = -1, decodes to i*m)",
+            ok && err < 1e-3);
+      // PermuteConjugate on the same encoding decodes to conj(m)
+      ctx->PermuteConjugate(t, e);
+      upload(back.mx_.data(), bx_of(t));
+      ctx->encoder_.Decode(dec, back);
+      err = 0;
+      for (size_t i = 0; i < msg.size(); i++)
+        err = std::max(err, std::abs(dec[i] - std::conj(msg[i])));
+      check("Context::PermuteConjugate decodes to conj(m)", err < 1e-3);
+    }
+    // HConj / HConjAdd / HRotAdd against the oracle's MultKey + permutation
+    {
+      std::vector<word> mb(qw), ma(qw), pb(qw), pa(qw);
+      orc_mult_key(mb.data(), ma.data(), hb1.data(), ha1.data(), kb.data(),
+                   ka.data(), L, L, main_p.data(), aux_p.data(), alpha, kLogN);
+      const uint32_t gconj = 2 * static_cast<uint32_t>(kN) - 1;
+      orc_permute(pb.data(), mb.data(), L, kLogN, gconj);
+      orc_permute(pa.data(), ma.data(), L, kLogN, gconj);
+      ctx->HConj(r, a, key);
+      check("Context::HConj", same(bx_of(r), pb) && same(ax_of(r), pa));
+      ctx->HConjAdd(r, a, b, key);
+      check("Context::HConjAdd", same(bx_of(r), lanes(pb, hb2, L, add)) &&
+                                     same(ax_of(r), lanes(pa, ha2, L, add)));
+      std::vector<word> hrb(qw), hra(qw);
+      orc_hrot(hrb.data(), hra.data(), hb1.data(), ha1.data(), kb.data(),
+               ka.data(), L, L, main_p.data(), aux_p.data(), alpha, kLogN, 5);
+      Ct c2;
+      ctx->Copy(c2, b);
+      ctx->HRotAdd(c2, a, c2, key, 5);
+      check("Context::HRotAdd (res aliases b)",
+            same(bx_of(c2), lanes(hrb, hb2, L, add)) &&
+                same(ax_of(c2), lanes(hra, ha2, L, add)));
+    }
+    // LevelDown by three levels: Mult by the level's unit constant, then
+    // Rescale, per level (Context.cpp:917-929), and the encoding survives
+    {
+      const int top = L - 1, target = L - 4;
+      std::vector<word> xb = hb1, xa = ha1;
+      for (int lv = top; lv > target; lv--) {
+        const int lim = lv + 1;
+        Constant<word> c1;
+        ctx->encoder_.EncodeConstant(c1, lv, param.GetScale(lv), 1.0);
+        const std::vector<word> h1 = download(c1.cx_.data(), lim);
+        std::vector<word> hb(lim * kN);
+        for (int l = 0; l < lim; l++)
+          for (size_t n = 0; n < kN; n++) hb[l * kN + n] = h1[l];
+        std::vector<word> tb = lanes(xb, hb, lim, mul),
+                          ta = lanes(xa, hb, lim, mul);
+        xb.assign((lim - 1) * kN, 0);
+        xa.assign((lim - 1) * kN, 0);
+        orc_rescale(xb.data(), tb.data(), lim, main_p.data(), 1, kLogN);
+        orc_rescale(xa.data(), ta.data(), lim, main_p.data(), 1, kLogN);
+      }
+      ctx->LevelDown(r, a, target);
+      bool ok = r.GetNP() == param.LevelToNP(target) && same(bx_of(r), xb) &&
+                same(ax_of(r), xa);
+      Ct e(np), d;
+      upload(e.bx_.data(), hm);
+      upload(e.ax_.data(), std::vector<word>(qw, 0));
+      e.SetScale(0x1p30);
+      e.SetNumSlots(1 << 10);
+      ctx->LevelDown(d, e, target);
+      const NPInfo tnp = param.LevelToNP(target);
+      Plaintext<word> back(tnp);
+      back.SetScale(d.GetScale());
+      back.SetNumSlots(1 << 10);
+      upload(back.mx_.data(), bx_of(d));
+      std::vector<Complex> dec;
+      ctx->encoder_.Decode(dec, back);
+      double err = 0;
+      for (size_t i = 0; i < msg.size(); i++)
+        err = std::max(err, std::abs(dec[i] - msg[i]));
+      check("Context::LevelDown (oracle, and the encoding survives)",
+            ok && err < 1e-3);
+    }
+  }
   // an invalid call throws cheddar::Error instead of exiting
   {
     bool threw = false;
