@@ -126,6 +126,17 @@ __device__ __forceinline__ uint32_t canon4(uint32_t x, uint32_t q) {
 
 __device__ __forceinline__ int pidx(int i) { return i + (i >> 4); }
 
+// Coalesced tile layout of the row passes: a workgroup owns kTileRows
+// consecutive rows (16 KiB contiguous); in store round v (0..3) thread t owns
+// the 16 bytes at tile offset 16 (t + 256 v), i.e. tile elements
+// 4 (t + 256 v) .. + 3.
+__device__ __forceinline__ uint32_t tile_byte(int tile) {
+  return static_cast<uint32_t>(tile) * (kTileRows * kCols * 4u);
+}
+__device__ __forceinline__ uint32_t tile_lane_byte(int v) {
+  return (threadIdx.x + 256u * v) * 16u;
+}
+
 // base of polynomial z: explicit list or base + z * stride
 __device__ __forceinline__ uint32_t *poly_dst(const NttArgs &a, int z) {
   return a.dst_list[0] != nullptr ? a.dst_list[z] : a.dst + z * a.dst_pstride;
@@ -165,6 +176,18 @@ template <typename T>
 __device__ __forceinline__ void st_nt(void *base, uint32_t byte_off, T v) {
   __builtin_nontemporal_store(
       v, reinterpret_cast<T *>(static_cast<char *>(base) + byte_off));
+}
+
+// the 4 words of store round v (tile_lane_byte) from the padded LDS tile
+// (rows of kRowPad words, column i at pidx(i))
+__device__ __forceinline__ u32x4 tile_lds4(const uint32_t *xt, int v) {
+  const int e = 4 * (threadIdx.x + 256 * v);
+  const uint32_t *p = xt + (e >> 8) * kRowPad;
+  const int cc = e & 255;
+  u32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; j++) o[j] = p[pidx(cc + j)];
+  return o;
 }
 
 // Per-limb arithmetic policy. Values between the two passes of a transform
@@ -336,7 +359,6 @@ __device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
   const int c = threadIdx.x & 15;
   const int r = threadIdx.x >> 4;
   const int row = blockIdx.x * kTileRows + r;
-  const uint32_t rbase = static_cast<uint32_t>(row * kCols) * 4u;
   T *xr = reinterpret_cast<T *>(xch) + r * kRowPad;
   uint32_t w1[15], w2[15];
 #pragma unroll
@@ -379,29 +401,38 @@ __device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
     }
   }
-  uint32_t out[16];
+  // canonical values back through LDS: each wave then stores 1 KiB of the
+  // tile's contiguous 16 KiB per instruction (a lane's own 16 words would
+  // be 16-byte pieces at a 64-byte stride, four times the cache lines per
+  // store instruction)
+  __syncthreads();  // every lane has read its exchange values
+  uint32_t *xu = reinterpret_cast<uint32_t *>(xr);
+#pragma unroll
+  for (int k = 0; k < 16; k++) xu[pidx(16 * c + k)] = ar.canon_fwd(x[k]);
+  __syncthreads();
+  const uint32_t *xt = reinterpret_cast<const uint32_t *>(xch);
+  char *tile = reinterpret_cast<char *>(dst) + tile_byte(blockIdx.x);
+  [[maybe_unused]] const int32_t qs = static_cast<int32_t>(q);
+  [[maybe_unused]] int32_t c2 = 0, c2q = 0;
   if constexpr (kEpi == kEpiModDown) {
-    // NTTPhase2ForModDown epilogue (NTT.cu:567-600); src2 (and its optional
-    // padding product) was loaded and prepared before the butterflies
-    const int32_t qs = static_cast<int32_t>(q);
-    const int32_t c2 = static_cast<int32_t>(a.cst2[lb.l]);
-    const int32_t c2q = static_cast<int32_t>(static_cast<uint32_t>(c2) * qinv);
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-      const int32_t v = static_cast<int32_t>(s2v[k]) -
-                        static_cast<int32_t>(ar.canon_fwd(x[k]));
-      out[k] = static_cast<uint32_t>(norm(mont(v, c2, c2q, qs), qs));
-    }
-  } else {
-#pragma unroll
-    for (int k = 0; k < 16; k++) out[k] = ar.canon_fwd(x[k]);
+    c2 = static_cast<int32_t>(a.cst2[lb.l]);
+    c2q = static_cast<int32_t>(static_cast<uint32_t>(c2) * qinv);
   }
-  uint4 *o4 = reinterpret_cast<uint4 *>(reinterpret_cast<char *>(dst) + rbase +
-                                        64u * c);
 #pragma unroll
-  for (int v = 0; v < 4; v++)
-    o4[v] = make_uint4(out[4 * v], out[4 * v + 1], out[4 * v + 2],
-                       out[4 * v + 3]);
+  for (int v = 0; v < 4; v++) {
+    u32x4 o = tile_lds4(xt, v);
+    if constexpr (kEpi == kEpiModDown) {
+      // NTTPhase2ForModDown epilogue (NTT.cu:567-600); src2 (and its
+      // optional padding product) was loaded before the butterflies
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int32_t d = static_cast<int32_t>(s2v[4 * v + j]) -
+                          static_cast<int32_t>(o[j]);
+        o[j] = static_cast<uint32_t>(norm(mont(d, c2, c2q, qs), qs));
+      }
+    }
+    st_nt<u32x4>(tile, tile_lane_byte(v), o);
+  }
 }
 
 template <int kEpi>
@@ -425,17 +456,19 @@ __global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
   uint32_t x[16];
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = ld_nt<uint32_t>(dst, rbase + (c + 16 * k) * 4u);
-  // ModDown epilogue operand: this thread's 16 output words of src2 (zero
-  // outside [src2_lo, src2_hi)), loaded with the data so their latency hides
-  // behind the butterflies
+  // ModDown epilogue operand: src2 at this thread's 16 output words of the
+  // coalesced store layout (zero outside [src2_lo, src2_hi)), loaded with the
+  // data so their latency hides behind the butterflies
   uint32_t s2v[16] = {};
   if constexpr (kEpi == kEpiModDown) {
     if (lb.l >= a.src2_lo && lb.l < a.src2_hi) {
       const uint32_t *s2p = a.src2 + blockIdx.z * a.src2_pstride +
                             (static_cast<size_t>(lb.l - a.src2_lo) << kLogN);
+      const char *s2t = reinterpret_cast<const char *>(s2p) +
+                        tile_byte(blockIdx.x);
 #pragma unroll
       for (int v = 0; v < 4; v++) {
-        const uint4 t = ld_nt<uint4>(s2p, rbase + 64u * c + 16u * v);
+        const uint4 t = ld_nt<uint4>(s2t, tile_lane_byte(v));
         s2v[4 * v] = t.x;
         s2v[4 * v + 1] = t.y;
         s2v[4 * v + 2] = t.z;
@@ -476,7 +509,6 @@ __device__ __forceinline__ void inv_rows_body(const NttArgs &a, const Limb &lb,
   const int c = threadIdx.x & 15;
   const int r = threadIdx.x >> 4;
   const int row = blockIdx.x * kTileRows + r;
-  const uint32_t rbase = static_cast<uint32_t>(row * kCols) * 4u;
   T *xr = reinterpret_cast<T *>(xch) + r * kRowPad;
   uint32_t w1[15], w2[15];
 #pragma unroll
@@ -519,8 +551,15 @@ __device__ __forceinline__ void inv_rows_body(const NttArgs &a, const Limb &lb,
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
     }
   }
+  // through LDS again so each wave stores 1 KiB contiguous per instruction
+  __syncthreads();  // every lane has read its exchange values
 #pragma unroll
-  for (int k = 0; k < 16; k++) st_nt<T>(dst, rbase + (c + 16 * k) * 4u, x[k]);
+  for (int k = 0; k < 16; k++) xr[pidx(c + 16 * k)] = x[k];
+  __syncthreads();
+  const uint32_t *xt = reinterpret_cast<const uint32_t *>(xch);
+  char *tile = reinterpret_cast<char *>(dst) + tile_byte(blockIdx.x);
+#pragma unroll
+  for (int v = 0; v < 4; v++) st_nt<u32x4>(tile, tile_lane_byte(v), tile_lds4(xt, v));
 }
 
 __global__ __launch_bounds__(256) void ntt_inv_rows(NttArgs a) {
