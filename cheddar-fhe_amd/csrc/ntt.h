@@ -44,6 +44,10 @@ struct NttArgs {
   // optional per-polynomial base pointers (used instead of base + z*stride
   // when dst_list[0] is set): polynomials in separate allocations
   uint32_t *dst_list[4];
+  // forward only: the source limbs do not overlap the destination, so the
+  // single-pass kernel (which reads every quarter of a limb while writing
+  // its own) may run
+  int src_disjoint;
 };
 
 // Fused ModUp row pass + evaluation-key inner product (PAccum) + CAccum.

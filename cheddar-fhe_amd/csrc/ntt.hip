@@ -1,11 +1,15 @@
 // Negacyclic NTT / INTT for N = 2^16 on gfx950.
 //
-// Four-step split N = 256 rows x 256 columns (index = row*256 + col).
-// Forward Cooley-Tukey stages 0..7 pair rows (a column pass), stages 8..15
-// pair columns inside one row (a row pass). Each pass is one kernel: one HBM
-// read and one HBM write of every limb. Inside a pass a thread holds 16
-// elements in registers, runs 4 radix-2 stages on them, exchanges through
-// LDS, and runs the next 4 stages (radix-16 x radix-16).
+// Two layouts of the same transform:
+// - Two passes (any call, in place included): four-step split N = 256 rows
+//   x 256 columns (index = row*256 + col). Forward Cooley-Tukey stages 0..7
+//   pair rows (a column pass), stages 8..15 pair columns inside one row (a
+//   row pass); each pass is one kernel, one HBM read and one HBM write of
+//   every limb. Inside a pass a thread holds 16 elements in registers, runs
+//   4 radix-2 stages on them, exchanges through LDS, and runs the next 4.
+// - Single pass (forward, source apart from destination): four workgroups
+//   per limb, one per output quarter, one HBM read and one HBM write of the
+//   limb (ntt_fwd_1p below).
 //
 // Semantics follow the reference exactly (bit-exact canonical outputs):
 //   forward: y[i] = sum_j x_j psi^{(2 brev(i)+1) j}, twiddle psi_rev[m+i]
@@ -15,12 +19,15 @@
 //   inverse: Gentleman-Sande with psi_inv_rev[m+i], computes N*intt; the
 //            N^-1 and any per-limb factor live in the epilogue constant,
 //            applied as MontMul(x, c) (NTT.cu:23-229, 673-813).
-// Arithmetic is the reference's signed lazy Montgomery butterfly
-// (NTTUtils.cuh:19-60) in Montgomery-Shoup form: with w' = w q^-1 mod 2^32,
-// MontMul(b, w) = mulhi(b, w) - mulhi(b w' mod 2^32, q): three 32-bit
-// multiplies, which gfx950 issues at full VALU rate. w' is derived on the
-// fly (one multiply per twiddle; scalar when the twiddle is wave-uniform).
+// Arithmetic. Primes below 2^30 use unsigned lazy butterflies whose
+// Montgomery product is the 64-bit multiply-add form (three instructions,
+// mont_mad); primes in [2^30, 2^31) use the reference's signed lazy
+// butterfly (NTTUtils.cuh:19-60) in Montgomery-Shoup form, MontMul(b, w) =
+// mulhi(b, w) - mulhi(b w' mod 2^32, q) with w' = w q^-1. The per-twiddle
+// companion (w (-q^-1) or w q^-1) is derived on the fly: one multiply per
+// twiddle, scalar when the twiddle is wave-uniform.
 #include <algorithm>
+#include <type_traits>
 
 #include "chd_device.h"
 #include "kernel_common.h"
@@ -87,35 +94,39 @@ __device__ __forceinline__ void gs_bfly(int32_t &a, int32_t &b, int32_t w,
   b = mont(d, w, wq, q);
 }
 
-// Lazy butterflies for q < 2^30 (4q < 2^32), unsigned values:
-// CT keeps [0, 4q) (Harvey), GS keeps [0, 2q). With d = mulhi(b,w) -
-// mulhi(b w' mod 2^32, q) in (-q, q) congruent to b w 2^-32 (unsigned
-// Montgomery, b < 2^32), the CT outputs are a + q +/- d.
-__device__ __forceinline__ int32_t mont_u(uint32_t b, uint32_t w, uint32_t wq,
-                                          uint32_t q) {
-  uint32_t hi = __umulhi(b, w);
-  uint32_t u = __umulhi(b * wq, q);
-  return static_cast<int32_t>(hi - u);
-}
-
+// Lazy butterflies for q < 2^30 (4q < 2^32), unsigned values: CT keeps
+// [0, 4q) (Harvey), GS keeps [0, 2q). The Montgomery product uses the
+// 64-bit multiply-add, which gfx950 issues at nearly the full VALU rate: for
+// b < 2^32, w < q and wn = w (-q^-1) mod 2^32,
+//   d = (b w + (b wn mod 2^32) q) / 2^32  (exact; b w 2^-32 mod q, in [0, 2q))
+// is three instructions (v_mad_u64_u32, v_mul_lo_u32, v_mad_u64_u32).
 __device__ __forceinline__ uint32_t umin(uint32_t a, uint32_t b) {
   return a < b ? a : b;
 }
 
-__device__ __forceinline__ void ct_lazy(uint32_t &a, uint32_t &b, uint32_t w,
-                                        uint32_t wq, uint32_t q) {
-  uint32_t x = umin(a, a - 2 * q) + q;     // [q, 3q)
-  uint32_t d = __umulhi(b, w) - __umulhi(b * wq, q);  // (-q, q) mod 2^32
-  b = x - d;                                // (0, 4q)
-  a = x + d;                                // (0, 4q)
+__device__ __forceinline__ uint32_t mont_mad(uint32_t b, uint32_t w,
+                                             uint32_t wn, uint32_t q) {
+  const uint64_t t = static_cast<uint64_t>(b) * w;
+  const uint32_t m = b * wn;
+  return static_cast<uint32_t>((static_cast<uint64_t>(m) * q + t) >> 32);
 }
 
+// CT: a, b in [0, 4q) -> a + d, a + 2q - d with a reduced to [0, 2q)
+__device__ __forceinline__ void ct_lazy(uint32_t &a, uint32_t &b, uint32_t w,
+                                        uint32_t wn, uint32_t q) {
+  const uint32_t ar = umin(a, a - 2 * q);   // [0, 2q)
+  const uint32_t d = mont_mad(b, w, wn, q);  // [0, 2q)
+  b = ar + 2 * q - d;                        // (0, 4q)
+  a = ar + d;                                // [0, 4q)
+}
+
+// GS: a, b in [0, 2q) -> a + b (reduced), (a - b) w
 __device__ __forceinline__ void gs_lazy(uint32_t &a, uint32_t &b, uint32_t w,
-                                        uint32_t wq, uint32_t q) {
-  uint32_t s = a + b;                       // [0, 4q)
-  uint32_t t = a + 2 * q - b;               // (0, 4q)
-  a = umin(s, s - 2 * q);                   // [0, 2q)
-  b = static_cast<uint32_t>(mont_u(t, w, wq, q)) + q;  // (0, 2q)
+                                        uint32_t wn, uint32_t q) {
+  const uint32_t s = a + b;                  // [0, 4q)
+  const uint32_t t = a + 2 * q - b;          // (0, 4q)
+  a = umin(s, s - 2 * q);                    // [0, 2q)
+  b = mont_mad(t, w, wn, q);                 // [0, 2q)
 }
 
 // [0, 4q) -> [0, q)
@@ -196,19 +207,24 @@ __device__ __forceinline__ u32x4 tile_lds4(const uint32_t *xt, int v) {
 template <bool kLazy>
 struct Arith;
 
+// twq(w) is the per-twiddle companion of w that ct / gs / mul take:
+// w (-q^-1) for the lazy form, w q^-1 for the reference form.
 template <>
 struct Arith<true> {
   using T = uint32_t;
   uint32_t q;
-  __device__ void ct(T &a, T &b, uint32_t w, uint32_t wq) const {
-    ct_lazy(a, b, w, wq, q);
+  uint32_t qn;  // -q^-1 mod 2^32
+  __device__ Arith(uint32_t q_, uint32_t qinv) : q(q_), qn(0u - qinv) {}
+  __device__ uint32_t twq(uint32_t w) const { return w * qn; }
+  __device__ void ct(T &a, T &b, uint32_t w, uint32_t wn) const {
+    ct_lazy(a, b, w, wn, q);
   }
-  __device__ void gs(T &a, T &b, uint32_t w, uint32_t wq) const {
-    gs_lazy(a, b, w, wq, q);
+  __device__ void gs(T &a, T &b, uint32_t w, uint32_t wn) const {
+    gs_lazy(a, b, w, wn, q);
   }
-  // MontMul(x, c) for any representable input, result in (0, 2q)
-  __device__ T mul(T x, uint32_t c, uint32_t cq) const {
-    return static_cast<uint32_t>(mont_u(x, c, cq, q)) + q;
+  // MontMul(x, c) for any representable input, result in [0, 2q)
+  __device__ T mul(T x, uint32_t c, uint32_t cn) const {
+    return mont_mad(x, c, cn, q);
   }
   __device__ uint32_t canon_fwd(T x) const { return canon4(x, q); }
   __device__ uint32_t canon_inv(T x) const { return umin(x, x - q); }
@@ -218,6 +234,10 @@ template <>
 struct Arith<false> {
   using T = int32_t;
   int32_t q;
+  uint32_t qinv;
+  __device__ Arith(uint32_t q_, uint32_t qinv_)
+      : q(static_cast<int32_t>(q_)), qinv(qinv_) {}
+  __device__ uint32_t twq(uint32_t w) const { return w * qinv; }
   __device__ void ct(T &a, T &b, uint32_t w, uint32_t wq) const {
     ct_bfly(a, b, static_cast<int32_t>(w), static_cast<int32_t>(wq), q);
   }
@@ -256,7 +276,7 @@ __device__ __forceinline__ void fwd_cols_body(const NttArgs &a, const Limb &lb,
                                               int32_t *xch) {
   using A = Arith<kLazy>;
   using T = typename A::T;
-  const A ar{static_cast<T>(q)};
+  const A ar(q, qinv);
   const uint32_t *tw = a.tab.tw + (static_cast<size_t>(lb.ti) << kLogN);
   const int c = threadIdx.x & (kTileCols - 1);
   const int rg = threadIdx.x / kTileCols;  // 0..15
@@ -273,7 +293,7 @@ __device__ __forceinline__ void fwd_cols_body(const NttArgs &a, const Limb &lb,
   for (int k = 0; k < 16; k++) x[k] = static_cast<T>(xin[k]);
   if constexpr (kPre) {
     const uint32_t ce = a.cst[lb.ci];
-    const uint32_t ceq = ce * qinv;
+    const uint32_t ceq = ar.twq(ce);
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = ar.mul(x[k], ce, ceq);
   }
@@ -284,7 +304,7 @@ __device__ __forceinline__ void fwd_cols_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
       const uint32_t w = tw[(1 << s) + g];
-      const uint32_t wq = w * qinv;
+      const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
     }
@@ -302,7 +322,7 @@ __device__ __forceinline__ void fwd_cols_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
     for (int g = 0; g < (1 << (s - 4)); g++, i++) {
       const uint32_t w = w2[i];
-      const uint32_t wq = w * qinv;
+      const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
     }
@@ -354,7 +374,7 @@ __device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
                                               const uint32_t (&s2v)[16]) {
   using A = Arith<kLazy>;
   using T = typename A::T;
-  const A ar{static_cast<T>(q)};
+  const A ar(q, qinv);
   const uint32_t *tw = a.tab.tw + (static_cast<size_t>(lb.ti) << kLogN);
   const int c = threadIdx.x & 15;
   const int r = threadIdx.x >> 4;
@@ -379,7 +399,7 @@ __device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
     for (int g = 0; g < (1 << s); g++, i++) {
       const uint32_t w = w1[i];
-      const uint32_t wq = w * qinv;
+      const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
     }
@@ -396,7 +416,7 @@ __device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
     for (int g = 0; g < (1 << s); g++, i++) {
       const uint32_t w = w2[i];
-      const uint32_t wq = w * qinv;
+      const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
     }
@@ -504,7 +524,7 @@ __device__ __forceinline__ void inv_rows_body(const NttArgs &a, const Limb &lb,
                                               int32_t *xch) {
   using A = Arith<kLazy>;
   using T = typename A::T;
-  const A ar{static_cast<T>(q)};
+  const A ar(q, qinv);
   const uint32_t *tw = a.tab.itw + (static_cast<size_t>(lb.ti) << kLogN);
   const int c = threadIdx.x & 15;
   const int r = threadIdx.x >> 4;
@@ -529,7 +549,7 @@ __device__ __forceinline__ void inv_rows_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
       const uint32_t w = w2[(1 << s) - 1 + g];
-      const uint32_t wq = w * qinv;
+      const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
     }
@@ -546,7 +566,7 @@ __device__ __forceinline__ void inv_rows_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
       const uint32_t w = w1[(1 << s) - 1 + g];
-      const uint32_t wq = w * qinv;
+      const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
     }
@@ -614,7 +634,7 @@ __device__ __forceinline__ void inv_cols_body(const NttArgs &a, const Limb &lb,
                                               int32_t *xch) {
   using A = Arith<kLazy>;
   using T = typename A::T;
-  const A ar{static_cast<T>(q)};
+  const A ar(q, qinv);
   const uint32_t *tw = a.tab.itw + (static_cast<size_t>(lb.ti) << kLogN);
   const int c = threadIdx.x & (kTileCols - 1);
   const int rg = threadIdx.x / kTileCols;
@@ -635,7 +655,7 @@ __device__ __forceinline__ void inv_cols_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
     for (int g = 0; g < (1 << (s - 4)); g++) {
       const uint32_t w = w2[(1 << (s - 4)) - 1 + g];
-      const uint32_t wq = w * qinv;
+      const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
     }
@@ -652,13 +672,13 @@ __device__ __forceinline__ void inv_cols_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
       const uint32_t w = tw[(1 << s) + g];
-      const uint32_t wq = w * qinv;
+      const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
     }
   }
   const uint32_t ce = a.cst[lb.ci];
-  const uint32_t ceq = ce * qinv;
+  const uint32_t ceq = ar.twq(ce);
   const int32_t qs = static_cast<int32_t>(q);
 #pragma unroll
   for (int k = 0; k < 16; k++) {
@@ -704,7 +724,7 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
                                             uint32_t qinv, int32_t *xch) {
   using A = Arith<kLazy>;
   using T = typename A::T;
-  const A ar{static_cast<T>(q)};
+  const A ar(q, qinv);
   const int32_t qs = static_cast<int32_t>(q);
   const int32_t qi = static_cast<int32_t>(qinv);
   const uint32_t *tw = a.tab.tw + (static_cast<size_t>(ti) << kLogN);
@@ -796,7 +816,7 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
 #pragma unroll
         for (int gg = 0; gg < (1 << s); gg++, i++) {
           const uint32_t w = w1[i];
-          const uint32_t wq = w * qinv;
+          const uint32_t wq = ar.twq(w);
 #pragma unroll
           for (int k = gg * 2 * h; k < gg * 2 * h + h; k++)
             ar.ct(x[k], x[k + h], w, wq);
@@ -815,7 +835,7 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
 #pragma unroll
         for (int gg = 0; gg < (1 << s); gg++, i++) {
           const uint32_t w = w2[i];
-          const uint32_t wq = w * qinv;
+          const uint32_t wq = ar.twq(w);
 #pragma unroll
           for (int k = gg * 2 * h; k < gg * 2 * h + h; k++)
             ar.ct(x[k], x[k + h], w, wq);
@@ -900,6 +920,247 @@ __global__ __launch_bounds__(256) void modup_keyacc(KeyAccArgs a) {
     keyacc_body<false>(a, l, aux, ti, q, qinv, xch);
 }
 
+// ------------------------------------------------------------------------
+// Single-pass forward NTT (out of place): four workgroups per limb, each
+// producing one output quarter (index bits 15..14 = j) from one HBM read of
+// the limb and one HBM write of its quarter; the intermediate never leaves
+// the CU. Stages 0 and 1 are the only ones that mix quarters: a workgroup
+// recomputes just the one of their four outputs that lies in its quarter,
+//   z_j[n'] = x0 + s1 w1 x1 + s0 w0 x2 + s0 s1 w0 w1 x3,   x_m = x[n' + 2^14 m]
+// (w0 = psi_rev[1], w1 = psi_rev[2 + (j >> 1)], s0 = -1 for j >= 2, s1 = -1
+// for odd j), the same residue the reference's first two butterfly stages
+// give (NTT.cu:231-338). Stages 2..15 then run in four register rounds of
+// the bits 13..10 | 9..6 | 5..2 | 1..0 with three LDS exchanges; the last
+// round owns 4 consecutive outputs per lane, so every wave stores 1 KiB
+// contiguous per instruction.
+// The four workgroups of a limb get block ids 8 apart (the same XCD under
+// round-robin dispatch) so three of the four reads of the limb hit in L2.
+// ------------------------------------------------------------------------
+constexpr int kQuarter = kN / 4;
+constexpr int kQLdsWords = kQuarter + kQuarter / 16;  // 4 pad words per 64
+__device__ __forceinline__ int qidx(int n) { return n + ((n >> 6) << 2); }
+
+
+// radix-16 over the 16 registers; stage t (0..3) has 2^t groups and group g
+// uses tw[base[t] + g]; kUniform: the twiddles are wave-uniform
+template <bool kUniform, typename A>
+__device__ __forceinline__ void radix16_1p(const A &ar,
+                                           typename A::T (&x)[16],
+                                           const uint32_t *tw,
+                                           const int (&base)[4]) {
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int h = 8 >> t;
+#pragma unroll
+    for (int g = 0; g < (1 << t); g++) {
+      uint32_t w = tw[base[t] + g];
+      if (kUniform) w = __builtin_amdgcn_readfirstlane(w);
+      const uint32_t wq = ar.twq(w);
+#pragma unroll
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
+    }
+  }
+}
+
+template <int kEpi, bool kPre, bool kLazy>
+__device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
+                                            int z, int j, uint32_t q,
+                                            uint32_t qinv, uint32_t *lds) {
+  using A = Arith<kLazy>;
+  using T = typename A::T;
+  const A ar(q, qinv);
+  const uint32_t *tw = a.tab.tw + (static_cast<size_t>(lb.ti) << kLogN);
+  const uint32_t *src =
+      a.src + z * a.src_pstride + (static_cast<size_t>(lb.sl) << kLogN);
+  uint32_t *dst = poly_dst(a, z) + (static_cast<size_t>(lb.l) << kLogN) +
+                  j * kQuarter;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const uint32_t w0 = tw[1];
+  const uint32_t w1 = tw[2 + (j >> 1)];
+  T x[16];
+  // ---- round 1: stages 0, 1 of quarter j (bits 15, 14), then 2..5
+  if constexpr (kLazy) {
+    // one 64-bit dot product and one reduction per output: with canonical
+    // inputs and constants below q < 2^30 the sum stays below q 2^32
+    const uint32_t qn = ar.qn;
+    const uint32_t w01 = mont_mad(w0, w1, w1 * qn, q);
+    uint32_t c[4];
+    c[0] = tw[0];  // ToMont(1)
+    c[1] = (j & 1) ? q - w1 : w1;
+    c[2] = (j >> 1) ? q - w0 : w0;
+    const uint32_t w01c = umin(w01, w01 - q);
+    c[3] = (((j >> 1) ^ j) & 1) ? q - w01c : w01c;
+    if constexpr (kPre) {
+      // Montgomery-conversion prologue folded into the constants
+      const uint32_t ce = a.cst[lb.ci];
+      const uint32_t cen = ce * qn;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t v = mont_mad(c[i], ce, cen, q);
+        c[i] = umin(v, v - q);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const uint32_t off = 4u * static_cast<uint32_t>((k << 10) | t);
+      const uint32_t x0 = ld_nt<uint32_t>(src, off);
+      const uint32_t x1 = ld_nt<uint32_t>(src, off + 4u * kQuarter);
+      const uint32_t x2 = ld_nt<uint32_t>(src, off + 8u * kQuarter);
+      const uint32_t x3 = ld_nt<uint32_t>(src, off + 12u * kQuarter);
+      const uint64_t acc = static_cast<uint64_t>(x0) * c[0] +
+                           static_cast<uint64_t>(x1) * c[1] +
+                           static_cast<uint64_t>(x2) * c[2] +
+                           static_cast<uint64_t>(x3) * c[3];
+      const uint32_t m = static_cast<uint32_t>(acc) * qn;
+      x[k] = static_cast<uint32_t>((static_cast<uint64_t>(m) * q + acc) >> 32);
+    }
+  } else {
+    // reference-form butterflies, keeping the half of each that lies in
+    // quarter j (NTTUtils.cuh:19-34)
+    const int32_t qs = static_cast<int32_t>(q);
+    const int32_t w0s = static_cast<int32_t>(w0);
+    const int32_t w0q = static_cast<int32_t>(w0 * qinv);
+    const int32_t w1s = static_cast<int32_t>(w1);
+    const int32_t w1q = static_cast<int32_t>(w1 * qinv);
+    int32_t ce = 0, ceq = 0;
+    if constexpr (kPre) {
+      ce = static_cast<int32_t>(a.cst[lb.ci]);
+      ceq = static_cast<int32_t>(static_cast<uint32_t>(ce) * qinv);
+    }
+    const bool hi0 = j >= 2, hi1 = j & 1;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const uint32_t off = 4u * static_cast<uint32_t>((k << 10) | t);
+      int32_t xm[4];
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        xm[m] = static_cast<int32_t>(
+            ld_nt<uint32_t>(src, off + 4u * kQuarter * m));
+        if constexpr (kPre) xm[m] = mont(xm[m], ce, ceq, qs);
+      }
+      ct_bfly(xm[0], xm[2], w0s, w0q, qs);
+      ct_bfly(xm[1], xm[3], w0s, w0q, qs);
+      int32_t ya = hi0 ? xm[2] : xm[0];
+      int32_t yb = hi0 ? xm[3] : xm[1];
+      ct_bfly(ya, yb, w1s, w1q, qs);
+      x[k] = hi1 ? yb : ya;
+    }
+  }
+  {
+    const int base[4] = {4 + j, 8 + 2 * j, 16 + 4 * j, 32 + 8 * j};
+    radix16_1p<true>(ar, x, tw, base);
+  }
+  T *xs = reinterpret_cast<T *>(lds);
+#pragma unroll
+  for (int k = 0; k < 16; k++) xs[qidx((k << 10) | t)] = x[k];
+  __syncthreads();
+  // ---- round 2: stages 6..9 (bits 9..6); lane = bits 5..0, wave = 13..10
+#pragma unroll
+  for (int k = 0; k < 16; k++) x[k] = xs[qidx((wave << 10) | (k << 6) | lane)];
+  {
+    const int hi = (j << 4) | wave;  // index bits 15..10
+    const int base[4] = {64 + hi, 128 + (hi << 1), 256 + (hi << 2),
+                         512 + (hi << 3)};
+    radix16_1p<true>(ar, x, tw, base);
+  }
+#pragma unroll
+  for (int k = 0; k < 16; k++) xs[qidx((wave << 10) | (k << 6) | lane)] = x[k];
+  __syncthreads();
+  // ---- round 3: stages 10..13 (bits 5..2); lane = bits 9..6 | bits 1..0
+  const int b96 = lane >> 2, b10 = lane & 3;
+#pragma unroll
+  for (int k = 0; k < 16; k++)
+    x[k] = xs[qidx((wave << 10) | (b96 << 6) | (k << 2) | b10)];
+  {
+    const int hi = (j << 8) | (wave << 4) | b96;  // index bits 15..6
+    const int base[4] = {1024 + hi, 2048 + (hi << 1), 4096 + (hi << 2),
+                         8192 + (hi << 3)};
+    radix16_1p<false>(ar, x, tw, base);
+  }
+#pragma unroll
+  for (int k = 0; k < 16; k++)
+    xs[qidx((wave << 10) | (b96 << 6) | (k << 2) | b10)] = x[k];
+  __syncthreads();
+  // ---- round 4: stages 14, 15 (bits 1..0); lane = bits 7..2, wave =
+  // bits 13..10, store round v = bits 9..8
+  const int32_t qs = static_cast<int32_t>(q);
+  [[maybe_unused]] int32_t c2 = 0, c2q = 0, pe = 0, peq = 0;
+  [[maybe_unused]] bool has_pad = false;
+  [[maybe_unused]] const uint32_t *s2p = nullptr;
+  if constexpr (kEpi == kEpiModDown) {
+    c2 = static_cast<int32_t>(a.cst2[lb.l]);
+    c2q = static_cast<int32_t>(static_cast<uint32_t>(c2) * qinv);
+    if (lb.l >= a.src2_lo && lb.l < a.src2_hi) {
+      s2p = a.src2 + z * a.src2_pstride +
+            (static_cast<size_t>(lb.l - a.src2_lo) << kLogN) + j * kQuarter;
+      if (a.pad != nullptr) {
+        has_pad = true;
+        pe = static_cast<int32_t>(a.pad[lb.l - a.src2_lo]);
+        peq = static_cast<int32_t>(static_cast<uint32_t>(pe) * qinv);
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int n = (wave << 10) | (v << 8) | (lane << 2);
+    const uint32_t boff = 4u * static_cast<uint32_t>(n);
+    u32x4 s2 = {0, 0, 0, 0};
+    if constexpr (kEpi == kEpiModDown)
+      if (s2p != nullptr) s2 = ld_nt<u32x4>(s2p, boff);
+    const u32x4 u = *reinterpret_cast<const u32x4 *>(&lds[qidx(n)]);
+    T y[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) y[i] = static_cast<T>(u[i]);
+    const int hi = (j << 12) | (wave << 8) | (v << 6) | lane;  // bits 15..2
+    const uint32_t wa = tw[16384 + hi];
+    const uint32_t waq = ar.twq(wa);
+    ar.ct(y[0], y[2], wa, waq);
+    ar.ct(y[1], y[3], wa, waq);
+    const uint32_t wb0 = tw[32768 + 2 * hi];
+    const uint32_t wb1 = tw[32768 + 2 * hi + 1];
+    ar.ct(y[0], y[1], wb0, ar.twq(wb0));
+    ar.ct(y[2], y[3], wb1, ar.twq(wb1));
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = ar.canon_fwd(y[i]);
+    if constexpr (kEpi == kEpiModDown) {
+      // NTTPhase2ForModDown epilogue (NTT.cu:567-600):
+      // MontMul(MontMul(src2, pad) - y, inv_prod), zero src2 outside
+      // [src2_lo, src2_hi)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        int32_t sv = static_cast<int32_t>(s2[i]);
+        if (has_pad) sv = norm(mont(sv, pe, peq, qs), qs);
+        const int32_t dv = sv - static_cast<int32_t>(o[i]);
+        o[i] = static_cast<uint32_t>(norm(mont(dv, c2, c2q, qs), qs));
+      }
+    }
+    st_nt<u32x4>(dst, boff, o);
+  }
+}
+
+// grid: 1D, 4 * roundup(limbs * polys, 8) blocks of 1024 threads
+template <int kEpi, bool kPre>
+__global__ __launch_bounds__(1024) void ntt_fwd_1p(NttArgs a, int num_limbs,
+                                                   int num_items) {
+  __shared__ __align__(16) uint32_t lds[kQLdsWords];
+  const int b = blockIdx.x;
+  const int slot = b >> 3;
+  const int j = slot & 3;
+  const int li = (slot >> 2) * 8 + (b & 7);
+  if (li >= num_items) return;
+  const int z = li / num_limbs;
+  const Limb lb = decode(a.map, li - z * num_limbs);
+  const uint32_t q = a.tab.q[lb.ti];
+  const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
+  if (q < (1u << 30))
+    fwd_1p_body<kEpi, kPre, true>(a, lb, z, j, q, qinv, lds);
+  else
+    fwd_1p_body<kEpi, kPre, false>(a, lb, z, j, q, qinv, lds);
+}
+
 }  // namespace
 
 hipError_t launch_ntt_fwd_cols(const NttArgs &a, int num_limbs, int num_z,
@@ -927,6 +1188,20 @@ hipError_t launch_modup_keyacc(const KeyAccArgs &a, hipStream_t s) {
 hipError_t launch_ntt_fwd(const NttArgs &a, int num_limbs, int num_polys,
                           bool pre_const, int epilogue, hipStream_t s) {
   if (num_limbs <= 0 || num_polys <= 0) return hipSuccess;
+  if (a.src_disjoint) {
+    const int items = num_limbs * num_polys;
+    dim3 g1(4 * ((items + 7) / 8 * 8));
+    if (epilogue == kEpiModDown)
+      hipLaunchKernelGGL((ntt_fwd_1p<kEpiModDown, false>), g1, dim3(1024), 0,
+                         s, a, num_limbs, items);
+    else if (pre_const)
+      hipLaunchKernelGGL((ntt_fwd_1p<kEpiStore, true>), g1, dim3(1024), 0, s,
+                         a, num_limbs, items);
+    else
+      hipLaunchKernelGGL((ntt_fwd_1p<kEpiStore, false>), g1, dim3(1024), 0, s,
+                         a, num_limbs, items);
+    return hipGetLastError();
+  }
   dim3 gc(kCols / kTileCols, num_limbs, num_polys);
   dim3 gr(kRows / kTileRows, num_limbs, num_polys);
   if (pre_const)
@@ -964,6 +1239,26 @@ hipError_t launch_ntt_inv(const NttArgs &a, int num_limbs, int num_polys,
 
 using namespace chd;
 
+namespace {
+// word span [lo, hi) that num_polys polynomials of num_limbs limbs starting
+// at base cover under limb map m (gaps and skips included)
+void limb_span(const uint32_t *base, long long pstride, int num_limbs,
+               int num_polys, const chd_limb_map &m, bool src_side,
+               uintptr_t *lo, uintptr_t *hi) {
+  const long long top_logical =
+      num_limbs - 1 + (m.skip_lo < num_limbs ? m.skip_len : 0);
+  const long long gap = src_side ? std::max(m.src_gap, 0) : 0;
+  const long long limbs = top_logical + 1 + gap;
+  const long long ps = std::max(pstride, 0LL);
+  *lo = reinterpret_cast<uintptr_t>(base);
+  *hi = *lo + 4ull * static_cast<unsigned long long>(
+                        (num_polys - 1) * ps + limbs * static_cast<long long>(kN));
+}
+bool disjoint(uintptr_t alo, uintptr_t ahi, uintptr_t blo, uintptr_t bhi) {
+  return ahi <= blo || bhi <= alo;
+}
+}  // namespace
+
 extern "C" int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m,
                              uint32_t *dst, long long dst_pstride,
                              const uint32_t *src, long long src_pstride,
@@ -979,6 +1274,10 @@ extern "C" int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m,
   a.map = *m;
   a.tab = *t;
   a.cst = pre_cst;
+  uintptr_t slo, shi, dlo, dhi;
+  limb_span(src, src_pstride, num_limbs, num_polys, *m, true, &slo, &shi);
+  limb_span(dst, dst_pstride, num_limbs, num_polys, *m, false, &dlo, &dhi);
+  a.src_disjoint = disjoint(slo, shi, dlo, dhi) ? 1 : 0;
   hipError_t e = launch_ntt_fwd(a, num_limbs, num_polys, pre_cst != nullptr,
                                 kEpiStore, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
@@ -1123,8 +1422,8 @@ extern "C" int chd_k_modup_keyacc(const chd_tables *t,
 
 extern "C" int chd_k_ntt_fwd_moddown_multi(
     const chd_tables *t, const chd_limb_map *m, uint32_t *const *dst,
-    int num_polys, int num_limbs, const uint32_t *src2,
-    long long src2_pstride, int src2_lo, int src2_hi,
+    int num_polys, int num_limbs, const uint32_t *src, long long src_pstride,
+    const uint32_t *src2, long long src2_pstride, int src2_lo, int src2_hi,
     const uint32_t *inv_prod, const uint32_t *pad, void *stream) {
   if (!t || !m || !dst || !inv_prod || num_limbs < 0 || num_polys < 1 ||
       num_polys > 4 || (src2 == nullptr && src2_hi > src2_lo))
@@ -1141,6 +1440,24 @@ extern "C" int chd_k_ntt_fwd_moddown_multi(
   a.dst = dst[0];
   a.map = *m;
   a.map.src_gap = 0;
+  if (src != nullptr) {
+    // separate source: single-pass kernel when no destination overlaps it
+    uintptr_t slo, shi;
+    limb_span(src, src_pstride, num_limbs, num_polys, a.map, true, &slo, &shi);
+    bool ok = true;
+    for (int p = 0; p < num_polys; p++) {
+      uintptr_t dlo, dhi;
+      limb_span(dst[p], 0, num_limbs, 1, a.map, false, &dlo, &dhi);
+      ok = ok && disjoint(slo, shi, dlo, dhi);
+    }
+    if (!ok)
+      return set_error(CHD_ERR_ARG,
+                       "chd_k_ntt_fwd_moddown_multi: source overlaps a "
+                       "destination");
+    a.src = src;
+    a.src_pstride = src_pstride;
+    a.src_disjoint = 1;
+  }
   a.tab = *t;
   a.src2 = src2;
   a.src2_pstride = src2_pstride;

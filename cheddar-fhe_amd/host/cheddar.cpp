@@ -1044,6 +1044,11 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
     jobs[p].skip_lo = INT_MAX;
     jobs[p].skip_len = 0;
   }
+  // BConv into a temporary so that the NTT below reads it and writes dst in
+  // one pass (the single-pass forward NTT cannot run in place)
+  Scratch conv(ws_, static_cast<size_t>(num_polys) * dst_len * n);
+  for (int p = 0; p < num_polys; p++)
+    jobs[p].dst = conv.data() + static_cast<size_t>(p) * dst_len * n;
   K(chd_k_bconv_batch(&ntt_.Tables(), &m, jobs, num_polys, CurrentStream()));
   const DeviceVector<word> &ipp =
       kind == Kind::ModDown   ? inv_prime_prod_
@@ -1062,7 +1067,9 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
   const int s2_lo = np_dst.num_ter_ - np_non_intt.num_ter_;
   const int s2_hi = s2_lo + np_non_intt.GetNumQ();
   K(chd_k_ntt_fwd_moddown_multi(&ntt_.Tables(), &m, dst.data(), num_polys,
-                                dst_len, src + static_cast<size_t>(src2_off) * n,
+                                dst_len, conv.data(),
+                                static_cast<long long>(dst_len) * n,
+                                src + static_cast<size_t>(src2_off) * n,
                                 src_pstride, s2_lo, s2_hi, ipp.data(), pad,
                                 CurrentStream()));
 }
@@ -1083,18 +1090,20 @@ Context<uint32_t>::Context(const Parameter<word> &param)
   {
     // arena for the largest call at the top level: HMult holds the tensor
     // (3 Lq), the accumulator (2 T) and ModUp's groups plus its INTT
-    // (beta T + Lq); ModDown's INTT (at most 2 (alpha + 2) limbs) and HRot's
-    // permute input (2 Lq) fit in what the ModUp part leaves
+    // (beta T + Lq); ModDown's INTT (at most 2 (alpha + 2) limbs) and BConv
+    // output (2 Lq) and HRot's permute input (2 Lq) fit in what the ModUp
+    // part leaves
     const NPInfo top = param_.LevelToNP(param_.max_level_);
     const size_t lq = top.GetNumQ();
     const size_t t = lq + param_.alpha_;
     const size_t beta = DivCeil(top.num_main_ + param_.GetMaxNumTer(),
                                 param_.alpha_);
-    const size_t hmult = 3 * lq + 2 * t +
-                         std::max(beta * t + lq, 2 * (param_.alpha_ + 2) + 2 * lq);
+    const size_t moddown = 2 * (param_.alpha_ + 2) + 2 * lq;
+    const size_t hmult =
+        3 * lq + 2 * t + std::max(beta * t + lq, moddown + 2 * lq);
     // the hoisted giant step holds three extended pairs and a ModDown
     // output while a key switch runs (Hoist.cu:939-957)
-    const size_t hoist = 6 * t + lq + beta * t + lq + 2 * (param_.alpha_ + 2);
+    const size_t hoist = 6 * t + lq + beta * t + lq + moddown;
     const size_t limbs = std::max(hmult, hoist);
     ws_.reset(new Workspace(limbs * param_.degree_));
   }

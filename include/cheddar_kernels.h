@@ -58,11 +58,14 @@ int chd_k_ntt_fwd_moddown(const chd_tables *t, const chd_limb_map *m,
                           int src2_lo, int src2_hi, const uint32_t *inv_prod,
                           const uint32_t *pad, void *stream);
 
-/* Same for num_polys (<= 4) polynomials in separate buffers dst[p] (in
- * place); src2 of polynomial p is at src2 + p * src2_pstride. */
+/* Same for num_polys (<= 4) polynomials in separate buffers dst[p];
+ * src2 of polynomial p is at src2 + p * src2_pstride. With src == NULL the
+ * NTT runs in place on dst[p]; otherwise its input is src + p * src_pstride,
+ * which must not overlap any dst[p] (one HBM pass instead of two). */
 int chd_k_ntt_fwd_moddown_multi(const chd_tables *t, const chd_limb_map *m,
                                 uint32_t *const *dst, int num_polys,
-                                int num_limbs, const uint32_t *src2,
+                                int num_limbs, const uint32_t *src,
+                                long long src_pstride, const uint32_t *src2,
                                 long long src2_pstride, int src2_lo,
                                 int src2_hi, const uint32_t *inv_prod,
                                 const uint32_t *pad, void *stream);

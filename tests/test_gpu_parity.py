@@ -54,11 +54,14 @@ def test_ntt_config2_batch(chd):
     assert np.array_equal(host(z), want_inv)
     plan.inverse(z, y, 32, 2, mont_conv=False)
     assert np.array_equal(host(z), x)
-    # in place, Montgomery conversion on input
-    y2 = dev(x)
-    plan.forward(y2, y2, 32, 2, mont_conv=True)
+    # Montgomery conversion on input: out of place (single-pass kernel,
+    # constant folded into its first stages) and in place (two passes)
     want_m = np.stack([_orc.ntt_batch(x[p].reshape(-1), 16, primes, 1)
                        .reshape(32, N) for p in range(2)])
+    plan.forward(y, src, 32, 2, mont_conv=True)
+    assert np.array_equal(host(y), want_m)
+    y2 = dev(x)
+    plan.forward(y2, y2, 32, 2, mont_conv=True)
     assert np.array_equal(host(y2), want_m)
 
 
@@ -78,9 +81,12 @@ def test_ntt_edge_inputs(chd, kind):
                       .astype(np.uint32) for p in primes])
     plan = chd.NttPlan(primes)
     y = zeros(4, N)
-    plan.forward(y, dev(x), 4, 1)
-    assert np.array_equal(host(y), _orc.ntt_batch(x.reshape(-1), 16,
-                                                  primes).reshape(4, N))
+    want = _orc.ntt_batch(x.reshape(-1), 16, primes).reshape(4, N)
+    plan.forward(y, dev(x), 4, 1)   # single pass (source apart)
+    assert np.array_equal(host(y), want)
+    yi = dev(x)
+    plan.forward(yi, yi, 4, 1)      # in place: two passes
+    assert np.array_equal(host(yi), want)
     z = zeros(4, N)
     plan.inverse(z, y, 4, 1, mont_conv=False)
     assert np.array_equal(host(z), x)
