@@ -319,7 +319,8 @@ def main():
             "limb_transforms_per_step": 128,
         },
         "roofline": {
-            "kernel": "forward NTT (ntt_fwd_cols + ntt_fwd_rows, 2 launches)",
+            "kernel": "forward NTT (ntt_fwd_1p: single pass, one launch, "
+                      "four workgroups per limb)",
             "bound": "hbm",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
