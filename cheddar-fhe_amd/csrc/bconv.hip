@@ -56,7 +56,7 @@ constexpr int kCoefPerBlock = (kThreads / 64) * kTilesPerWave * 16;
 constexpr int kPlaneBytes = 64 * 16;   // one digit plane of a 16-dst tile
 
 struct BconvBatch {
-  chd_bconv_job job[CHD_MAX_JOBS];
+  chd_bconv_job job[CHD_MAX_BCONV_JOBS];
 };
 
 // four signed byte digits of a centred value |c| < 2^30, packed as int8 x4
@@ -225,7 +225,7 @@ extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
 extern "C" int chd_k_bconv_batch(const chd_tables *t, const chd_limb_map *m,
                                  const chd_bconv_job *jobs, int num_jobs,
                                  void *stream) {
-  if (!t || !m || !jobs || num_jobs < 1 || num_jobs > CHD_MAX_JOBS)
+  if (!t || !m || !jobs || num_jobs < 1 || num_jobs > CHD_MAX_BCONV_JOBS)
     return set_error(CHD_ERR_ARG, "chd_k_bconv_batch: invalid argument");
   BconvBatch b{};
   for (int j = 0; j < num_jobs; j++) {

@@ -41,21 +41,26 @@ struct NttArgs {
   int group_alpha;
   int group_shift;
   int group_limbs;
+  // with several inputs in group mode, grid.z runs over (input, group) and
+  // the group is blockIdx.z % group_period (0: blockIdx.z)
+  int group_period;
   // optional per-polynomial base pointers (used instead of base + z*stride
   // when dst_list[0] is set): polynomials in separate allocations
-  uint32_t *dst_list[4];
+  uint32_t *dst_list[CHD_MAX_JOBS];
   // forward only: the source limbs do not overlap the destination, so the
   // single-pass kernel (which reads every quarter of a limb while writing
   // its own) may run
   int src_disjoint;
 };
 
-// Fused ModUp row pass + evaluation-key inner product (PAccum) + CAccum.
-constexpr int kMaxGroups = CHD_MAX_JOBS;
-struct KeyAccArgs : chd_keyacc_args {
+// Fused ModUp row pass + evaluation-key inner product (PAccum) + CAccum for
+// up to CHD_MAX_JOBS independent key switches of one level (grid.z = job).
+struct KeyAccBatch {
   chd_tables tab;
+  chd_keyacc_args job[CHD_MAX_JOBS];
 };
-hipError_t launch_modup_keyacc(const KeyAccArgs &a, hipStream_t s);
+hipError_t launch_modup_keyacc(const KeyAccBatch &a, int num_jobs,
+                               hipStream_t s);
 
 // Forward NTT over grid (limbs, polys); pre_const multiplies the input by
 // MontMul(x, cst[limb]) first (Montgomery conversion).

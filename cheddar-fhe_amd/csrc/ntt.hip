@@ -337,7 +337,8 @@ __global__ __launch_bounds__(512) void ntt_fwd_cols(NttArgs a) {
   __shared__ int32_t xch[kRows * kTileCols];
   LimbMap m = a.map;
   if (a.group_alpha > 0) {
-    const int g = blockIdx.z;
+    const int g = a.group_period > 0 ? static_cast<int>(blockIdx.z) % a.group_period
+                                     : static_cast<int>(blockIdx.z);
     m.skip_lo = group_lo(g, a.group_alpha, a.group_shift);
     m.skip_len =
         group_hi(g, a.group_alpha, a.group_shift, m.num_q) - m.skip_lo;
@@ -460,7 +461,8 @@ __global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
   __shared__ int32_t xch[kTileRows * kRowPad];
   LimbMap m = a.map;
   if (a.group_alpha > 0) {
-    const int g = blockIdx.z;
+    const int g = a.group_period > 0 ? static_cast<int>(blockIdx.z) % a.group_period
+                                     : static_cast<int>(blockIdx.z);
     m.skip_lo = group_lo(g, a.group_alpha, a.group_shift);
     m.skip_len =
         group_hi(g, a.group_alpha, a.group_shift, m.num_q) - m.skip_lo;
@@ -729,7 +731,8 @@ __global__ __launch_bounds__(512) void ntt_inv_cols(NttArgs a) {
 // The ModUp output never goes back to HBM. grid (kRows/kTileRows, L+alpha).
 // ------------------------------------------------------------------------
 template <bool kLazy>
-__device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
+__device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
+                                            const chd_tables &tab, int l,
                                             bool aux, int ti, uint32_t q,
                                             uint32_t qinv, int32_t *xch) {
   using A = Arith<kLazy>;
@@ -737,7 +740,7 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
   const A ar(q, qinv);
   const int32_t qs = static_cast<int32_t>(q);
   const int32_t qi = static_cast<int32_t>(qinv);
-  const uint32_t *tw = a.tab.tw + (static_cast<size_t>(ti) << kLogN);
+  const uint32_t *tw = tab.tw + (static_cast<size_t>(ti) << kLogN);
   const int c = threadIdx.x & 15;
   const int r = threadIdx.x >> 4;
   const int row = blockIdx.x * kTileRows + r;
@@ -917,17 +920,19 @@ __device__ __forceinline__ void keyacc_body(const KeyAccArgs &a, int l,
   }
 }
 
-__global__ __launch_bounds__(256) void modup_keyacc(KeyAccArgs a) {
+// grid (kRows / kTileRows, num_q + alpha, jobs)
+__global__ __launch_bounds__(256) void modup_keyacc(KeyAccBatch b) {
   __shared__ int32_t xch[kTileRows * kRowPad];
+  const chd_keyacc_args &a = b.job[blockIdx.z];
   const int l = blockIdx.y;
   const bool aux = l >= a.num_q;
   const int ti = a.tab_off + l + (aux ? a.tab_gap : 0);
-  const uint32_t q = a.tab.q[ti];
-  const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[ti]);
+  const uint32_t q = b.tab.q[ti];
+  const uint32_t qinv = static_cast<uint32_t>(b.tab.qinv[ti]);
   if (q < (1u << 30))
-    keyacc_body<true>(a, l, aux, ti, q, qinv, xch);
+    keyacc_body<true>(a, b.tab, l, aux, ti, q, qinv, xch);
   else
-    keyacc_body<false>(a, l, aux, ti, q, qinv, xch);
+    keyacc_body<false>(a, b.tab, l, aux, ti, q, qinv, xch);
 }
 
 // ------------------------------------------------------------------------
@@ -1189,8 +1194,9 @@ hipError_t launch_ntt_fwd_rows(const NttArgs &a, int num_limbs, int num_z,
   return hipGetLastError();
 }
 
-hipError_t launch_modup_keyacc(const KeyAccArgs &a, hipStream_t s) {
-  dim3 g(kRows / kTileRows, a.num_q + a.alpha);
+hipError_t launch_modup_keyacc(const KeyAccBatch &a, int num_jobs,
+                               hipStream_t s) {
+  dim3 g(kRows / kTileRows, a.job[0].num_q + a.job[0].alpha, num_jobs);
   hipLaunchKernelGGL(modup_keyacc, g, dim3(256), 0, s, a);
   return hipGetLastError();
 }
@@ -1379,10 +1385,21 @@ extern "C" int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
                                     int num_groups, int alpha, int group_shift,
                                     int group_limbs, int with_rows,
                                     void *stream) {
-  if (!t || !m || !modup || group_limbs < m->num_q ||
+  return chd_k_ntt_fwd_groups_batch(t, m, modup, group_stride, num_groups, 1,
+                                    alpha, group_shift, group_limbs,
+                                    with_rows, stream);
+}
+
+extern "C" int chd_k_ntt_fwd_groups_batch(
+    const chd_tables *t, const chd_limb_map *m, uint32_t *modup,
+    long long group_stride, int num_groups, int num_inputs, int alpha,
+    int group_shift, int group_limbs, int with_rows, void *stream) {
+  if (!t || !m || !modup || group_limbs < m->num_q || num_inputs < 1 ||
+      num_inputs > CHD_MAX_JOBS ||
       !groups_valid(num_groups, alpha, group_shift, m->num_q))
     return set_error(CHD_ERR_ARG, "chd_k_ntt_fwd_groups: invalid argument");
   NttArgs a{};
+  a.group_period = num_groups;
   a.src = modup;
   a.dst = modup;
   a.src_pstride = group_stride;
@@ -1399,31 +1416,53 @@ extern "C" int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
     min_skip = std::min(min_skip, group_hi(g, alpha, group_shift, m->num_q) -
                                       group_lo(g, alpha, group_shift));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = launch_ntt_fwd_cols(a, group_limbs - min_skip, num_groups, s);
+  const int nz = num_groups * num_inputs;
+  hipError_t e = launch_ntt_fwd_cols(a, group_limbs - min_skip, nz, s);
   if (e == hipSuccess && with_rows)
-    e = launch_ntt_fwd_rows(a, group_limbs - min_skip, num_groups, s);
+    e = launch_ntt_fwd_rows(a, group_limbs - min_skip, nz, s);
   if (e != hipSuccess)
     return set_error(CHD_ERR_HIP, std::string("chd_k_ntt_fwd_groups: ") +
                                       hipGetErrorString(e));
   return 0;
 }
 
+namespace {
+const char *keyacc_job_error(const chd_keyacc_args *a) {
+  const bool tensor = a->a1 != nullptr;
+  if (!a->modup || !a->p_prod || !a->acc_b || !a->acc_a || a->alpha < 1 ||
+      (tensor ? !a->b1 || !a->b2 || !a->a2 : !a->d) ||
+      a->beta > CHD_MAX_JOBS ||
+      !groups_valid(a->beta, a->alpha, a->group_shift, a->num_q))
+    return "invalid argument";
+  for (int g = 0; g < a->beta; g++)
+    if (!a->kb[g] || !a->ka[g]) return "null key pointer";
+  return nullptr;
+}
+}  // namespace
+
 extern "C" int chd_k_modup_keyacc(const chd_tables *t,
                                   const chd_keyacc_args *args, void *stream) {
-  const bool tensor = args && args->a1 != nullptr;
-  if (!t || !args || !args->modup || !args->p_prod || !args->acc_b ||
-      !args->acc_a || args->alpha < 1 ||
-      (tensor ? !args->b1 || !args->b2 || !args->a2 : !args->d) ||
-      args->beta > kMaxGroups ||
-      !groups_valid(args->beta, args->alpha, args->group_shift, args->num_q))
+  return chd_k_modup_keyacc_batch(t, args, 1, stream);
+}
+
+extern "C" int chd_k_modup_keyacc_batch(const chd_tables *t,
+                                        const chd_keyacc_args *jobs,
+                                        int num_jobs, void *stream) {
+  if (!t || !jobs || num_jobs < 1 || num_jobs > CHD_MAX_JOBS)
     return set_error(CHD_ERR_ARG, "chd_k_modup_keyacc: invalid argument");
-  for (int g = 0; g < args->beta; g++)
-    if (!args->kb[g] || !args->ka[g])
-      return set_error(CHD_ERR_ARG, "chd_k_modup_keyacc: null key pointer");
-  KeyAccArgs a;
-  static_cast<chd_keyacc_args &>(a) = *args;
-  a.tab = *t;
-  hipError_t e = launch_modup_keyacc(a, static_cast<hipStream_t>(stream));
+  KeyAccBatch b{};
+  b.tab = *t;
+  for (int j = 0; j < num_jobs; j++) {
+    if (const char *err = keyacc_job_error(&jobs[j]))
+      return set_error(CHD_ERR_ARG, std::string("chd_k_modup_keyacc: ") + err);
+    // one grid covers every job: the limb ranges must agree
+    if (jobs[j].num_q != jobs[0].num_q || jobs[j].alpha != jobs[0].alpha)
+      return set_error(CHD_ERR_ARG,
+                       "chd_k_modup_keyacc: jobs of different levels");
+    b.job[j] = jobs[j];
+  }
+  hipError_t e =
+      launch_modup_keyacc(b, num_jobs, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
     return set_error(CHD_ERR_HIP, std::string("chd_k_modup_keyacc: ") +
                                       hipGetErrorString(e));
@@ -1436,7 +1475,7 @@ extern "C" int chd_k_ntt_fwd_moddown_multi(
     const uint32_t *src2, long long src2_pstride, int src2_lo, int src2_hi,
     const uint32_t *inv_prod, const uint32_t *pad, void *stream) {
   if (!t || !m || !dst || !inv_prod || num_limbs < 0 || num_polys < 1 ||
-      num_polys > 4 || (src2 == nullptr && src2_hi > src2_lo))
+      num_polys > CHD_MAX_JOBS || (src2 == nullptr && src2_hi > src2_lo))
     return set_error(CHD_ERR_ARG,
                      "chd_k_ntt_fwd_moddown_multi: invalid argument");
   NttArgs a{};

@@ -867,6 +867,50 @@ void ModSwitchHandler<uint32_t>::ModUpGroups(word *modup,
                          with_rows ? 1 : 0, CurrentStream()));
 }
 
+void ModSwitchHandler<uint32_t>::ModUpGroupsBatch(word *modup,
+                                                  long long group_stride,
+                                                  const word *src,
+                                                  long long src_stride,
+                                                  int num_inputs,
+                                                  word *intt) const {
+  const NPInfo np = param_.LevelToNP(level_, 0);
+  const int num_q = np.GetNumQ();
+  const int n = param_.degree_;
+  const int groups = NumGroups();
+  AssertTrue(num_inputs >= 1 && num_inputs <= CHD_MAX_JOBS,
+             "ModUp: 1 to CHD_MAX_JOBS inputs per batch");
+  AssertTrue(groups * num_inputs <= CHD_MAX_BCONV_JOBS,
+             "ModUp: too many groups in one batch");
+  // INTTAndMultConst(centre) of every input (ModSwitch.cu:442-447)
+  const chd_limb_map mi = NoSkipMap(param_, np);
+  const long long ilen = static_cast<long long>(num_q) * n;
+  K(chd_k_ntt_inv(&ntt_.Tables(), &mi, intt, ilen, src, src_stride, num_q,
+                  num_inputs, mod_up1_.data(), 1, CurrentStream()));
+  NPInfo np_aux = np;
+  np_aux.num_aux_ = num_aux_;
+  chd_limb_map m = NoSkipMap(param_, np_aux);
+  chd_bconv_job jobs[CHD_MAX_BCONV_JOBS] = {};
+  for (int i = 0; i < num_inputs; i++)
+    for (int z = 0; z < groups; z++) {
+      const int s0 = GroupLo(z), s1 = GroupHi(z);
+      const SwitchTable &st = mod_up_[z];
+      chd_bconv_job &jb = jobs[i * groups + z];
+      jb.dst = modup + (static_cast<long long>(i) * groups + z) * group_stride;
+      jb.src = reinterpret_cast<const int32_t *>(intt) + i * ilen +
+               static_cast<size_t>(s0) * n;
+      jb.table = st.table.as<void>();
+      jb.src_len = st.src_len;
+      jb.dst_len = st.dst_len;
+      jb.skip_lo = s0;
+      jb.skip_len = s1 - s0;
+    }
+  K(chd_k_bconv_batch(&ntt_.Tables(), &m, jobs, groups * num_inputs,
+                      CurrentStream()));
+  K(chd_k_ntt_fwd_groups_batch(&ntt_.Tables(), &m, modup, group_stride,
+                               groups, num_inputs, num_aux_, group_shift_,
+                               num_q + num_aux_, 0, CurrentStream()));
+}
+
 // src/core/ModSwitch.cu:429-509
 void ModSwitchHandler<uint32_t>::ModUp(std::vector<DvView<word>> &dst,
                                        const DvConstView<word> &src) const {
@@ -983,8 +1027,8 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
                                               Kind kind) const {
   const int n = param_.degree_;
   const int num_polys = static_cast<int>(dst.size());
-  AssertTrue(num_polys >= 1 && num_polys <= 4,
-             "ModDown: 1 to 4 polynomials per call");
+  AssertTrue(num_polys >= 1 && num_polys <= CHD_MAX_JOBS,
+             "ModDown: 1 to CHD_MAX_JOBS polynomials per call");
   AssertTrue(kind == Kind::ModDown || level_ > 0,
              "Not enough q primes to rescale");
   const int num_src_aux = kind == Kind::Rescale ? 0 : num_aux_;
@@ -1239,6 +1283,67 @@ void Context<uint32_t>::KeyAccumulate(int level, word *acc_b, word *acc_a,
     k.a2 = tb->ax;
   }
   K(chd_k_modup_keyacc(&ntt_handler_.Tables(), &k, CurrentStream()));
+}
+
+void Context<uint32_t>::KeyMultExtBatchV(int level, int num,
+                                         word *const *acc_b,
+                                         word *const *acc_a, const word *d,
+                                         long long d_stride,
+                                         const word *add_b,
+                                         long long add_stride,
+                                         const EvkRef *const *keys) const {
+  const NPInfo a_np = param_.LevelToNP(level);
+  const int n = param_.degree_;
+  const int num_q = a_np.GetNumQ();
+  const int num_aux = param_.alpha_;
+  AssertTrue(num >= 1 && num <= CHD_MAX_JOBS,
+             "KeyMultExtBatch: 1 to CHD_MAX_JOBS inputs per batch");
+  const int prime_offset = param_.GetMaxNumTer() - a_np.num_ter_;
+  const int beta = DivCeil(num_q + prime_offset, num_aux);
+  const auto &ms = mod_switch_handlers_.at(level);
+  AssertTrue(ms.GetBeta() == beta, "MultKeyNoModDown: beta mismatch");
+  const int groups = ms.NumGroups();
+  const int first = ms.FirstGroup();
+  AssertTrue(groups <= CHD_MAX_JOBS, "MultKeyNoModDown: dnum too large");
+  const int total = num_q + num_aux;
+  const long long gs = static_cast<long long>(total) * n;
+  Workspace::Use use_ws(ws_.get());
+  Scratch buf(ws_.get(), static_cast<size_t>(num) * groups * gs +
+                             static_cast<size_t>(num) * num_q * n);
+  ms.ModUpGroupsBatch(buf.data(), gs, d, d_stride, num,
+                      buf.data() + static_cast<size_t>(num) * groups * gs);
+  chd_keyacc_args jobs[CHD_MAX_JOBS] = {};
+  for (int i = 0; i < num; i++) {
+    const EvkRef &key = *keys[i];
+    AssertTrue(key.np.num_aux_ == num_aux,
+               "Invalid setting for MultKeyNoModDown");
+    AssertTrue(static_cast<int>(key.bx.size()) >= beta &&
+                   key.bx.size() == key.ax.size(),
+               "Beta mismatch");
+    chd_keyacc_args &k = jobs[i];
+    k.num_q = num_q;
+    k.tab_off = param_.TerLeft(a_np);
+    k.tab_gap = param_.MainLeft(a_np);
+    k.alpha = num_aux;
+    k.beta = groups;
+    k.group_shift = ms.GroupShift();
+    k.modup = buf.data() + static_cast<size_t>(i) * groups * gs;
+    k.group_stride = gs;
+    k.d = d + i * d_stride;
+    for (int z = 0; z < groups; z++) {
+      k.kb[z] = key.bx[first + z] + static_cast<size_t>(prime_offset) * n;
+      k.ka[z] = key.ax[first + z] + static_cast<size_t>(prime_offset) * n;
+    }
+    k.key_gap =
+        static_cast<long long>(key.np.GetNumQ() - prime_offset - num_q) * n;
+    AssertTrue(k.key_gap >= 0, "MultKeyNoModDown: key level below input level");
+    k.p_prod = GetPProd(a_np).data();
+    k.acc_b = acc_b[i];
+    k.acc_a = acc_a[i];
+    k.add_b = add_b + i * add_stride;
+  }
+  K(chd_k_modup_keyacc_batch(&ntt_handler_.Tables(), jobs, num,
+                             CurrentStream()));
 }
 
 // src/core/Context.cpp:862-871 with 714-737 / 559-607
@@ -1961,26 +2066,49 @@ void HoistHandler<uint32_t>::GiantStep(const Context<word> &ctx, Ct &res,
   // 2. giant-step rotations (EvaluateGiantStepOptimized, Hoist.cu:895-957):
   //    fin = acc_0 + sum_{g != 0} Permute(KS(ModUp(ModDown(acc_g.a))) with
   //    acc_g.b added, g)
-  // giant step 0 (the first, indices ascend) accumulates in place
+  // giant step 0 (the first, indices ascend) accumulates in place. The
+  // other giant steps are independent until their permuted sum, so they
+  // run in batches of up to CHD_MAX_JOBS: one ModDown, one ModUp, one key
+  // accumulation and one permute-accumulate launch sequence per batch
+  // (modular sums, so the batching leaves every residue as it was).
   const bool has0 = gs_indices_.front() == 0;
-  Scratch fin_buf(ws, has0 ? 0 : 2 * tw), tmp(ws, 2 * tw),
-      down(ws, static_cast<size_t>(num_q) * n);
+  const int first_gi = has0 ? 1 : 0;
+  const int batch = std::max(1, std::min(CHD_MAX_JOBS, num_gs - first_gi));
+  Scratch fin_buf(ws, has0 ? 0 : 2 * tw),
+      tmp(ws, static_cast<size_t>(batch) * 2 * tw),
+      down(ws, static_cast<size_t>(batch) * num_q * n);
   word *const finp = has0 ? acc_b(0) : fin_buf.data();
   bool first = !has0;
-  for (int gi = has0 ? 1 : 0; gi < num_gs; gi++) {
-    const int g = gs_indices_[gi];
-    ms.ModDownMulti({down.data()}, acc_b(gi) + tw, 0,
+  const long long dlen = static_cast<long long>(num_q) * n;
+  for (int g0 = first_gi; g0 < num_gs; g0 += batch) {
+    const int cnt = std::min(batch, num_gs - g0);
+    // ModDown of every accumulator's a (acc_a of giant step gi sits at
+    // acc_b(gi) + tw, 2 tw words apart)
+    std::vector<word *> dd(cnt);
+    for (int i = 0; i < cnt; i++) dd[i] = down.data() + i * dlen;
+    ms.ModDownMulti(dd, acc_b(g0) + tw, static_cast<long long>(2 * tw),
                     ModSwitchHandler<word>::Kind::ModDown);
-    ctx.KeyMultExtV(pt_level_, tmp.data(), tmp.data() + tw, down.data(),
-                    acc_b(gi), key_of(g));
-    chd_perm_src s = {};
-    s.src[0] = tmp.data();
-    s.src[1] = tmp.data() + tw;
-    s.galois = ctx.elem_handler_.PermuteAmountToGaloisFactor(g);
+    std::vector<Context<word>::EvkRef> keys;
+    keys.reserve(cnt);
+    const Context<word>::EvkRef *kp[CHD_MAX_JOBS];
+    word *tb[CHD_MAX_JOBS], *ta[CHD_MAX_JOBS];
+    chd_perm_src ps[CHD_MAX_JOBS] = {};
+    for (int i = 0; i < cnt; i++) {
+      const int g = gs_indices_[g0 + i];
+      keys.push_back(key_of(g));
+      tb[i] = tmp.data() + static_cast<size_t>(i) * 2 * tw;
+      ta[i] = tb[i] + tw;
+      ps[i].src[0] = tb[i];
+      ps[i].src[1] = ta[i];
+      ps[i].galois = ctx.elem_handler_.PermuteAmountToGaloisFactor(g);
+    }
+    for (int i = 0; i < cnt; i++) kp[i] = &keys[i];
+    ctx.KeyMultExtBatchV(pt_level_, cnt, tb, ta, down.data(), dlen,
+                         acc_b(g0), static_cast<long long>(2 * tw), kp);
     word *dp[2] = {finp, finp + tw};
     const word *s0[2] = {finp, finp + tw};
     K(chd_k_permute_accum(&ctx.ntt_handler_.Tables(), &m, dp, 2,
-                          first ? nullptr : s0, 0, &s, 1, total,
+                          first ? nullptr : s0, 0, ps, cnt, total,
                           CurrentStream()));
     first = false;
   }

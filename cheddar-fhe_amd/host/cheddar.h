@@ -495,6 +495,14 @@ class ModSwitchHandler<uint32_t> {
   void ModUpGroups(word *modup, long long group_stride,
                    const DvConstView<word> &src, word *intt,
                    bool with_rows, const word *src_mul = nullptr) const;
+  // ModUpGroups (column passes only) of num_inputs (<= CHD_MAX_JOBS)
+  // independent inputs of this level in one launch per phase: input i is
+  // src + i * src_stride (num_q limbs), its group z goes to
+  // modup + (i * NumGroups() + z) * group_stride, and intt holds
+  // num_inputs * num_q limbs of scratch.
+  void ModUpGroupsBatch(word *modup, long long group_stride, const word *src,
+                        long long src_stride, int num_inputs,
+                        word *intt) const;
 
   enum class Kind { ModDown, Rescale, ModDownAndRescale };
   // ModDownWorker for several polynomials at once: polynomial p of the
@@ -664,6 +672,15 @@ class Context<uint32_t> {
   // groups, plus add_b (q + alpha limbs) on the b part.
   void KeyMultExtV(int level, word *acc_b, word *acc_a, const word *d,
                    const word *add_b, const EvkRef &key) const;
+  // KeyMultExtV of num (<= CHD_MAX_JOBS) independent inputs at one level,
+  // each with its own key: input i is d + i * d_stride, its add_b is
+  // add_b + i * add_stride and its result goes to (acc_b[i], acc_a[i]).
+  // One launch per phase for all of them (the giant steps of Hoist.cu:
+  // 895-957 are independent until their permuted sum).
+  void KeyMultExtBatchV(int level, int num, word *const *acc_b,
+                        word *const *acc_a, const word *d, long long d_stride,
+                        const word *add_b, long long add_stride,
+                        const EvkRef *const *keys) const;
   static EvkRef RefOfKey(const Evk &k);
   DvConstView<word> PProd(const NPInfo &np) const { return GetPProd(np); }
 

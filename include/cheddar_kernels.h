@@ -58,7 +58,7 @@ int chd_k_ntt_fwd_moddown(const chd_tables *t, const chd_limb_map *m,
                           int src2_lo, int src2_hi, const uint32_t *inv_prod,
                           const uint32_t *pad, void *stream);
 
-/* Same for num_polys (<= 4) polynomials in separate buffers dst[p];
+/* Same for num_polys (<= CHD_MAX_JOBS) polynomials in separate buffers dst[p];
  * src2 of polynomial p is at src2 + p * src2_pstride. With src == NULL the
  * NTT runs in place on dst[p]; otherwise its input is src + p * src_pstride,
  * which must not overlap any dst[p] (one HBM pass instead of two). */
@@ -100,11 +100,13 @@ int chd_k_bconv(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
                 const int32_t *src, int src_len, int dst_len,
                 const void *table, void *stream);
 
-/* Batched BConv: up to CHD_MAX_JOBS independent conversions in one launch
+/* Batched BConv: up to CHD_MAX_BCONV_JOBS independent conversions in one launch
  * (the beta groups of ModUp, or the two polynomials of ModDown). Each job
  * has its own source, table, lengths and skip range; all share the prime
  * mapping of m (dst positions are logical limbs of one level). */
 #define CHD_MAX_JOBS 8
+/* a BConv launch takes more jobs: every group of several ModUps */
+#define CHD_MAX_BCONV_JOBS 32
 typedef struct chd_bconv_job {
   uint32_t *dst;
   const int32_t *src;
@@ -126,6 +128,14 @@ int chd_k_ntt_fwd_groups(const chd_tables *t, const chd_limb_map *m,
                          uint32_t *modup, long long group_stride,
                          int num_groups, int alpha, int group_shift,
                          int group_limbs, int with_rows, void *stream);
+/* The same for num_inputs (<= CHD_MAX_JOBS) ModUps of one level in one
+ * launch: group g of input i at modup + (i * num_groups + g) * group_stride
+ * (the batched giant steps of Hoist.cu:895-957). */
+int chd_k_ntt_fwd_groups_batch(const chd_tables *t, const chd_limb_map *m,
+                               uint32_t *modup, long long group_stride,
+                               int num_groups, int num_inputs, int alpha,
+                               int group_shift, int group_limbs,
+                               int with_rows, void *stream);
 
 /* Fused ModUp row pass + evaluation-key inner product + CAccum
  * (Context.cpp:609-712, ElementWise.cu:225-366):
@@ -165,6 +175,10 @@ typedef struct chd_keyacc_args {
 } chd_keyacc_args;
 int chd_k_modup_keyacc(const chd_tables *t, const chd_keyacc_args *args,
                        void *stream);
+/* num_jobs (<= CHD_MAX_JOBS) independent key accumulations of one level
+ * (same num_q and alpha; own inputs, keys and outputs each) in one launch. */
+int chd_k_modup_keyacc_batch(const chd_tables *t, const chd_keyacc_args *jobs,
+                             int num_jobs, void *stream);
 
 /* Tensor (ElementWise.cu:504-575, 921-953): Karatsuba product of
  * (b1,a1) x (b2,a2) -> (bx, ax, rx) over num_limbs limbs. src2 == src1
