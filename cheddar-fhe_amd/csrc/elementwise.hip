@@ -364,6 +364,51 @@ __global__ __launch_bounds__(kThreads) void gs_fused_kernel(chd_tables t,
 }
 
 
+// Wide giant-step accumulation: a thread owns one coefficient of one limb
+// and the accumulators of kGs giant steps, so a launch reads every baby step
+// once for all of them. Plaintext addresses come from a device table
+// (wave-uniform scalar loads); every entry is valid (absent pairs point at a
+// zero plaintext), so the loop has no branches and each baby step's kGs
+// loads issue together.
+template <int kGs>
+__global__ __launch_bounds__(kThreads) void gs_wide_kernel(chd_tables t,
+                                                         chd_limb_map m,
+                                                         chd_gs_wide_args a) {
+  const LimbIdx li = limb_of(t, m);
+  const size_t o = (static_cast<size_t>(li.l) << kLogN) +
+                   blockIdx.x * kThreads + threadIdx.x;
+  uint32_t rb[kGs], ra[kGs];
+  if (a.add_to_dst) {
+#pragma unroll
+    for (int g = 0; g < kGs; g++) {
+      rb[g] = a.dst_b[g][o];
+      ra[g] = a.dst_a[g][o];
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < kGs; g++) rb[g] = ra[g] = 0u;
+  }
+  for (int b = 0; b < a.num_bs; b++) {
+    const int32_t xb = static_cast<int32_t>(a.bs_b[b][o]);
+    const int32_t xa = static_cast<int32_t>(a.bs_a[b][o]);
+    const uint32_t *const *row = a.pt_table + b;
+    int32_t mm[kGs];
+#pragma unroll
+    for (int g = 0; g < kGs; g++)
+      mm[g] = static_cast<int32_t>(row[g * a.pt_stride][o]);
+#pragma unroll
+    for (int g = 0; g < kGs; g++) {
+      rb[g] = add_mod(rb[g], mont_mul(mm[g], xb, li.q, li.qinv), li.q);
+      ra[g] = add_mod(ra[g], mont_mul(mm[g], xa, li.q, li.qinv), li.q);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < kGs; g++) {
+    a.dst_b[g][o] = rb[g];
+    a.dst_a[g][o] = ra[g];
+  }
+}
+
 // Element-wise arithmetic (ElementWise.cu:33-220 Sum / Sub / Neg / Mult /
 // AddConst / SubConst / SubOppositeConst / MultConst, 600-660
 // MultImaginaryUnit; Basic.cuh:169-260 for the canonical forms).
@@ -618,6 +663,46 @@ extern "C" int chd_k_gs_fused(const chd_tables *t, const chd_limb_map *m,
   hipLaunchKernelGGL(gs_fused_kernel, g, dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), *t, *m, *args);
   return check_launch("chd_k_gs_fused");
+}
+
+extern "C" int chd_k_gs_fused_wide(const chd_tables *t, const chd_limb_map *m,
+                                   const chd_gs_wide_args *args, int num_limbs,
+                                   void *stream) {
+  if (!t || !m || !args || !args->pt_table || args->num_bs < 1 ||
+      args->num_bs > CHD_GS_MAX_BS || args->pt_stride < args->num_bs ||
+      num_limbs < 0 || m->skip_len != 0)
+    return set_error(CHD_ERR_ARG, "chd_k_gs_fused_wide: invalid argument");
+  const int ng = args->num_gs;
+  if (ng != 8 && ng != 16 && ng != 24 && ng != 28 && ng != 32)
+    return set_error(CHD_ERR_ARG,
+                     "chd_k_gs_fused_wide: num_gs must be 8, 16, 24, 28 or 32");
+  for (int b = 0; b < args->num_bs; b++)
+    if (!args->bs_b[b] || !args->bs_a[b])
+      return set_error(CHD_ERR_ARG, "chd_k_gs_fused_wide: null baby step");
+  for (int g = 0; g < ng; g++)
+    if (!args->dst_b[g] || !args->dst_a[g])
+      return set_error(CHD_ERR_ARG, "chd_k_gs_fused_wide: null destination");
+  if (num_limbs == 0) return 0;
+  dim3 g(kN / kThreads, num_limbs);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (ng) {
+    case 8:
+      hipLaunchKernelGGL(gs_wide_kernel<8>, g, dim3(kThreads), 0, s, *t, *m, *args);
+      break;
+    case 16:
+      hipLaunchKernelGGL(gs_wide_kernel<16>, g, dim3(kThreads), 0, s, *t, *m, *args);
+      break;
+    case 24:
+      hipLaunchKernelGGL(gs_wide_kernel<24>, g, dim3(kThreads), 0, s, *t, *m, *args);
+      break;
+    case 28:
+      hipLaunchKernelGGL(gs_wide_kernel<28>, g, dim3(kThreads), 0, s, *t, *m, *args);
+      break;
+    default:
+      hipLaunchKernelGGL(gs_wide_kernel<32>, g, dim3(kThreads), 0, s, *t, *m, *args);
+      break;
+  }
+  return check_launch("chd_k_gs_fused_wide");
 }
 
 extern "C" int chd_k_elementwise(const chd_tables *t, const chd_limb_map *m,

@@ -1665,6 +1665,32 @@ HoistHandler<uint32_t>::HoistHandler(ConstContextPtr<word> context,
   AssertTrue(gs_indices_.size() == 1 || gs_indices_.front() == 0,
              "Hoist: a giant step 0 is required with several giant steps");
   AssertTrue(bs_indices_.size() <= 64, "Hoist: too many baby steps");
+  const int num_gs = static_cast<int>(gs_indices_.size());
+  if (num_gs > CHD_GS_MAX_GS && num_gs <= CHD_GS_WIDE_GS &&
+      bs_indices_.size() <= CHD_GS_MAX_BS) {
+    for (int w : {16, 24, 28, 32})
+      if (wide_gs_ == 0 && num_gs <= w) wide_gs_ = w;
+    const size_t pt_words = static_cast<size_t>(np.GetNumTotal()) * n;
+    zero_pt_.Resize(pt_words * sizeof(word));
+    HipCheck(hipMemset(zero_pt_.as<void>(), 0, pt_words * sizeof(word)),
+             "hipMemset");
+    if (wide_gs_ > num_gs) dummy_out_.Resize(2 * pt_words * sizeof(word));
+    std::vector<const word *> table;
+    table.reserve(static_cast<size_t>(wide_gs_) * bs_indices_.size());
+    for (int k = 0; k < wide_gs_; k++) {
+      const std::map<int, Pt> *pmap =
+          k < num_gs ? &pt_map_.at(gs_indices_[k]) : nullptr;
+      for (int b : bs_indices_) {
+        const word *p = zero_pt_.as<const word>();
+        if (pmap != nullptr) {
+          auto it = pmap->find(b);
+          if (it != pmap->end()) p = it->second.mx_.data();
+        }
+        table.push_back(p);
+      }
+    }
+    pt_table_.Upload(table);
+  }
 }
 
 // Hoist.cu:178-204: the baby and giant steps must be 0, s, 2s, ..., ks
@@ -2036,7 +2062,33 @@ void HoistHandler<uint32_t>::GiantStep(const Context<word> &ctx, Ct &res,
   const std::vector<int> bsv(bs_indices_.begin(), bs_indices_.end());
   Scratch accs(ws, static_cast<size_t>(num_gs) * 2 * tw);
   auto acc_b = [&](int gi) { return accs.data() + static_cast<size_t>(gi) * 2 * tw; };
-  for (int g0 = 0; g0 < num_gs; g0 += CHD_GS_MAX_GS) {
+  if (wide_gs_ > 0) {
+    // every giant step in one launch: each baby step is read once
+    // (plaintext addresses from the handler's table)
+    const word *const *table = pt_table_.as<const word *>();
+    for (size_t b0 = 0; b0 < bsv.size(); b0 += CHD_GS_MAX_BS) {
+      const int bcnt = static_cast<int>(
+          std::min<size_t>(CHD_GS_MAX_BS, bsv.size() - b0));
+      chd_gs_wide_args a{};
+      a.num_bs = bcnt;
+      a.num_gs = wide_gs_;
+      a.add_to_dst = b0 > 0 ? 1 : 0;
+      a.pt_stride = static_cast<int>(bsv.size());
+      a.pt_table = table + b0;
+      for (int j = 0; j < bcnt; j++) {
+        const Ct &ct = bs.at(bsv[b0 + j]);
+        a.bs_b[j] = ct.bx_.data();
+        a.bs_a[j] = ct.ax_.data();
+      }
+      for (int k = 0; k < wide_gs_; k++) {
+        a.dst_b[k] = k < num_gs ? acc_b(k) : dummy_out_.as<word>();
+        a.dst_a[k] = k < num_gs ? acc_b(k) + tw : dummy_out_.as<word>() + tw;
+      }
+      K(chd_k_gs_fused_wide(&ctx.ntt_handler_.Tables(), &m, &a, total,
+                            CurrentStream()));
+    }
+  }
+  for (int g0 = 0; wide_gs_ == 0 && g0 < num_gs; g0 += CHD_GS_MAX_GS) {
     const int gcnt = std::min(CHD_GS_MAX_GS, num_gs - g0);
     for (size_t b0 = 0; b0 < bsv.size(); b0 += CHD_GS_MAX_BS) {
       const int bcnt = static_cast<int>(

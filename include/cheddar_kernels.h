@@ -254,6 +254,22 @@ typedef struct chd_gs_args {
 int chd_k_gs_fused(const chd_tables *t, const chd_limb_map *m,
                    const chd_gs_args *args, int num_limbs, void *stream);
 
+/* The same for num_gs = 8, 16, 24, 28 or 32 giant steps in one launch, so
+ * each baby step is read once for all of them: one coefficient per thread
+ * with every giant step's accumulators in registers. The plaintext
+ * addresses are a device array pt_table[g * pt_stride + b]; every entry must
+ * be a valid plaintext (point absent pairs at a zero plaintext). */
+#define CHD_GS_WIDE_GS 32
+typedef struct chd_gs_wide_args {
+  int num_bs, num_gs, add_to_dst, pt_stride;
+  const uint32_t *bs_b[CHD_GS_MAX_BS], *bs_a[CHD_GS_MAX_BS];
+  const uint32_t *const *pt_table;
+  uint32_t *dst_b[CHD_GS_WIDE_GS], *dst_a[CHD_GS_WIDE_GS];
+} chd_gs_wide_args;
+int chd_k_gs_fused_wide(const chd_tables *t, const chd_limb_map *m,
+                        const chd_gs_wide_args *args, int num_limbs,
+                        void *stream);
+
 #define CHD_MAX_BS 8
 #define CHD_MAX_BS_GROUPS 4
 typedef struct chd_bs_args {

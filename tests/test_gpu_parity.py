@@ -357,3 +357,27 @@ def test_hoist_evaluate_config5_level(chd, ks):
         h.run(out, (dev(b), dev(a)), dkeys)
         assert np.array_equal(host(out[0]), wb)
         assert np.array_equal(host(out[1]), wa)
+
+
+def test_hoist_evaluate_many_giant_steps(chd, ks):
+    """12 giant steps at L = 20: the wide giant-step accumulation (one launch
+    for every giant step, padded to 16 with zero plaintexts) and the batched
+    giant-step key switches (a batch of 8 and one of 3), with absent pairs"""
+    import hoist_ref
+    param, ctx, main, aux = ks
+    L = 20
+    r = rng(520)
+    bsi, gsi = [0, 1, 2], [3 * k for k in range(12)]
+    pts = {(g, s): uniform_limbs(r, main[:L] + aux) for g in gsi for s in bsi
+           if (g, s) not in ((6, 1), (33, 2))}
+    keys = _rot_keys(r, main, aux, sorted(set(bsi[1:] + gsi[1:])))
+    dkeys = {k: ([dev(x) for x in v[0]], [dev(x) for x in v[1]])
+             for k, v in keys.items()}
+    dpts = {k: dev(v) for k, v in pts.items()}
+    b, a = uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L])
+    wb, wa = hoist_ref.evaluate(b, a, pts, keys, L, 24, main, aux, 16)
+    h = chd.Hoist(ctx, L - 1, gsi, bsi, dpts)
+    out = (zeros(L - 1, N), zeros(L - 1, N))
+    h.run(out, (dev(b), dev(a)), dkeys)
+    assert np.array_equal(host(out[0]), wb)
+    assert np.array_equal(host(out[1]), wa)
