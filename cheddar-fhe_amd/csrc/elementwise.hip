@@ -364,48 +364,60 @@ __global__ __launch_bounds__(kThreads) void gs_fused_kernel(chd_tables t,
 }
 
 
-// Wide giant-step accumulation: a thread owns one coefficient of one limb
-// and the accumulators of kGs giant steps, so a launch reads every baby step
-// once for all of them. Plaintext addresses come from a device table
-// (wave-uniform scalar loads); every entry is valid (absent pairs point at a
-// zero plaintext), so the loop has no branches and each baby step's kGs
-// loads issue together.
-template <int kGs>
+// Wide giant-step accumulation: the 4 waves of a workgroup share 256
+// coefficients of one limb (4 per lane, 16-byte loads) and each owns kGw of
+// the launch's 4 kGw giant steps, so a launch reads every baby step once
+// from HBM for all of them (the other waves' reads of it hit in cache).
+// Plaintext addresses come from a device table (wave-uniform scalar loads);
+// every entry is valid (absent pairs point at a zero plaintext), so the loop
+// has no branches and each baby step's kGw loads issue together.
+template <int kGw>
 __global__ __launch_bounds__(kThreads) void gs_wide_kernel(chd_tables t,
                                                          chd_limb_map m,
                                                          chd_gs_wide_args a) {
   const LimbIdx li = limb_of(t, m);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const size_t o = (static_cast<size_t>(li.l) << kLogN) +
-                   blockIdx.x * kThreads + threadIdx.x;
-  uint32_t rb[kGs], ra[kGs];
-  if (a.add_to_dst) {
+                   blockIdx.x * (64 * kPerThread) + (threadIdx.x & 63) * kPerThread;
+  const int g0 = wave * kGw;
+  uint32_t rb[kGw][4], ra[kGw][4];
 #pragma unroll
-    for (int g = 0; g < kGs; g++) {
-      rb[g] = a.dst_b[g][o];
-      ra[g] = a.dst_a[g][o];
+  for (int g = 0; g < kGw; g++) {
+    if (a.add_to_dst) {
+      const uint4 vb = ld4(a.dst_b[g0 + g] + o), va = ld4(a.dst_a[g0 + g] + o);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        rb[g][i] = get(vb, i);
+        ra[g][i] = get(va, i);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) rb[g][i] = ra[g][i] = 0u;
     }
-  } else {
-#pragma unroll
-    for (int g = 0; g < kGs; g++) rb[g] = ra[g] = 0u;
   }
   for (int b = 0; b < a.num_bs; b++) {
-    const int32_t xb = static_cast<int32_t>(a.bs_b[b][o]);
-    const int32_t xa = static_cast<int32_t>(a.bs_a[b][o]);
-    const uint32_t *const *row = a.pt_table + b;
-    int32_t mm[kGs];
+    const uint4 xb = ld4(a.bs_b[b] + o), xa = ld4(a.bs_a[b] + o);
+    const uint32_t *const *row = a.pt_table + g0 * a.pt_stride + b;
+    uint4 mv[kGw];
 #pragma unroll
-    for (int g = 0; g < kGs; g++)
-      mm[g] = static_cast<int32_t>(row[g * a.pt_stride][o]);
+    for (int g = 0; g < kGw; g++) mv[g] = ld4(row[g * a.pt_stride] + o);
 #pragma unroll
-    for (int g = 0; g < kGs; g++) {
-      rb[g] = add_mod(rb[g], mont_mul(mm[g], xb, li.q, li.qinv), li.q);
-      ra[g] = add_mod(ra[g], mont_mul(mm[g], xa, li.q, li.qinv), li.q);
-    }
+    for (int g = 0; g < kGw; g++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int32_t mm = static_cast<int32_t>(get(mv[g], i));
+        rb[g][i] = add_mod(rb[g][i],
+                           mont_mul(mm, static_cast<int32_t>(get(xb, i)), li.q,
+                                    li.qinv), li.q);
+        ra[g][i] = add_mod(ra[g][i],
+                           mont_mul(mm, static_cast<int32_t>(get(xa, i)), li.q,
+                                    li.qinv), li.q);
+      }
   }
 #pragma unroll
-  for (int g = 0; g < kGs; g++) {
-    a.dst_b[g][o] = rb[g];
-    a.dst_a[g][o] = ra[g];
+  for (int g = 0; g < kGw; g++) {
+    st4(a.dst_b[g0 + g] + o, make_uint4(rb[g][0], rb[g][1], rb[g][2], rb[g][3]));
+    st4(a.dst_a[g0 + g] + o, make_uint4(ra[g][0], ra[g][1], ra[g][2], ra[g][3]));
   }
 }
 
@@ -683,23 +695,24 @@ extern "C" int chd_k_gs_fused_wide(const chd_tables *t, const chd_limb_map *m,
     if (!args->dst_b[g] || !args->dst_a[g])
       return set_error(CHD_ERR_ARG, "chd_k_gs_fused_wide: null destination");
   if (num_limbs == 0) return 0;
-  dim3 g(kN / kThreads, num_limbs);
+  static_assert(kThreads == 256, "gs_wide_kernel splits giant steps over 4 waves");
+  dim3 g(kN / (64 * kPerThread), num_limbs);
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (ng) {
     case 8:
-      hipLaunchKernelGGL(gs_wide_kernel<8>, g, dim3(kThreads), 0, s, *t, *m, *args);
+      hipLaunchKernelGGL(gs_wide_kernel<2>, g, dim3(kThreads), 0, s, *t, *m, *args);
       break;
     case 16:
-      hipLaunchKernelGGL(gs_wide_kernel<16>, g, dim3(kThreads), 0, s, *t, *m, *args);
+      hipLaunchKernelGGL(gs_wide_kernel<4>, g, dim3(kThreads), 0, s, *t, *m, *args);
       break;
     case 24:
-      hipLaunchKernelGGL(gs_wide_kernel<24>, g, dim3(kThreads), 0, s, *t, *m, *args);
+      hipLaunchKernelGGL(gs_wide_kernel<6>, g, dim3(kThreads), 0, s, *t, *m, *args);
       break;
     case 28:
-      hipLaunchKernelGGL(gs_wide_kernel<28>, g, dim3(kThreads), 0, s, *t, *m, *args);
+      hipLaunchKernelGGL(gs_wide_kernel<7>, g, dim3(kThreads), 0, s, *t, *m, *args);
       break;
     default:
-      hipLaunchKernelGGL(gs_wide_kernel<32>, g, dim3(kThreads), 0, s, *t, *m, *args);
+      hipLaunchKernelGGL(gs_wide_kernel<8>, g, dim3(kThreads), 0, s, *t, *m, *args);
       break;
   }
   return check_launch("chd_k_gs_fused_wide");
