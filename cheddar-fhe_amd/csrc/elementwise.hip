@@ -364,18 +364,38 @@ __global__ __launch_bounds__(kThreads) void gs_fused_kernel(chd_tables t,
 }
 
 
+// sum of up to four products of canonical residues (each < q^2 < 2^62, so
+// the sum fits 64 bits) times 2^-32 mod q, canonical: with T = hi 2^32 + lo,
+// T 2^-32 = hi + lo 2^-32 (mod q), where hi < 4 q^2 / 2^32 < 2q and the
+// Montgomery reduction of lo is in [0, q]. qn = -q^-1 mod 2^32.
+__device__ __forceinline__ uint32_t reduce_sum4(uint64_t t, uint32_t q,
+                                                uint32_t qn) {
+  const uint32_t lo = static_cast<uint32_t>(t);
+  uint32_t hi = static_cast<uint32_t>(t >> 32);
+  hi = hi < q ? hi : hi - q;                       // [0, q)
+  const uint32_t m = lo * qn;
+  const uint32_t r = static_cast<uint32_t>(
+      (static_cast<uint64_t>(m) * q + lo) >> 32);  // [0, q]
+  const uint32_t s = hi + r;                       // [0, 2q)
+  return s < q ? s : s - q;
+}
+
 // Wide giant-step accumulation: the 4 waves of a workgroup share 256
 // coefficients of one limb (4 per lane, 16-byte loads) and each owns kGw of
 // the launch's 4 kGw giant steps, so a launch reads every baby step once
 // from HBM for all of them (the other waves' reads of it hit in cache).
 // Plaintext addresses come from a device table (wave-uniform scalar loads);
-// every entry is valid (absent pairs point at a zero plaintext), so the loop
-// has no branches and each baby step's kGw loads issue together.
+// every entry is valid (absent pairs point at a zero plaintext) and baby
+// steps come in fours (padded with zero ones), so the loop has no branches.
+// Four products of a giant step are summed in 64 bits and reduced once,
+// which equals the sum of their MontMuls mod q (the reference's
+// MontMul-then-add, GSFusedKernel of Hoist.cu:80-118, in canonical form).
 template <int kGw>
 __global__ __launch_bounds__(kThreads) void gs_wide_kernel(chd_tables t,
                                                          chd_limb_map m,
                                                          chd_gs_wide_args a) {
   const LimbIdx li = limb_of(t, m);
+  const uint32_t qn = 0u - static_cast<uint32_t>(li.qinv);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const size_t o = (static_cast<size_t>(li.l) << kLogN) +
                    blockIdx.x * (64 * kPerThread) + (threadIdx.x & 63) * kPerThread;
@@ -395,24 +415,32 @@ __global__ __launch_bounds__(kThreads) void gs_wide_kernel(chd_tables t,
       for (int i = 0; i < 4; i++) rb[g][i] = ra[g][i] = 0u;
     }
   }
-  for (int b = 0; b < a.num_bs; b++) {
-    const uint4 xb = ld4(a.bs_b[b] + o), xa = ld4(a.bs_a[b] + o);
-    const uint32_t *const *row = a.pt_table + g0 * a.pt_stride + b;
-    uint4 mv[kGw];
+  for (int b0 = 0; b0 < a.num_bs; b0 += 4) {
+    uint4 xb[4], xa[4];
 #pragma unroll
-    for (int g = 0; g < kGw; g++) mv[g] = ld4(row[g * a.pt_stride] + o);
+    for (int j = 0; j < 4; j++) {
+      xb[j] = ld4(a.bs_b[b0 + j] + o);
+      xa[j] = ld4(a.bs_a[b0 + j] + o);
+    }
+    const uint32_t *const *row = a.pt_table + g0 * a.pt_stride + b0;
 #pragma unroll
-    for (int g = 0; g < kGw; g++)
+    for (int g = 0; g < kGw; g++) {
+      uint4 mv[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) mv[j] = ld4(row[g * a.pt_stride + j] + o);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int32_t mm = static_cast<int32_t>(get(mv[g], i));
-        rb[g][i] = add_mod(rb[g][i],
-                           mont_mul(mm, static_cast<int32_t>(get(xb, i)), li.q,
-                                    li.qinv), li.q);
-        ra[g][i] = add_mod(ra[g][i],
-                           mont_mul(mm, static_cast<int32_t>(get(xa, i)), li.q,
-                                    li.qinv), li.q);
+        uint64_t tb = 0, ta = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const uint64_t mm = get(mv[j], i);
+          tb += mm * get(xb[j], i);
+          ta += mm * get(xa[j], i);
+        }
+        rb[g][i] = add_mod(rb[g][i], reduce_sum4(tb, li.q, qn), li.q);
+        ra[g][i] = add_mod(ra[g][i], reduce_sum4(ta, li.q, qn), li.q);
       }
+    }
   }
 #pragma unroll
   for (int g = 0; g < kGw; g++) {
@@ -681,8 +709,8 @@ extern "C" int chd_k_gs_fused_wide(const chd_tables *t, const chd_limb_map *m,
                                    const chd_gs_wide_args *args, int num_limbs,
                                    void *stream) {
   if (!t || !m || !args || !args->pt_table || args->num_bs < 1 ||
-      args->num_bs > CHD_GS_MAX_BS || args->pt_stride < args->num_bs ||
-      num_limbs < 0 || m->skip_len != 0)
+      args->num_bs > CHD_GS_MAX_BS || args->num_bs % 4 != 0 ||
+      args->pt_stride < args->num_bs || num_limbs < 0 || m->skip_len != 0)
     return set_error(CHD_ERR_ARG, "chd_k_gs_fused_wide: invalid argument");
   const int ng = args->num_gs;
   if (ng != 8 && ng != 16 && ng != 24 && ng != 28 && ng != 32)

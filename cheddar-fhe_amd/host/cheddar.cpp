@@ -1675,11 +1675,15 @@ HoistHandler<uint32_t>::HoistHandler(ConstContextPtr<word> context,
     HipCheck(hipMemset(zero_pt_.as<void>(), 0, pt_words * sizeof(word)),
              "hipMemset");
     if (wide_gs_ > num_gs) dummy_out_.Resize(2 * pt_words * sizeof(word));
+    // baby steps in fours: padding columns (and the padding baby steps
+    // themselves, at run time) are the zero plaintext
+    wide_bs_ = (static_cast<int>(bs_indices_.size()) + 3) / 4 * 4;
     std::vector<const word *> table;
-    table.reserve(static_cast<size_t>(wide_gs_) * bs_indices_.size());
+    table.reserve(static_cast<size_t>(wide_gs_) * wide_bs_);
     for (int k = 0; k < wide_gs_; k++) {
       const std::map<int, Pt> *pmap =
           k < num_gs ? &pt_map_.at(gs_indices_[k]) : nullptr;
+      int j = 0;
       for (int b : bs_indices_) {
         const word *p = zero_pt_.as<const word>();
         if (pmap != nullptr) {
@@ -1687,7 +1691,9 @@ HoistHandler<uint32_t>::HoistHandler(ConstContextPtr<word> context,
           if (it != pmap->end()) p = it->second.mx_.data();
         }
         table.push_back(p);
+        j++;
       }
+      for (; j < wide_bs_; j++) table.push_back(zero_pt_.as<const word>());
     }
     pt_table_.Upload(table);
   }
@@ -2064,29 +2070,25 @@ void HoistHandler<uint32_t>::GiantStep(const Context<word> &ctx, Ct &res,
   auto acc_b = [&](int gi) { return accs.data() + static_cast<size_t>(gi) * 2 * tw; };
   if (wide_gs_ > 0) {
     // every giant step in one launch: each baby step is read once
-    // (plaintext addresses from the handler's table)
-    const word *const *table = pt_table_.as<const word *>();
-    for (size_t b0 = 0; b0 < bsv.size(); b0 += CHD_GS_MAX_BS) {
-      const int bcnt = static_cast<int>(
-          std::min<size_t>(CHD_GS_MAX_BS, bsv.size() - b0));
-      chd_gs_wide_args a{};
-      a.num_bs = bcnt;
-      a.num_gs = wide_gs_;
-      a.add_to_dst = b0 > 0 ? 1 : 0;
-      a.pt_stride = static_cast<int>(bsv.size());
-      a.pt_table = table + b0;
-      for (int j = 0; j < bcnt; j++) {
-        const Ct &ct = bs.at(bsv[b0 + j]);
-        a.bs_b[j] = ct.bx_.data();
-        a.bs_a[j] = ct.ax_.data();
-      }
-      for (int k = 0; k < wide_gs_; k++) {
-        a.dst_b[k] = k < num_gs ? acc_b(k) : dummy_out_.as<word>();
-        a.dst_a[k] = k < num_gs ? acc_b(k) + tw : dummy_out_.as<word>() + tw;
-      }
-      K(chd_k_gs_fused_wide(&ctx.ntt_handler_.Tables(), &m, &a, total,
-                            CurrentStream()));
+    // (plaintext addresses from the handler's table; baby steps padded to
+    // wide_bs_ with the zero plaintext)
+    chd_gs_wide_args a{};
+    a.num_bs = wide_bs_;
+    a.num_gs = wide_gs_;
+    a.add_to_dst = 0;
+    a.pt_stride = wide_bs_;
+    a.pt_table = pt_table_.as<const word *>();
+    for (int j = 0; j < wide_bs_; j++) {
+      const bool real = j < static_cast<int>(bsv.size());
+      a.bs_b[j] = real ? bs.at(bsv[j]).bx_.data() : zero_pt_.as<word>();
+      a.bs_a[j] = real ? bs.at(bsv[j]).ax_.data() : zero_pt_.as<word>();
     }
+    for (int k = 0; k < wide_gs_; k++) {
+      a.dst_b[k] = k < num_gs ? acc_b(k) : dummy_out_.as<word>();
+      a.dst_a[k] = k < num_gs ? acc_b(k) + tw : dummy_out_.as<word>() + tw;
+    }
+    K(chd_k_gs_fused_wide(&ctx.ntt_handler_.Tables(), &m, &a, total,
+                          CurrentStream()));
   }
   for (int g0 = 0; wide_gs_ == 0 && g0 < num_gs; g0 += CHD_GS_MAX_GS) {
     const int gcnt = std::min(CHD_GS_MAX_GS, num_gs - g0);

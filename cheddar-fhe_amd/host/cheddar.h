@@ -788,11 +788,12 @@ class HoistHandler<uint32_t> {
   std::vector<int> gs_indices_;
   bool gs_only_ = false;  // a giant-step-only map, evaluated converted
   // wide giant-step accumulation (more than CHD_GS_MAX_GS giant steps, at
-  // most CHD_GS_WIDE_GS): device table of plaintext addresses
-  // [giant step][baby step] in gs_indices_ x bs_indices_ order, padded to
-  // wide_gs_ rows; absent pairs and padding rows point at zero_pt_, padding
-  // rows write to dummy_out_ (never read). Built once at construction.
-  int wide_gs_ = 0;
+  // most CHD_GS_WIDE_GS, at most CHD_GS_MAX_BS baby steps): device table of
+  // plaintext addresses [giant step][baby step] in gs_indices_ x
+  // bs_indices_ order, padded to wide_gs_ rows and wide_bs_ (a multiple of
+  // 4) columns; absent pairs and padding point at zero_pt_, padding rows
+  // write to dummy_out_ (never read). Built once at construction.
+  int wide_gs_ = 0, wide_bs_ = 0;
   DevBuf pt_table_, zero_pt_, dummy_out_;
 };
 

@@ -255,10 +255,10 @@ int chd_k_gs_fused(const chd_tables *t, const chd_limb_map *m,
                    const chd_gs_args *args, int num_limbs, void *stream);
 
 /* The same for num_gs = 8, 16, 24, 28 or 32 giant steps in one launch, so
- * each baby step is read once for all of them: one coefficient per thread
- * with every giant step's accumulators in registers. The plaintext
- * addresses are a device array pt_table[g * pt_stride + b]; every entry must
- * be a valid plaintext (point absent pairs at a zero plaintext). */
+ * each baby step is read once for all of them. num_bs must be a multiple of
+ * 4 (pad with zero baby steps). The plaintext addresses are a device array
+ * pt_table[g * pt_stride + b]; every entry must be a valid plaintext (point
+ * absent pairs at a zero plaintext). Inputs must be canonical residues. */
 #define CHD_GS_WIDE_GS 32
 typedef struct chd_gs_wide_args {
   int num_bs, num_gs, add_to_dst, pt_stride;
