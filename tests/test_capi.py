@@ -73,3 +73,91 @@ def test_null_arguments_return_status(chd):
     t = ctypes.c_void_p()
     st = chd.lib.chd_bconv_plan_create(ctypes.byref(t), 16, None, 0, None, 0)
     assert st == -1
+
+
+# ---- argument checks of the batched kernel entry points (host side only:
+# every call below is rejected before anything is launched)
+P = ctypes.c_void_p
+
+
+class Tables(ctypes.Structure):
+    _fields_ = [(n, P) for n in ("q", "qinv", "qd", "qinvd", "rinv", "tw",
+                                 "itw")]
+
+
+class LimbMap(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("num_q", "skip_lo", "skip_len",
+                                            "src_gap", "tab_off", "tab_gap",
+                                            "cst_gap")]
+
+
+class GsWideArgs(ctypes.Structure):
+    _fields_ = [("num_bs", ctypes.c_int), ("num_gs", ctypes.c_int),
+                ("add_to_dst", ctypes.c_int), ("pt_stride", ctypes.c_int),
+                ("bs_b", P * 32), ("bs_a", P * 32), ("pt_table", P),
+                ("dst_b", P * 32), ("dst_a", P * 32)]
+
+
+FAKE = P(0x1000)  # never dereferenced: the calls fail their checks first
+
+
+def _kernel_lib(chd):
+    lib = chd.lib
+    lib.chd_k_gs_fused_wide.argtypes = [ctypes.POINTER(Tables),
+                                        ctypes.POINTER(LimbMap),
+                                        ctypes.POINTER(GsWideArgs),
+                                        ctypes.c_int, P]
+    lib.chd_k_modup_keyacc_batch.argtypes = [ctypes.POINTER(Tables), P,
+                                             ctypes.c_int, P]
+    lib.chd_k_ntt_fwd_groups_batch.argtypes = [
+        ctypes.POINTER(Tables), ctypes.POINTER(LimbMap), P, ctypes.c_longlong,
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+        ctypes.c_int, P]
+    lib.chd_k_ntt_fwd_moddown_multi.argtypes = [
+        ctypes.POINTER(Tables), ctypes.POINTER(LimbMap), ctypes.POINTER(P),
+        ctypes.c_int, ctypes.c_int, P, ctypes.c_longlong, P,
+        ctypes.c_longlong, ctypes.c_int, ctypes.c_int, P, P, P]
+    return lib
+
+
+def test_gs_fused_wide_checks(chd):
+    lib = _kernel_lib(chd)
+    t, m = Tables(), LimbMap(num_q=20)
+    a = GsWideArgs(num_bs=4, num_gs=12, pt_stride=4, pt_table=FAKE)
+    for j in range(4):
+        a.bs_b[j] = a.bs_a[j] = FAKE
+    for g in range(32):
+        a.dst_b[g] = a.dst_a[g] = FAKE
+    # giant steps must be padded to 8, 16, 24, 28 or 32
+    assert lib.chd_k_gs_fused_wide(t, m, a, 28, None) == -1
+    assert b"num_gs" in chd.lib.chd_last_error()
+    # baby steps come in fours
+    a.num_gs, a.num_bs = 16, 3
+    assert lib.chd_k_gs_fused_wide(t, m, a, 28, None) == -1
+    a.num_bs, a.pt_table = 4, None
+    assert lib.chd_k_gs_fused_wide(t, m, a, 28, None) == -1
+
+
+def test_batched_entry_points_reject_bad_counts(chd):
+    lib = _kernel_lib(chd)
+    t, m = Tables(), LimbMap(num_q=20, skip_lo=1 << 30)
+    # more key accumulations than one launch takes, or none
+    assert lib.chd_k_modup_keyacc_batch(t, FAKE, 9, None) == -1
+    assert lib.chd_k_modup_keyacc_batch(t, FAKE, 0, None) == -1
+    # ModUp column passes of too many inputs
+    assert lib.chd_k_ntt_fwd_groups_batch(t, m, FAKE, 1 << 20, 3, 9, 8, 0,
+                                          28, 0, None) == -1
+
+
+def test_moddown_ntt_rejects_overlapping_source(chd):
+    lib = _kernel_lib(chd)
+    t, m = Tables(), LimbMap(num_q=20, skip_lo=1 << 30)
+    n = 1 << 16
+    base = 0x10000000
+    dst = (P * 2)(P(base), P(base + 40 * 4 * n))
+    # the source starts inside dst[1]: the single-pass NTT cannot run
+    src = P(base + 45 * 4 * n)
+    st = lib.chd_k_ntt_fwd_moddown_multi(t, m, dst, 2, 20, src, 20 * n, None,
+                                         0, 0, 0, FAKE, None, None)
+    assert st == -1
+    assert b"overlaps" in chd.lib.chd_last_error()
