@@ -67,6 +67,9 @@ hipError_t launch_modup_keyacc(const KeyAccBatch &a, int num_jobs,
 hipError_t launch_ntt_fwd(const NttArgs &a, int num_limbs, int num_polys,
                           bool pre_const, int epilogue, hipStream_t s);
 // Inverse NTT (kernels compute N * intt; the N^-1 is in the constant)
+// the inverse's second pass alone (in place on a.dst)
+hipError_t launch_ntt_inv_cols(const NttArgs &a, int num_limbs, int num_polys,
+                               int epilogue, hipStream_t s);
 hipError_t launch_ntt_inv(const NttArgs &a, int num_limbs, int num_polys,
                           int epilogue, hipStream_t s);
 // column pass only (ModUp group mode uses grid.z = groups)

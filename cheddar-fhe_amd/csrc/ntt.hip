@@ -518,16 +518,17 @@ __global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
     fwd_rows_body<kEpi, false>(a, lb, x, q, qinv, dst, xch, s2v);
 }
 
-// inverse, row pass: GS stages 15..8 (src -> dst, dst left unreduced)
+// inverse, row pass: GS stages 15..8 of this workgroup's 16-row tile (row
+// tile blockIdx.x) with the limb's inverse twiddles tw; xin holds columns
+// 16c .. 16c+15 of the thread's row; dst (the limb) is left unreduced.
 template <bool kLazy>
-__device__ __forceinline__ void inv_rows_body(const NttArgs &a, const Limb &lb,
+__device__ __forceinline__ void inv_rows_body(const uint32_t *tw,
                                               uint32_t (&xin)[16], uint32_t q,
                                               uint32_t qinv, uint32_t *dst,
                                               int32_t *xch) {
   using A = Arith<kLazy>;
   using T = typename A::T;
   const A ar(q, qinv);
-  const uint32_t *tw = a.tab.itw + (static_cast<size_t>(lb.ti) << kLogN);
   const int c = threadIdx.x & 15;
   const int r = threadIdx.x >> 4;
   const int row = blockIdx.x * kTileRows + r;
@@ -631,10 +632,11 @@ __global__ __launch_bounds__(256) void ntt_inv_rows(NttArgs a) {
   uint32_t x[16];
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = xr[pidx(16 * c + k)];
+  const uint32_t *itw = a.tab.itw + (static_cast<size_t>(lb.ti) << kLogN);
   if (q < (1u << 30))
-    inv_rows_body<true>(a, lb, x, q, qinv, dst, xch);
+    inv_rows_body<true>(itw, x, q, qinv, dst, xch);
   else
-    inv_rows_body<false>(a, lb, x, q, qinv, dst, xch);
+    inv_rows_body<false>(itw, x, q, qinv, dst, xch);
 }
 
 // inverse, column pass: GS stages 7..0 (in place on dst) + constant epilogue
@@ -907,6 +909,18 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
     }
   }
   (void)qs;
+  if (a.intt_b != nullptr && l >= a.intt_lo) {
+    // first pass of ModDown's INTT (INTTForModDown, NTT.cu:973-1128) on
+    // this limb of both accumulators, straight from the registers; the
+    // accumulator itself is not stored
+    const uint32_t *itw = tab.itw + (static_cast<size_t>(ti) << kLogN);
+    const size_t ioff = static_cast<size_t>(l - a.intt_lo) << kLogN;
+    __syncthreads();  // the group row passes' LDS reads are done
+    inv_rows_body<kLazy>(itw, accb, q, qinv, a.intt_b + ioff, xch);
+    __syncthreads();  // ... and the first polynomial's store reads
+    inv_rows_body<kLazy>(itw, acca, q, qinv, a.intt_a + ioff, xch);
+    return;
+  }
   uint32_t *ob = a.acc_b + loff;
   uint32_t *oa = a.acc_a + loff;
 #pragma unroll
@@ -1233,22 +1247,27 @@ hipError_t launch_ntt_fwd(const NttArgs &a, int num_limbs, int num_polys,
   return hipGetLastError();
 }
 
+hipError_t launch_ntt_inv_cols(const NttArgs &a, int num_limbs, int num_polys,
+                               int epilogue, hipStream_t s) {
+  dim3 gc(kCols / kTileCols, num_limbs, num_polys);
+  if (epilogue == kEpiConstCentre)
+    hipLaunchKernelGGL(ntt_inv_cols<kEpiConstCentre>, gc, dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL(ntt_inv_cols<kEpiConst>, gc, dim3(512), 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_ntt_inv(const NttArgs &a, int num_limbs, int num_polys,
                           int epilogue, hipStream_t s) {
   if (num_limbs <= 0 || num_polys <= 0) return hipSuccess;
   dim3 gr(kRows / kTileRows, num_limbs, num_polys);
-  dim3 gc(kCols / kTileCols, num_limbs, num_polys);
   hipLaunchKernelGGL(ntt_inv_rows, gr, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // the column pass works in place on dst
   NttArgs b = a;
   b.map.src_gap = 0;
-  if (epilogue == kEpiConstCentre)
-    hipLaunchKernelGGL(ntt_inv_cols<kEpiConstCentre>, gc, dim3(512), 0, s, b);
-  else
-    hipLaunchKernelGGL(ntt_inv_cols<kEpiConst>, gc, dim3(512), 0, s, b);
-  return hipGetLastError();
+  return launch_ntt_inv_cols(b, num_limbs, num_polys, epilogue, s);
 }
 
 }  // namespace chd
@@ -1367,6 +1386,32 @@ extern "C" int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m,
                         stream);
 }
 
+extern "C" int chd_k_ntt_inv_cols(const chd_tables *t, const chd_limb_map *m,
+                                  uint32_t *dst, long long dst_pstride,
+                                  int num_limbs, int num_polys,
+                                  const uint32_t *cst, int centre,
+                                  void *stream) {
+  if (!t || !m || !dst || !cst || num_limbs < 0 || num_polys < 0)
+    return set_error(CHD_ERR_ARG, "chd_k_ntt_inv_cols: invalid argument");
+  if (num_limbs == 0 || num_polys == 0) return 0;
+  NttArgs a{};
+  a.src = dst;
+  a.dst = dst;
+  a.src_pstride = dst_pstride;
+  a.dst_pstride = dst_pstride;
+  a.map = *m;
+  a.map.src_gap = 0;
+  a.tab = *t;
+  a.cst = cst;
+  hipError_t e = launch_ntt_inv_cols(a, num_limbs, num_polys,
+                                     centre ? kEpiConstCentre : kEpiConst,
+                                     static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return set_error(CHD_ERR_HIP, std::string("chd_k_ntt_inv_cols: ") +
+                                      hipGetErrorString(e));
+  return 0;
+}
+
 extern "C" int chd_k_ntt_inv_mul(const chd_tables *t, const chd_limb_map *m,
                                  uint32_t *dst, long long dst_pstride,
                                  const uint32_t *src, const uint32_t *src_mul,
@@ -1436,6 +1481,10 @@ const char *keyacc_job_error(const chd_keyacc_args *a) {
     return "invalid argument";
   for (int g = 0; g < a->beta; g++)
     if (!a->kb[g] || !a->ka[g]) return "null key pointer";
+  if ((a->intt_b == nullptr) != (a->intt_a == nullptr) ||
+      (a->intt_b != nullptr &&
+       (a->intt_lo < 0 || a->intt_lo >= a->num_q + a->alpha)))
+    return "invalid INTT output";
   return nullptr;
 }
 }  // namespace

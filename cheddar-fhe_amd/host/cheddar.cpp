@@ -1021,10 +1021,26 @@ void ModSwitchHandler<uint32_t>::ModDownWorker(DvView<word> &dst,
 
 // ModDownWorker over num_polys polynomials with one launch per phase:
 // INTTForModDown (centre), BConv, NTTForModDown.
+bool ModSwitchHandler<uint32_t>::ModDownInttRange(Kind kind, int *first,
+                                                  int *count) const {
+  if (kind == Kind::Rescale || (kind != Kind::ModDown && level_ == 0))
+    return false;
+  const NPInfo np_src = param_.LevelToNP(level_, num_aux_);
+  const NPInfo np_dst =
+      param_.LevelToNP(kind == Kind::ModDown ? level_ : level_ - 1, 0);
+  const NPInfo np_non_intt(std::min(np_src.num_main_, np_dst.num_main_),
+                           std::min(np_src.num_ter_, np_dst.num_ter_), 0);
+  if (np_src.num_ter_ > np_non_intt.num_ter_) return false;  // ter limbs
+  *first = np_src.num_ter_ + np_non_intt.num_main_;
+  *count = np_src.GetNumTotal() - np_non_intt.GetNumTotal();
+  return true;
+}
+
 void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
                                               const word *src,
                                               long long src_pstride,
-                                              Kind kind) const {
+                                              Kind kind,
+                                              word *intt_rows) const {
   const int n = param_.degree_;
   const int num_polys = static_cast<int>(dst.size());
   AssertTrue(num_polys >= 1 && num_polys <= CHD_MAX_JOBS,
@@ -1046,7 +1062,8 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
              "ModDown: constant table mismatch");
   const long long ilen = static_cast<long long>(src_len) * n;
   Workspace::Use use_ws(ws_);
-  Scratch intt(ws_, static_cast<size_t>(num_polys) * ilen);
+  Scratch intt_buf(ws_, intt_rows ? 0 : static_cast<size_t>(num_polys) * ilen);
+  word *const intt = intt_rows ? intt_rows : intt_buf.data();
   for (int p = 0; p < num_polys; p++) {
     AssertTrue(dst[p] != nullptr, "ModDown: null destination");
     // INTTForModDown requires src != dst per polynomial
@@ -1074,14 +1091,20 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
     mi.tab_gap = param_.GetMaxNumMain() + np_non_intt.num_ter_;
     mi.src_gap = np_src.GetNumQ() - mi.num_q;
   }
-  K(chd_k_ntt_inv(&ntt_.Tables(), &mi, intt.data(), ilen, src + off,
-                  src_pstride, src_len, num_polys, st.const1.data(), 1,
-                  CurrentStream()));
+  if (intt_rows != nullptr) {
+    // the first pass was done by the key accumulation (ModDownInttRange)
+    AssertTrue(!intt_on_ter, "ModDown: fused INTT needs main INTT limbs");
+    K(chd_k_ntt_inv_cols(&ntt_.Tables(), &mi, intt, ilen, src_len, num_polys,
+                         st.const1.data(), 1, CurrentStream()));
+  } else {
+    K(chd_k_ntt_inv(&ntt_.Tables(), &mi, intt, ilen, src + off, src_pstride,
+                    src_len, num_polys, st.const1.data(), 1, CurrentStream()));
+  }
   chd_limb_map m = NoSkipMap(param_, np_dst);
   chd_bconv_job jobs[CHD_MAX_JOBS] = {};
   for (int p = 0; p < num_polys; p++) {
     jobs[p].dst = dst[p];
-    jobs[p].src = reinterpret_cast<const int32_t *>(intt.data()) + p * ilen;
+    jobs[p].src = reinterpret_cast<const int32_t *>(intt) + p * ilen;
     jobs[p].table = st.table.as<void>();
     jobs[p].src_len = src_len;
     jobs[p].dst_len = dst_len;
@@ -1212,6 +1235,35 @@ void Context<uint32_t>::KeyMultTensorV(int level, word *acc_b, word *acc_a,
   KeyAccumulate(level, acc_b, acc_a, nullptr, nullptr, nullptr, &a, &b, key);
 }
 
+// KeyAccumulate followed by ModDown (or ModDownAndRescale) into res, with
+// ModDown's first INTT pass done by the key accumulation when the INTT limbs
+// are contiguous (no terminal limb dropped); the accumulator limbs that the
+// INTT covers are then never stored.
+void Context<uint32_t>::KeySwitchDown(int level, CtRef res, const word *d,
+                                      const word *cb, const word *ca,
+                                      const CtCRef *ta, const CtCRef *tb,
+                                      const EvkRef &key, bool rescale) const {
+  const int n = param_.degree_;
+  const int num_q = param_.LevelToNP(level).GetNumQ();
+  const int total = num_q + param_.alpha_;
+  const auto kind = rescale ? ModSwitchHandler<word>::Kind::ModDownAndRescale
+                            : ModSwitchHandler<word>::Kind::ModDown;
+  const auto &ms = mod_switch_handlers_.at(level);
+  int first = 0, count = 0;
+  const bool fused = ms.ModDownInttRange(kind, &first, &count);
+  Workspace::Use use_ws(ws_.get());
+  Scratch acc(ws_.get(), static_cast<size_t>(2) * total * n);
+  Scratch rows(ws_.get(), fused ? static_cast<size_t>(2) * count * n : 0);
+  word *acc_b = acc.data();
+  word *acc_a = acc.data() + static_cast<size_t>(total) * n;
+  word *rows_b = fused ? rows.data() : nullptr;
+  word *rows_a = fused ? rows.data() + static_cast<size_t>(count) * n : nullptr;
+  KeyAccumulate(level, acc_b, acc_a, d, cb, ca, ta, tb, key, nullptr, rows_b,
+                rows_a, first);
+  ms.ModDownMulti({res.bx, res.ax}, acc_b, static_cast<long long>(total) * n,
+                  kind, rows_b);
+}
+
 void Context<uint32_t>::KeyMultExtV(int level, word *acc_b, word *acc_a,
                                     const word *d, const word *add_b,
                                     const EvkRef &key) const {
@@ -1223,7 +1275,8 @@ void Context<uint32_t>::KeyAccumulate(int level, word *acc_b, word *acc_a,
                                       const word *d, const word *cb,
                                       const word *ca, const CtCRef *ta,
                                       const CtCRef *tb, const EvkRef &key,
-                                      const word *add_b) const {
+                                      const word *add_b, word *intt_b,
+                                      word *intt_a, int intt_lo) const {
   const NPInfo a_np = param_.LevelToNP(level);
   const int n = param_.degree_;
   const int num_q = a_np.GetNumQ();
@@ -1273,6 +1326,9 @@ void Context<uint32_t>::KeyAccumulate(int level, word *acc_b, word *acc_a,
   k.acc_b = acc_b;
   k.acc_a = acc_a;
   k.add_b = add_b;
+  k.intt_b = intt_b;
+  k.intt_a = intt_a;
+  k.intt_lo = intt_lo;
   if (tensor) {
     k.d = nullptr;
     k.cb = nullptr;
@@ -1349,21 +1405,9 @@ void Context<uint32_t>::KeyMultExtBatchV(int level, int num,
 // src/core/Context.cpp:862-871 with 714-737 / 559-607
 void Context<uint32_t>::HMultV(int level, CtRef res, CtCRef a, CtCRef b,
                                const EvkRef &key, bool rescale) const {
-  const NPInfo np = param_.LevelToNP(level);
-  const int n = param_.degree_;
-  const int num_q = np.GetNumQ();
-  const int total = num_q + param_.alpha_;
-  Workspace::Use use_ws(ws_.get());
-  Scratch acc(ws_.get(), static_cast<size_t>(2) * total * n);
-  word *acc_b = acc.data();
-  word *acc_a = acc.data() + static_cast<size_t>(total) * n;
-  // Tensor fused into ModUp's INTT and the key accumulation
-  KeyMultTensorV(level, acc_b, acc_a, a, b, key);
   AssertTrue(!rescale || level > 0, "Not enough q primes to rescale");
-  mod_switch_handlers_.at(level).ModDownMulti(
-      {res.bx, res.ax}, acc_b, static_cast<long long>(total) * n,
-      rescale ? ModSwitchHandler<word>::Kind::ModDownAndRescale
-              : ModSwitchHandler<word>::Kind::ModDown);
+  // Tensor fused into ModUp's INTT and the key accumulation
+  KeySwitchDown(level, res, nullptr, nullptr, nullptr, &a, &b, key, rescale);
 }
 
 // src/core/Context.cpp:739-774
@@ -1385,17 +1429,7 @@ void Context<uint32_t>::RescaleV(int level, CtRef res, CtCRef a) const {
 // src/core/Context.cpp:584-607
 void Context<uint32_t>::MultKeyV(int level, CtRef res, CtCRef a,
                                  const EvkRef &key) const {
-  const int n = param_.degree_;
-  const int num_q = param_.LevelToNP(level).GetNumQ();
-  const int total = num_q + param_.alpha_;
-  Workspace::Use use_ws(ws_.get());
-  Scratch acc(ws_.get(), static_cast<size_t>(2) * total * n);
-  word *acc_b = acc.data();
-  word *acc_a = acc.data() + static_cast<size_t>(total) * n;
-  KeyMultNoModDownV(level, acc_b, acc_a, a.ax, a.bx, nullptr, key);
-  mod_switch_handlers_.at(level).ModDownMulti(
-      {res.bx, res.ax}, acc_b, static_cast<long long>(total) * n,
-      ModSwitchHandler<word>::Kind::ModDown);
+  KeySwitchDown(level, res, a.ax, a.bx, nullptr, nullptr, nullptr, key, false);
 }
 
 void Context<uint32_t>::PermuteV(int level, CtRef res, CtCRef a,

@@ -508,8 +508,17 @@ class ModSwitchHandler<uint32_t> {
   // ModDownWorker for several polynomials at once: polynomial p of the
   // source starts at src + p * src_pstride (words), its result goes to
   // dst[p] (separate buffers allowed).
+  // intt_rows: when given, the first pass of the INTT (stages 15..8) of the
+  // INTT limbs is already there ([polynomial][limb] of the INTT limbs, as
+  // the key accumulation leaves it), and only the second pass runs.
   void ModDownMulti(const std::vector<word *> &dst, const word *src,
-                    long long src_pstride, Kind kind) const;
+                    long long src_pstride, Kind kind,
+                    word *intt_rows = nullptr) const;
+  // The source limbs a ModDown / ModDownAndRescale of this level transforms
+  // back (its INTT limbs): [*first, *first + *count), contiguous. False when
+  // they include terminal limbs (then they are not contiguous) or for
+  // Rescale.
+  bool ModDownInttRange(Kind kind, int *first, int *count) const;
 
  private:
   struct SwitchTable {       // one source set -> destination set
@@ -696,7 +705,11 @@ class Context<uint32_t> {
   void KeyAccumulate(int level, word *acc_b, word *acc_a, const word *d,
                      const word *cb, const word *ca, const CtCRef *ta,
                      const CtCRef *tb, const EvkRef &key,
-                     const word *add_b = nullptr) const;
+                     const word *add_b = nullptr, word *intt_b = nullptr,
+                     word *intt_a = nullptr, int intt_lo = 0) const;
+  void KeySwitchDown(int level, CtRef res, const word *d, const word *cb,
+                     const word *ca, const CtCRef *ta, const CtCRef *tb,
+                     const EvkRef &key, bool rescale) const;
   DeviceVector<word> p_prod_;
   std::unique_ptr<Workspace> ws_;
   // EncodeConstant(1.0) at each level's default scale, for LevelDown

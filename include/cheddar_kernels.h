@@ -77,6 +77,14 @@ int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
                   long long src_pstride, int num_limbs, int num_polys,
                   const uint32_t *cst, int centre, void *stream);
 
+/* Second pass of chd_k_ntt_inv alone (stages 7..0 and the epilogue, in
+ * place on dst), for data whose first pass another kernel produced
+ * (chd_keyacc_args intt_b / intt_a). */
+int chd_k_ntt_inv_cols(const chd_tables *t, const chd_limb_map *m,
+                       uint32_t *dst, long long dst_pstride, int num_limbs,
+                       int num_polys, const uint32_t *cst, int centre,
+                       void *stream);
+
 /* chd_k_ntt_inv of the element-wise Montgomery product MontMul(src, src_mul)
  * (src_mul laid out like src). With src = a.ax, src_mul = b.ax this is the
  * Tensor's rx (ElementWise.cu:504-546) fed straight into ModUp's
@@ -172,6 +180,11 @@ typedef struct chd_keyacc_args {
   /* when set, added to acc_b on every limb (q and aux), unscaled: the
    * extended-basis b of a giant-step accumulator (Hoist.cu:940-957) */
   const uint32_t *add_b;
+  /* when set (both), limbs l >= intt_lo of the accumulators are not stored:
+   * the first pass of ModDown's INTT (stages 15..8, unreduced) goes to
+   * intt_{b,a} + (l - intt_lo) N instead, for chd_k_ntt_inv_cols to finish */
+  uint32_t *intt_b, *intt_a;
+  int intt_lo;
 } chd_keyacc_args;
 int chd_k_modup_keyacc(const chd_tables *t, const chd_keyacc_args *args,
                        void *stream);
