@@ -84,6 +84,22 @@ __device__ __forceinline__ uint32_t sub_mod(uint32_t a, uint32_t b,
   return d < e ? d : e;
 }
 
+// sum of up to four products of canonical residues (each < q^2 < 2^62, so
+// the sum fits 64 bits) times 2^-32 mod q, canonical: with T = hi 2^32 + lo,
+// T 2^-32 = hi + lo 2^-32 (mod q), where hi < 4 q^2 / 2^32 < 2q and the
+// Montgomery reduction of lo is in [0, q]. qn = -q^-1 mod 2^32.
+__device__ __forceinline__ uint32_t reduce_sum4(uint64_t t, uint32_t q,
+                                                uint32_t qn) {
+  const uint32_t lo = static_cast<uint32_t>(t);
+  uint32_t hi = static_cast<uint32_t>(t >> 32);
+  hi = hi < q ? hi : hi - q;                       // [0, q)
+  const uint32_t m = lo * qn;
+  const uint32_t r = static_cast<uint32_t>(
+      (static_cast<uint64_t>(m) * q + lo) >> 32);  // [0, q]
+  const uint32_t s = hi + r;                       // [0, 2q)
+  return s < q ? s : s - q;
+}
+
 // ModUp dnum groups sit on the chain's positions: a level missing `shift`
 // limbs of its first group owns limbs [lo, hi) in group g
 // (ModSwitch.cu:440-470 with prime_offset mod alpha)

@@ -364,22 +364,6 @@ __global__ __launch_bounds__(kThreads) void gs_fused_kernel(chd_tables t,
 }
 
 
-// sum of up to four products of canonical residues (each < q^2 < 2^62, so
-// the sum fits 64 bits) times 2^-32 mod q, canonical: with T = hi 2^32 + lo,
-// T 2^-32 = hi + lo 2^-32 (mod q), where hi < 4 q^2 / 2^32 < 2q and the
-// Montgomery reduction of lo is in [0, q]. qn = -q^-1 mod 2^32.
-__device__ __forceinline__ uint32_t reduce_sum4(uint64_t t, uint32_t q,
-                                                uint32_t qn) {
-  const uint32_t lo = static_cast<uint32_t>(t);
-  uint32_t hi = static_cast<uint32_t>(t >> 32);
-  hi = hi < q ? hi : hi - q;                       // [0, q)
-  const uint32_t m = lo * qn;
-  const uint32_t r = static_cast<uint32_t>(
-      (static_cast<uint64_t>(m) * q + lo) >> 32);  // [0, q]
-  const uint32_t s = hi + r;                       // [0, 2q)
-  return s < q ? s : s - q;
-}
-
 // Wide giant-step accumulation: the 4 waves of a workgroup share 256
 // coefficients of one limb (4 per lane, 16-byte loads) and each owns kGw of
 // the launch's 4 kGw giant steps, so a launch reads every baby step once

@@ -753,22 +753,53 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
   // the first group) instead of living in 30 registers across the loop
   const size_t loff = static_cast<size_t>(l) << kLogN;
   const size_t koff = loff + (aux ? a.key_gap : 0);
+  // The inner product and CAccum are sums of products of canonical residues
+  // (the reference adds MontMul results, Context.cpp:609-712). Here each
+  // product goes into a 64-bit sum with one v_mad_u64_u32; at most four
+  // products share a sum (< 4 q^2 < 2^64), which one Montgomery reduction
+  // folds into the canonical accumulators: the same residue,
+  // sum(a_i b_i) 2^-32 mod q.
+  const uint32_t qn = 0u - qinv;
+  uint64_t sb[16], sa[16];
   uint32_t accb[16], acca[16];
 #pragma unroll
-  for (int k = 0; k < 16; k++) accb[k] = acca[k] = 0;
+  for (int k = 0; k < 16; k++) {
+    sb[k] = sa[k] = 0;
+    accb[k] = acca[k] = 0;
+  }
+  int nprod = 0;        // products in sb / sa (uniform)
+  bool folded = false;  // accb / acca hold earlier products
+  auto fold = [&]() {
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const uint32_t rb = reduce_sum4(sb[k], q, qn);
+      const uint32_t ra = reduce_sum4(sa[k], q, qn);
+      accb[k] = folded ? add_mod(accb[k], rb, q) : rb;
+      acca[k] = folded ? add_mod(acca[k], ra, q) : ra;
+      sb[k] = sa[k] = 0;
+    }
+    folded = true;
+    nprod = 0;
+  };
   bool synced = false;
   for (int g = 0; g < a.beta; g++) {
     const int own_lo = group_lo(g, a.alpha, a.group_shift);
     const int own_hi = group_hi(g, a.alpha, a.group_shift, a.num_q);
+    const bool own = l >= own_lo && l < own_hi;
+    // this group adds the key product, and on a tensor-mode own limb the
+    // CAccum product as well
+    const int np = own && a.a1 != nullptr ? 2 : 1;
+    if (nprod + np > 4) fold();
+    nprod += np;
     uint32_t u[16];
-    if (l >= own_lo && l < own_hi) {
+    if (own) {
       // own limb: the input itself (ModSwitch.cu:466-470 copies it); in
       // tensor mode the input is rx = MontMul(a1, a2), and the CAccum of
       // this q limb (Context.cpp:684-699) is done here too, from the same
       // loads of the two ciphertexts: bx = MontMul(b1, b2),
       // ax = MontMul(b1 - q + a1, b2 - q + a2) - bx - rx (ElementWise.cu:504-546)
       if (a.a1 != nullptr) {
-        const int32_t pp = static_cast<int32_t>(a.p_prod[l]);
+        const uint64_t pp = a.p_prod[l];
 #pragma unroll
         for (int v = 0; v < 4; v++) {
           const uint4 vb1 = ld_at<uint4>(a.b1 + loff, cbase + 16u * v);
@@ -792,12 +823,8 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
             const uint32_t ax = sub_mod(
                 sub_mod(mont_mul(s1, s2, q, qi), bb, q), rr, q);
             u[4 * v + j] = rr;
-            accb[4 * v + j] = add_mod(
-                accb[4 * v + j], mont_mul(pp, static_cast<int32_t>(bb), q, qi),
-                q);
-            acca[4 * v + j] = add_mod(
-                acca[4 * v + j], mont_mul(pp, static_cast<int32_t>(ax), q, qi),
-                q);
+            sb[4 * v + j] += pp * bb;
+            sa[4 * v + j] += pp * ax;
           }
         }
       } else {
@@ -869,14 +896,32 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
       const uint32_t kav[4] = {ta.x, ta.y, ta.z, ta.w};
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const int32_t uv = static_cast<int32_t>(u[4 * v + j]);
-        accb[4 * v + j] = add_mod(
-            accb[4 * v + j], mont_mul(uv, static_cast<int32_t>(kbv[j]), q, qi), q);
-        acca[4 * v + j] = add_mod(
-            acca[4 * v + j], mont_mul(uv, static_cast<int32_t>(kav[j]), q, qi), q);
+        const uint64_t uv = u[4 * v + j];
+        sb[4 * v + j] += uv * kbv[j];
+        sa[4 * v + j] += uv * kav[j];
       }
     }
   }
+  if (!aux && a.a1 == nullptr && a.cb != nullptr) {
+    // CAccum (Context.cpp:684-699): acc += p_prod * ct (bx, and ax if given)
+    if (nprod + 1 > 4) fold();
+    nprod += 1;
+    const uint64_t pp = a.p_prod[l];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      uint4 tb = ld_at<uint4>(a.cb + loff, cbase + 16u * v);
+      const uint32_t cbv[4] = {tb.x, tb.y, tb.z, tb.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) sb[4 * v + j] += pp * cbv[j];
+      if (a.ca != nullptr) {
+        uint4 ta = ld_at<uint4>(a.ca + loff, cbase + 16u * v);
+        const uint32_t cav[4] = {ta.x, ta.y, ta.z, ta.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) sa[4 * v + j] += pp * cav[j];
+      }
+    }
+  }
+  fold();
   if (a.add_b != nullptr) {
     // extended-basis b of a giant-step accumulator, added on every limb
 #pragma unroll
@@ -885,27 +930,6 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
       const uint32_t tv[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
       for (int j = 0; j < 4; j++) accb[4 * v + j] = add_mod(accb[4 * v + j], tv[j], q);
-    }
-  }
-  if (!aux && a.a1 == nullptr && a.cb != nullptr) {
-    // CAccum (Context.cpp:684-699): acc += p_prod * ct (bx, and ax if given)
-    const int32_t pp = static_cast<int32_t>(a.p_prod[l]);
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      uint4 tb = ld_at<uint4>(a.cb + loff, cbase + 16u * v);
-      const uint32_t cbv[4] = {tb.x, tb.y, tb.z, tb.w};
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        accb[4 * v + j] = add_mod(
-            accb[4 * v + j], mont_mul(pp, static_cast<int32_t>(cbv[j]), q, qi), q);
-      if (a.ca != nullptr) {
-        uint4 ta = ld_at<uint4>(a.ca + loff, cbase + 16u * v);
-        const uint32_t cav[4] = {ta.x, ta.y, ta.z, ta.w};
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          acca[4 * v + j] = add_mod(
-              acca[4 * v + j], mont_mul(pp, static_cast<int32_t>(cav[j]), q, qi), q);
-      }
     }
   }
   (void)qs;
@@ -938,7 +962,9 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
 __global__ __launch_bounds__(256) void modup_keyacc(KeyAccBatch b) {
   __shared__ int32_t xch[kTileRows * kRowPad];
   const chd_keyacc_args &a = b.job[blockIdx.z];
-  const int l = blockIdx.y;
+  // limbs in reverse: the aux limbs, which carry a row pass per group and
+  // the INTT row passes, are dispatched first and do not form the tail
+  const int l = static_cast<int>(gridDim.y - 1 - blockIdx.y);
   const bool aux = l >= a.num_q;
   const int ti = a.tab_off + l + (aux ? a.tab_gap : 0);
   const uint32_t q = b.tab.q[ti];
