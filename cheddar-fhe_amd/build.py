@@ -28,24 +28,27 @@ COMMON = [
 DEVICE = ["-x", "hip", "--offload-arch=" + ARCH,
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
+# BConv's MFMA results go straight to VGPRs (no accumulator-register copies)
+MFMA_VGPR = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+
 SOURCES = [
-    ("csrc/ntt.hip", True),
-    ("csrc/bconv.hip", True),
-    ("csrc/elementwise.hip", True),
-    ("host/device_tables.cpp", False),
-    ("host/cheddar.cpp", False),
-    ("host/encoder.cpp", False),
-    ("host/param_json.cpp", False),
-    ("host/context_ops.cpp", False),
-    ("host/capi.cpp", False),
+    ("csrc/ntt.hip", True, []),
+    ("csrc/bconv.hip", True, MFMA_VGPR),
+    ("csrc/elementwise.hip", True, []),
+    ("host/device_tables.cpp", False, []),
+    ("host/cheddar.cpp", False, []),
+    ("host/encoder.cpp", False, []),
+    ("host/param_json.cpp", False, []),
+    ("host/context_ops.cpp", False, []),
+    ("host/capi.cpp", False, []),
 ]
 
 
-def compile_one(rel, device):
+def compile_one(rel, device, extra):
     src = os.path.join(PKG, rel)
     obj = os.path.join(OBJ_DIR, rel.replace("/", "_") + ".o")
     if device:
-        cmd = [HIPCC] + COMMON + DEVICE + ["-c", src, "-o", obj]
+        cmd = [HIPCC] + COMMON + DEVICE + extra + ["-c", src, "-o", obj]
     else:
         cmd = [HIPCC] + COMMON + ["-D__HIP_PLATFORM_AMD__", "-c", src, "-o",
                                   obj]

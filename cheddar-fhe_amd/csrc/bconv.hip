@@ -19,8 +19,11 @@
 //   dst[k][n]   = (acc_0 + 2^8 acc_1 + 2^16 acc_2 + 2^24 acc_3) mod p_k
 //
 // which is congruent to sum_i c_i U[k][i]. |acc_c| <= 64 * 128 * 128 = 2^20,
-// so the recombination (< 2^45) is exact in fp64 and one fp64 reduction gives
-// the canonical residue: bit-identical to the reference for every input.
+// so the planes pair up exactly in int32 (acc_0 + 2^8 acc_1 and
+// acc_2 + 2^8 acc_3, each below 2^30), one fp64 fma joins the pairs exactly
+// (< 2^47), and one fp64 reduction gives the canonical residue:
+// bit-identical to the reference for every input. The MFMA results are
+// kept in VGPRs (the build passes -amdgpu-mfma-vgpr-form for this file).
 //
 // One v_mfma_i32_16x16x64_i8 multiplies a 16-coefficient x 64 (sources x
 // bytes, zero-padded beyond 4 * src_len) tile by a 64 x 16-destination tile
@@ -134,10 +137,12 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
         uint32_t o[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          double y = __builtin_fma(static_cast<double>(d[3][i]), 16777216.0,
-                                   static_cast<double>(d[2][i]) * 65536.0);
-          y = __builtin_fma(static_cast<double>(d[1][i]), 256.0, y);
-          y += static_cast<double>(d[0][i]);
+          // pairs of planes in int32 (|acc_c| <= 2^21, so |lo|, |hi| < 2^30),
+          // then one exact fp64 fma: y = lo + 2^16 hi, |y| < 2^47
+          const int32_t lo = d[0][i] + d[1][i] * 256;
+          const int32_t hi = d[2][i] + d[3][i] * 256;
+          const double y = __builtin_fma(static_cast<double>(hi), 65536.0,
+                                         static_cast<double>(lo));
           o[i] = reduce_f64(y, p, pinv);
         }
         const int n = n_wave + mt * 16 + 4 * g;
