@@ -171,6 +171,13 @@ __device__ __forceinline__ void st_at(void *base, uint32_t byte_off, T v) {
 // loads: with many concurrent streams the hint evicts a half-used line before
 // the next instruction reads its other half (twice the traffic, measured).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// Wave-uniform read of a table no kernel writes (twiddles, constants): through
+// the constant address space it becomes a scalar load into an SGPR instead
+// of a vector load plus v_readfirstlane.
+typedef const __attribute__((address_space(4))) uint32_t cu32;
+__device__ __forceinline__ uint32_t ld_uniform(const uint32_t *p, int i) {
+  return ((cu32 *)p)[i];
+}
 template <typename T>
 __device__ __forceinline__ T ld_nt(const void *base, uint32_t byte_off) {
   const char *p = static_cast<const char *>(base) + byte_off;
@@ -303,7 +310,7 @@ __device__ __forceinline__ void fwd_cols_body(const NttArgs &a, const Limb &lb,
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
-      const uint32_t w = tw[(1 << s) + g];
+      const uint32_t w = ld_uniform(tw, (1 << s) + g);
       const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
@@ -685,7 +692,7 @@ __device__ __forceinline__ void inv_cols_body(const NttArgs &a, const Limb &lb,
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
-      const uint32_t w = tw[(1 << s) + g];
+      const uint32_t w = ld_uniform(tw, (1 << s) + g);
       const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
@@ -1008,13 +1015,21 @@ __device__ __forceinline__ void radix16_1p(const A &ar,
     const int h = 8 >> t;
 #pragma unroll
     for (int g = 0; g < (1 << t); g++) {
-      uint32_t w = tw[base[t] + g];
-      if (kUniform) w = __builtin_amdgcn_readfirstlane(w);
+      const uint32_t w = kUniform ? ld_uniform(tw, base[t] + g) : tw[base[t] + g];
       const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
     }
   }
+}
+
+// orders a wave's LDS writes before its later LDS reads of the same words
+// written by other lanes of that wave: a wave's LDS instructions execute in
+// program order, so only the compiler has to be kept from reordering them
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 template <int kEpi, bool kPre, bool kLazy>
@@ -1032,8 +1047,8 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const uint32_t w0 = tw[1];
-  const uint32_t w1 = tw[2 + (j >> 1)];
+  const uint32_t w0 = ld_uniform(tw, 1);
+  const uint32_t w1 = ld_uniform(tw, 2 + (j >> 1));
   T x[16];
   // ---- round 1: stages 0, 1 of quarter j (bits 15, 14), then 2..5
   if constexpr (kLazy) {
@@ -1042,7 +1057,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
     const uint32_t qn = ar.qn;
     const uint32_t w01 = mont_mad(w0, w1, w1 * qn, q);
     uint32_t c[4];
-    c[0] = tw[0];  // ToMont(1)
+    c[0] = ld_uniform(tw, 0);  // ToMont(1)
     c[1] = (j & 1) ? q - w1 : w1;
     c[2] = (j >> 1) ? q - w0 : w0;
     const uint32_t w01c = umin(w01, w01 - q);
@@ -1111,6 +1126,9 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
   for (int k = 0; k < 16; k++) xs[qidx((k << 10) | t)] = x[k];
   __syncthreads();
+  // From here on each wave reads and writes only its own 1024-element block
+  // (index bits 13..10 = wave), so the exchanges of rounds 3 and 4 need no
+  // workgroup barrier.
   // ---- round 2: stages 6..9 (bits 9..6); lane = bits 5..0, wave = 13..10
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = xs[qidx((wave << 10) | (k << 6) | lane)];
@@ -1122,7 +1140,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   }
 #pragma unroll
   for (int k = 0; k < 16; k++) xs[qidx((wave << 10) | (k << 6) | lane)] = x[k];
-  __syncthreads();
+  wave_lds_sync();
   // ---- round 3: stages 10..13 (bits 5..2); lane = bits 9..6 | bits 1..0
   const int b96 = lane >> 2, b10 = lane & 3;
 #pragma unroll
@@ -1137,7 +1155,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
   for (int k = 0; k < 16; k++)
     xs[qidx((wave << 10) | (b96 << 6) | (k << 2) | b10)] = x[k];
-  __syncthreads();
+  wave_lds_sync();
   // ---- round 4: stages 14, 15 (bits 1..0); lane = bits 7..2, wave =
   // bits 13..10, store round v = bits 9..8
   const int32_t qs = static_cast<int32_t>(q);
