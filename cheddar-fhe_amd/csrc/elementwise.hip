@@ -36,6 +36,13 @@ __device__ __forceinline__ LimbIdx limb_of(const chd_tables &t,
 __device__ __forceinline__ uint4 ld4(const uint32_t *p) {
   return *reinterpret_cast<const uint4 *>(p);
 }
+// streaming read of data used once (the giant steps' plaintexts): the hint
+// keeps it from evicting the baby steps the other waves still read
+__device__ __forceinline__ uint4 ld4_once(const uint32_t *p) {
+  typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+  const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 __device__ __forceinline__ void st4(uint32_t *p, uint4 v) {
   *reinterpret_cast<uint4 *>(p) = v;
 }
@@ -282,6 +289,7 @@ __global__ __launch_bounds__(kThreads) void bs_fused_kernel(chd_tables t,
     pb[3] = mont_mul(static_cast<int32_t>(v.w), pp, li.q, li.qinv);
   }
   const size_t koff = loff + (li.aux ? a.key_gap : 0);
+  const uint32_t qn = 0u - static_cast<uint32_t>(li.qinv);
   for (int k = 0; k < a.num_rot; k++) {
     uint32_t tb[4], ta[4];
 #pragma unroll
@@ -289,16 +297,26 @@ __global__ __launch_bounds__(kThreads) void bs_fused_kernel(chd_tables t,
       tb[i] = pb[i];
       ta[i] = 0;
     }
+    // key products of canonical residues summed in 64 bits, four at most
+    // per Montgomery reduction (the same residue as summing MontMuls);
+    // the key tiles are read once, with the streaming hint
+    uint64_t sb[4] = {0, 0, 0, 0}, sa[4] = {0, 0, 0, 0};
     for (int g = 0; g < a.beta; g++) {
-      const uint4 kb = ld4(a.kb[k][g] + koff + c0);
-      const uint4 ka = ld4(a.ka[k][g] + koff + c0);
+      const uint4 kb = ld4_once(a.kb[k][g] + koff + c0);
+      const uint4 ka = ld4_once(a.ka[k][g] + koff + c0);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int32_t uv = static_cast<int32_t>(u[g][i]);
-        tb[i] = add_mod(tb[i], mont_mul(uv, static_cast<int32_t>(get(kb, i)),
-                                        li.q, li.qinv), li.q);
-        ta[i] = add_mod(ta[i], mont_mul(uv, static_cast<int32_t>(get(ka, i)),
-                                        li.q, li.qinv), li.q);
+        const uint64_t uv = u[g][i];
+        sb[i] += uv * get(kb, i);
+        sa[i] += uv * get(ka, i);
+      }
+      if ((g & 3) == 3 || g == a.beta - 1) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          tb[i] = add_mod(tb[i], reduce_sum4(sb[i], li.q, qn), li.q);
+          ta[i] = add_mod(ta[i], reduce_sum4(sa[i], li.q, qn), li.q);
+          sb[i] = sa[i] = 0;
+        }
       }
     }
 #pragma unroll
@@ -411,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void gs_wide_kernel(chd_tables t,
     for (int g = 0; g < kGw; g++) {
       uint4 mv[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++) mv[j] = ld4(row[g * a.pt_stride + j] + o);
+      for (int j = 0; j < 4; j++) mv[j] = ld4_once(row[g * a.pt_stride + j] + o);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         uint64_t tb = 0, ta = 0;
