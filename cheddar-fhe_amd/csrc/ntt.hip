@@ -761,7 +761,8 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
   const size_t loff = static_cast<size_t>(l) << kLogN;
   const size_t koff = loff + (aux ? a.key_gap : 0);
   // The inner product and CAccum are sums of products of canonical residues
-  // (the reference adds MontMul results, Context.cpp:609-712). Here each
+  // (the reference adds MontMul results, CPAccum in ElementWise.cu:225-287,
+  // called from Context.cpp:609-712). Here each
   // product goes into a 64-bit sum with one v_mad_u64_u32; at most four
   // products share a sum (< 4 q^2 < 2^64), which one Montgomery reduction
   // folds into the canonical accumulators: the same residue,
