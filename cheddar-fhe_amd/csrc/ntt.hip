@@ -1337,6 +1337,19 @@ void limb_span(const uint32_t *base, long long pstride, int num_limbs,
 bool disjoint(uintptr_t alo, uintptr_t ahi, uintptr_t blo, uintptr_t bhi) {
   return ahi <= blo || bhi <= alo;
 }
+// the ModDown epilogue operand src2 of num_polys polynomials: limbs
+// [src2_lo, src2_hi) of the output read src2 limbs 0 .. src2_hi - src2_lo
+bool src2_disjoint(const uint32_t *src2, long long src2_pstride,
+                   int src2_lo, int src2_hi, int num_polys, uintptr_t dlo,
+                   uintptr_t dhi) {
+  if (src2 == nullptr || src2_hi <= src2_lo) return true;
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(src2);
+  const uintptr_t hi =
+      lo + 4ull * static_cast<unsigned long long>(
+                      (num_polys - 1) * std::max(src2_pstride, 0LL) +
+                      static_cast<long long>(src2_hi - src2_lo) * kN);
+  return disjoint(lo, hi, dlo, dhi);
+}
 }  // namespace
 
 extern "C" int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m,
@@ -1375,6 +1388,13 @@ extern "C" int chd_k_ntt_fwd_moddown(const chd_tables *t,
   if (!t || !m || !dst || !inv_prod || num_limbs < 0 ||
       (src2 == nullptr && src2_hi > src2_lo) || src2 == dst)
     return set_error(CHD_ERR_ARG, "chd_k_ntt_fwd_moddown: invalid argument");
+  {
+    uintptr_t dlo, dhi;
+    limb_span(dst, 0, num_limbs, 1, *m, false, &dlo, &dhi);
+    if (!src2_disjoint(src2, 0, src2_lo, src2_hi, 1, dlo, dhi))
+      return set_error(CHD_ERR_ARG,
+                       "chd_k_ntt_fwd_moddown: src2 overlaps the destination");
+  }
   NttArgs a{};
   a.src = dst;
   a.dst = dst;
@@ -1574,9 +1594,17 @@ extern "C" int chd_k_ntt_fwd_moddown_multi(
                      "chd_k_ntt_fwd_moddown_multi: invalid argument");
   NttArgs a{};
   for (int p = 0; p < num_polys; p++) {
-    if (!dst[p] || dst[p] == src2)
+    if (!dst[p])
       return set_error(CHD_ERR_ARG,
                        "chd_k_ntt_fwd_moddown_multi: invalid destination");
+    // every workgroup reads src2 while others write: no overlap at all
+    uintptr_t dlo, dhi;
+    limb_span(dst[p], 0, num_limbs, 1, *m, false, &dlo, &dhi);
+    if (!src2_disjoint(src2, src2_pstride, src2_lo, src2_hi, num_polys, dlo,
+                       dhi))
+      return set_error(CHD_ERR_ARG,
+                       "chd_k_ntt_fwd_moddown_multi: src2 overlaps a "
+                       "destination");
     a.dst_list[p] = dst[p];
   }
   a.src = dst[0];

@@ -6,6 +6,8 @@
 #include <numeric>
 #include <climits>
 #include <cmath>
+#include <exception>
+#include <thread>
 
 #include "cheddar_amd.h"
 #include "chd_device.h"
@@ -1616,11 +1618,13 @@ HoistHandler<uint32_t>::PtMap HoistHandler<uint32_t>::EncodeMap(
     int pt_level, double pt_scale, bool suppress_bs_swap) {
   AssertTrue(!hoist_map.empty(), "Hoist: hoist_map should not be empty");
   const int alpha = context.param_.alpha_;
-  PtMap out;
-  auto encode = [&](int g, int b, const Message &msg) {
-    Pt &pt = out[g].try_emplace(b, NPInfo(0, 0, 0)).first->second;
-    context.encoder_.Encode(pt, pt_level, pt_scale, msg, alpha);
+  const Encoder<word> &enc = context.encoder_;
+  struct Job {
+    int g, b;
+    const Message *msg;
+    Message rotated;
   };
+  std::vector<Job> jobs;
   if (hoist_map.size() == 1 && hoist_map.begin()->first == 0 &&
       !suppress_bs_swap) {
     // single giant step: baby step b becomes giant step b with baby step 0,
@@ -1630,11 +1634,45 @@ HoistHandler<uint32_t>::PtMap HoistHandler<uint32_t>::EncodeMap(
       AssertTrue(sz > 0, "Hoist: empty message");
       Message rot(sz);
       for (size_t i = 0; i < sz; i++) rot[(i + b) % sz] = msg[i];
-      encode(b, 0, rot);
+      jobs.push_back(Job{b, 0, nullptr, std::move(rot)});
     }
   } else {
     for (const auto &[g, bs_map] : hoist_map)
-      for (const auto &[b, msg] : bs_map) encode(g, b, msg);
+      for (const auto &[b, msg] : bs_map) jobs.push_back(Job{g, b, &msg, {}});
+  }
+  // the host halves (special IFFT and residues) of up to `width` plaintexts
+  // run on as many threads, then their uploads and NTTs in order
+  const size_t width = std::max<size_t>(
+      1, std::min<size_t>(16, std::thread::hardware_concurrency()));
+  PtMap out;
+  std::vector<std::vector<word>> mx(width);
+  std::vector<int> slots(width);
+  std::vector<std::exception_ptr> err(width);
+  for (size_t start = 0; start < jobs.size(); start += width) {
+    const size_t count = std::min(width, jobs.size() - start);
+    auto host_half = [&](size_t k) {
+      try {
+        const Job &j = jobs[start + k];
+        std::vector<Complex> padded =
+            Encoder<word>::PadToPowerOfTwo(j.msg ? *j.msg : j.rotated);
+        slots[k] = static_cast<int>(padded.size());
+        mx[k] = enc.CoefficientResidues(pt_level, pt_scale, std::move(padded),
+                                        alpha);
+      } catch (...) {
+        err[k] = std::current_exception();
+      }
+    };
+    std::vector<std::thread> threads;
+    for (size_t k = 1; k < count; k++) threads.emplace_back(host_half, k);
+    host_half(0);
+    for (std::thread &t : threads) t.join();
+    for (size_t k = 0; k < count; k++)
+      if (err[k]) std::rethrow_exception(err[k]);
+    for (size_t k = 0; k < count; k++) {
+      const Job &j = jobs[start + k];
+      Pt &pt = out[j.g].try_emplace(j.b, NPInfo(0, 0, 0)).first->second;
+      enc.EncodeResidues(pt, pt_level, pt_scale, slots[k], mx[k], alpha);
+    }
   }
   return out;
 }

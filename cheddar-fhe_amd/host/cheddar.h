@@ -41,6 +41,10 @@ struct Error : std::runtime_error {
 inline void AssertTrue(bool c, const std::string &msg) {
   if (!c) throw Error("ERROR: " + msg);
 }
+// literal messages: no string is built unless the check fails
+inline void AssertTrue(bool c, const char *msg) {
+  if (!c) throw Error(std::string("ERROR: ") + msg);
+}
 [[noreturn]] inline void Fail(const std::string &msg) {
   throw Error("ERROR: " + msg);
 }
@@ -585,6 +589,15 @@ class Encoder<uint32_t> {
   std::vector<word> CoefficientResidues(int level, double scale,
                                         std::vector<Complex> data,
                                         int num_aux = 0) const;
+  // Encode in two halves: the message zero-padded to a power of two slots,
+  // and the device half (upload of CoefficientResidues' output, NTT with
+  // Montgomery conversion). CoefficientResidues is const and reads only
+  // immutable tables, so several threads may run it at once.
+  static std::vector<Complex> PadToPowerOfTwo(
+      const std::vector<Complex> &message);
+  void EncodeResidues(Plaintext<word> &ptxt, int level, double scale,
+                      int slots, const std::vector<word> &mx,
+                      int num_aux = 0) const;
   void SpecialIFFT(std::vector<Complex> &data) const;
   void SpecialFFT(std::vector<Complex> &data) const;
 

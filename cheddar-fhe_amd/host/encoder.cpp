@@ -45,6 +45,10 @@ uint32_t Pow2Mod(int e, uint32_t p) {  // 2^e mod p, e >= 0
 uint32_t TruncMod(double x, uint32_t p) {
   AssertTrue(std::isfinite(x), "Encode: message value is not finite");
   const double t = std::trunc(x);
+  // |t| < p (almost every coefficient of an encoded message): no division
+  if (t >= 0.0 && t < static_cast<double>(p)) return static_cast<uint32_t>(t);
+  if (t < 0.0 && -t < static_cast<double>(p))
+    return p - static_cast<uint32_t>(-t);
   if (std::fabs(t) < 0x1p63) {
     int64_t r = static_cast<int64_t>(t) % static_cast<int64_t>(p);
     if (r < 0) r += p;
@@ -202,13 +206,32 @@ void Encoder<uint32_t>::Encode(Plaintext<word> &ptxt, int level, double scale,
                                const std::vector<Complex> &message,
                                int num_aux) const {
   AssertTrue(ntt_handler_ != nullptr, "Encode: host-only encoder");
-  const int len = static_cast<int>(message.size());
-  const int slots = 1 << Log2CeilInt(len);
-  std::vector<Complex> padded(slots);
-  std::copy(message.begin(), message.end(), padded.begin());
+  std::vector<Complex> padded = PadToPowerOfTwo(message);
+  const int slots = static_cast<int>(padded.size());
   const std::vector<word> mx =
       CoefficientResidues(level, scale, std::move(padded), num_aux);
+  EncodeResidues(ptxt, level, scale, slots, mx, num_aux);
+}
+
+std::vector<Complex> Encoder<uint32_t>::PadToPowerOfTwo(
+    const std::vector<Complex> &message) {
+  const int len = static_cast<int>(message.size());
+  std::vector<Complex> padded(static_cast<size_t>(1) << Log2CeilInt(len));
+  std::copy(message.begin(), message.end(), padded.begin());
+  return padded;
+}
+
+// the device half of Encode: upload the residues, NTT with Montgomery
+// conversion
+void Encoder<uint32_t>::EncodeResidues(Plaintext<word> &ptxt, int level,
+                                       double scale, int slots,
+                                       const std::vector<word> &mx,
+                                       int num_aux) const {
+  AssertTrue(ntt_handler_ != nullptr, "Encode: host-only encoder");
   const NPInfo np = param_.LevelToNP(level, num_aux);
+  AssertTrue(mx.size() == static_cast<size_t>(np.GetNumTotal()) *
+                              static_cast<size_t>(param_.degree_),
+             "Encode: residues do not match the level");
   Plaintext<word> out(np, param_.degree_);
   HipCheck(hipMemcpyAsync(out.mx_.data(), mx.data(), mx.size() * sizeof(word),
                           hipMemcpyHostToDevice, CurrentStream()),
@@ -217,7 +240,7 @@ void Encoder<uint32_t>::Encode(Plaintext<word> &ptxt, int level, double scale,
   const int aux_words = num_aux * param_.degree_;
   DvView<word> v = out.mx_.View(aux_words);
   ntt_handler_->NTT(v, np, out.mx_.ConstView(aux_words), true);
-  // mx is this call's host memory: the copy has to finish before it goes
+  // mx is the caller's host memory: the copy has to finish before it goes
   HipCheck(hipStreamSynchronize(CurrentStream()), "hipStreamSynchronize");
   out.SetNumSlots(slots);
   out.SetScale(scale);

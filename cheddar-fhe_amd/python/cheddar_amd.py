@@ -7,6 +7,7 @@ loudly if the HIP library has not been built.
 """
 import ctypes
 import os
+import weakref
 
 import numpy as np
 
@@ -124,6 +125,14 @@ def ptr_array(ts):
     return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
 
 
+def _own(obj, h, destroy):
+    """obj takes ownership of handle h: destroy(h) runs once, when obj is
+    collected or at interpreter exit (bound now, so it never depends on
+    module globals that exit may already have cleared)"""
+    obj.h = h
+    obj._finalizer = weakref.finalize(obj, destroy, h)
+
+
 def current_stream():
     import torch
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -138,12 +147,8 @@ class NttPlan:
         _check(lib.chd_ntt_plan_create(ctypes.byref(h), log_n,
                                        _u32_array(self.primes),
                                        len(self.primes)))
-        self.h = h
+        _own(self, h, lib.chd_ntt_plan_destroy)
 
-    def __del__(self):
-        if getattr(self, "h", None):
-            lib.chd_ntt_plan_destroy(self.h)
-            self.h = None
 
     def forward(self, dst, src, num_limbs, num_polys=1, mont_conv=False,
                 stream=None):
@@ -170,12 +175,8 @@ class BconvPlan:
         _check(lib.chd_bconv_plan_create(ctypes.byref(h), log_n,
                                          _u32_array(self.src), len(self.src),
                                          _u32_array(self.dst), len(self.dst)))
-        self.h = h
+        _own(self, h, lib.chd_bconv_plan_destroy)
 
-    def __del__(self):
-        if getattr(self, "h", None):
-            lib.chd_bconv_plan_destroy(self.h)
-            self.h = None
 
     def constants(self):
         import numpy as np
@@ -204,7 +205,7 @@ class Param:
             (ctypes.c_int * len(lc))(*lc), len(level_config),
             _u32_array(main_primes), len(main_primes),
             _u32_array(aux_primes), len(aux_primes), None, 0))
-        self.h = h
+        _own(self, h, lib.chd_param_destroy)
         self.main = [int(p) for p in main_primes]
         self.aux = [int(p) for p in aux_primes]
         self.alpha = lib.chd_param_alpha(h)
@@ -218,7 +219,7 @@ class Param:
         self = cls.__new__(cls)
         h = ctypes.c_void_p()
         _check(lib.chd_param_create_json(ctypes.byref(h), text.encode()))
-        self.h = h
+        _own(self, h, lib.chd_param_destroy)
         d = json.loads(text)
         self.main = [int(p) for p in d["main_primes"]]
         self.ter = [int(p) for p in d.get("terminal_primes", [])]
@@ -232,21 +233,25 @@ class Param:
     def num_q(self, level):
         return lib.chd_param_num_q(self.h, level)
 
-    def encode_coefficients(self, level, num_aux, scale, msg, log_n=LOG_N):
+    def encode_coefficients(self, level, num_aux, scale, msg, log_n=LOG_N,
+                            out=None):
         """host half of the encoder: (residues [limbs][N] before the NTT,
-        padded slot count)"""
+        padded slot count); out: an optional uint32 buffer of that size"""
         re, im = _split(msg)
-        out = np.zeros((self.num_q(level) + num_aux) << log_n, np.uint32)
+        words = (self.num_q(level) + num_aux) << log_n
+        if out is None:
+            out = np.zeros(words, np.uint32)
+        elif (out.dtype != np.uint32 or out.size != words or
+              not out.flags["C_CONTIGUOUS"]):
+            raise ValueError("encode_coefficients: out must be a contiguous "
+                             "uint32 array of %d words" % words)
+        out = out.reshape(-1)
         slots = lib.chd_encode_coefficients(self.h, level, num_aux, scale, re,
                                             im, re.size, out)
         if slots < 0:
             _check(slots)
         return out.reshape(-1, 1 << log_n), slots
 
-    def __del__(self):
-        if getattr(self, "h", None):
-            lib.chd_param_destroy(self.h)
-            self.h = None
 
 
 class Context:
@@ -254,12 +259,8 @@ class Context:
         self.param = param
         h = ctypes.c_void_p()
         _check(lib.chd_context_create(ctypes.byref(h), param.h))
-        self.h = h
+        _own(self, h, lib.chd_context_destroy)
 
-    def __del__(self):
-        if getattr(self, "h", None):
-            lib.chd_context_destroy(self.h)
-            self.h = None
 
     def beta(self, level):
         return lib.chd_context_beta(self.h, level)
@@ -398,7 +399,7 @@ class Hoist:
             (ctypes.c_int * len(gs))(*gs), len(bs),
             (ctypes.c_int * len(bs))(*bs), parr,
             stream if stream is not None else current_stream()))
-        self.h = h
+        _own(self, h, lib.chd_hoist_destroy)
 
     @classmethod
     def from_messages(cls, ctx, level, pt_scale, gs, bs, msgs,
@@ -423,13 +424,9 @@ class Hoist:
             (ctypes.c_int * len(bs))(*bs), re, im, ln,
             1 if suppress_bs_swap else 0,
             stream if stream is not None else current_stream()))
-        self.h = h
+        _own(self, h, lib.chd_hoist_destroy)
         return self
 
-    def __del__(self):
-        if getattr(self, "h", None):
-            lib.chd_hoist_destroy(self.h)
-            self.h = None
 
     @classmethod
     def linear_transform(cls, ctx, level, pt_scale, dim, diags, bs, gs=1,
@@ -449,7 +446,7 @@ class Hoist:
             (ctypes.c_int * len(idx))(*idx), re, im, bs, gs, pre_rotation,
             additional_pt_rot,
             stream if stream is not None else current_stream()))
-        self.h = h
+        _own(self, h, lib.chd_hoist_destroy)
         return self
 
     def required_rotations(self, min_ks=False):

@@ -631,6 +631,7 @@ void orc_paccum(uint32_t *acc_b, uint32_t *acc_a, const uint32_t *modup,
   size_t n = (size_t)1 << log_n;
   int total = L + alpha;
   size_t key_stride = (size_t)(max_q + alpha) * n;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
   for (int l = 0; l < total; l++) {
     uint32_t q = primes[l];
     uint64_t ri = r_inv(q);
@@ -692,6 +693,23 @@ void orc_caccum(uint32_t *acc, const uint32_t *ct, const uint32_t *p_prod,
   }
 }
 
+/* GSFusedKernel (Hoist.cu:80-118): the giant-step accumulator gains
+ * MontMul(plaintext, baby step) per (giant, baby) pair, canonical sums */
+void orc_pmult_accum(uint32_t *acc, const uint32_t *pt, const uint32_t *x,
+                     int num_limbs, const uint32_t *primes, int log_n) {
+  size_t n = (size_t)1 << log_n;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+  for (int l = 0; l < num_limbs; l++) {
+    uint32_t q = primes[l];
+    uint64_t ri = r_inv(q);
+    for (size_t c = 0; c < n; c++) {
+      size_t i = (size_t)l * n + c;
+      uint64_t m = (uint64_t)pt[i] * x[i] % q * ri % q;
+      acc[i] = (uint32_t)((acc[i] + m) % q);
+    }
+  }
+}
+
 void orc_p_prod(uint32_t *p_prod, const uint32_t *q_primes, int L,
                 const uint32_t *p_primes, int alpha) {
   for (int l = 0; l < L; l++) {
@@ -706,6 +724,7 @@ void orc_permute(uint32_t *dst, const uint32_t *src, int num_limbs, int log_n,
                  uint32_t galois) {
   size_t n = (size_t)1 << log_n;
   uint32_t mask = (uint32_t)(2 * n - 1);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
   for (int l = 0; l < num_limbs; l++) {
     for (size_t x = 0; x < n; x++) {
       uint32_t e = orc_bitrev((uint32_t)x, log_n + 1) + 1;

@@ -130,6 +130,11 @@ void orc_paccum_ex(uint32_t *acc_b, uint32_t *acc_a, const uint32_t *modup,
 /* acc[l] += MontMul(p_prod[l], ct[l]) for l < L */
 void orc_caccum(uint32_t *acc, const uint32_t *ct, const uint32_t *p_prod,
                 int L, const uint32_t *primes, int log_n);
+/* acc[l] = (acc[l] + MontMul(pt[l], x[l])) mod q_l over num_limbs limbs:
+ * one term of the giant-step plaintext accumulation (GSFusedKernel,
+ * Hoist.cu:80-118); threaded over limbs (orc_set_threads) */
+void orc_pmult_accum(uint32_t *acc, const uint32_t *pt, const uint32_t *x,
+                     int num_limbs, const uint32_t *primes, int log_n);
 /* p_prod[l] = ToMont(prod(P) mod q_l) (Context.cpp:85-98) */
 void orc_p_prod(uint32_t *p_prod, const uint32_t *q_primes, int L,
                 const uint32_t *p_primes, int alpha);

@@ -59,6 +59,7 @@ def _load():
         "orc_paccum": (None, [_u32p, _u32p, _u32p, _int, _u32p, _u32p, _int,
                               _int, _int, _u32p, _int]),
         "orc_caccum": (None, [_u32p, _u32p, _u32p, _int, _u32p, _int]),
+        "orc_pmult_accum": (None, [_u32p, _u32p, _u32p, _int, _u32p, _int]),
         "orc_p_prod": (None, [_u32p, _u32p, _int, _u32p, _int]),
         "orc_permute": (None, [_u32p, _u32p, _int, _int, _u32]),
         "orc_galois_factor": (_u32, [_int, _int]),
@@ -210,6 +211,13 @@ def permute(src, log_n, galois):
     dst = np.zeros_like(src)
     lib.orc_permute(dst, src, src.size >> log_n, log_n, galois)
     return dst
+
+
+def pmult_accum(acc, pt, x, primes, log_n):
+    """acc += MontMul(pt, x) limb by limb, in place (acc: uint32 C array)"""
+    assert acc.dtype == np.uint32 and acc.flags["C_CONTIGUOUS"]
+    lib.orc_pmult_accum(acc, u32(pt), u32(x), len(primes), u32(primes), log_n)
+    return acc
 
 
 def p_prod(q_primes, p_primes):

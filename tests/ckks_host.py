@@ -37,10 +37,16 @@ def crt_centre(residues, primes):
 
 def to_ntt_mont(coeffs, primes, log_n):
     """integer coefficient vector (Python ints or int64) -> NTT(x R) limbs"""
-    coeffs = [int(v) for v in coeffs]
     limbs = np.zeros((len(primes), 1 << log_n), np.uint32)
-    for i, p in enumerate(primes):
-        limbs[i] = np.array([v % p for v in coeffs], dtype=np.uint32)
+    c = np.asarray(coeffs)
+    if c.dtype.kind in "iu":
+        c = c.astype(np.int64)
+        for i, p in enumerate(primes):
+            limbs[i] = np.mod(c, p).astype(np.uint32)
+    else:
+        coeffs = [int(v) for v in coeffs]
+        for i, p in enumerate(primes):
+            limbs[i] = np.array([v % p for v in coeffs], dtype=np.uint32)
     return _orc.ntt_batch(limbs.reshape(-1), log_n, primes, mont=1).reshape(
         len(primes), -1)
 
@@ -91,12 +97,16 @@ class Keys:
             out[i] = ((p - a[i].astype(np.uint64)) % p).astype(np.uint32)
         return out
 
-    def uniform(self, primes):
-        return np.stack([self.rng.integers(0, p, self.n, dtype=np.uint64)
-                         .astype(np.uint32) for p in primes])
+    def uniform(self, primes, rng=None):
+        rng = self.rng if rng is None else rng
+        out = np.empty((len(primes), self.n), np.uint32)
+        for i, p in enumerate(primes):
+            out[i] = rng.integers(0, p, self.n, dtype=np.uint64)
+        return out
 
-    def small(self, bound=4):
-        return self.rng.integers(-bound, bound + 1, self.n)
+    def small(self, bound=4, rng=None):
+        rng = self.rng if rng is None else rng
+        return rng.integers(-bound, bound + 1, self.n)
 
     def encrypt(self, m, L):
         """(b, a) over q_0..q_{L-1} with b = -a s + m + e"""
@@ -112,33 +122,42 @@ class Keys:
         v = self._add(b, self._mul(a, self.s_ntt[:L], primes), primes)
         return from_ntt_mont(v, primes, self.log_n)
 
-    def switch_key(self, s_new, max_q, s_enc=None):
+    def switch_key(self, s_new, max_q, s_enc=None, rng=None):
         """evk for target secret s_new (coefficients) encrypted under s_enc
         (default s), beta groups of (max_q + alpha) limbs;
-        bx_g = -a_g s_enc + e_g + P s_new on group g (UserInterface.cu:366)."""
+        bx_g = -a_g s_enc + e_g + P s_new on group g (UserInterface.cu:366).
+        Vectorised over all limbs of a group (one modulus per row); rng
+        (default: the secret's generator) draws a and the errors."""
         alpha = len(self.p)
         primes = self.q[:max_q] + self.p
         beta = (max_q + alpha - 1) // alpha
-        if s_enc is None:
-            s_cur = np.concatenate([self.s_ntt[:max_q],
-                                    self.s_ntt[len(self.q):]])
-        else:
-            s_cur = self.ntt_of(s_enc, primes)
-        t = self.ntt_of(s_new, primes)
+        total = len(primes)
+        own = np.concatenate([self.s_ntt[:max_q], self.s_ntt[len(self.q):]])
+        s_cur = own if s_enc is None else self.ntt_of(s_enc, primes)
+        t = own if s_new is self.s else self.ntt_of(s_new, primes)
+        pc = np.array(primes, np.uint64)[:, None]
+        r_inv = np.array([pow(R, -1, p) for p in primes], np.uint64)[:, None]
         P = 1
         for p in self.p:
             P *= p
+        p_mod = np.array([P % p for p in primes], np.uint64)[:, None]
+        # errors of every group in one batched NTT
+        e = np.zeros((beta, total, self.n), np.uint32)
+        for g in range(beta):
+            c = self.small(rng=rng).astype(np.int64)
+            e[g] = np.mod(c[None, :], pc.astype(np.int64)).astype(np.uint32)
+        e = _orc.ntt_batch(e.reshape(-1), self.log_n, primes * beta,
+                           mont=1).reshape(beta, total, self.n)
+        s64 = s_cur.astype(np.uint64)
+        pt = t.astype(np.uint64) * p_mod % pc  # MontMul(t, ToMont(P mod q))
         kb, ka = [], []
         for g in range(beta):
-            a = self.uniform(primes)
-            b = self._add(self._neg(self._mul(a, s_cur, primes), primes),
-                          self.ntt_of(self.small(), primes), primes)
-            for i in range(g * alpha, min((g + 1) * alpha, max_q)):
-                q = primes[i]
-                pm = (P % q) * R % q  # ToMont(P mod q)
-                add = mont_mul_vec(t[i], np.full(self.n, pm, np.uint32), q)
-                b[i] = ((b[i].astype(np.uint64) + add) % q).astype(np.uint32)
-            kb.append(b)
+            a = self.uniform(primes, rng)
+            a_s = (a.astype(np.uint64) * s64 % pc) * r_inv % pc
+            b = (e[g].astype(np.uint64) + pc - a_s) % pc
+            lo, hi = g * alpha, min((g + 1) * alpha, max_q)
+            b[lo:hi] = (b[lo:hi] + pt[lo:hi]) % pc[lo:hi]
+            kb.append(b.astype(np.uint32))
             ka.append(a)
         return np.stack(kb), np.stack(ka)
 
@@ -146,12 +165,12 @@ class Keys:
         s2 = negacyclic_mul(self.s, self.s)
         return self.switch_key(s2, max_q)
 
-    def rot_key(self, galois, max_q):
+    def rot_key(self, galois, max_q, rng=None):
         """HRot key-switches first and permutes after (Context.cpp:776-791),
         so the key encrypts s under s(X^(g^-1)) (UserInterface.cu:279-306)"""
         g_inv = pow(galois, -1, 2 * self.n)
         return self.switch_key(self.s, max_q,
-                               s_enc=automorphism(self.s, g_inv))
+                               s_enc=automorphism(self.s, g_inv), rng=rng)
 
 
 def negacyclic_mul(a, b):
@@ -166,13 +185,15 @@ def negacyclic_mul(a, b):
 
 
 def automorphism(a, g):
-    """coefficients of a(X^g) mod X^N + 1"""
+    """coefficients of a(X^g) mod X^N + 1 (g odd: j -> j g mod N is a
+    permutation, so every output coefficient receives exactly one term)"""
+    a = np.asarray(a)
+    if a.dtype.kind in "iu":
+        a = a.astype(np.int64)
     n = len(a)
-    out = np.zeros(n, dtype=object)
-    for j, v in enumerate(np.asarray(a, dtype=object)):
-        e = (j * g) % (2 * n)
-        if e >= n:
-            out[e - n] -= v
-        else:
-            out[e] += v
+    assert g % 2 == 1
+    e = (np.arange(n, dtype=np.int64) * g) % (2 * n)
+    neg = e >= n
+    out = np.zeros(n, dtype=np.int64 if a.dtype.kind == "i" else object)
+    out[np.where(neg, e - n, e)] = np.where(neg, -a, a)
     return out

@@ -72,7 +72,9 @@ def baby_step(ct_b, ct_a, key, rot, L, max_q, q_primes, p_primes, log_n,
 def evaluate(ct_b, ct_a, pts, keys, L, max_q, q_primes, p_primes, log_n):
     """res = ModDownAndRescale(sum_g Rot_g(sum_b pt[g, b] * bs[b])) with the
     giant steps' double hoisting. pts: {(g, b): L + alpha limbs}; keys:
-    {rot: (key_b, key_a)}. Returns (res_b, res_a) of L - 1 limbs."""
+    {rot: (key_b, key_a)} (any mappings: each plaintext is read once, each
+    key's pair used before the next key is looked up). Returns (res_b,
+    res_a) of L - 1 limbs."""
     q = list(q_primes[:L])
     p = list(p_primes)
     primes = q + p
@@ -89,8 +91,9 @@ def evaluate(ct_b, ct_a, pts, keys, L, max_q, q_primes, p_primes, log_n):
         for b in bs_idx:
             if (g, b) not in pts:
                 continue
-            ab = _add(ab, _mul(pts[(g, b)], bs[b][0], primes), primes)
-            aa = _add(aa, _mul(pts[(g, b)], bs[b][1], primes), primes)
+            pt = pts[(g, b)]
+            _orc.pmult_accum(ab, pt, bs[b][0], primes, log_n)
+            _orc.pmult_accum(aa, pt, bs[b][1], primes, log_n)
         acc[g] = (ab, aa)
     fb = acc[0][0] if 0 in acc else np.zeros((L + len(p), n), np.uint32)
     fa = acc[0][1] if 0 in acc else np.zeros((L + len(p), n), np.uint32)

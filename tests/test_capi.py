@@ -117,6 +117,9 @@ def _kernel_lib(chd):
         ctypes.POINTER(Tables), ctypes.POINTER(LimbMap), ctypes.POINTER(P),
         ctypes.c_int, ctypes.c_int, P, ctypes.c_longlong, P,
         ctypes.c_longlong, ctypes.c_int, ctypes.c_int, P, P, P]
+    lib.chd_k_ntt_fwd_moddown.argtypes = [
+        ctypes.POINTER(Tables), ctypes.POINTER(LimbMap), P, ctypes.c_int, P,
+        ctypes.c_int, ctypes.c_int, P, P, P]
     return lib
 
 
@@ -161,3 +164,47 @@ def test_moddown_ntt_rejects_overlapping_source(chd):
                                          0, 0, 0, FAKE, None, None)
     assert st == -1
     assert b"overlaps" in chd.lib.chd_last_error()
+
+
+def test_moddown_ntt_rejects_overlapping_src2(chd):
+    """the epilogue operand src2 may not overlap any destination, also when
+    it starts between two destination limbs rather than on one"""
+    lib = _kernel_lib(chd)
+    t, m = Tables(), LimbMap(num_q=20, skip_lo=1 << 30)
+    n = 1 << 16
+    base = 0x10000000
+    dst = (P * 2)(P(base), P(base + 40 * 4 * n))
+    src = P(base + 100 * 4 * n)            # disjoint from both
+    for src2 in (P(base + 45 * 4 * n),     # inside dst[1]
+                 P(base + 39 * 4 * n)):    # runs from dst[0]'s gap into dst[1]
+        st = lib.chd_k_ntt_fwd_moddown_multi(t, m, dst, 2, 20, src, 20 * n,
+                                             src2, 20 * n, 0, 20, FAKE, None,
+                                             None)
+        assert st == -1
+        assert b"src2 overlaps" in chd.lib.chd_last_error()
+    st = lib.chd_k_ntt_fwd_moddown(t, m, P(base), 20, P(base + 19 * 4 * n),
+                                   0, 20, FAKE, None, None)
+    assert st == -1
+    assert b"src2 overlaps" in chd.lib.chd_last_error()
+
+
+def test_binding_handles_released_cleanly_at_exit():
+    """handles still alive at interpreter exit are destroyed through the
+    function bound when they were made, not through module globals that
+    exit has already cleared: nothing is printed to stderr"""
+    import subprocess
+    import sys
+    code = (
+        "import sys\n"
+        "sys.path.insert(0, %r)\n"
+        "sys.path.insert(0, %r)\n"
+        "import cheddar_amd\n"
+        "from gpu_util import config4\n"
+        "main, aux, levels = config4()\n"
+        "keep = [cheddar_amd.Param(main, aux, levels) for _ in range(3)]\n"
+        % (os.path.join(ROOT, "cheddar-fhe_amd", "python"),
+           os.path.join(ROOT, "tests")))
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    assert res.stderr.strip() == "", res.stderr

@@ -373,6 +373,35 @@ def test_paccum_caccum_direct_sum():
     assert np.array_equal(acc_b[L:], before[L:])
 
 
+def test_pmult_accum_direct_sum():
+    """the giant-step plaintext accumulation: acc = sum_b pt_b x_b R^-1 mod p
+    with Python integers, including the residues 0 and p - 1, and the same
+    result with threads"""
+    log_n = 7
+    primes = Q30[:3] + Q31[:2]
+    n = 1 << log_n
+    r = rng(65)
+    terms = [(np.stack([uniform(r, p, n) for p in primes]),
+              np.stack([uniform(r, p, n) for p in primes])) for _ in range(5)]
+    for l, p in enumerate(primes):  # extreme residues in the first columns
+        terms[0][0][l, :2] = (0, p - 1)
+        terms[0][1][l, :2] = (p - 1, p - 1)
+    outs = []
+    for threads in (1, 4):
+        _orc.lib.orc_set_threads(threads)
+        acc = np.zeros((len(primes), n), np.uint32)
+        for pt, x in terms:
+            _orc.pmult_accum(acc, pt, x, primes, log_n)
+        outs.append(acc)
+    _orc.lib.orc_set_threads(1)
+    for l, p in enumerate(primes):
+        want = sum(pt[l].astype(object) * x[l].astype(object)
+                   for pt, x in terms)
+        assert outs[0][l].tolist() == [int(v) * pow(R, -1, p) % p
+                                       for v in want]
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_permute_composition_and_coefficient_map():
     log_n = 8
     q = Q30[5]
