@@ -35,6 +35,7 @@ SOURCES = [
     ("csrc/ntt.hip", True, []),
     ("csrc/bconv.hip", True, MFMA_VGPR),
     ("csrc/elementwise.hip", True, []),
+    ("csrc/hmult_noalloc.hip", True, []),
     ("host/device_tables.cpp", False, []),
     ("host/cheddar.cpp", False, []),
     ("host/encoder.cpp", False, []),

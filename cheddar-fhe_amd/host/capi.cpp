@@ -8,6 +8,7 @@
 #include <vector>
 
 #include "cheddar.h"
+#include "capi_internal.h"
 #include "cheddar_amd.h"
 #include "kernel_common.h"
 #include "prime_math.h"
@@ -33,6 +34,8 @@ int check_launch(const char *where) {
 using cheddar::Context;
 using cheddar::Parameter;
 using chd::set_error;
+using chd_capi::LevelOk;
+using chd_capi::MakeEvk;
 using word = uint32_t;
 
 struct chd_ntt_plan {
@@ -47,20 +50,6 @@ struct chd_bconv_plan {
   int src_len = 0, dst_len = 0;
 };
 
-struct chd_param {
-  std::unique_ptr<Parameter<word>> p;
-};
-
-struct chd_context {
-  std::shared_ptr<Context<word>> c;
-};
-
-#define CHD_TRY try {
-#define CHD_CATCH(name)                                            \
-  }                                                                \
-  catch (const std::exception &e) {                                \
-    return set_error(CHD_ERR_STATE, std::string(name ": ") + e.what()); \
-  }
 
 extern "C" const char *chd_last_error(void) { return g_err.c_str(); }
 extern "C" const char *chd_version(void) { return "cheddar-amd 0.1 gfx950"; }
@@ -265,33 +254,6 @@ extern "C" int chd_context_beta(const chd_context *ctx, int level) {
   if (!ctx || level < 0 || level > ctx->c->param_.max_level_) return -1;
   return ctx->c->mod_switch_handlers_.at(level).GetBeta();
 }
-
-namespace {
-bool LevelOk(const chd_context *ctx, int level) {
-  return ctx && level >= 0 && level <= ctx->c->param_.max_level_;
-}
-
-Context<word>::EvkRef MakeEvk(const chd_context *ctx,
-                              const uint32_t *const *bx,
-                              const uint32_t *const *ax, int beta) {
-  const auto &p = ctx->c->param_;
-  Context<word>::EvkRef r;
-  r.np = cheddar::NPInfo(p.GetMaxNumMain(), p.GetMaxNumTer(), p.alpha_);
-  for (int g = 0; g < beta; g++) {
-    if (!bx[g] || !ax[g]) throw cheddar::Error("null evaluation-key pointer");
-    r.bx.push_back(bx[g]);
-    r.ax.push_back(ax[g]);
-  }
-  return r;
-}
-}  // namespace
-
-#define CHD_CALL(name, cond, ...)                                       \
-  if (!(cond)) return set_error(CHD_ERR_ARG, name ": invalid argument"); \
-  CHD_TRY cheddar::StreamScope scope(static_cast<hipStream_t>(stream));  \
-  __VA_ARGS__;                                                          \
-  return chd::check_launch(name);                                       \
-  CHD_CATCH(name)
 
 extern "C" int chd_tensor(const chd_context *ctx, int level, uint32_t *res_bx,
                           uint32_t *res_ax, uint32_t *res_rx,

@@ -41,6 +41,7 @@ StreamScope::~StreamScope() { g_stream = prev_; }
 
 Workspace::Workspace(size_t words) {
   buf_.Resize(words * sizeof(uint32_t));
+  base_ = buf_.as<uint32_t>();
   cap_ = words;
   HipCheck(hipEventCreateWithFlags(&done_, hipEventDisableTiming),
            "hipEventCreateWithFlags");
@@ -85,17 +86,33 @@ Workspace::Use::~Use() {
   if (ws_ != nullptr) ws_->Leave();
 }
 
+Workspace::External::External(Workspace *ws, uint32_t *base, size_t words)
+    : ws_(ws), saved_base_(ws->base_), saved_cap_(ws->cap_) {
+  AssertTrue(ws->depth_ > 0 && ws->top_ == 0 && !ws->strict_,
+             "Workspace: external memory needs an idle guarded workspace");
+  AssertTrue(base != nullptr && (reinterpret_cast<uintptr_t>(base) & 255) == 0,
+             "Workspace: external memory must be 256-byte aligned");
+  ws->base_ = base;
+  ws->cap_ = words & ~static_cast<size_t>(63);
+  ws->strict_ = true;
+}
+
+Workspace::External::~External() {
+  ws_->base_ = saved_base_;
+  ws_->cap_ = saved_cap_;
+  ws_->top_ = 0;
+  ws_->strict_ = false;
+}
+
 uint32_t *Workspace::Push(size_t words) {
   const size_t w = (words + 63) & ~static_cast<size_t>(63);  // 256-byte steps
   if (w > cap_ - top_) return nullptr;
-  uint32_t *p = buf_.as<uint32_t>() + top_;
+  uint32_t *p = base_ + top_;
   top_ += w;
   return p;
 }
 
-void Workspace::Pop(uint32_t *p) {
-  top_ = static_cast<size_t>(p - buf_.as<uint32_t>());
-}
+void Workspace::Pop(uint32_t *p) { top_ = static_cast<size_t>(p - base_); }
 
 Scratch::Scratch(Workspace *ws, size_t words) {
   if (words == 0) return;
@@ -105,6 +122,9 @@ Scratch::Scratch(Workspace *ws, size_t words) {
       ws_ = ws;
       return;
     }
+    if (ws->Strict())
+      throw Error("ERROR: the temporaries of this call exceed the scratch "
+                  "memory it was given");
   }
   s_ = CurrentStream();
   HipCheck(hipMallocAsync(reinterpret_cast<void **>(&p_),
@@ -1038,6 +1058,28 @@ bool ModSwitchHandler<uint32_t>::ModDownInttRange(Kind kind, int *first,
   return true;
 }
 
+void ModSwitchHandler<uint32_t>::ModDownShape(Kind kind, NPInfo *np_src,
+                                              NPInfo *np_dst,
+                                              NPInfo *np_non_intt) const {
+  const int num_src_aux = kind == Kind::Rescale ? 0 : num_aux_;
+  *np_src = param_.LevelToNP(level_, num_src_aux);
+  *np_dst = param_.LevelToNP(kind == Kind::ModDown ? level_ : level_ - 1, 0);
+  *np_non_intt = NPInfo(std::min(np_src->num_main_, np_dst->num_main_),
+                        std::min(np_src->num_ter_, np_dst->num_ter_), 0);
+}
+
+size_t ModSwitchHandler<uint32_t>::ModDownScratchWords(
+    Kind kind, int num_polys, bool intt_rows_given) const {
+  NPInfo np_src, np_dst, np_non_intt;
+  ModDownShape(kind, &np_src, &np_dst, &np_non_intt);
+  const size_t n = param_.degree_;
+  const size_t src_len = np_src.GetNumTotal() - np_non_intt.GetNumTotal();
+  const size_t dst_len = np_dst.GetNumTotal();
+  // ModDownMulti's INTT output (unless given) and BConv output
+  return (intt_rows_given ? 0 : num_polys * src_len * n) +
+         num_polys * dst_len * n;
+}
+
 void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
                                               const word *src,
                                               long long src_pstride,
@@ -1049,12 +1091,8 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
              "ModDown: 1 to CHD_MAX_JOBS polynomials per call");
   AssertTrue(kind == Kind::ModDown || level_ > 0,
              "Not enough q primes to rescale");
-  const int num_src_aux = kind == Kind::Rescale ? 0 : num_aux_;
-  const NPInfo np_src = param_.LevelToNP(level_, num_src_aux);
-  const NPInfo np_dst =
-      param_.LevelToNP(kind == Kind::ModDown ? level_ : level_ - 1, 0);
-  const NPInfo np_non_intt(std::min(np_src.num_main_, np_dst.num_main_),
-                           std::min(np_src.num_ter_, np_dst.num_ter_), 0);
+  NPInfo np_src, np_dst, np_non_intt;
+  ModDownShape(kind, &np_src, &np_dst, &np_non_intt);
   const int src_len = np_src.GetNumTotal() - np_non_intt.GetNumTotal();
   const int dst_len = np_dst.GetNumTotal();
   const SwitchTable &st = kind == Kind::ModDown   ? mod_down_
@@ -1264,6 +1302,24 @@ void Context<uint32_t>::KeySwitchDown(int level, CtRef res, const word *d,
                 rows_a, first);
   ms.ModDownMulti({res.bx, res.ax}, acc_b, static_cast<long long>(total) * n,
                   kind, rows_b);
+}
+
+size_t Context<uint32_t>::KeySwitchScratchWords(int level,
+                                                bool rescale) const {
+  // KeySwitchDown: accumulator and ModDown's first INTT pass for the whole
+  // call, then KeyAccumulate's ModUp groups and INTT or ModDownMulti's
+  // temporaries, one after the other
+  const size_t n = param_.degree_;
+  const size_t num_q = param_.LevelToNP(level).GetNumQ();
+  const size_t total = num_q + param_.alpha_;
+  const auto kind = rescale ? ModSwitchHandler<word>::Kind::ModDownAndRescale
+                            : ModSwitchHandler<word>::Kind::ModDown;
+  const auto &ms = mod_switch_handlers_.at(level);
+  int first = 0, count = 0;
+  const bool fused = ms.ModDownInttRange(kind, &first, &count);
+  const size_t acc = 2 * total * n + (fused ? 2 * count * n : 0);
+  const size_t modup = ms.NumGroups() * total * n + num_q * n;
+  return acc + std::max(modup, ms.ModDownScratchWords(kind, 2, fused));
 }
 
 void Context<uint32_t>::KeyMultExtV(int level, word *acc_b, word *acc_a,

@@ -217,15 +217,35 @@ class Workspace {
    private:
     Workspace *ws_;
   };
+  // For one guarded call, temporaries come from caller-given device memory
+  // [base, base + words) instead of the arena, and running out of it throws
+  // instead of allocating. Taken inside a Use guard of this workspace with
+  // no temporary live; the arena is back when the guard ends.
+  class External {
+   public:
+    External(Workspace *ws, uint32_t *base, size_t words);
+    ~External();
+    External(const External &) = delete;
+    External &operator=(const External &) = delete;
+
+   private:
+    Workspace *ws_;
+    uint32_t *saved_base_;
+    size_t saved_cap_;
+  };
   // nullptr when the arena has no room left
   uint32_t *Push(size_t words);
   void Pop(uint32_t *p);
   size_t Capacity() const { return cap_; }
+  // no fallback allocation allowed (an External guard is active)
+  bool Strict() const { return strict_; }
 
  private:
   void Enter();
   void Leave() noexcept;
   DevBuf buf_;
+  uint32_t *base_ = nullptr;
+  bool strict_ = false;
   size_t cap_ = 0, top_ = 0;
   int depth_ = 0;
   hipEvent_t done_ = nullptr;
@@ -236,7 +256,8 @@ class Workspace {
 
 // A temporary of `words` words: from the arena when one is given and has
 // room, otherwise stream-ordered (hipMallocAsync / hipFreeAsync on the
-// current stream). Must be released in LIFO order (automatic scope).
+// current stream), or an Error when the workspace is strict. Must be
+// released in LIFO order (automatic scope).
 class Scratch {
  public:
   Scratch(Workspace *ws, size_t words);
@@ -523,6 +544,10 @@ class ModSwitchHandler<uint32_t> {
   // they include terminal limbs (then they are not contiguous) or for
   // Rescale.
   bool ModDownInttRange(Kind kind, int *first, int *count) const;
+  // words of workspace temporaries ModDownMulti takes for num_polys
+  // polynomials (intt_rows_given: the first INTT pass is supplied)
+  size_t ModDownScratchWords(Kind kind, int num_polys,
+                             bool intt_rows_given) const;
 
  private:
   struct SwitchTable {       // one source set -> destination set
@@ -537,6 +562,9 @@ class ModSwitchHandler<uint32_t> {
                    int restore_hi = 0) const;
   void ModDownWorker(DvView<word> &dst, const DvConstView<word> &src,
                      Kind kind) const;
+  // source, destination and untransformed prime sets of a ModDown kind
+  void ModDownShape(Kind kind, NPInfo *np_src, NPInfo *np_dst,
+                    NPInfo *np_non_intt) const;
   const int level_;
   const int num_aux_;
   const int beta_;
@@ -688,6 +716,8 @@ class Context<uint32_t> {
   void PermuteV(int level, CtRef res, CtCRef a, int galois_amount) const;
   // scratch arena of this context (sized for HMult / HRot at the top level)
   Workspace *GetWorkspace() const { return ws_.get(); }
+  // peak words of workspace temporaries of HMultV / MultKeyV at a level
+  size_t KeySwitchScratchWords(int level, bool rescale) const;
   // MultKeyNoModDown of an extended-basis accumulator (Context.cpp:609-643,
   // as the giant step of Hoist.cu:939-957 uses it): the ModUp of d (q limbs,
   // level's prime count), multiplied by the key and summed over the dnum

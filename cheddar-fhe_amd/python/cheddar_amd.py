@@ -65,6 +65,8 @@ _SIGS = {
     "chd_rescale_poly": (_i, [_vp, _i, _vp, _vp, _vp]),
     "chd_mod_down_and_rescale": (_i, [_vp, _i, _vp, _vp, _vp]),
     "chd_hmult": (_i, [_vp, _i] + [_vp] * 6 + [_pp, _pp, _i, _i, _vp]),
+    "chd_hmult_noalloc": (_i, [_vp, _i] + [_vp] * 6 + [_pp, _pp, _i, _i,
+                                                     _vp]),
     "chd_rescale": (_i, [_vp, _i] + [_vp] * 4 + [_vp]),
     "chd_mult_key": (_i, [_vp, _i] + [_vp] * 4 + [_pp, _pp, _i, _vp]),
     "chd_hrot": (_i, [_vp, _i] + [_vp] * 4 + [_pp, _pp, _i, _i, _i, _vp]),
@@ -295,6 +297,16 @@ class Context:
                              ptr(a[0]), ptr(a[1]), ptr(b[0]), ptr(b[1]),
                              ptr_array(evk_b), ptr_array(evk_a), len(evk_b),
                              int(bool(rescale)), self._s(stream)))
+
+    def hmult_noalloc(self, level, res, a, b, evk_b, evk_a, rescale=True,
+                      stream=None):
+        """hmult with its temporaries in the library's static device array
+        (no device allocation)"""
+        _check(lib.chd_hmult_noalloc(self.h, level, ptr(res[0]), ptr(res[1]),
+                                     ptr(a[0]), ptr(a[1]), ptr(b[0]),
+                                     ptr(b[1]), ptr_array(evk_b),
+                                     ptr_array(evk_a), len(evk_b),
+                                     int(bool(rescale)), self._s(stream)))
 
     def rescale(self, level, res, a, stream=None):
         _check(lib.chd_rescale(self.h, level, ptr(res[0]), ptr(res[1]),

@@ -145,6 +145,23 @@ int chd_hmult(const chd_context *ctx, int level, uint32_t *res_bx,
               const uint32_t *b_bx, const uint32_t *b_ax,
               const uint32_t *const *evk_bx, const uint32_t *const *evk_ax,
               int evk_beta, int rescale, void *stream);
+/* chd_hmult without allocation. No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). Same arguments,
+ * kernels and results as chd_hmult; the key-switch temporaries come from a
+ * static 64 MiB device array (one per GPU, held until the process ends)
+ * instead of the context's arena, and the call makes no hipMalloc, hipFree
+ * or other allocating call. A level whose HMult needs more than 64 MiB of
+ * temporaries (more than 24 q limbs with alpha = 8, dnum 3) is rejected
+ * with CHD_ERR_INVALID_ARGUMENT. Every call on one GPU shares that array:
+ * calls that overlap on one GPU (other streams, threads or contexts) race;
+ * order them. */
+int chd_hmult_noalloc(const chd_context *ctx, int level, uint32_t *res_bx,
+                      uint32_t *res_ax, const uint32_t *a_bx,
+                      const uint32_t *a_ax, const uint32_t *b_bx,
+                      const uint32_t *b_ax, const uint32_t *const *evk_bx,
+                      const uint32_t *const *evk_ax, int evk_beta,
+                      int rescale, void *stream);
 /* Context::Rescale of a two-polynomial ciphertext (Context.cpp:739-774) */
 int chd_rescale(const chd_context *ctx, int level, uint32_t *res_bx,
                 uint32_t *res_ax, const uint32_t *a_bx, const uint32_t *a_ax,
