@@ -37,6 +37,7 @@ SOURCES = [
     ("csrc/elementwise.hip", True, []),
     ("csrc/hmult_noalloc.hip", True, []),
     ("host/device_tables.cpp", False, []),
+    ("host/memory_pool.cpp", False, []),
     ("host/cheddar.cpp", False, []),
     ("host/encoder.cpp", False, []),
     ("host/param_json.cpp", False, []),

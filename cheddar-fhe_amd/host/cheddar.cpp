@@ -1193,6 +1193,11 @@ Context<uint32_t>::Context(const Parameter<word> &param)
       elem_handler_(param, ntt_handler_),
       ntt_handler_(param),
       encoder_(param, ntt_handler_) {
+  // the reference's MemoryPool member (Context.h:84): this parameter set's
+  // bins in the device pool every DeviceVector draws from
+  MemoryPool::Current().AddBins(static_cast<size_t>(param_.degree_) *
+                                    sizeof(word),
+                                param_.alpha_, param_.L_);
   Ciphertext<word>::SetDegree(param_.degree_);
   {
     // arena for the largest call at the top level: HMult holds the tensor

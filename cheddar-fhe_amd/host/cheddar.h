@@ -32,6 +32,7 @@
 
 #include "cheddar_kernels.h"
 #include "device_tables.h"
+#include "memory_pool.h"
 
 namespace cheddar {
 
@@ -166,19 +167,84 @@ class DvConstView {
   int total_, aux_;
 };
 
-// Owning device vector (hipMalloc; the reference uses an RMM pool).
+// Owning device vector (include/core/DeviceVector.h:80-125): memory from
+// the device's MemoryPool, taken and given back in the order of the stream
+// current when it is (re)allocated, as the reference's rmm::device_uvector
+// takes it from its pool on its stream. resize keeps the first
+// min(old, new) words and reallocates only beyond the capacity.
 template <typename word>
 class DeviceVector {
  public:
   DeviceVector() = default;
   explicit DeviceVector(size_t n) { resize(n); }
-  void resize(size_t n) {
-    buf_.Resize(n * sizeof(word));
-    n_ = n;
+  ~DeviceVector() { Free(); }
+  DeviceVector(const DeviceVector &) = delete;
+  DeviceVector &operator=(const DeviceVector &) = delete;
+  DeviceVector(DeviceVector &&o) noexcept
+      : p_(o.p_),
+        n_(o.n_),
+        reserved_(o.reserved_),
+        stream_(o.stream_),
+        pool_(o.pool_) {
+    o.p_ = nullptr;
+    o.n_ = o.reserved_ = 0;
   }
+  DeviceVector &operator=(DeviceVector &&o) noexcept {
+    if (this != &o) {
+      Free();
+      p_ = o.p_;
+      n_ = o.n_;
+      reserved_ = o.reserved_;
+      stream_ = o.stream_;
+      pool_ = o.pool_;
+      o.p_ = nullptr;
+      o.n_ = o.reserved_ = 0;
+    }
+    return *this;
+  }
+  void resize(size_t n) {
+    if (n * sizeof(word) <= reserved_) {
+      n_ = n;
+      return;
+    }
+    const hipStream_t s = CurrentStream();
+    size_t reserved = 0;
+    MemoryPool &pool = MemoryPool::Current();
+    word *p = static_cast<word *>(pool.Allocate(n * sizeof(word), s,
+                                                &reserved));
+    if (n_ != 0) {
+      const hipError_t e = hipMemcpyAsync(p, p_, n_ * sizeof(word),
+                                          hipMemcpyDeviceToDevice, s);
+      if (e != hipSuccess) {
+        pool.Deallocate(p, reserved, s);
+        HipCheck(e, "hipMemcpyAsync");
+      }
+    }
+    // the old block's last use is the copy above, on s
+    if (p_ != nullptr) pool_->Deallocate(p_, reserved_, s);
+    p_ = p;
+    n_ = n;
+    reserved_ = reserved;
+    stream_ = s;
+    pool_ = &pool;
+  }
+  // gives the memory back (the reference's shrink_to_fit of an empty vector)
+  void shrink_to_fit() {
+    if (n_ == 0) Free();
+  }
+  // DeviceVector.cpp:75-85: size more words, the new ones zero
+  void ZeroExtend(size_t size) {
+    if (size == 0) return;
+    const size_t old = n_;
+    resize(old + size);
+    HipCheck(hipMemsetAsync(p_ + old, 0, size * sizeof(word), stream_),
+             "hipMemsetAsync");
+  }
+  hipStream_t stream() const { return stream_; }
   size_t size() const { return n_; }
-  word *data() { return buf_.as<word>(); }
-  const word *data() const { return buf_.as<word>(); }
+  size_t capacity() const { return reserved_ / sizeof(word); }
+  word *data() { return p_; }
+  const word *data() const { return p_; }
   DvView<word> View(int aux_size = 0, int front = 0) {
     return DvView<word>(data() + front, static_cast<int>(n_) - front, aux_size);
   }
@@ -188,9 +254,46 @@ class DeviceVector {
   }
 
  private:
-  DevBuf buf_;
-  size_t n_ = 0;
+  void Free() noexcept {
+    if (p_ != nullptr) pool_->Deallocate(p_, reserved_, stream_);
+    p_ = nullptr;
+    n_ = reserved_ = 0;
+  }
+  word *p_ = nullptr;
+  size_t n_ = 0, reserved_ = 0;
+  hipStream_t stream_ = nullptr;
+  MemoryPool *pool_ = nullptr;  // the pool of the device it came from
 };
+
+// the reference's host-side vector (DeviceVector.h:15, a thrust host_vector)
+template <typename word>
+using HostVector = std::vector<word>;
+
+// DeviceVector.cpp:101-125: copies in the destination's stream order (the
+// host side must stay valid until the copy has run)
+template <typename word>
+void CopyHostToDevice(DeviceVector<word> &dst, const std::vector<word> &src) {
+  dst.resize(src.size());
+  HipCheck(hipMemcpyAsync(dst.data(), src.data(), src.size() * sizeof(word),
+                          hipMemcpyHostToDevice, dst.stream()),
+           "hipMemcpyAsync");
+}
+template <typename word>
+void CopyDeviceToHost(std::vector<word> &dst, const DeviceVector<word> &src) {
+  dst.resize(src.size());
+  HipCheck(hipMemcpyAsync(dst.data(), src.data(), src.size() * sizeof(word),
+                          hipMemcpyDeviceToHost, src.stream()),
+           "hipMemcpyAsync");
+}
+template <typename word>
+void CopyDeviceToDevice(DeviceVector<word> &dst,
+                        const DeviceVector<word> &src) {
+  dst.resize(src.size());
+  if (src.data() == dst.data()) return;
+  HipCheck(hipMemcpyAsync(dst.data(), src.data(), src.size() * sizeof(word),
+                          hipMemcpyDeviceToDevice, dst.stream()),
+           "hipMemcpyAsync");
+}
 
 // Device scratch arena of one Context. Key-switch temporaries (the
 // reference's per-call RMM allocations, ModSwitch.cu:442,597;

@@ -185,6 +185,58 @@ int main() {
           same(download(c.bx_.data(), (L - 1) * kN), wbr) &&
               same(download(c.ax_.data(), (L - 1) * kN), war));
   }
+  // the device pool behind DeviceVector (MemoryPool.cpp:5-35): the
+  // reference's bins for this parameter set, and result ciphertexts made per
+  // call (the reference's usage) served from it once warm
+  {
+    const std::vector<size_t> want_bins = {
+        512,    2048,    8192,    32768,   131072,  262144,
+        524288, 1048576, 2097152, 4194304, 6291456, 8388608};
+    check("memory pool bins", MemoryPool::Current().Bins() == want_bins);
+    bool ok = true;
+    size_t warm = 0;
+    const size_t reuses0 = MemoryPool::Current().GetStats().reuses;
+    for (int i = 0; i < 20; i++) {
+      Ct res;
+      ctx->HMult(res, a, b, key, true);
+      ok = ok && same(download(res.bx_.data(), (L - 1) * kN), wbr) &&
+           same(download(res.ax_.data(), (L - 1) * kN), war);
+      if (i == 1) warm = MemoryPool::Current().GetStats().device_allocations;
+    }
+    const MemoryPool::Stats st = MemoryPool::Current().GetStats();
+    check("HMult with a new result ciphertext per call", ok);
+    check("per-call results come from the pool, no device allocation",
+          st.device_allocations == warm && st.reuses - reuses0 >= 38);
+  }
+  // DeviceVector::resize keeps the leading words (device_uvector::resize),
+  // ZeroExtend appends zeros (DeviceVector.cpp:75-85)
+  {
+    const std::vector<word> head(hb1.begin(), hb1.begin() + 4 * kN);
+    DeviceVector<word> v(4 * kN);
+    upload(v.data(), head);
+    const word *p0 = v.data();
+    v.resize(2 * kN);
+    check("DeviceVector shrink keeps memory and data",
+          v.data() == p0 &&
+              same(download(v.data(), 2 * kN),
+                   std::vector<word>(head.begin(), head.begin() + 2 * kN)));
+    v.resize(6 * kN);
+    check("DeviceVector growth keeps the leading words",
+          v.size() == 6 * kN &&
+              same(download(v.data(), 2 * kN),
+                   std::vector<word>(head.begin(), head.begin() + 2 * kN)));
+    v.ZeroExtend(kN);
+    const std::vector<word> tail = download(v.data() + 6 * kN, kN);
+    check("DeviceVector ZeroExtend",
+          v.size() == 7 * kN &&
+              same(tail, std::vector<word>(kN, 0)));
+    HostVector<word> back;
+    DeviceVector<word> w;
+    CopyHostToDevice(w, head);
+    CopyDeviceToHost(back, w);
+    HipCheck(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    check("CopyHostToDevice / CopyDeviceToHost", same(back, head));
+  }
   // MultKey and HRot (Context.cpp:584-607, 776-791)
   {
     Ct mk, rot;
