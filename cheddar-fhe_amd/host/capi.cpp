@@ -126,25 +126,8 @@ extern "C" int chd_bconv_plan_create(chd_bconv_plan **out, int log_degree,
   plan->dst_chain = std::make_unique<cheddar::ChainTables>(log_degree, dst);
   plan->src_len = src_len;
   plan->dst_len = dst_len;
-  plan->const1.assign(src_len, 1);
-  plan->const2.assign(static_cast<size_t>(src_len) * dst_len, 0);
-  const word n = 1u << log_degree;
-  // PopulateModSwitchConstants (src/core/ModSwitch.cu:320-370)
-  for (int i = 0; i < src_len; i++) {
-    word v = 1;
-    for (int j = 0; j < src_len; j++)
-      if (j != i) v = pm::mulmod(v, src[j], src[i]);
-    plan->const1[i] = pm::invmod(pm::mulmod(v, n, src[i]), src[i]);
-  }
-  for (int k = 0; k < dst_len; k++)
-    for (int i = 0; i < src_len; i++) {
-      word acc = 1;
-      for (int j = 0; j < src_len; j++)
-        if (j != i) acc = pm::mulmod(acc, src[j], dst[k]);
-      acc = pm::to_mont(pm::to_mont(acc, dst[k]), dst[k]);
-      plan->const2[static_cast<size_t>(k) * src_len + i] =
-          pm::normalize(acc, dst[k]);
-    }
+  pm::modswitch_constants(src, dst, 1u << log_degree, 0, 0, &plan->const1,
+                          &plan->const2);
   std::vector<unsigned char> packed(
       static_cast<size_t>(chd_bconv_table_size(src_len, dst_len)));
   int st = chd_bconv_table_pack(packed.data(), plan->const2.data(), dst.data(),

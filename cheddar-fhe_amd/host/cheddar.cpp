@@ -794,27 +794,10 @@ void ModSwitchHandler<uint32_t>::BuildSwitch(
     const std::vector<word> &dst, int restore_lo, int restore_hi) const {
   const int sl = static_cast<int>(src.size());
   const int dl = static_cast<int>(dst.size());
-  std::vector<word> c1(sl, 1);
-  std::vector<int32_t> c2(static_cast<size_t>(sl) * dl);
-  for (int i = 0; i < sl; i++) {
-    word v = 1;
-    for (int j = 0; j < sl; j++)
-      if (j != i) v = pm::mulmod(v, src[j] % src[i], src[i]);
-    v = pm::mulmod(v, static_cast<word>(param_.degree_) % src[i], src[i]);
-    c1[i] = pm::invmod(v, src[i]);
-    // BitPacker: the restored primes' product folded in (kept as a plain
-    // residue, as the reference does)
-    for (int j = restore_lo; j < restore_hi; j++)
-      c1[i] = pm::mulmod(c1[i], dst[j] % src[i], src[i]);
-  }
-  for (int k = 0; k < dl; k++)
-    for (int i = 0; i < sl; i++) {
-      word acc = 1;
-      for (int j = 0; j < sl; j++)
-        if (j != i) acc = pm::mulmod(acc, src[j] % dst[k], dst[k]);
-      acc = pm::to_mont(pm::to_mont(acc, dst[k]), dst[k]);
-      c2[static_cast<size_t>(k) * sl + i] = pm::normalize(acc, dst[k]);
-    }
+  std::vector<word> c1;
+  std::vector<int32_t> c2;
+  pm::modswitch_constants(src, dst, static_cast<word>(param_.degree_),
+                          restore_lo, restore_hi, &c1, &c2);
   st.src_len = sl;
   st.dst_len = dl;
   st.const1.resize(sl);

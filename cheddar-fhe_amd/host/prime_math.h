@@ -97,5 +97,39 @@ inline uint32_t bitrev(uint32_t i, int bits) {
   return r;
 }
 
+// Base-conversion constants from the source primes to the destination
+// primes (PopulateModSwitchConstants, ModSwitch.cu:320-370), degree n:
+//   const1[i]    = (n prod_{j != i} s_j)^-1 mod s_i, times the product of
+//                  the restored destination primes [restore_lo, restore_hi)
+//                  (BitPacker, ModSwitch.cu:372-411), plain residues;
+//   const2[k][i] = centre(ToMont(ToMont(prod_{j != i} s_j mod d_k))), the
+//                  "double Montgomery" table of the matrix product.
+inline void modswitch_constants(const std::vector<uint32_t> &src,
+                                const std::vector<uint32_t> &dst, uint32_t n,
+                                int restore_lo, int restore_hi,
+                                std::vector<uint32_t> *const1,
+                                std::vector<int32_t> *const2) {
+  const size_t sl = src.size(), dl = dst.size();
+  const1->assign(sl, 1);
+  const2->assign(sl * dl, 0);
+  for (size_t i = 0; i < sl; i++) {
+    uint32_t v = 1;
+    for (size_t j = 0; j < sl; j++)
+      if (j != i) v = mulmod(v, src[j] % src[i], src[i]);
+    v = mulmod(v, n % src[i], src[i]);
+    (*const1)[i] = invmod(v, src[i]);
+    for (int j = restore_lo; j < restore_hi; j++)
+      (*const1)[i] = mulmod((*const1)[i], dst[j] % src[i], src[i]);
+  }
+  for (size_t k = 0; k < dl; k++)
+    for (size_t i = 0; i < sl; i++) {
+      uint32_t acc = 1;
+      for (size_t j = 0; j < sl; j++)
+        if (j != i) acc = mulmod(acc, src[j] % dst[k], dst[k]);
+      acc = to_mont(to_mont(acc, dst[k]), dst[k]);
+      (*const2)[k * sl + i] = normalize(acc, dst[k]);
+    }
+}
+
 }  // namespace pm
 }  // namespace cheddar

@@ -284,6 +284,110 @@ int main() {
                                         wup.begin() + (g + 1) * kw));
     check("mod_switch_handlers_[level].ModUp", ok);
   }
+  // elem_handler_ seams the reference's extensions call directly
+  // (Hoist.cu:484, UserInterface.cu:185): PAccum with polynomial commons
+  // (ElementWise.cu:1396-1435) over aux-extended polynomials, more
+  // accumulands than one launch takes plus an extra addend; CAccum with
+  // per-limb constants; Tensor; Permute
+  {
+    const NPInfo npx = param.LevelToNP(L - 1, alpha);
+    const int tl = npx.GetNumTotal();
+    const size_t tw = static_cast<size_t>(tl) * kN;
+    const std::vector<word> &chain = chain_k;  // main then aux primes
+    const int num_acc = 11;                    // two launches of <= 8
+    std::vector<std::vector<word>> hct(num_acc + 1), hcm(num_acc), hct2(num_acc + 1);
+    std::vector<DeviceVector<word>> dct, dcm, dct2;
+    auto to_dev = [&](const std::vector<word> &h) {
+      DeviceVector<word> d(h.size());
+      upload(d.data(), h);
+      return d;
+    };
+    for (int j = 0; j <= num_acc; j++) {
+      hct[j] = uniform(chain, tl);
+      hct2[j] = uniform(chain, tl);
+      dct.push_back(to_dev(hct[j]));
+      dct2.push_back(to_dev(hct2[j]));
+      if (j < num_acc) {
+        hcm[j] = uniform(chain, tl);
+        dcm.push_back(to_dev(hcm[j]));
+      }
+    }
+    const int aux_words = alpha * static_cast<int>(kN);
+    std::vector<std::vector<DvConstView<word>>> srcs;
+    std::vector<DvConstView<word>> commons;
+    for (int j = 0; j <= num_acc; j++)
+      srcs.push_back({dct[j].ConstView(aux_words), dct2[j].ConstView(aux_words)});
+    for (int j = 0; j < num_acc; j++) commons.push_back(dcm[j].ConstView(aux_words));
+    DeviceVector<word> o1(tw), o2(tw);
+    std::vector<DvView<word>> out{o1.View(aux_words), o2.View(aux_words)};
+    ctx->elem_handler_.PAccum(out, npx, srcs, commons);
+    bool ok = true;
+    for (int p = 0; p < 2 && ok; p++) {
+      const std::vector<word> got = download(p ? o2.data() : o1.data(), tw);
+      const auto &hs = p ? hct2 : hct;
+      for (int l = 0; l < tl && ok; l++)
+        for (size_t c = 0; c < kN && ok; c++) {
+          const size_t i = l * kN + c;
+          uint64_t acc = hs[num_acc][i];
+          for (int j = 0; j < num_acc; j++)
+            acc += orc_mont_mul(hs[j][i], hcm[j][i], chain[l]);
+          ok = got[i] == acc % chain[l];
+        }
+    }
+    check("elem_handler_.PAccum (polynomial commons, 11 + extra addend)", ok);
+
+    // CAccum: one Montgomery constant per limb (a Constant's cx_)
+    const int num_c = 3;
+    std::vector<std::vector<word>> hc(num_c);
+    std::vector<DeviceVector<word>> dc;
+    std::vector<DvConstView<word>> cviews;
+    std::vector<std::vector<DvConstView<word>>> csrcs;
+    for (int j = 0; j < num_c; j++) {
+      hc[j].resize(tl);
+      for (int l = 0; l < tl; l++) hc[j][l] = next64() % chain[l];
+      dc.push_back(to_dev(hc[j]));
+      cviews.push_back(dc[j].ConstView(alpha));
+      csrcs.push_back({dct[j].ConstView(aux_words)});
+    }
+    std::vector<DvView<word>> cout{o1.View(aux_words)};
+    ctx->elem_handler_.CAccum(cout, npx, csrcs, cviews);
+    ok = true;
+    {
+      const std::vector<word> got = download(o1.data(), tw);
+      for (int l = 0; l < tl && ok; l++)
+        for (size_t c = 0; c < kN && ok; c++) {
+          const size_t i = l * kN + c;
+          uint64_t acc = 0;
+          for (int j = 0; j < num_c; j++)
+            acc += orc_mont_mul(hct[j][i], hc[j][l], chain[l]);
+          ok = got[i] == acc % chain[l];
+        }
+    }
+    check("elem_handler_.CAccum (per-limb constants)", ok);
+
+    // Tensor (ElementWise.cu:921-953) and Permute (ElementWise.cu:966-999)
+    DeviceVector<word> tb(qw), ta(qw), tr(qw);
+    std::vector<DvView<word>> tdst{tb.View(), ta.View(), tr.View()};
+    ctx->elem_handler_.Tensor(tdst, np, {a.bx_.ConstView(), a.ax_.ConstView()},
+                              {b.bx_.ConstView(), b.ax_.ConstView()});
+    std::vector<word> wtb(qw), wta(qw), wtr(qw);
+    orc_tensor(wtb.data(), wta.data(), wtr.data(), hb1.data(), ha1.data(),
+               hb2.data(), ha2.data(), L, main_p.data(), kLogN);
+    check("elem_handler_.Tensor", same(download(tb.data(), qw), wtb) &&
+                                      same(download(ta.data(), qw), wta) &&
+                                      same(download(tr.data(), qw), wtr));
+    std::vector<DvView<word>> pdst{tb.View(), ta.View()};
+    ctx->elem_handler_.Permute(pdst, np, 77,
+                               {a.bx_.ConstView(), a.ax_.ConstView()});
+    std::vector<word> wpb(qw), wpa(qw);
+    const uint32_t gal = ctx->elem_handler_.PermuteAmountToGaloisFactor(77);
+    orc_permute(wpb.data(), hb1.data(), L, kLogN, gal);
+    orc_permute(wpa.data(), ha1.data(), L, kLogN, gal);
+    check("elem_handler_.Permute(77)",
+          gal == orc_galois_factor(77, kLogN) &&
+              same(download(tb.data(), qw), wpb) &&
+              same(download(ta.data(), qw), wpa));
+  }
   // encoder member (Context.h:88): Encode / Decode round trip within the
   // reference's EncodeDecode tolerance (Testbed.h:93), EncodeConstant
   {

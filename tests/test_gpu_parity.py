@@ -328,9 +328,10 @@ def test_hoist_baby_steps_config5_level(chd, ks):
 
 
 def test_hoist_evaluate_config5_level(chd, ks):
-    """double-hoisted BSGS at L = 20: 10 baby steps (two fused launches, two
-    accumulation chunks) and 3 giant steps; the one-shot entry point and a
-    handler run twice (buffer reuse) on different ciphertexts"""
+    """double-hoisted BSGS at L = 20: 10 baby steps (two fused baby-step
+    launches of up to 8 rotations, one accumulation chunk) and 3 giant
+    steps; the one-shot entry point and a handler run twice (buffer reuse)
+    on different ciphertexts"""
     import hoist_ref
     param, ctx, main, aux = ks
     L = 20
@@ -381,3 +382,33 @@ def test_hoist_evaluate_many_giant_steps(chd, ks):
     h.run(out, (dev(b), dev(a)), dkeys)
     assert np.array_equal(host(out[0]), wb)
     assert np.array_equal(host(out[1]), wa)
+
+
+def test_hoist_evaluate_chunked_accumulation(chd, ks):
+    """36 baby steps x 9 giant steps at L = 20: more baby steps than one
+    accumulation launch takes (32), so the second chunk adds onto the first
+    one's sums (add_to_dst), and more giant steps than one launch holds (8),
+    so two giant-step launches and two batches of giant-step key switches
+    run; with absent pairs"""
+    import hoist_ref
+    param, ctx, main, aux = ks
+    L = 20
+    r = rng(530)
+    bsi, gsi = list(range(36)), [36 * k for k in range(9)]
+    pts = {(g, s): uniform_limbs(r, main[:L] + aux) for g in gsi for s in bsi
+           if (g, s) not in ((36, 33), (288, 2), (144, 0))}
+    keys = _rot_keys(r, main, aux, sorted(set(bsi[1:] + gsi[1:])))
+    dkeys = {k: ([dev(x) for x in v[0]], [dev(x) for x in v[1]])
+             for k, v in keys.items()}
+    dpts = {k: dev(v) for k, v in pts.items()}
+    b, a = uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L])
+    print("hoist 36 baby x 9 giant steps", flush=True)
+    h = chd.Hoist(ctx, L - 1, gsi, bsi, dpts)
+    out = (zeros(L - 1, N), zeros(L - 1, N))
+    h.run(out, (dev(b), dev(a)), dkeys)
+    got_b, got_a = host(out[0]), host(out[1])
+    del dpts, dkeys
+    _orc.lib.orc_set_threads(8)
+    wb, wa = hoist_ref.evaluate(b, a, pts, keys, L, 24, main, aux, 16)
+    assert np.array_equal(got_b, wb)
+    assert np.array_equal(got_a, wa)

@@ -287,27 +287,40 @@ def test_mod_down_known_answer(kind):
     assert np.array_equal(out, want)
 
 
-def test_mod_down_rounding_bound():
-    """Random input: out * P = Z - X with |X| <= alpha P / 2 (mod Q)."""
+@pytest.mark.parametrize("kind", ["moddown", "rescale", "merged"])
+def test_mod_down_rounding_bound(kind):
+    """Random input: out * D = Z - X (mod Q_out) with |X| <= s D / 2, D the
+    product of the s primes divided out (P, q_top, or q_top P): each dropped
+    prime contributes its centred residue times D / d_i."""
     log_n, alpha = 8, 3
-    qp, pp = Q30[:3], Q31[:alpha]
-    primes = qp + pp
-    P = 1
-    for p in pp:
-        P *= p
+    qp, pp = Q30[:8], Q31[:alpha]
+    if kind == "moddown":
+        primes, keep, dropped = qp + pp, len(qp), pp
+    elif kind == "rescale":
+        primes, keep, dropped = qp, len(qp) - 1, qp[-1:]
+    else:
+        primes, keep, dropped = qp + pp, len(qp) - 1, qp[-1:] + pp
+    D = 1
+    for d in dropped:
+        D *= d
     Q = 1
-    for q in qp:
+    for q in qp[:keep]:
         Q *= q
+    assert len(dropped) * D < Q >> 60  # the bound says something mod Q
     src = np.stack([uniform(rng(40 + i), p, 1 << log_n)
                     for i, p in enumerate(primes)])
-    out = _orc.mod_down(src, primes, len(qp), log_n)
-    Zc = ck.from_ntt_mont(src[: len(qp)], qp, log_n)
-    Yc = ck.from_ntt_mont(out, qp, log_n)
+    out = _orc.mod_down(src, primes, keep, log_n)
+    Zc = ck.from_ntt_mont(src[:keep], qp[:keep], log_n)
+    Yc = ck.from_ntt_mont(out, qp[:keep], log_n)
+    worst = 0
     for z, y in zip(Zc, Yc):
-        d = (z - y * P) % Q
+        d = (z - y * D) % Q
         if d > Q // 2:
             d -= Q
-        assert abs(d) <= alpha * P // 2
+        assert abs(d) <= len(dropped) * D // 2
+        worst = max(worst, abs(d))
+    # the bound is not slack by orders of magnitude: X really is of size D
+    assert worst > D // 16
 
 
 # --------------------------------------------------------------------------
@@ -467,6 +480,9 @@ def test_hmult_decrypts(sem, L):
     xa = _orc.rescale(sa, keys.q, L, 1, LOG_N_SEM)
     dec1 = keys.decrypt(xb, xa, L - 1)
     assert max(abs(d - int(p) / qt) for d, p in zip(dec1, prod)) < 64
+    # one rounding (by q_top P) against two (by P, then by q_top): the
+    # merged form is a different function, not a refactoring of the other
+    assert not (np.array_equal(rb, xb) and np.array_equal(ra, xa))
 
 
 def test_hrot_decrypts(sem):
