@@ -27,6 +27,17 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "cheddar-fhe_amd", "python"))
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, MI355X
+# config 3 BConv: 8 limbs in + 40 limbs out; useful int8 operations of the
+# byte-split product (16 byte products per 32 x 32-bit product, 2 ops each)
+BCONV_BYTES = 48 * 4 * (1 << 16)
+BCONV_INT8_OPS = 2 * 16 * (1 << 16) * 8 * 40
+# its measured HBM bytes per launch (profiles/bconv_config3_traffic.md:
+# FETCH_SIZE 1097.5 KiB x 2 + WRITE_SIZE 10240 KiB)
+BCONV_TRAFFIC = int((1097.5 * 2 + 10240) * 1024)
+# config 4 HMult compulsory bytes: 4 x 24 input limbs, 3 x 2 x 32 key limbs,
+# 2 x 23 output limbs
+HMULT_BYTES = (96 + 192 + 46) * 4 * (1 << 16)
 N = 1 << 16
 LIMB_BYTES = 4 * N
 # one limb-transform moves one limb in and one limb out (algorithmic bytes)
@@ -44,7 +55,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU-baseline leg")
     ap.add_argument("--only", choices=["ntt_fwd", "ntt_inv", "hmult",
-                                       "bconv", "copy", "hoist"],
+                                       "hmult_cold", "bconv", "bconv_cold",
+                                       "copy", "hoist"],
                     help="run only this workload's timed loop (for "
                          "profiling); prints its average time")
     return ap.parse_args()
@@ -106,60 +118,81 @@ def bench_ntt(chd, steps, warmup):
     return ms, fwd_ms, inv_ms, warm_ms, ok
 
 
-def bench_hmult(chd, iters=20):
-    import numpy as np
-    import torch
+def _config4_context(chd):
     from chd_primes import ntt_primes
     main, aux = ntt_primes(30, 24), ntt_primes(31, 8)
     param = chd.Param(main, aux, [(i, 0) for i in range(1, 25)])
-    ctx = chd.Context(param)
+    return main, aux, chd.Context(param)
+
+
+def bench_hmult(chd, iters=20, cold=False):
+    """config 4: HMult with merged rescale at L = 24. warm: the same inputs
+    and key every step (working set resident in the 256 MB MALL); cold:
+    steps rotate over distinct input/key sets spanning more than twice the
+    MALL, so inputs and keys come from HBM"""
+    import numpy as np
+    import torch
+    main, aux, ctx = _config4_context(chd)
     rng = np.random.default_rng(0xC0FFEE04)
 
     def limbs(primes):
         a = np.stack([rng.integers(0, p, N, dtype=np.uint64) for p in primes])
         return torch.from_numpy(a.astype(np.uint32).view(np.int32)).cuda()
-    a = (limbs(main), limbs(main))
-    b = (limbs(main), limbs(main))
-    kb = [limbs(main + aux) for _ in range(3)]
-    ka = [limbs(main + aux) for _ in range(3)]
+    set_bytes = (4 * 24 + 6 * 32) * LIMB_BYTES
+    nsets = (2 * MALL_BYTES) // set_bytes + 2 if cold else 1
+    base = [limbs(main) for _ in range(4)] + [limbs(main + aux)
+                                              for _ in range(6)]
+    sets = [base] + [[t.clone() for t in base] for _ in range(nsets - 1)]
     res = (torch.empty(23, N, dtype=torch.int32, device="cuda"),
            torch.empty(23, N, dtype=torch.int32, device="cuda"))
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
 
-    def run(_):
-        ctx.hmult(23, res, a, b, kb, ka, rescale=True, stream=sp)
-    for _ in range(3):
-        run(0)
+    def run(i):
+        t = sets[i % nsets]
+        ctx.hmult(23, res, (t[0], t[1]), (t[2], t[3]), t[4:7], t[7:10],
+                  rescale=True, stream=sp)
+    for i in range(3):
+        run(i)
     torch.cuda.synchronize()
-    return event_time_ms(run, iters, stream) / iters
+    return event_time_ms(run, iters, stream) / iters, nsets * set_bytes
 
 
 def bench_hoist(chd, iters=5):
-    """config 5's shape: a 768 x 768 BSGS linear transform (28 baby steps,
-    28 giant steps, 768 diagonal plaintexts) on one ciphertext at L = 20 of
-    the config-4 chain, double hoisting. Residues are synthetic uniform
-    values below every prime (the plaintexts are not encoder output)."""
+    """config 5: the 768 x 768 BSGS linear transform (28 baby steps, 28
+    giant steps 28 k, 54 rotation keys) on one ciphertext at L = 20 of the
+    config-4 chain, double hoisting. The 768 plaintexts are the generalised
+    diagonals of a seeded W ~ N(0, 0.02), each rotated by its giant step,
+    encoded by the library at scale 2^30 into 2^15 slots with the alpha aux
+    primes (the reference's message constructor); ciphertext and keys are
+    seeded uniform residues."""
+    import numpy as np
     import torch
-    from chd_primes import ntt_primes
-    main, aux = ntt_primes(30, 24), ntt_primes(31, 8)
-    param = chd.Param(main, aux, [(i, 0) for i in range(1, 25)])
-    ctx = chd.Context(param)
-    L, level = 20, 19
+    main, aux, ctx = _config4_context(chd)
+    L, level, dim, slots = 20, 19, 768, 1 << 15
+    r = np.random.default_rng(0xC0FFEE05)
+    W = r.normal(0.0, 0.02, (dim, dim))
+    bs = list(range(28))
+    gs = [28 * k for k in range(28)]
+    rows = np.arange(dim)
+    msgs = {}
+    for g in gs:
+        for b in bs:
+            if g + b < dim:
+                diag = np.zeros(slots)
+                diag[:dim] = W[rows, (rows + g + b) % dim]
+                msgs[(g, b)] = np.roll(diag, g).astype(np.complex128)
+    h = chd.Hoist.from_messages(ctx, level, 2.0 ** 30, gs, bs, msgs)
+    del msgs
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0xC0FFEE05)
 
     def limbs(n):
         return torch.randint(0, 1 << 29, (n, N), dtype=torch.int32,
                              device="cuda", generator=gen)
-    bs = list(range(28))
-    gs = [28 * k for k in range(28)]
-    pts = {(g, b): limbs(L + 8) for g in gs for b in bs if g + b < 768}
-    rots = sorted(set(bs[1:] + gs[1:]))
-    keys = {r: ([limbs(32) for _ in range(3)], [limbs(32) for _ in range(3)])
-            for r in rots}
-    h = chd.Hoist(ctx, level, gs, bs, pts)
-    del pts
+    rots = h.required_rotations()
+    keys = {rot: ([limbs(32) for _ in range(3)], [limbs(32) for _ in range(3)])
+            for rot in rots}
     ct = (limbs(L), limbs(L))
     res = (torch.empty(L - 1, N, dtype=torch.int32, device="cuda"),
            torch.empty(L - 1, N, dtype=torch.int32, device="cuda"))
@@ -168,11 +201,19 @@ def bench_hoist(chd, iters=5):
     for _ in range(2):
         h.run(res, ct, keys, stream=sp)
     torch.cuda.synchronize()
-    return event_time_ms(lambda i: h.run(res, ct, keys, stream=sp), iters,
-                         stream) / iters
+    ms = event_time_ms(lambda i: h.run(res, ct, keys, stream=sp), iters,
+                       stream) / iters
+    # bytes every evaluation has to read once: the plaintexts (L + alpha
+    # limbs each) and, per key switch (27 baby + 27 giant), the key's
+    # dnum groups over L + alpha limbs
+    assert len(rots) == 54
+    compulsory = (dim * (L + 8) + len(rots) * 3 * 2 * (L + 8)) * LIMB_BYTES
+    return ms, compulsory
 
 
-def bench_bconv(chd, iters=50):
+def bench_bconv(chd, iters=50, cold=False):
+    """config 3: BConv 8 -> 40 limbs. cold: steps rotate over distinct
+    source/destination sets spanning more than twice the MALL"""
     import numpy as np
     import torch
     from chd_primes import ntt_primes
@@ -181,46 +222,120 @@ def bench_bconv(chd, iters=50):
     rng = np.random.default_rng(0xC0FFEE03)
     x = np.stack([rng.integers(-((p - 1) // 2), (p - 1) // 2 + 1, N)
                   for p in src_p]).astype(np.int32)
-    src = torch.from_numpy(x).cuda()
-    dst = torch.empty(40, N, dtype=torch.int32, device="cuda")
+    set_bytes = 48 * LIMB_BYTES
+    nsets = (2 * MALL_BYTES) // set_bytes + 2 if cold else 1
+    src0 = torch.from_numpy(x).cuda()
+    srcs = [src0] + [src0.clone() for _ in range(nsets - 1)]
+    dsts = [torch.empty(40, N, dtype=torch.int32, device="cuda")
+            for _ in range(nsets)]
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
-    for _ in range(3):
-        plan.apply(dst, src, stream=sp)
+
+    def run(i):
+        plan.apply(dsts[i % nsets], srcs[i % nsets], stream=sp)
+    for i in range(3):
+        run(i)
     torch.cuda.synchronize()
-    return event_time_ms(lambda i: plan.apply(dst, src, stream=sp), iters,
-                         stream) / iters
+    return event_time_ms(run, iters, stream) / iters
 
 
-def cpu_baseline(seconds=10.0):
-    """Oracle's scalar Montgomery NTT + INTT (1 thread) on a bounded sample
-    of the config-2 workload: repeated 8-limb batches for ~`seconds`."""
+def _cpu_facts():
+    import subprocess
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        gcc = subprocess.run(["gcc", "-dumpfullversion"], capture_output=True,
+                             text=True, timeout=10).stdout.strip()
+    except (OSError, subprocess.SubprocessError):
+        gcc = "?"
+    flags = "?"
+    with open(os.path.join(ROOT, "oracle", "Makefile")) as f:
+        for line in f:
+            if line.startswith("CFLAGS"):
+                flags = line.split("=", 1)[1].strip()
+    # the box's CPU share for one GPU is 16 threads, whatever the host has
+    threads = min(16, len(os.sched_getaffinity(0)))
+    return model, "gcc %s %s" % (gcc, flags), threads
+
+
+def cpu_baseline(seconds=8.0):
+    """The oracle (scalar C restatement) timed on this host on bounded
+    samples of the same workloads: the config-2 NTT + INTT (8-limb batches,
+    ~`seconds` on one thread and again on all the threads of the box's
+    share), one config-4 HMult with merged rescale, and the config-3
+    BConv, each on 1 thread and on all threads."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import _orc  # the checker library, timed here only as the CPU baseline
     from chd_primes import ntt_primes
+    model, compiler, threads = _cpu_facts()
     primes = ntt_primes(30, 32)[:8]
     rng = np.random.default_rng(0xC0FFEE02)
     x = np.stack([rng.integers(0, p, N, dtype=np.uint64)
                   for p in primes]).astype(np.uint32).reshape(-1)
-    _orc.lib.orc_set_threads(1)
     pr = _orc.u32(primes)
-    _orc.lib.orc_ntt_batch(x, 8, 16, pr, 0)   # warm the twiddle cache
-    _orc.lib.orc_intt_batch(x, 8, 16, pr, 0)
-    done, t0 = 0, time.perf_counter()
-    while True:
-        _orc.lib.orc_ntt_batch(x, 8, 16, pr, 0)
+
+    def ntt_rate(nthreads, budget):
+        _orc.lib.orc_set_threads(nthreads)
+        _orc.lib.orc_ntt_batch(x, 8, 16, pr, 0)   # warm the twiddle cache
         _orc.lib.orc_intt_batch(x, 8, 16, pr, 0)
-        done += 16
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": done / el, "unit": "limb-transforms/s", "cores": 1,
+        done, t0 = 0, time.perf_counter()
+        while True:
+            _orc.lib.orc_ntt_batch(x, 8, 16, pr, 0)
+            _orc.lib.orc_intt_batch(x, 8, 16, pr, 0)
+            done += 16
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return done / el, done, el
+    one, done1, el1 = ntt_rate(1, seconds)
+    many, _, _ = ntt_rate(threads, seconds / 4)
+
+    # config 4 HMult and config 3 BConv on the oracle
+    main, aux = ntt_primes(30, 24), ntt_primes(31, 8)
+    r = np.random.default_rng(0xC0FFEE04)
+
+    def uni(ps):
+        return np.stack([r.integers(0, p, N, dtype=np.uint64)
+                         for p in ps]).astype(np.uint32)
+    b1, a1, b2, a2 = (uni(main) for _ in range(4))
+    kb = np.stack([uni(main + aux) for _ in range(3)])
+    ka = np.stack([uni(main + aux) for _ in range(3)])
+    src_p, dst_p = ntt_primes(30, 8), ntt_primes(31, 40)
+    xs = np.stack([r.integers(-((p - 1) // 2), (p - 1) // 2 + 1, N)
+                   for p in src_p]).astype(np.int32)
+    _, table = _orc.modswitch_consts(src_p, dst_p, 16)
+
+    def per_call_us(fn, nthreads, reps):
+        _orc.lib.orc_set_threads(nthreads)
+        fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        return (time.perf_counter() - t0) / reps * 1e6
+    hm = lambda: _orc.hmult(b1, a1, b2, a2, kb, ka, 24, 24, main, aux, 16, 1)  # noqa: E731
+    bc = lambda: _orc.bconv(xs, table, dst_p, 16)  # noqa: E731
+    hm1, hmn = per_call_us(hm, 1, 2), per_call_us(hm, threads, 4)
+    bc1, bcn = per_call_us(bc, 1, 20), per_call_us(bc, threads, 40)
+    _orc.lib.orc_set_threads(1)
+    return {"value": one, "unit": "limb-transforms/s", "cores": 1,
             "kind": "port",
             "sample": "%d limb-transforms (8-limb NTT+INTT batches of the "
-                      "config-2 primes, N=2^16) in %.1f s, scalar C "
-                      "Montgomery restatement, gcc -O2, 1 thread"
-                      % (done, el)}
+                      "config-2 primes, N=2^16) in %.1f s on 1 thread; the "
+                      "same for %.1f s on %d threads; one config-4 HMult "
+                      "(merged rescale) x2 / x4 and one config-3 BConv x20 / "
+                      "x40" % (done1, el1, seconds / 4, threads),
+            "cpu_model": model, "compiler": compiler,
+            "all_cores": {"value": many, "unit": "limb-transforms/s",
+                          "cores": threads},
+            "hmult_us_config4": {"cores_1": hm1, "cores_%d" % threads: hmn},
+            "bconv_us_config3": {"cores_1": bc1, "cores_%d" % threads: bcn}}
 
 
 def run_only(chd, what, steps):
@@ -229,11 +344,15 @@ def run_only(chd, what, steps):
     import torch
     from chd_primes import ntt_primes
     if what == "hmult":
-        return bench_hmult(chd, steps) * 1e3
+        return bench_hmult(chd, steps)[0] * 1e3
+    if what == "hmult_cold":
+        return bench_hmult(chd, steps, cold=True)[0] * 1e3
     if what == "bconv":
         return bench_bconv(chd, steps) * 1e3
+    if what == "bconv_cold":
+        return bench_bconv(chd, steps, cold=True) * 1e3
     if what == "hoist":
-        return bench_hoist(chd, steps) * 1e3
+        return bench_hoist(chd, steps)[0] * 1e3
     if what == "copy":
         # plain device copy of COPY_BYTES: the reference point that scales
         # the FETCH_SIZE / WRITE_SIZE counters into HBM bytes
@@ -293,11 +412,18 @@ def main():
         print("NTT round trip changed the data", file=sys.stderr)
         sys.exit(1)
     lt = 128 * args.steps / (ms / 1e3)
-    hmult_us = bench_hmult(chd) * 1e3
+    hmult_us = bench_hmult(chd)[0] * 1e3
+    hmult_cold_us, hmult_set = bench_hmult(chd, cold=True)
+    hmult_cold_us *= 1e3
     bconv_us = bench_bconv(chd) * 1e3
-    hoist_ms = bench_hoist(chd)
+    bconv_cold_us = bench_bconv(chd, cold=True) * 1e3
+    hoist_ms, hoist_bytes = bench_hoist(chd)
     fwd_bytes = 64 * LIMB_TRANSFORM_BYTES
     achieved = fwd_bytes / (fwd_ms / 1e3) / 1e9
+    bconv_gbs = BCONV_BYTES / (bconv_cold_us / 1e6) / 1e9
+    bconv_tops = BCONV_INT8_OPS / (bconv_cold_us / 1e6) / 1e12
+    hmult_gbs = HMULT_BYTES / (hmult_cold_us / 1e6) / 1e9
+    hoist_gbs = hoist_bytes / (hoist_ms / 1e3) / 1e9
     line = {
         "metric": "NTT limb-transforms/s @N=2^16; HMult keyswitch us; "
                   "% HBM/MFMA roofline",
@@ -311,7 +437,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "u32",
-        "data": "synthetic (seeded uniform residues)",
+        "data": "synthetic (seeded uniform residues; config-5 weights "
+                "seeded N(0, 0.02), encoded by the library)",
         "config": {
             "workload": "config2: batched NTT+INTT of one ciphertext, 2 polys "
                         "x 32 limbs, N=2^16, 30-bit primes, limb-major, "
@@ -328,17 +455,47 @@ def main():
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": traffic_from_profile(),
         },
+        "roofline_bconv": {
+            "kernel": "bconv_mfma, config 3 (8 -> 40 limbs), inputs cold",
+            "bound": "hbm",
+            "achieved": bconv_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": bconv_gbs / HBM_PEAK_GBS,
+            "traffic": BCONV_TRAFFIC,
+            "mfma": {"achieved": bconv_tops, "peak": INT8_PEAK_TOPS,
+                     "unit": "TOP/s (int8, useful byte products)",
+                     "frac": bconv_tops / INT8_PEAK_TOPS},
+        },
+        "roofline_hmult": {
+            "kernel": "HMult key switch + merged rescale, config 4 (8 "
+                      "launches), inputs and key cold",
+            "bound": "hbm",
+            "achieved": hmult_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": hmult_gbs / HBM_PEAK_GBS,
+            "traffic": None,
+            "note": "achieved = compulsory %d B (96 limbs in, 192 key limbs, "
+                    "46 limbs out) / HMult time" % HMULT_BYTES,
+        },
         "extra": {
             "ntt_forward_us": fwd_ms * 1e3,
             "ntt_inverse_us": inv_ms * 1e3,
             "ntt_forward_warm_mall_us": warm_ms * 1e3,
             "hmult_keyswitch_us_config4": hmult_us,
+            "hmult_keyswitch_us_config4_cold": hmult_cold_us,
             "bconv_us_config3_warm": bconv_us,
-            "hoist_bsgs_ms_config5_shape": hoist_ms,
-            "notes": "hmult: warm (same key and inputs each step), host "
-                     "enqueue included; hoist: 768x768 BSGS (28 baby, 28 "
-                     "giant steps, 54 rotation keys, 768 plaintexts) at "
-                     "L=20, synthetic plaintexts",
+            "bconv_us_config3_cold": bconv_cold_us,
+            "hoist_bsgs_ms_config5": hoist_ms,
+            "hoist_bsgs_config5_hbm_frac": hoist_gbs / HBM_PEAK_GBS,
+            "notes": "hmult: warm = same key and inputs each step, cold = "
+                     "%d MiB of distinct input/key sets rotated; host "
+                     "enqueue included. hoist: 768x768 BSGS (28 baby, 28 "
+                     "giant steps, 54 rotation keys) at L=20 on the "
+                     "library's encodings of a seeded N(0, 0.02) weight; "
+                     "HBM fraction against the %d B of plaintexts and keys "
+                     "one evaluation reads" % (hmult_set >> 20, hoist_bytes),
         },
     }
     nsets = max(4, (2 * MALL_BYTES) // (2 * 32 * LIMB_BYTES) + 1)
