@@ -1024,6 +1024,26 @@ __device__ __forceinline__ void radix16_1p(const A &ar,
   }
 }
 
+// radix-16 with the 15 twiddles of its four stages preloaded:
+// w[(1 << t) - 1 + g] is group g of stage t
+template <typename A>
+__device__ __forceinline__ void radix16_pre(const A &ar,
+                                            typename A::T (&x)[16],
+                                            const uint32_t (&w)[15]) {
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int h = 8 >> t;
+#pragma unroll
+    for (int g = 0; g < (1 << t); g++) {
+      const uint32_t wv = w[(1 << t) - 1 + g];
+      const uint32_t wq = ar.twq(wv);
+#pragma unroll
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++)
+        ar.ct(x[k], x[k + h], wv, wq);
+    }
+  }
+}
+
 // orders a wave's LDS writes before its later LDS reads of the same words
 // written by other lanes of that wave: a wave's LDS instructions execute in
 // program order, so only the compiler has to be kept from reordering them
@@ -1048,6 +1068,30 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  // Twiddles of rounds 2-4, requested before the round-1 loads: after the
+  // workgroup barrier every wave of the CU computes at once, and a round
+  // that first waited for its twiddles would leave the VALUs idle
+  // (round 2: wave-uniform, w[(1 << s) - 1 + g] = psi_rev[((64 + hi) << s)
+  // + g]; round 3: per lane, the same from 1024; round 4: per store round).
+  uint32_t w2[15], w3[15], w4[4][3];
+  {
+    const int hi2 = (j << 4) | wave;                       // bits 15..10
+    const int hi3 = (j << 8) | (wave << 4) | (lane >> 2);  // bits 15..6
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+#pragma unroll
+      for (int g = 0; g < (1 << s); g++) {
+        w2[(1 << s) - 1 + g] = ld_uniform(tw, ((64 + hi2) << s) + g);
+        w3[(1 << s) - 1 + g] = tw[((1024 + hi3) << s) + g];
+      }
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int hi4 = (j << 12) | (wave << 8) | (v << 6) | lane;  // 15..2
+      w4[v][0] = tw[16384 + hi4];
+      w4[v][1] = tw[32768 + 2 * hi4];
+      w4[v][2] = tw[32768 + 2 * hi4 + 1];
+    }
+  }
   const uint32_t w0 = ld_uniform(tw, 1);
   const uint32_t w1 = ld_uniform(tw, 2 + (j >> 1));
   T x[16];
@@ -1133,12 +1177,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   // ---- round 2: stages 6..9 (bits 9..6); lane = bits 5..0, wave = 13..10
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = xs[qidx((wave << 10) | (k << 6) | lane)];
-  {
-    const int hi = (j << 4) | wave;  // index bits 15..10
-    const int base[4] = {64 + hi, 128 + (hi << 1), 256 + (hi << 2),
-                         512 + (hi << 3)};
-    radix16_1p<true>(ar, x, tw, base);
-  }
+  radix16_pre(ar, x, w2);
 #pragma unroll
   for (int k = 0; k < 16; k++) xs[qidx((wave << 10) | (k << 6) | lane)] = x[k];
   wave_lds_sync();
@@ -1147,12 +1186,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
   for (int k = 0; k < 16; k++)
     x[k] = xs[qidx((wave << 10) | (b96 << 6) | (k << 2) | b10)];
-  {
-    const int hi = (j << 8) | (wave << 4) | b96;  // index bits 15..6
-    const int base[4] = {1024 + hi, 2048 + (hi << 1), 4096 + (hi << 2),
-                         8192 + (hi << 3)};
-    radix16_1p<false>(ar, x, tw, base);
-  }
+  radix16_pre(ar, x, w3);
 #pragma unroll
   for (int k = 0; k < 16; k++)
     xs[qidx((wave << 10) | (b96 << 6) | (k << 2) | b10)] = x[k];
@@ -1187,13 +1221,12 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
     T y[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) y[i] = static_cast<T>(u[i]);
-    const int hi = (j << 12) | (wave << 8) | (v << 6) | lane;  // bits 15..2
-    const uint32_t wa = tw[16384 + hi];
+    const uint32_t wa = w4[v][0];
     const uint32_t waq = ar.twq(wa);
     ar.ct(y[0], y[2], wa, waq);
     ar.ct(y[1], y[3], wa, waq);
-    const uint32_t wb0 = tw[32768 + 2 * hi];
-    const uint32_t wb1 = tw[32768 + 2 * hi + 1];
+    const uint32_t wb0 = w4[v][1];
+    const uint32_t wb1 = w4[v][2];
     ar.ct(y[0], y[1], wb0, ar.twq(wb0));
     ar.ct(y[2], y[3], wb1, ar.twq(wb1));
     u32x4 o;
