@@ -525,11 +525,29 @@ __global__ __launch_bounds__(256) void ntt_fwd_rows(NttArgs a) {
     fwd_rows_body<kEpi, false>(a, lb, x, q, qinv, dst, xch, s2v);
 }
 
+// twiddles of the inverse row pass for this thread of a 16-row tile (row
+// tile blockIdx.x): w2 for stages 15..12 (columns 16c + k), w1 for stages
+// 11..8 (the row's)
+__device__ __forceinline__ void inv_row_twiddles(const uint32_t *itw,
+                                                 uint32_t (&w1)[15],
+                                                 uint32_t (&w2)[15]) {
+  const int c = threadIdx.x & 15;
+  const int row = blockIdx.x * kTileRows + (threadIdx.x >> 4);
+#pragma unroll
+  for (int s = 0, i = 0; s < 4; s++)
+#pragma unroll
+    for (int g = 0; g < (1 << s); g++, i++) {
+      w2[i] = itw[(4096 << s) + (row << (4 + s)) + (c << s) + g];
+      w1[i] = itw[(256 << s) + (row << s) + g];
+    }
+}
+
 // inverse, row pass: GS stages 15..8 of this workgroup's 16-row tile (row
 // tile blockIdx.x) with the limb's inverse twiddles tw; xin holds columns
 // 16c .. 16c+15 of the thread's row; dst (the limb) is left unreduced.
 template <bool kLazy>
-__device__ __forceinline__ void inv_rows_body(const uint32_t *tw,
+__device__ __forceinline__ void inv_rows_body(const uint32_t (&w1)[15],
+                                              const uint32_t (&w2)[15],
                                               uint32_t (&xin)[16], uint32_t q,
                                               uint32_t qinv, uint32_t *dst,
                                               int32_t *xch) {
@@ -538,17 +556,7 @@ __device__ __forceinline__ void inv_rows_body(const uint32_t *tw,
   const A ar(q, qinv);
   const int c = threadIdx.x & 15;
   const int r = threadIdx.x >> 4;
-  const int row = blockIdx.x * kTileRows + r;
   T *xr = reinterpret_cast<T *>(xch) + r * kRowPad;
-  uint32_t w1[15], w2[15];
-#pragma unroll
-  for (int s = 0, i = 0; s < 4; s++)
-#pragma unroll
-    for (int g = 0; g < (1 << s); g++, i++) {
-      w2[i] = tw[(4096 << s) + (row << (4 + s)) + (c << s) + g];
-      w1[i] = tw[(256 << s) + (row << s) + g];
-    }
-
   T x[16];
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = static_cast<T>(xin[k]);
@@ -607,6 +615,11 @@ __global__ __launch_bounds__(256) void ntt_inv_rows(NttArgs a) {
   u32x4 v4[4];
 #pragma unroll
   for (int v = 0; v < 4; v++) v4[v] = ld_at<u32x4>(tile, tile_lane_byte(v));
+  // twiddles of both half-passes, requested with the tile so their latency
+  // hides behind its load and the LDS regrouping (stages 15..12: columns
+  // 16c + k; stages 11..8: the row's)
+  uint32_t w1[15], w2[15];
+  inv_row_twiddles(a.tab.itw + (static_cast<size_t>(lb.ti) << kLogN), w1, w2);
   const uint32_t q = a.tab.q[lb.ti];
   const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
   if (a.src_mul != nullptr) {
@@ -639,11 +652,10 @@ __global__ __launch_bounds__(256) void ntt_inv_rows(NttArgs a) {
   uint32_t x[16];
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = xr[pidx(16 * c + k)];
-  const uint32_t *itw = a.tab.itw + (static_cast<size_t>(lb.ti) << kLogN);
   if (q < (1u << 30))
-    inv_rows_body<true>(itw, x, q, qinv, dst, xch);
+    inv_rows_body<true>(w1, w2, x, q, qinv, dst, xch);
   else
-    inv_rows_body<false>(itw, x, q, qinv, dst, xch);
+    inv_rows_body<false>(w1, w2, x, q, qinv, dst, xch);
 }
 
 // inverse, column pass: GS stages 7..0 (in place on dst) + constant epilogue
@@ -660,12 +672,17 @@ __device__ __forceinline__ void inv_cols_body(const NttArgs &a, const Limb &lb,
   const int c = threadIdx.x & (kTileCols - 1);
   const int rg = threadIdx.x / kTileCols;
   const uint32_t col = blockIdx.x * kTileCols + c;
-  uint32_t w2[15];
+  uint32_t w2[15], w1[15];
 #pragma unroll
   for (int s = 4, i = 0; s < 8; s++)
 #pragma unroll
     for (int g = 0; g < (1 << (s - 4)); g++, i++)
       w2[i] = tw[(1 << s) + (rg << (s - 4)) + g];
+  // the second half's (wave-uniform) twiddles and the epilogue constant,
+  // requested now so that no wave waits for them after the barrier
+#pragma unroll
+  for (int i = 0; i < 15; i++) w1[i] = ld_uniform(tw, 1 + i);
+  const uint32_t ce = a.cst[lb.ci];
 
   T x[16];
 #pragma unroll
@@ -692,13 +709,12 @@ __device__ __forceinline__ void inv_cols_body(const NttArgs &a, const Limb &lb,
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
-      const uint32_t w = ld_uniform(tw, (1 << s) + g);
+      const uint32_t w = w1[(1 << s) - 1 + g];
       const uint32_t wq = ar.twq(w);
 #pragma unroll
       for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
     }
   }
-  const uint32_t ce = a.cst[lb.ci];
   const uint32_t ceq = ar.twq(ce);
   const int32_t qs = static_cast<int32_t>(q);
 #pragma unroll
@@ -945,12 +961,13 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
     // first pass of ModDown's INTT (INTTForModDown, NTT.cu:973-1128) on
     // this limb of both accumulators, straight from the registers; the
     // accumulator itself is not stored
-    const uint32_t *itw = tab.itw + (static_cast<size_t>(ti) << kLogN);
+    uint32_t w1[15], w2[15];
+    inv_row_twiddles(tab.itw + (static_cast<size_t>(ti) << kLogN), w1, w2);
     const size_t ioff = static_cast<size_t>(l - a.intt_lo) << kLogN;
     __syncthreads();  // the group row passes' LDS reads are done
-    inv_rows_body<kLazy>(itw, accb, q, qinv, a.intt_b + ioff, xch);
+    inv_rows_body<kLazy>(w1, w2, accb, q, qinv, a.intt_b + ioff, xch);
     __syncthreads();  // ... and the first polynomial's store reads
-    inv_rows_body<kLazy>(itw, acca, q, qinv, a.intt_a + ioff, xch);
+    inv_rows_body<kLazy>(w1, w2, acca, q, qinv, a.intt_a + ioff, xch);
     return;
   }
   uint32_t *ob = a.acc_b + loff;
