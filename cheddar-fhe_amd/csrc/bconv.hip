@@ -7,23 +7,24 @@
 // c_i are centred int32 residues (the INTT epilogue's output, |c| < 2^30) and
 // T is the reference's "double Montgomery" table centre(qhat_i R^2 mod p_k).
 //
-// Byte-digit decomposition. The host folds the 2^-32 into the table,
-// U[k][i] = centre(T[k][i] 2^-32 mod p_k), and expands it over the four byte
-// positions of a source: V[k][(i,b)] = centre(U[k][i] 256^b mod p_k). A
+// Byte-digit decomposition. The host expands the table over the four byte
+// positions of a source: V[k][(i,b)] = centre(T[k][i] 256^b mod p_k). A
 // centred source c splits into signed digits d_0..d_3 in [-128, 127] with
 // c = sum_b d_b 256^b; the packed word (c + 0x808080) ^ 0x808080 holds exactly
 // those four int8 digits, so a source costs two VALU ops to decompose. V is
 // split the same way into digit planes v_0..v_3 (packed on the host). Then
 //
 //   acc_c[n][k] = sum_{(i,b)} d_b(c_i[n]) v_c[k][(i,b)]      (int8 MFMA, K=64)
-//   dst[k][n]   = (acc_0 + 2^8 acc_1 + 2^16 acc_2 + 2^24 acc_3) mod p_k
+//   dst[k][n]   = (acc_0 + 2^8 acc_1 + 2^16 acc_2 + 2^24 acc_3) 2^-32 mod p_k
 //
-// which is congruent to sum_i c_i U[k][i]. |acc_c| <= 64 * 128 * 128 = 2^20,
-// so the planes pair up exactly in int32 (acc_0 + 2^8 acc_1 and
-// acc_2 + 2^8 acc_3, each below 2^30), one fp64 fma joins the pairs exactly
-// (< 2^47), and one fp64 reduction gives the canonical residue:
-// bit-identical to the reference for every input. The MFMA results are
-// kept in VGPRs (the build passes -amdgpu-mfma-vgpr-form for this file).
+// which is congruent to sum_i c_i T[k][i] 2^-32. |acc_c| <= 64 * 128 * 128 =
+// 2^20, so the planes pair up exactly in int32 (acc_0 + 2^8 acc_1 and
+// acc_2 + 2^8 acc_3, each below 2^30), one 64-bit multiply-add joins the
+// pairs exactly (< 2^47), and one signed Montgomery reduction (the
+// reference's, Basic.cuh:72-88) gives the residue times 2^-32: the canonical
+// result is bit-identical to the reference's for every input. The MFMA
+// results are kept in VGPRs (the build passes -amdgpu-mfma-vgpr-form for
+// this file).
 //
 // One v_mfma_i32_16x16x64_i8 multiplies a 16-coefficient x 64 (sources x
 // bytes, zero-padded beyond 4 * src_len) tile by a 64 x 16-destination tile
@@ -118,8 +119,8 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
     const int pos = k + (k >= jb.skip_lo ? jb.skip_len : 0);
     const bool aux = pos >= m.num_q;
     const int ti = m.tab_off + pos + (aux ? m.tab_gap : 0);
-    const double p = live ? t.qd[ti] : 1.0;
-    const double pinv = live ? t.qinvd[ti] : 1.0;
+    const uint32_t p = live ? t.q[ti] : 1u;
+    const int32_t pinv = live ? t.qinv[ti] : 1;
 #pragma unroll
     for (int mt = 0; mt < kTilesPerWave; mt++) {
       v4i d[4];
@@ -137,13 +138,17 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
         uint32_t o[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          // pairs of planes in int32 (|acc_c| <= 2^21, so |lo|, |hi| < 2^30),
-          // then one exact fp64 fma: y = lo + 2^16 hi, |y| < 2^47
+          // pairs of planes in int32 (|acc_c| <= 2^21, so |lo|, |hi| <
+          // 2^30), one 64-bit multiply-add y = lo + 2^16 hi (|y| < 2^47,
+          // far inside the (-p 2^31, p 2^31) a signed Montgomery reduction
+          // takes), reduced to y 2^-32 in (-p, p), then made canonical
           const int32_t lo = d[0][i] + d[1][i] * 256;
           const int32_t hi = d[2][i] + d[3][i] * 256;
-          const double y = __builtin_fma(static_cast<double>(hi), 65536.0,
-                                         static_cast<double>(lo));
-          o[i] = reduce_f64(y, p, pinv);
+          const int64_t y = static_cast<int64_t>(hi) * 65536 + lo;
+          const uint32_t u =
+              static_cast<uint32_t>(mont_reduce_lazy(y, p, pinv));
+          const uint32_t up = u + p;
+          o[i] = u < up ? u : up;  // unsigned min: u + p when negative
         }
         const int n = n_wave + mt * 16 + 4 * g;
         *reinterpret_cast<uint4 *>(jb.dst + (static_cast<size_t>(pos) << kLogN) +
@@ -184,23 +189,12 @@ extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
   std::memset(out, 0, static_cast<size_t>(tiles) * nk * 4 * kPlaneBytes);
   for (int k = 0; k < dst_len; k++) {
     const int64_t p = dst_primes[k];
-    // 2^-32 mod p by extended Euclid on (p, 2^32 mod p)
-    int64_t r0 = p, r1 = static_cast<int64_t>((1ull << 32) % static_cast<uint64_t>(p));
-    int64_t t0 = 0, t1 = 1;
-    while (r1 != 0) {
-      int64_t qq = r0 / r1, tmp = t0 - qq * t1;
-      t0 = t1;
-      t1 = tmp;
-      tmp = r0 - qq * r1;
-      r0 = r1;
-      r1 = tmp;
-    }
-    const int64_t rinv = t0 < 0 ? t0 + p : t0;
     const int tt = k / 16, col = k % 16;
     for (int i = 0; i < src_len; i++) {
-      const int64_t tv = centre_mod(table_ref[static_cast<size_t>(k) * src_len + i], p);
-      const int64_t u = centre_mod((tv < 0 ? tv + p : tv) * rinv, p);
-      int64_t ub = u < 0 ? u + p : u;  // U * 256^b, canonical
+      // the reference's table entry T itself: the kernel's Montgomery
+      // reduction supplies the 2^-32
+      const int64_t u = centre_mod(table_ref[static_cast<size_t>(k) * src_len + i], p);
+      int64_t ub = u < 0 ? u + p : u;  // T * 256^b, canonical
       for (int bb = 0; bb < 4; bb++) {
         const int64_t v = centre_mod(ub, p);  // |v| < 2^30
         // signed digits of v: (v + 0x808080) has unsigned low bytes e_0..e_2
