@@ -1,7 +1,10 @@
 """Builds lib/libcheddar_amd.so (HIP kernels for gfx950 + C++ host + C-ABI).
 
-Usage: python cheddar-fhe_amd/build.py [--jobs N]
+Usage: python cheddar-fhe_amd/build.py [--jobs N] [--phase-timestamps DIR]
 Compiles every source each time it is called (hipcc, no cache).
+--phase-timestamps builds an instrumented copy into DIR instead (the forward
+NTT records per-wave phase timestamps; tests/cpp/ntt_phase_timeline.cpp reads
+them).
 """
 import argparse
 import concurrent.futures as cf
@@ -46,9 +49,9 @@ SOURCES = [
 ]
 
 
-def compile_one(rel, device, extra):
+def compile_one(rel, device, extra, obj_dir=OBJ_DIR):
     src = os.path.join(PKG, rel)
-    obj = os.path.join(OBJ_DIR, rel.replace("/", "_") + ".o")
+    obj = os.path.join(obj_dir, rel.replace("/", "_") + ".o")
     if device:
         cmd = [HIPCC] + COMMON + DEVICE + extra + ["-c", src, "-o", obj]
     else:
@@ -61,23 +64,36 @@ def compile_one(rel, device, extra):
     return obj
 
 
-def build(jobs=8):
-    os.makedirs(OUT_DIR, exist_ok=True)
-    os.makedirs(OBJ_DIR, exist_ok=True)
+def build(jobs=8, phase_timestamps=None):
+    """phase_timestamps: a directory for an instrumented copy of the library
+    (the forward NTT's per-wave phase timestamps, for measurement only);
+    the product library is not touched then"""
+    out_dir, obj_dir, lib, extra = OUT_DIR, OBJ_DIR, LIB, []
+    if phase_timestamps:
+        out_dir = os.path.abspath(phase_timestamps)
+        obj_dir = os.path.join(out_dir, "_build")
+        lib = os.path.join(out_dir, "libcheddar_amd.so")
+        extra = ["-DCHD_PHASE_TIMESTAMPS"]
+    os.makedirs(out_dir, exist_ok=True)
+    os.makedirs(obj_dir, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: compile_one(*s), SOURCES))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(
+            lambda s: compile_one(s[0], s[1], s[2] + (extra if s[1] else []),
+                                  obj_dir), SOURCES))
+    tmp = lib + ".tmp"
     cmd = [HIPCC, "-shared", "--offload-arch=" + ARCH, "-o", tmp] + objs
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError("link failed: %s\n%s" % (res.stdout, res.stderr))
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--phase-timestamps", metavar="DIR",
+                    help="build an instrumented copy into DIR instead")
     a = ap.parse_args()
-    print(build(a.jobs))
+    print(build(a.jobs, a.phase_timestamps))
     sys.exit(0)

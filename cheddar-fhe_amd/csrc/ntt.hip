@@ -1016,6 +1016,26 @@ __global__ __launch_bounds__(256) void modup_keyacc(KeyAccBatch b) {
 // The four workgroups of a limb get block ids 8 apart (the same XCD under
 // round-robin dispatch) so three of the four reads of the limb hit in L2.
 // ------------------------------------------------------------------------
+// Opt-in instrumentation (built only with CHD_PHASE_TIMESTAMPS, never in
+// the product library): each wave of ntt_fwd_1p writes the 100 MHz
+// real-time clock at its phase boundaries (start, round-1 loads done, round 1
+// done, barrier passed, round 2 done, round 3 done, stores done) into a
+// buffer of 8 words per wave, lane 0 with an ordinary vector store.
+#ifdef CHD_PHASE_TIMESTAMPS
+__device__ unsigned long long *g_phase_ts = nullptr;
+__device__ int g_phase_waves = 0;
+__device__ __forceinline__ void phase_mark(int slot) {
+  const int wid = blockIdx.x * 16 + (threadIdx.x >> 6);
+  const unsigned long long now = __builtin_amdgcn_s_memrealtime();
+  if ((threadIdx.x & 63) == 0 && g_phase_ts != nullptr &&
+      wid < g_phase_waves && slot >= 0 && slot < 8)
+    g_phase_ts[wid * 8 + slot] = now;
+}
+#define CHD_PHASE(k) phase_mark(k)
+#else
+#define CHD_PHASE(k)
+#endif
+
 constexpr int kQuarter = kN / 4;
 constexpr int kQLdsWords = kQuarter + kQuarter / 16;  // 4 pad words per 64
 __device__ __forceinline__ int qidx(int n) { return n + ((n >> 6) << 2); }
@@ -1085,6 +1105,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  CHD_PHASE(0);
   // Twiddles of rounds 2-4, requested before the round-1 loads: after the
   // workgroup barrier every wave of the CU computes at once, and a round
   // that first waited for its twiddles would leave the VALUs idle
@@ -1180,14 +1201,17 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
       x[k] = hi1 ? yb : ya;
     }
   }
+  CHD_PHASE(1);
   {
     const int base[4] = {4 + j, 8 + 2 * j, 16 + 4 * j, 32 + 8 * j};
     radix16_1p<true>(ar, x, tw, base);
   }
+  CHD_PHASE(2);
   T *xs = reinterpret_cast<T *>(lds);
 #pragma unroll
   for (int k = 0; k < 16; k++) xs[qidx((k << 10) | t)] = x[k];
   __syncthreads();
+  CHD_PHASE(3);
   // From here on each wave reads and writes only its own 1024-element block
   // (index bits 13..10 = wave), so the exchanges of rounds 3 and 4 need no
   // workgroup barrier.
@@ -1198,6 +1222,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
   for (int k = 0; k < 16; k++) xs[qidx((wave << 10) | (k << 6) | lane)] = x[k];
   wave_lds_sync();
+  CHD_PHASE(4);
   // ---- round 3: stages 10..13 (bits 5..2); lane = bits 9..6 | bits 1..0
   const int b96 = lane >> 2, b10 = lane & 3;
 #pragma unroll
@@ -1208,6 +1233,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   for (int k = 0; k < 16; k++)
     xs[qidx((wave << 10) | (b96 << 6) | (k << 2) | b10)] = x[k];
   wave_lds_sync();
+  CHD_PHASE(5);
   // ---- round 4: stages 14, 15 (bits 1..0); lane = bits 7..2, wave =
   // bits 13..10, store round v = bits 9..8
   const int32_t qs = static_cast<int32_t>(q);
@@ -1263,6 +1289,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
     }
     st_nt<u32x4>(dst, boff, o);
   }
+  CHD_PHASE(6);
 }
 
 // grid: 1D, 4 * roundup(limbs * polys, 8) blocks of 1024 threads
@@ -1428,6 +1455,22 @@ extern "C" int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m,
                                       hipGetErrorString(e));
   return 0;
 }
+
+#ifdef CHD_PHASE_TIMESTAMPS
+// the instrumented build only: where ntt_fwd_1p's waves write their phase
+// timestamps (8 words per wave, waves = 16 per workgroup); NULL stops them
+extern "C" int chd_debug_phase_timestamps(unsigned long long *buf,
+                                          int waves) {
+  if (buf == nullptr) waves = 0;
+  if (waves < 0) return set_error(CHD_ERR_ARG, "invalid wave count");
+  if (hipMemcpyToSymbol(HIP_SYMBOL(g_phase_ts), &buf, sizeof(buf)) !=
+          hipSuccess ||
+      hipMemcpyToSymbol(HIP_SYMBOL(g_phase_waves), &waves, sizeof(waves)) !=
+          hipSuccess)
+    return set_error(CHD_ERR_HIP, "chd_debug_phase_timestamps");
+  return 0;
+}
+#endif
 
 extern "C" int chd_k_ntt_fwd_moddown(const chd_tables *t,
                                      const chd_limb_map *m, uint32_t *dst,

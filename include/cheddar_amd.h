@@ -93,7 +93,7 @@ int chd_param_create(chd_param **out, int log_degree, double base_scale,
                      int num_levels, const uint32_t *main_primes, int num_main,
                      const uint32_t *aux_primes, int num_aux,
                      const uint32_t *ter_primes, int num_ter);
-/* A parameter set from the reference's JSON layout (parameters/*.json:
+/* A parameter set from the reference's JSON layout (the files in parameters/:
  * log_degree, log_default_scale, default_encryption_level, main_primes,
  * terminal_primes, auxiliary_primes, level_config, additional_base), the
  * file's text in json_text (unittest/Testbed.h:95-179). */
