@@ -36,8 +36,7 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
   const int n = 1 << log_degree;
   const size_t T = primes.size();
   std::vector<int32_t> qinv(T);
-  std::vector<double> qd(T), qinvd(T);
-  std::vector<uint32_t> rinv(T), ninv(T), ninv_mont(T), r2(T);
+  std::vector<uint32_t> ninv(T), ninv_mont(T), r2(T);
   std::vector<uint32_t> tw(T * n), itw(T * n);
   for (size_t i = 0; i < T; i++) {
     const uint32_t q = primes[i];
@@ -45,9 +44,6 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
       throw std::invalid_argument("prime " + std::to_string(q) +
                                   " is not an NTT-friendly prime below 2^31");
     qinv[i] = pm::inv_mod_base(q);
-    qd[i] = static_cast<double>(q);
-    qinvd[i] = 1.0 / static_cast<double>(q);
-    rinv[i] = pm::invmod(static_cast<uint32_t>((1ull << 32) % q), q);
     ninv[i] = pm::invmod(static_cast<uint32_t>(n % q), q);
     ninv_mont[i] = pm::to_mont(ninv[i], q);
     r2[i] = pm::to_mont(pm::to_mont(1, q), q);
@@ -66,9 +62,6 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
   }
   q_.Upload(primes);
   qinv_.Upload(qinv);
-  qd_.Upload(qd);
-  qinvd_.Upload(qinvd);
-  rinv_.Upload(rinv);
   tw_.Upload(tw);
   itw_.Upload(itw);
   ninv_.Upload(ninv);
@@ -76,9 +69,6 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
   r2_.Upload(r2);
   tab_.q = q_.as<uint32_t>();
   tab_.qinv = qinv_.as<int32_t>();
-  tab_.qd = qd_.as<double>();
-  tab_.qinvd = qinvd_.as<double>();
-  tab_.rinv = rinv_.as<uint32_t>();
   tab_.tw = tw_.as<uint32_t>();
   tab_.itw = itw_.as<uint32_t>();
 }

@@ -24,9 +24,6 @@ extern "C" {
 typedef struct chd_tables {
   const uint32_t *q;        /* [T] primes                                 */
   const int32_t *qinv;      /* [T] q^-1 mod 2^32 (signed)                 */
-  const double *qd;         /* [T] q as double                            */
-  const double *qinvd;      /* [T] 1/q                                    */
-  const uint32_t *rinv;     /* [T] 2^-32 mod q                            */
   const uint32_t *tw;       /* [T][N] ToMont(psi^brev(j))                 */
   const uint32_t *itw;      /* [T][N] ToMont(psi^-brev(j))                */
 } chd_tables;

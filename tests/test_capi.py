@@ -81,8 +81,7 @@ P = ctypes.c_void_p
 
 
 class Tables(ctypes.Structure):
-    _fields_ = [(n, P) for n in ("q", "qinv", "qd", "qinvd", "rinv", "tw",
-                                 "itw")]
+    _fields_ = [(n, P) for n in ("q", "qinv", "tw", "itw")]
 
 
 class LimbMap(ctypes.Structure):
