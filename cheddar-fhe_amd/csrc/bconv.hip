@@ -69,11 +69,33 @@ __device__ __forceinline__ int digits(int32_t c) {
   return static_cast<int>((static_cast<uint32_t>(c) + 0x808080u) ^ 0x808080u);
 }
 
+// the four digit planes of destination tile tt, K chunk ch (zero beyond the
+// job's chunks)
+template <int kChunks>
+__device__ __forceinline__ void load_planes(v4i (&bp)[kChunks][4],
+                                            const v4i *__restrict__ tab,
+                                            int tt, int nk, int lane) {
+#pragma unroll
+  for (int ch = 0; ch < kChunks; ch++) {
+    if (ch < nk) {
+      const v4i *tp = tab + (static_cast<size_t>(tt * nk + ch) * 4) * 64 + lane;
+      bp[ch][0] = tp[0];
+      bp[ch][1] = tp[64];
+      bp[ch][2] = tp[128];
+      bp[ch][3] = tp[192];
+    } else {
+      const v4i z = {0, 0, 0, 0};
+      bp[ch][0] = bp[ch][1] = bp[ch][2] = bp[ch][3] = z;
+    }
+  }
+}
+
 template <int kChunks>
 __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
                                                        chd_limb_map m,
                                                        BconvBatch b) {
-  const chd_bconv_job &jb = b.job[blockIdx.z];
+  // the job by value: its fields stay in scalar registers
+  const chd_bconv_job jb = b.job[blockIdx.z];
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int g = lane >> 4;
@@ -83,8 +105,11 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
   const v4i *__restrict__ tab = static_cast<const v4i *>(jb.table);
   // this job's K chunks (its table holds exactly that many per tile)
   const int nk = kChunks == 1 ? 1 : (jb.src_len + kChunkSrc - 1) / kChunkSrc;
-  // A operands of this wave's coefficient tiles, per K chunk
-  v4i a[kChunks][kTilesPerWave];
+  // Source words of this wave's coefficient tiles, per K chunk. Every load
+  // is issued (sources beyond src_len read the last source and are zeroed
+  // after), so they are all in flight together instead of one guarded load
+  // at a time.
+  int32_t cw[kChunks][kTilesPerWave][4];
 #pragma unroll
   for (int ch = 0; ch < kChunks; ch++)
 #pragma unroll
@@ -93,49 +118,66 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const int i = kChunkSrc * ch + 4 * g + j;
-        const int32_t c =
-            i < jb.src_len ? src[(static_cast<size_t>(i) << kLogN) + n] : 0;
-        a[ch][mt][j] = digits(c);
+        const int ic = min(i, jb.src_len - 1);
+        cw[ch][mt][j] = src[(static_cast<size_t>(ic) << kLogN) + n];
       }
     }
   const int tiles = (jb.dst_len + 15) >> 4;
-  for (int tt = 0; tt < tiles; tt++) {
-    v4i bp[kChunks][4];
-#pragma unroll
-    for (int ch = 0; ch < kChunks; ch++) {
-      if (ch < nk) {
-        const v4i *tp =
-            tab + (static_cast<size_t>(tt * nk + ch) * 4) * 64 + lane;
-        bp[ch][0] = tp[0];
-        bp[ch][1] = tp[64];
-        bp[ch][2] = tp[128];
-        bp[ch][3] = tp[192];
-      } else {
-        const v4i z = {0, 0, 0, 0};
-        bp[ch][0] = bp[ch][1] = bp[ch][2] = bp[ch][3] = z;
-      }
-    }
-    const int k = tt * 16 + r;
-    const bool live = k < jb.dst_len;
-    const int pos = k + (k >= jb.skip_lo ? jb.skip_len : 0);
+  // prime of this lane's destination in tile tt (dead lanes beyond dst_len
+  // take the last destination's: their results are not stored)
+  auto prime_of = [&](int tt, uint32_t &p, int32_t &pinv, int &pos) {
+    const int kc = min(tt * 16 + r, jb.dst_len - 1);
+    pos = kc + (kc >= jb.skip_lo ? jb.skip_len : 0);
     const bool aux = pos >= m.num_q;
     const int ti = m.tab_off + pos + (aux ? m.tab_gap : 0);
-    const uint32_t p = live ? t.q[ti] : 1u;
-    const int32_t pinv = live ? t.qinv[ti] : 1;
+    p = t.q[ti];
+    pinv = t.qinv[ti];
+  };
+  // destination tile 0's primes and planes, requested with the sources
+  uint32_t p;
+  int32_t pinv;
+  int pos;
+  prime_of(0, p, pinv, pos);
+  v4i bp[kChunks][4];
+  load_planes<kChunks>(bp, tab, 0, nk, lane);
+  // A operands (the sources' signed digits)
+  v4i a[kChunks][kTilesPerWave];
 #pragma unroll
-    for (int mt = 0; mt < kTilesPerWave; mt++) {
-      v4i d[4];
+  for (int ch = 0; ch < kChunks; ch++)
+#pragma unroll
+    for (int mt = 0; mt < kTilesPerWave; mt++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int i = kChunkSrc * ch + 4 * g + j;
+        a[ch][mt][j] = digits(i < jb.src_len ? cw[ch][mt][j] : 0);
+      }
+  for (int tt = 0; tt < tiles; tt++) {
+    const bool live = tt * 16 + r < jb.dst_len;
+    // the MFMAs of this tile, then the next tile's primes and planes go out
+    // while this tile is recombined and stored
+    v4i d[kTilesPerWave][4];
+#pragma unroll
+    for (int mt = 0; mt < kTilesPerWave; mt++)
 #pragma unroll
       for (int pl = 0; pl < 4; pl++) {
         const v4i z = {0, 0, 0, 0};
-        d[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0][mt], bp[0][pl], z,
-                                                      0, 0, 0);
+        d[mt][pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0][mt], bp[0][pl],
+                                                          z, 0, 0, 0);
 #pragma unroll
         for (int ch = 1; ch < kChunks; ch++)
-          d[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[ch][mt], bp[ch][pl],
-                                                        d[pl], 0, 0, 0);
+          d[mt][pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+              a[ch][mt], bp[ch][pl], d[mt][pl], 0, 0, 0);
       }
-      if (live) {
+    const uint32_t pc = p;
+    const int32_t pinvc = pinv;
+    const int posc = pos;
+    if (tt + 1 < tiles) {
+      prime_of(tt + 1, p, pinv, pos);
+      load_planes<kChunks>(bp, tab, tt + 1, nk, lane);
+    }
+    if (live) {
+#pragma unroll
+      for (int mt = 0; mt < kTilesPerWave; mt++) {
         uint32_t o[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -143,12 +185,12 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
           // 2^30), one 64-bit multiply-add y = lo + 2^16 hi (|y| < 2^47,
           // far inside the (-p 2^31, p 2^31) a signed Montgomery reduction
           // takes), reduced to y 2^-32 in (-p, p), then made canonical
-          const int32_t lo = d[0][i] + d[1][i] * 256;
-          const int32_t hi = d[2][i] + d[3][i] * 256;
+          const int32_t lo = d[mt][0][i] + d[mt][1][i] * 256;
+          const int32_t hi = d[mt][2][i] + d[mt][3][i] * 256;
           const int64_t y = static_cast<int64_t>(hi) * 65536 + lo;
           const uint32_t u =
-              static_cast<uint32_t>(mont_reduce_lazy(y, p, pinv));
-          const uint32_t up = u + p;
+              static_cast<uint32_t>(mont_reduce_lazy(y, pc, pinvc));
+          const uint32_t up = u + pc;
           o[i] = u < up ? u : up;  // unsigned min: u + p when negative
         }
         // streaming store: the 16 destinations of a lane group are 16
@@ -158,7 +200,7 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
         const v4u ov = {o[0], o[1], o[2], o[3]};
         __builtin_nontemporal_store(
             ov, reinterpret_cast<v4u *>(
-                    jb.dst + (static_cast<size_t>(pos) << kLogN) + n));
+                    jb.dst + (static_cast<size_t>(posc) << kLogN) + n));
       }
     }
   }
