@@ -59,10 +59,28 @@ constexpr int kMaxSrc = kChunkSrc * kMaxChunks;
 constexpr int kTilesPerWave = 2;
 constexpr int kCoefPerBlock = (kThreads / 64) * kTilesPerWave * 16;
 constexpr int kPlaneBytes = 64 * 16;   // one digit plane of a 16-dst tile
+static_assert(kTilesPerWave == 2,
+              "a packed last tile carries exactly the wave's two coefficient "
+              "tiles");
 
 struct BconvBatch {
   chd_bconv_job job[CHD_MAX_BCONV_JOBS];
 };
+
+// A job with at most 8 sources uses only K 0..31 of the MFMA (8 sources x 4
+// bytes). When its last destination tile is at most half full (1..8 of 16
+// destinations), that tile is "packed": the second K half carries a second
+// group of 16 coefficients, and destination columns 8..15 repeat columns
+// 0..7 for that group, so no lane of the tile computes a dead destination:
+//   A row r = [coefficient n_wave + r, K 0..31 | coefficient n_wave + 16 + r,
+//              K 32..63]
+//   B column c < 8 = [V(16 t + c) | 0],  column c >= 8 = [0 | V(16 t + c - 8)]
+// The host table layout and the kernel both follow this rule.
+__host__ __device__ __forceinline__ bool packed_last_tile(int src_len,
+                                                         int dst_len) {
+  const int rem = dst_len & 15;
+  return src_len <= 8 && rem != 0 && rem <= 8;
+}
 
 // four signed byte digits of a centred value |c| < 2^30, packed as int8 x4
 __device__ __forceinline__ int digits(int32_t c) {
@@ -105,28 +123,39 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
   const v4i *__restrict__ tab = static_cast<const v4i *>(jb.table);
   // this job's K chunks (its table holds exactly that many per tile)
   const int nk = kChunks == 1 ? 1 : (jb.src_len + kChunkSrc - 1) / kChunkSrc;
+  const int tiles = (jb.dst_len + 15) >> 4;
+  // at most 8 sources: lanes 32..63 (K 32..63, zero rows of B in the other
+  // tiles) hold the sources of the second coefficient group instead
+  const bool narrow = jb.src_len <= 8;
+  const bool packed = packed_last_tile(jb.src_len, jb.dst_len);
+  const int regular = packed ? tiles - 1 : tiles;
   // Source words of this wave's coefficient tiles, per K chunk. Every load
   // is issued (sources beyond src_len read the last source and are zeroed
   // after), so they are all in flight together instead of one guarded load
   // at a time.
   int32_t cw[kChunks][kTilesPerWave][4];
+  int si[kChunks][4];  // source index of each word (the same for both mt)
 #pragma unroll
   for (int ch = 0; ch < kChunks; ch++)
 #pragma unroll
     for (int mt = 0; mt < kTilesPerWave; mt++) {
-      const int n = n_wave + mt * 16 + r;
+      const bool second = ch == 0 && narrow && g >= 2;
+      const int n = n_wave + (mt == 1 || second ? 16 : 0) + r;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const int i = kChunkSrc * ch + 4 * g + j;
+        const int i = ch == 0 && narrow ? 4 * (g & 1) + j
+                                        : kChunkSrc * ch + 4 * g + j;
+        si[ch][j] = i;
         const int ic = min(i, jb.src_len - 1);
         cw[ch][mt][j] = src[(static_cast<size_t>(ic) << kLogN) + n];
       }
     }
-  const int tiles = (jb.dst_len + 15) >> 4;
   // prime of this lane's destination in tile tt (dead lanes beyond dst_len
-  // take the last destination's: their results are not stored)
+  // take the last destination's: their results are not stored); the packed
+  // tile's column c stands for destination 16 t + (c & 7)
   auto prime_of = [&](int tt, uint32_t &p, int32_t &pinv, int &pos) {
-    const int kc = min(tt * 16 + r, jb.dst_len - 1);
+    const int col = packed && tt == tiles - 1 ? (r & 7) : r;
+    const int kc = min(tt * 16 + col, jb.dst_len - 1);
     pos = kc + (kc >= jb.skip_lo ? jb.skip_len : 0);
     const bool aux = pos >= m.num_q;
     const int ti = m.tab_off + pos + (aux ? m.tab_gap : 0);
@@ -147,11 +176,34 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
 #pragma unroll
     for (int mt = 0; mt < kTilesPerWave; mt++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int i = kChunkSrc * ch + 4 * g + j;
-        a[ch][mt][j] = digits(i < jb.src_len ? cw[ch][mt][j] : 0);
-      }
-  for (int tt = 0; tt < tiles; tt++) {
+      for (int j = 0; j < 4; j++)
+        a[ch][mt][j] = digits(si[ch][j] < jb.src_len ? cw[ch][mt][j] : 0);
+  // Recombination of the four planes of one MFMA output (4 coefficients of
+  // one destination): pairs of planes in int32 (|acc_c| <= 2^21, so |lo|,
+  // |hi| < 2^30), one 64-bit multiply-add y = lo + 2^16 hi (|y| < 2^47, far
+  // inside the (-p 2^31, p 2^31) a signed Montgomery reduction takes),
+  // reduced to y 2^-32 in (-p, p), then made canonical. Streaming store: the
+  // 16 destinations of a lane group are 16 limbs apart, and keeping them out
+  // of the caches measured 1.5 % faster per HMult (both of its BConv
+  // launches).
+  auto finish = [&](const v4i (&d)[4], uint32_t pc, int32_t pinvc, int posc,
+                    int n) {
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int32_t lo = d[0][i] + d[1][i] * 256;
+      const int32_t hi = d[2][i] + d[3][i] * 256;
+      const int64_t y = static_cast<int64_t>(hi) * 65536 + lo;
+      const uint32_t u = static_cast<uint32_t>(mont_reduce_lazy(y, pc, pinvc));
+      const uint32_t up = u + pc;
+      o[i] = u < up ? u : up;  // unsigned min: u + p when negative
+    }
+    const v4u ov = {o[0], o[1], o[2], o[3]};
+    __builtin_nontemporal_store(
+        ov, reinterpret_cast<v4u *>(jb.dst +
+                                    (static_cast<size_t>(posc) << kLogN) + n));
+  };
+  for (int tt = 0; tt < regular; tt++) {
     const bool live = tt * 16 + r < jb.dst_len;
     // the MFMAs of this tile, then the next tile's primes and planes go out
     // while this tile is recombined and stored
@@ -177,32 +229,22 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
     }
     if (live) {
 #pragma unroll
-      for (int mt = 0; mt < kTilesPerWave; mt++) {
-        uint32_t o[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          // pairs of planes in int32 (|acc_c| <= 2^21, so |lo|, |hi| <
-          // 2^30), one 64-bit multiply-add y = lo + 2^16 hi (|y| < 2^47,
-          // far inside the (-p 2^31, p 2^31) a signed Montgomery reduction
-          // takes), reduced to y 2^-32 in (-p, p), then made canonical
-          const int32_t lo = d[mt][0][i] + d[mt][1][i] * 256;
-          const int32_t hi = d[mt][2][i] + d[mt][3][i] * 256;
-          const int64_t y = static_cast<int64_t>(hi) * 65536 + lo;
-          const uint32_t u =
-              static_cast<uint32_t>(mont_reduce_lazy(y, pc, pinvc));
-          const uint32_t up = u + pc;
-          o[i] = u < up ? u : up;  // unsigned min: u + p when negative
-        }
-        // streaming store: the 16 destinations of a lane group are 16
-        // limbs apart, and keeping them out of the caches measured 1.5 %
-        // faster per HMult (both of its BConv launches)
-        const int n = n_wave + mt * 16 + 4 * g;
-        const v4u ov = {o[0], o[1], o[2], o[3]};
-        __builtin_nontemporal_store(
-            ov, reinterpret_cast<v4u *>(
-                    jb.dst + (static_cast<size_t>(posc) << kLogN) + n));
-      }
+      for (int mt = 0; mt < kTilesPerWave; mt++)
+        finish(d[mt], pc, pinvc, posc, n_wave + mt * 16 + 4 * g);
     }
+  }
+  if (packed) {
+    // the last tile, both coefficient groups at once (one K chunk: nk is 1
+    // for at most 8 sources); its primes and planes are already loaded
+    v4i d[4];
+#pragma unroll
+    for (int pl = 0; pl < 4; pl++) {
+      const v4i z = {0, 0, 0, 0};
+      d[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0][0], bp[0][pl], z, 0,
+                                                    0, 0);
+    }
+    if ((tiles - 1) * 16 + (r & 7) < jb.dst_len)
+      finish(d, p, pinv, pos, n_wave + (r >> 3) * 16 + 4 * g);
   }
 }
 
@@ -233,11 +275,15 @@ extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
     return set_error(CHD_ERR_ARG, "chd_bconv_table_pack: invalid argument");
   const int tiles = (dst_len + 15) / 16;
   const int nk = (src_len + kChunkSrc - 1) / kChunkSrc;
+  const bool packed = packed_last_tile(src_len, dst_len);
   int8_t *out = static_cast<int8_t *>(host_out);
   std::memset(out, 0, static_cast<size_t>(tiles) * nk * 4 * kPlaneBytes);
   for (int k = 0; k < dst_len; k++) {
     const int64_t p = dst_primes[k];
     const int tt = k / 16, col = k % 16;
+    // a packed last tile holds each destination twice: column col with K
+    // 0..31 and column col + 8 with K 32..63
+    const int copies = packed && tt == tiles - 1 ? 2 : 1;
     for (int i = 0; i < src_len; i++) {
       // the reference's table entry T itself: the kernel's Montgomery
       // reduction supplies the 2^-32
@@ -254,14 +300,16 @@ extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
         dig[3] = static_cast<int8_t>(w >> 24);
         // K index of (i, bb): its chunk, and its lane / byte in that
         // chunk's B operand
-        const int kk = 4 * i + bb;
-        const int ch = kk / 64;
-        const int lane = ((kk % 64) / 16) * 16 + col;
-        const int byte = kk % 16;
-        for (int c = 0; c < 4; c++)
-          out[(((static_cast<size_t>(tt) * nk + ch) * 4 + c) * 64 + lane) *
-                  16 +
-              byte] = dig[c];
+        for (int cp = 0; cp < copies; cp++) {
+          const int kk = 4 * i + bb + 32 * cp;
+          const int ch = kk / 64;
+          const int lane = ((kk % 64) / 16) * 16 + col + 8 * cp;
+          const int byte = kk % 16;
+          for (int c = 0; c < 4; c++)
+            out[(((static_cast<size_t>(tt) * nk + ch) * 4 + c) * 64 + lane) *
+                    16 +
+                byte] = dig[c];
+        }
         ub = (ub * 256) % p;
       }
     }
