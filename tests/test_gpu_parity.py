@@ -130,6 +130,25 @@ def test_bconv_two_k_chunks(chd, src_len):
     assert np.array_equal(host(out), _orc.bconv(x, o2, dst_p, 16))
 
 
+@pytest.mark.parametrize("src_len,dst_len", [
+    (1, 1), (3, 5), (8, 8), (8, 9), (7, 16), (8, 17), (5, 23), (8, 24),
+    (8, 25), (9, 24), (16, 8), (16, 24), (2, 40)])
+def test_bconv_tile_shapes(chd, src_len, dst_len):
+    """full, partial and packed last destination tiles: with at most 8
+    sources a last tile of 1..8 destinations carries both coefficient groups
+    of a wave in the two K halves; 9 or more sources, or more than 8 in the
+    last tile, keep the plain layout"""
+    src_p, dst_p = Q30[:src_len], Q31[:dst_len]
+    plan = chd.BconvPlan(src_p, dst_p)
+    _, o2 = _orc.modswitch_consts(src_p, dst_p, 16)
+    x = centred_limbs(rng(100 + 50 * src_len + dst_len), src_p)
+    x[:, :32] = np.array([(p - 1) // 2 for p in src_p], np.int32)[:, None]
+    x[:, 32:64] = -x[:, :32]
+    out = zeros(dst_len, N)
+    plan.apply(out, dev(x.view(np.uint32)))
+    assert np.array_equal(host(out), _orc.bconv(x, o2, dst_p, 16))
+
+
 # --------------------------------------------------- key-switch pipeline ----
 @pytest.fixture(scope="module")
 def ks(chd):
