@@ -1292,9 +1292,12 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   for (int v = 0; v < 4; v++) {
     const int n = (wave << 10) | (b96 << 6) | ((4 * v + b10) << 2);
     const uint32_t boff = 4u * static_cast<uint32_t>(n);
+    // src2 with default (temporal) loads: a quad reads 64 of a line's 128
+    // bytes per store round and the next round reads the rest, which the
+    // streaming hint would have evicted (2.1 us slower per HMult, measured)
     u32x4 s2 = {0, 0, 0, 0};
     if constexpr (kEpi == kEpiModDown)
-      if (s2p != nullptr) s2 = ld_nt<u32x4>(s2p, boff);
+      if (s2p != nullptr) s2 = ld_at<u32x4>(s2p, boff);
     T y[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) y[i] = x[4 * v + i];
