@@ -3,8 +3,10 @@
 // instrumented library (cheddar-fhe_amd/build.py --phase-timestamps DIR),
 // whose waves record the 100 MHz real-time clock at each phase boundary;
 // prints, per boundary, the spread over all waves of the time since the
-// first wave started. Exits with an error on the product library, which has
-// no timestamp hook.
+// first wave started. The argument (default 500) is the number of forwards
+// run back to back, first without and then with timestamps, so the table
+// (the last forward's) shows the kernel at sustained clocks. Exits with an
+// error on the product library, which has no timestamp hook.
 #include <hip/hip_runtime.h>
 #include <dlfcn.h>
 
@@ -50,7 +52,7 @@ std::vector<uint32_t> ntt_primes(int bits, int count) {
 }  // namespace
 
 int main(int argc, char **argv) {
-  const int reps = argc > 1 ? std::atoi(argv[1]) : 3;
+  const int warmup = argc > 1 ? std::max(1, std::atoi(argv[1])) : 500;
   using set_fn = int (*)(unsigned long long *, int);
   auto set_ts = reinterpret_cast<set_fn>(
       dlsym(RTLD_DEFAULT, "chd_debug_phase_timestamps"));
@@ -83,39 +85,51 @@ int main(int argc, char **argv) {
                           "round 1",        "barrier passed",
                           "round 2",        "round 3",
                           "round 4+stores"};
-  for (int rep = 0; rep < reps; rep++) {
-    CK(hipMemset(ts, 0, (size_t)waves * 8 * sizeof(unsigned long long)));
-    if (set_ts(ts, waves)) {
-      std::printf("%s\n", chd_last_error());
-      return 1;
-    }
-    CK(hipDeviceSynchronize());
+  // warm-up: forwards back to back without timestamps (sustained clocks)
+  if (set_ts(nullptr, 0)) {
+    std::printf("%s\n", chd_last_error());
+    return 1;
+  }
+  for (int rep = 0; rep < warmup; rep++)
     if (chd_ntt_forward(plan, dst, src, L, P, 0, nullptr)) {
       std::printf("%s\n", chd_last_error());
       return 1;
     }
-    CK(hipDeviceSynchronize());
-    CK(hipMemcpy(t.data(), ts, t.size() * sizeof(unsigned long long),
-                 hipMemcpyDeviceToHost));
-    unsigned long long t0 = ~0ull, tend = 0;
-    for (int w = 0; w < waves; w++) {
-      t0 = std::min(t0, t[w * 8]);
-      tend = std::max(tend, t[w * 8 + 6]);
+  // the instrumented forward, right behind the warm-up ones on the stream
+  CK(hipMemsetAsync(ts, 0, (size_t)waves * 8 * sizeof(unsigned long long),
+                    nullptr));
+  CK(hipDeviceSynchronize());
+  if (set_ts(ts, waves)) {
+    std::printf("%s\n", chd_last_error());
+    return 1;
+  }
+  for (int rep = 0; rep < warmup; rep++)
+    if (chd_ntt_forward(plan, dst, src, L, P, 0, nullptr)) {
+      std::printf("%s\n", chd_last_error());
+      return 1;
     }
-    std::printf("run %d: first wave start -> last wave end %.2f us\n", rep,
-                (tend - t0) / 100.0);
-    if (rep + 1 < reps) continue;
-    for (int k = 0; k < 7; k++) {
-      std::vector<double> v;
-      for (int w = 0; w < waves; w++)
-        if (t[w * 8 + k]) v.push_back((t[w * 8 + k] - t0) / 100.0);
-      if (v.empty()) continue;
-      std::sort(v.begin(), v.end());
-      std::printf("%-15s waves %4zu  min %6.2f  p10 %6.2f  p50 %6.2f  "
-                  "p90 %6.2f  max %6.2f us\n",
-                  names[k], v.size(), v[0], v[v.size() / 10],
-                  v[v.size() / 2], v[v.size() * 9 / 10], v.back());
-    }
+  CK(hipDeviceSynchronize());
+  CK(hipMemcpy(t.data(), ts, t.size() * sizeof(unsigned long long),
+               hipMemcpyDeviceToHost));
+  // every forward above wrote the same slots: the table is the last one
+  unsigned long long t0 = ~0ull, tend = 0;
+  for (int w = 0; w < waves; w++) {
+    t0 = std::min(t0, t[w * 8]);
+    tend = std::max(tend, t[w * 8 + 6]);
+  }
+  std::printf("last of %d instrumented forwards (after %d plain ones): "
+              "first wave start -> last wave end %.2f us\n",
+              warmup, warmup, (tend - t0) / 100.0);
+  for (int k = 0; k < 7; k++) {
+    std::vector<double> v;
+    for (int w = 0; w < waves; w++)
+      if (t[w * 8 + k]) v.push_back((t[w * 8 + k] - t0) / 100.0);
+    if (v.empty()) continue;
+    std::sort(v.begin(), v.end());
+    std::printf("%-15s waves %4zu  min %6.2f  p10 %6.2f  p50 %6.2f  "
+                "p90 %6.2f  max %6.2f us\n",
+                names[k], v.size(), v[0], v[v.size() / 10], v[v.size() / 2],
+                v[v.size() * 9 / 10], v.back());
   }
   set_ts(nullptr, 0);
   CK(hipFree(ts));
