@@ -108,7 +108,7 @@ __device__ __forceinline__ void load_planes(v4i (&bp)[kChunks][4],
   }
 }
 
-template <int kChunks>
+template <int kChunks, bool kStream>
 __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
                                                        chd_limb_map m,
                                                        BconvBatch b) {
@@ -182,10 +182,12 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
   // one destination): pairs of planes in int32 (|acc_c| <= 2^21, so |lo|,
   // |hi| < 2^30), one 64-bit multiply-add y = lo + 2^16 hi (|y| < 2^47, far
   // inside the (-p 2^31, p 2^31) a signed Montgomery reduction takes),
-  // reduced to y 2^-32 in (-p, p), then made canonical. Streaming store: the
-  // 16 destinations of a lane group are 16 limbs apart, and keeping them out
-  // of the caches measured 1.5 % faster per HMult (both of its BConv
-  // launches).
+  // reduced to y 2^-32 in (-p, p), then made canonical. Stores: inside a
+  // key switch (the batch entry) the next launch, the NTT, reads the result
+  // right away, so it is written with default (temporal) stores and stays in
+  // the caches (3 % faster per HMult than streaming stores, measured); a
+  // standalone conversion (kStream) writes with the streaming hint (config 3
+  // 6.0 -> 5.5 us in the kernel trace, measured).
   auto finish = [&](const v4i (&d)[4], uint32_t pc, int32_t pinvc, int posc,
                     int n) {
     uint32_t o[4];
@@ -199,9 +201,12 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
       o[i] = u < up ? u : up;  // unsigned min: u + p when negative
     }
     const v4u ov = {o[0], o[1], o[2], o[3]};
-    __builtin_nontemporal_store(
-        ov, reinterpret_cast<v4u *>(jb.dst +
-                                    (static_cast<size_t>(posc) << kLogN) + n));
+    v4u *dp = reinterpret_cast<v4u *>(jb.dst +
+                                      (static_cast<size_t>(posc) << kLogN) + n);
+    if constexpr (kStream)
+      __builtin_nontemporal_store(ov, dp);
+    else
+      *dp = ov;
   };
   for (int tt = 0; tt < regular; tt++) {
     const bool live = tt * 16 + r < jb.dst_len;
@@ -317,9 +322,10 @@ extern "C" int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
   return 0;
 }
 
-extern "C" int chd_k_bconv_batch(const chd_tables *t, const chd_limb_map *m,
-                                 const chd_bconv_job *jobs, int num_jobs,
-                                 void *stream) {
+namespace {
+int launch_bconv(const chd_tables *t, const chd_limb_map *m,
+                 const chd_bconv_job *jobs, int num_jobs, bool stream_out,
+                 void *stream) {
   if (!t || !m || !jobs || num_jobs < 1 || num_jobs > CHD_MAX_BCONV_JOBS)
     return set_error(CHD_ERR_ARG, "chd_k_bconv_batch: invalid argument");
   BconvBatch b{};
@@ -333,13 +339,26 @@ extern "C" int chd_k_bconv_batch(const chd_tables *t, const chd_limb_map *m,
   int max_src = 0;
   for (int j = 0; j < num_jobs; j++) max_src = std::max(max_src, jobs[j].src_len);
   dim3 g(kN / kCoefPerBlock, 1, num_jobs);
-  if (max_src <= kChunkSrc)
-    hipLaunchKernelGGL(bconv_mfma<1>, g, dim3(kThreads), 0,
-                       static_cast<hipStream_t>(stream), *t, *m, b);
-  else
-    hipLaunchKernelGGL(bconv_mfma<2>, g, dim3(kThreads), 0,
-                       static_cast<hipStream_t>(stream), *t, *m, b);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (max_src <= kChunkSrc) {
+    if (stream_out)
+      hipLaunchKernelGGL((bconv_mfma<1, true>), g, dim3(kThreads), 0, s, *t, *m, b);
+    else
+      hipLaunchKernelGGL((bconv_mfma<1, false>), g, dim3(kThreads), 0, s, *t, *m, b);
+  } else {
+    if (stream_out)
+      hipLaunchKernelGGL((bconv_mfma<2, true>), g, dim3(kThreads), 0, s, *t, *m, b);
+    else
+      hipLaunchKernelGGL((bconv_mfma<2, false>), g, dim3(kThreads), 0, s, *t, *m, b);
+  }
   return check_launch("chd_k_bconv_batch");
+}
+}  // namespace
+
+extern "C" int chd_k_bconv_batch(const chd_tables *t, const chd_limb_map *m,
+                                 const chd_bconv_job *jobs, int num_jobs,
+                                 void *stream) {
+  return launch_bconv(t, m, jobs, num_jobs, false, stream);
 }
 
 extern "C" int chd_k_bconv(const chd_tables *t, const chd_limb_map *m,
@@ -349,5 +368,5 @@ extern "C" int chd_k_bconv(const chd_tables *t, const chd_limb_map *m,
       src_len > kMaxSrc || dst_len < 1)
     return set_error(CHD_ERR_ARG, "chd_k_bconv: invalid argument");
   chd_bconv_job j{dst, src, table, src_len, dst_len, m->skip_lo, m->skip_len};
-  return chd_k_bconv_batch(t, m, &j, 1, stream);
+  return launch_bconv(t, m, &j, 1, true, stream);
 }

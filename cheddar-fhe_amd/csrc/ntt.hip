@@ -1010,10 +1010,9 @@ __global__ __launch_bounds__(256) void modup_keyacc(KeyAccBatch b) {
 // (w0 = psi_rev[1], w1 = psi_rev[2 + (j >> 1)], s0 = -1 for j >= 2, s1 = -1
 // for odd j), the same residue the reference's first two butterfly stages
 // give (NTT.cu:231-338). Stages 2..15 then run in four register rounds of
-// the bits 13..10 | 9..6 | 5..2 | 1..0: two LDS exchanges, then DPP quad
-// transposes before the last round, which owns 4 consecutive outputs per
-// lane (each quad stores 64 contiguous bytes per instruction, a wave's four
-// store rounds cover its 4 KiB block).
+// the bits 13..10 | 9..6 | 5..2 | 1..0 with three LDS exchanges; the last
+// round owns 4 consecutive outputs per lane, so every wave stores 1 KiB
+// contiguous per instruction.
 // The four workgroups of a limb get block ids 8 apart (the same XCD under
 // round-robin dispatch) so three of the four reads of the limb hit in L2.
 // ------------------------------------------------------------------------
@@ -1125,10 +1124,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
       }
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-      // group (bits 15..2) of this lane's store round v: after the quad
-      // transposes lane b of quad q holds group k = 4 v + b of row q
-      const int hi4 =
-          (j << 12) | (wave << 8) | ((lane >> 2) << 4) | (4 * v + (lane & 3));
+      const int hi4 = (j << 12) | (wave << 8) | (v << 6) | lane;  // 15..2
       w4[v][0] = tw[16384 + hi4];
       w4[v][1] = tw[32768 + 2 * hi4];
       w4[v][2] = tw[32768 + 2 * hi4 + 1];
@@ -1233,44 +1229,13 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   for (int k = 0; k < 16; k++)
     x[k] = xs[qidx((wave << 10) | (b96 << 6) | (k << 2) | b10)];
   radix16_pre(ar, x, w3);
-  // Round 4 pairs the elements that differ in bits 1..0, which sit in the
-  // four lanes of a quad (b10), one per register x[k]. A 4 x 4 transpose
-  // inside each quad for each register group x[4v .. 4v+3] (two DPP
-  // quad_perm exchanges, lanes b ^ 2 then b ^ 1) leaves lane b with group
-  // k = 4 v + b's four elements in x[4v .. 4v+3], without an LDS round trip.
 #pragma unroll
-  for (int v = 0; v < 4; v++) {
-    int r[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) r[i] = static_cast<int>(x[4 * v + i]);
-    {
-      int t[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        t[i] = __builtin_amdgcn_mov_dpp(r[i], 0x4E, 0xF, 0xF, false);  // b ^ 2
-      const bool hi = (lane & 2) != 0;
-      r[0] = hi ? t[2] : r[0];
-      r[1] = hi ? t[3] : r[1];
-      r[2] = hi ? r[2] : t[0];
-      r[3] = hi ? r[3] : t[1];
-    }
-    {
-      int t[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        t[i] = __builtin_amdgcn_mov_dpp(r[i], 0xB1, 0xF, 0xF, false);  // b ^ 1
-      const bool od = (lane & 1) != 0;
-      r[0] = od ? t[1] : r[0];
-      r[1] = od ? r[1] : t[0];
-      r[2] = od ? t[3] : r[2];
-      r[3] = od ? r[3] : t[2];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) x[4 * v + i] = static_cast<T>(r[i]);
-  }
+  for (int k = 0; k < 16; k++)
+    xs[qidx((wave << 10) | (b96 << 6) | (k << 2) | b10)] = x[k];
+  wave_lds_sync();
   CHD_PHASE(5);
-  // ---- round 4: stages 14, 15 (bits 1..0); store round v: this lane's
-  // group k = 4 v + b10 of row b96 (bits 9..6) of the wave's block
+  // ---- round 4: stages 14, 15 (bits 1..0); lane = bits 7..2, wave =
+  // bits 13..10, store round v = bits 9..8
   const int32_t qs = static_cast<int32_t>(q);
   [[maybe_unused]] int32_t c2 = 0, c2q = 0, pe = 0, peq = 0;
   [[maybe_unused]] bool has_pad = false;
@@ -1290,17 +1255,15 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   }
 #pragma unroll
   for (int v = 0; v < 4; v++) {
-    const int n = (wave << 10) | (b96 << 6) | ((4 * v + b10) << 2);
+    const int n = (wave << 10) | (v << 8) | (lane << 2);
     const uint32_t boff = 4u * static_cast<uint32_t>(n);
-    // src2 with default (temporal) loads: a quad reads 64 of a line's 128
-    // bytes per store round and the next round reads the rest, which the
-    // streaming hint would have evicted (2.1 us slower per HMult, measured)
     u32x4 s2 = {0, 0, 0, 0};
     if constexpr (kEpi == kEpiModDown)
-      if (s2p != nullptr) s2 = ld_at<u32x4>(s2p, boff);
+      if (s2p != nullptr) s2 = ld_nt<u32x4>(s2p, boff);
+    const u32x4 u = *reinterpret_cast<const u32x4 *>(&lds[qidx(n)]);
     T y[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) y[i] = x[4 * v + i];
+    for (int i = 0; i < 4; i++) y[i] = static_cast<T>(u[i]);
     const uint32_t wa = w4[v][0];
     const uint32_t waq = ar.twq(wa);
     ar.ct(y[0], y[2], wa, waq);

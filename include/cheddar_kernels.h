@@ -97,7 +97,10 @@ int chd_k_ntt_inv_mul(const chd_tables *t, const chd_limb_map *m,
  * sources, 1 <= src_len <= 32. table = chd_bconv_table_size(src_len,
  * dst_len) bytes made by chd_bconv_table_pack from the reference-form
  * table T (dst-major).
- * pos(k) = k + (k >= skip_lo ? skip_len : 0); prime of pos via m->tab_*. */
+ * pos(k) = k + (k >= skip_lo ? skip_len : 0); prime of pos via m->tab_*.
+ * chd_k_bconv writes its result with streaming stores (a standalone
+ * conversion); chd_k_bconv_batch, the key switch's entry, with default
+ * stores so that the next launch finds the result in the caches. */
 long long chd_bconv_table_size(int src_len, int dst_len);
 int chd_bconv_table_pack(void *host_out, const int32_t *table_ref,
                          const uint32_t *dst_primes, int src_len, int dst_len);
