@@ -137,6 +137,16 @@ __device__ __forceinline__ uint32_t canon4(uint32_t x, uint32_t q) {
 
 __device__ __forceinline__ int pidx(int i) { return i + (i >> 4); }
 
+// orders a wave's LDS writes before its later LDS reads of the same words
+// written by other lanes of that wave: a wave's LDS instructions execute in
+// program order, so only the compiler has to be kept from reordering them
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+
 // Coalesced tile layout of the row passes: a workgroup owns kTileRows
 // consecutive rows (16 KiB contiguous); in store round v (0..3) thread t owns
 // the 16 bytes at tile offset 16 (t + 256 v), i.e. tile elements
@@ -770,7 +780,12 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
   const int r = threadIdx.x >> 4;
   const int row = blockIdx.x * kTileRows + r;
   const uint32_t rbase = static_cast<uint32_t>(row * kCols) * 4u;
-  const uint32_t cbase = rbase + 64u * c;  // this thread's 16 contiguous words
+  // Element ownership of the products: register k = 4v + j holds column
+  // 4c + 64v + j of the thread's row, so the 16 threads of a row move 256
+  // contiguous bytes per 16-byte access (keys, CAccum inputs, outputs). A
+  // row's 16 threads are lanes of one wave: its LDS exchanges need only a
+  // wave-level fence.
+  const uint32_t obase = rbase + 16u * c;
   T *xr = reinterpret_cast<T *>(xch) + r * kRowPad;
   // twiddles are (re)loaded inside each group's row pass (cache hits after
   // the first group) instead of living in 30 registers across the loop
@@ -805,7 +820,6 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
     folded = true;
     nprod = 0;
   };
-  bool synced = false;
   for (int g = 0; g < a.beta; g++) {
     const int own_lo = group_lo(g, a.alpha, a.group_shift);
     const int own_hi = group_hi(g, a.alpha, a.group_shift, a.num_q);
@@ -826,10 +840,10 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
         const uint64_t pp = a.p_prod[l];
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-          const uint4 vb1 = ld_at<uint4>(a.b1 + loff, cbase + 16u * v);
-          const uint4 va1 = ld_at<uint4>(a.a1 + loff, cbase + 16u * v);
-          const uint4 vb2 = ld_at<uint4>(a.b2 + loff, cbase + 16u * v);
-          const uint4 va2 = ld_at<uint4>(a.a2 + loff, cbase + 16u * v);
+          const uint4 vb1 = ld_at<uint4>(a.b1 + loff, obase + 256u * v);
+          const uint4 va1 = ld_at<uint4>(a.a1 + loff, obase + 256u * v);
+          const uint4 vb2 = ld_at<uint4>(a.b2 + loff, obase + 256u * v);
+          const uint4 va2 = ld_at<uint4>(a.a2 + loff, obase + 256u * v);
           const uint32_t x1[4] = {vb1.x, vb1.y, vb1.z, vb1.w};
           const uint32_t y1[4] = {va1.x, va1.y, va1.z, va1.w};
           const uint32_t x2[4] = {vb2.x, vb2.y, vb2.z, vb2.w};
@@ -855,7 +869,7 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
         const uint32_t *dl = a.d + loff;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-          uint4 t = ld_at<uint4>(dl, cbase + 16u * v);
+          uint4 t = ld_at<uint4>(dl, obase + 256u * v);
           u[4 * v] = t.x;
           u[4 * v + 1] = t.y;
           u[4 * v + 2] = t.z;
@@ -888,13 +902,12 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
             ar.ct(x[k], x[k + h], w, wq);
         }
       }
-      if (synced) __syncthreads();  // previous group's LDS reads are done
 #pragma unroll
       for (int k = 0; k < 16; k++) xr[pidx(c + 16 * k)] = x[k];
-      __syncthreads();
+      wave_lds_sync();
 #pragma unroll
       for (int k = 0; k < 16; k++) x[k] = xr[pidx(16 * c + k)];
-      synced = true;
+      wave_lds_sync();
 #pragma unroll
       for (int s = 0, i = 0; s < 4; s++) {
         const int h = 8 >> s;
@@ -907,15 +920,21 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
             ar.ct(x[k], x[k + h], w, wq);
         }
       }
+      // columns 16c + k -> the product ownership 4c + 64v + j
 #pragma unroll
-      for (int k = 0; k < 16; k++) u[k] = ar.canon_fwd(x[k]);
+      for (int k = 0; k < 16; k++) xr[pidx(16 * c + k)] = x[k];
+      wave_lds_sync();
+#pragma unroll
+      for (int k = 0; k < 16; k++)
+        u[k] = ar.canon_fwd(xr[pidx(4 * c + 64 * (k >> 2) + (k & 3))]);
+      wave_lds_sync();
     }
     const uint32_t *kbp = a.kb[g] + koff;
     const uint32_t *kap = a.ka[g] + koff;
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-      uint4 tb = ld_at<uint4>(kbp, cbase + 16u * v);
-      uint4 ta = ld_at<uint4>(kap, cbase + 16u * v);
+      uint4 tb = ld_at<uint4>(kbp, obase + 256u * v);
+      uint4 ta = ld_at<uint4>(kap, obase + 256u * v);
       const uint32_t kbv[4] = {tb.x, tb.y, tb.z, tb.w};
       const uint32_t kav[4] = {ta.x, ta.y, ta.z, ta.w};
 #pragma unroll
@@ -933,12 +952,12 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
     const uint64_t pp = a.p_prod[l];
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-      uint4 tb = ld_at<uint4>(a.cb + loff, cbase + 16u * v);
+      uint4 tb = ld_at<uint4>(a.cb + loff, obase + 256u * v);
       const uint32_t cbv[4] = {tb.x, tb.y, tb.z, tb.w};
 #pragma unroll
       for (int j = 0; j < 4; j++) sb[4 * v + j] += pp * cbv[j];
       if (a.ca != nullptr) {
-        uint4 ta = ld_at<uint4>(a.ca + loff, cbase + 16u * v);
+        uint4 ta = ld_at<uint4>(a.ca + loff, obase + 256u * v);
         const uint32_t cav[4] = {ta.x, ta.y, ta.z, ta.w};
 #pragma unroll
         for (int j = 0; j < 4; j++) sa[4 * v + j] += pp * cav[j];
@@ -950,7 +969,7 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
     // extended-basis b of a giant-step accumulator, added on every limb
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-      const uint4 t = ld_at<uint4>(a.add_b + loff, cbase + 16u * v);
+      const uint4 t = ld_at<uint4>(a.add_b + loff, obase + 256u * v);
       const uint32_t tv[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
       for (int j = 0; j < 4; j++) accb[4 * v + j] = add_mod(accb[4 * v + j], tv[j], q);
@@ -964,9 +983,20 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
     uint32_t w1[15], w2[15];
     inv_row_twiddles(tab.itw + (static_cast<size_t>(ti) << kLogN), w1, w2);
     const size_t ioff = static_cast<size_t>(l - a.intt_lo) << kLogN;
-    __syncthreads();  // the group row passes' LDS reads are done
+    // back to columns 16c + k, the row pass's input ownership (the group
+    // row passes' LDS accesses were this wave's own)
+    auto to_rows = [&](uint32_t(&acc)[16]) {
+#pragma unroll
+      for (int k = 0; k < 16; k++)
+        xr[pidx(4 * c + 64 * (k >> 2) + (k & 3))] = acc[k];
+      wave_lds_sync();
+#pragma unroll
+      for (int k = 0; k < 16; k++) acc[k] = xr[pidx(16 * c + k)];
+    };
+    to_rows(accb);
     inv_rows_body<kLazy>(w1, w2, accb, q, qinv, a.intt_b + ioff, xch);
-    __syncthreads();  // ... and the first polynomial's store reads
+    __syncthreads();  // the first polynomial's store reads cross rows
+    to_rows(acca);
     inv_rows_body<kLazy>(w1, w2, acca, q, qinv, a.intt_a + ioff, xch);
     return;
   }
@@ -974,10 +1004,10 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
   uint32_t *oa = a.acc_a + loff;
 #pragma unroll
   for (int v = 0; v < 4; v++) {
-    st_at<uint4>(ob, cbase + 16u * v,
+    st_at<uint4>(ob, obase + 256u * v,
                  make_uint4(accb[4 * v], accb[4 * v + 1], accb[4 * v + 2],
                             accb[4 * v + 3]));
-    st_at<uint4>(oa, cbase + 16u * v,
+    st_at<uint4>(oa, obase + 256u * v,
                  make_uint4(acca[4 * v], acca[4 * v + 1], acca[4 * v + 2],
                             acca[4 * v + 3]));
   }
@@ -1079,15 +1109,6 @@ __device__ __forceinline__ void radix16_pre(const A &ar,
         ar.ct(x[k], x[k + h], wv, wq);
     }
   }
-}
-
-// orders a wave's LDS writes before its later LDS reads of the same words
-// written by other lanes of that wave: a wave's LDS instructions execute in
-// program order, so only the compiler has to be kept from reordering them
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 template <int kEpi, bool kPre, bool kLazy>
