@@ -392,11 +392,15 @@ __global__ __launch_bounds__(kThreads) void gs_fused_kernel(chd_tables t,
 // Four products of a giant step are summed in 64 bits and reduced once,
 // which equals the sum of their MontMuls mod q (the reference's
 // MontMul-then-add, GSFusedKernel of Hoist.cu:80-118, in canonical form).
-template <int kGw>
-__global__ __launch_bounds__(kThreads) void gs_wide_kernel(chd_tables t,
-                                                         chd_limb_map m,
-                                                         chd_gs_wide_args a) {
-  const LimbIdx li = limb_of(t, m);
+// kSmall (q < 2^30): a sum of four products of canonical residues is below
+// 4 q^2 < q 2^32, so one Montgomery reduction maps it to (sum) 2^-32 in
+// [0, 2q), and the accumulators stay in [0, 2q) until the final store.
+// Otherwise (q < 2^31) the sum is reduced by reduce_sum4 to [0, q) and
+// accumulated canonically.
+template <int kGw, bool kSmall>
+__device__ __forceinline__ void gs_wide_body(const chd_gs_wide_args &a,
+                                             const LimbIdx &li) {
+  const uint32_t q = li.q;
   const uint32_t qn = 0u - static_cast<uint32_t>(li.qinv);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const size_t o = (static_cast<size_t>(li.l) << kLogN) +
@@ -417,6 +421,17 @@ __global__ __launch_bounds__(kThreads) void gs_wide_kernel(chd_tables t,
       for (int i = 0; i < 4; i++) rb[g][i] = ra[g][i] = 0u;
     }
   }
+  auto acc = [&](uint32_t &r, uint64_t t) {
+    if constexpr (kSmall) {
+      const uint32_t m = static_cast<uint32_t>(t) * qn;
+      const uint32_t d =
+          static_cast<uint32_t>((static_cast<uint64_t>(m) * q + t) >> 32);
+      const uint32_t s = r + d;  // [0, 4q)
+      r = s < s - 2 * q ? s : s - 2 * q;
+    } else {
+      r = add_mod(r, reduce_sum4(t, q, qn), q);
+    }
+  };
   for (int b0 = 0; b0 < a.num_bs; b0 += 4) {
     uint4 xb[4], xa[4];
 #pragma unroll
@@ -439,16 +454,34 @@ __global__ __launch_bounds__(kThreads) void gs_wide_kernel(chd_tables t,
           tb += mm * get(xb[j], i);
           ta += mm * get(xa[j], i);
         }
-        rb[g][i] = add_mod(rb[g][i], reduce_sum4(tb, li.q, qn), li.q);
-        ra[g][i] = add_mod(ra[g][i], reduce_sum4(ta, li.q, qn), li.q);
+        acc(rb[g][i], tb);
+        acc(ra[g][i], ta);
       }
     }
   }
 #pragma unroll
   for (int g = 0; g < kGw; g++) {
+    if constexpr (kSmall) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        rb[g][i] = rb[g][i] < rb[g][i] - q ? rb[g][i] : rb[g][i] - q;
+        ra[g][i] = ra[g][i] < ra[g][i] - q ? ra[g][i] : ra[g][i] - q;
+      }
+    }
     st4(a.dst_b[g0 + g] + o, make_uint4(rb[g][0], rb[g][1], rb[g][2], rb[g][3]));
     st4(a.dst_a[g0 + g] + o, make_uint4(ra[g][0], ra[g][1], ra[g][2], ra[g][3]));
   }
+}
+
+template <int kGw>
+__global__ __launch_bounds__(kThreads) void gs_wide_kernel(chd_tables t,
+                                                         chd_limb_map m,
+                                                         chd_gs_wide_args a) {
+  const LimbIdx li = limb_of(t, m);
+  if (li.q < (1u << 30))
+    gs_wide_body<kGw, true>(a, li);
+  else
+    gs_wide_body<kGw, false>(a, li);
 }
 
 // Element-wise arithmetic (ElementWise.cu:33-220 Sum / Sub / Neg / Mult /
