@@ -6,6 +6,10 @@ primes = 1 mod 2^17, limb-major. One step = forward NTT of all 64 limbs
 followed by the inverse NTT (128 limb-transforms). value = limb-transforms/s
 with inputs resident in HBM; the input/output buffers rotate over a set
 larger than the 256 MB MALL so the timed traffic comes from HBM.
+Consecutive steps are independent ciphertexts and alternate over three HIP
+streams (a buffer set always on the same stream), so one step's load phase
+runs beside another's butterflies; the one-stream step time, the latency
+of one batch, is reported next to it.
 
 The same JSON line carries the other two parts of the metric: the HMult
 key-switch time at config 4 (L = 24, dnum = 3, alpha = 8, merged
@@ -45,6 +49,16 @@ LIMB_TRANSFORM_BYTES = 2 * LIMB_BYTES
 MALL_BYTES = 256 << 20
 # calibration copy: 1 GiB each way, far beyond L2 and the 256 MiB MALL
 COPY_BYTES = 1 << 30
+# the headline's consecutive steps alternate over this many streams
+NTT_STREAMS = 3
+
+
+def ntt_sets():
+    """buffer sets of the headline loop: more than twice the MALL per role,
+    a multiple of NTT_STREAMS so that set j is only ever used on stream
+    j % NTT_STREAMS"""
+    n = max(4, (2 * MALL_BYTES) // (2 * 32 * LIMB_BYTES) + 1)
+    return (n + NTT_STREAMS - 1) // NTT_STREAMS * NTT_STREAMS
 
 
 def parse():
@@ -80,8 +94,7 @@ def bench_ntt(chd, steps, warmup):
     from chd_primes import ntt_primes
     primes = ntt_primes(30, 32)
     plan = chd.NttPlan(primes)
-    set_bytes = 2 * 32 * LIMB_BYTES
-    nsets = max(4, (2 * MALL_BYTES) // set_bytes + 1)  # > 2x MALL per role
+    nsets = ntt_sets()
     rng = np.random.default_rng(0xC0FFEE02)
     host = np.stack([np.stack([rng.integers(0, p, N, dtype=np.uint64)
                                for p in primes]) for _ in range(2)])
@@ -91,10 +104,13 @@ def bench_ntt(chd, steps, warmup):
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
 
-    def step(i):
+    streams = [torch.cuda.Stream() for _ in range(NTT_STREAMS)]
+    sps = [ctypes.c_void_p(x.cuda_stream) for x in streams]
+
+    def step_on(i, p):
         s, d = srcs[i % nsets], dsts[i % nsets]
-        plan.forward(d, s, 32, 2, stream=sp)
-        plan.inverse(s, d, 32, 2, mont_conv=False, stream=sp)
+        plan.forward(d, s, 32, 2, stream=p)
+        plan.inverse(s, d, 32, 2, mont_conv=False, stream=p)
 
     # Per-direction timings (reported, and the forward one is the roofline's)
     # come first, over at least 200 calls each: back to back they keep the
@@ -113,15 +129,31 @@ def bench_ntt(chd, steps, warmup):
     warm_ms = event_time_ms(lambda i: plan.forward(dsts[0], srcs[0], 32, 2,
                                                    stream=sp), sub,
                             stream) / sub
-    # the headline: W warmup steps, then exactly K timed steps
+    # one step at a time on one stream: the latency of one batch
+    one_ms = event_time_ms(lambda i: step_on(i, sp), sub, stream) / sub
+    # the headline: W warmup steps, then exactly K timed steps, step i on
+    # stream i % NTT_STREAMS (set i % nsets, so a set never changes stream)
     for i in range(warmup):
-        step(i)
+        step_on(i, sps[i % NTT_STREAMS])
     torch.cuda.synchronize()
-    ms = event_time_ms(step, steps, stream)
+    # an event at the start and the end of each stream's share; the timed
+    # span runs from the earliest start to the latest end (no cross-stream
+    # waits added to the loop)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in streams]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in streams]
+    for ev, x in zip(starts, streams):
+        ev.record(x)
+    for i in range(steps):
+        step_on(i, sps[i % NTT_STREAMS])
+    for ev, x in zip(ends, streams):
+        ev.record(x)
     torch.cuda.synchronize()
+    t0 = starts[0]
+    ms = (max(t0.elapsed_time(ev) for ev in ends) -
+          min([0.0] + [t0.elapsed_time(ev) for ev in starts[1:]]))
     # the inverse with mont_conv=False returns the input: check it stayed put
     ok = all(torch.equal(srcs[i], base) for i in range(nsets))
-    return ms, fwd_ms, inv_ms, warm_ms, ok
+    return ms, fwd_ms, inv_ms, warm_ms, one_ms, ok
 
 
 def _config4_context(chd):
@@ -423,7 +455,8 @@ def main():
     hmult_cold_us *= 1e3
     bconv_us = bench_bconv(chd) * 1e3
     bconv_cold_us = bench_bconv(chd, cold=True) * 1e3
-    ms, fwd_ms, inv_ms, warm_ms, ok = bench_ntt(chd, args.steps, args.warmup)
+    ms, fwd_ms, inv_ms, warm_ms, one_ms, ok = bench_ntt(chd, args.steps,
+                                                        args.warmup)
     if not ok:
         print("NTT round trip changed the data", file=sys.stderr)
         sys.exit(1)
@@ -452,7 +485,8 @@ def main():
         "config": {
             "workload": "config2: batched NTT+INTT of one ciphertext, 2 polys "
                         "x 32 limbs, N=2^16, 30-bit primes, limb-major, "
-                        "buffers rotated over %d MiB" % 0,
+                        "buffers rotated over %d MiB, consecutive steps "
+                        "over %d streams" % (0, NTT_STREAMS),
             "limb_transforms_per_step": 128,
         },
         "roofline": {
@@ -493,6 +527,7 @@ def main():
             "ntt_forward_us": fwd_ms * 1e3,
             "ntt_inverse_us": inv_ms * 1e3,
             "ntt_forward_warm_mall_us": warm_ms * 1e3,
+            "ntt_step_us_one_stream": one_ms * 1e3,
             "hmult_keyswitch_us_config4": hmult_us,
             "hmult_keyswitch_us_config4_cold": hmult_cold_us,
             "bconv_us_config3_warm": bconv_us,
@@ -503,19 +538,24 @@ def main():
                      "steps) runs last, right after the per-direction "
                      "timings (>= 200 calls each), so it starts at "
                      "sustained clocks; right after an idle GPU the same "
-                     "loop reads ~8 %% slower. "
+                     "loop reads ~8 %% slower. Its consecutive steps "
+                     "(independent ciphertexts, separate buffer sets) "
+                     "alternate over %d HIP streams, so one step's loads "
+                     "run beside another's butterflies; "
+                     "ntt_step_us_one_stream is one step at a time on one "
+                     "stream (the latency of one batch). "
                      "hmult: warm = same key and inputs each step, cold = "
                      "%d MiB of distinct input/key sets rotated; host "
                      "enqueue included. hoist: 768x768 BSGS (28 baby, 28 "
                      "giant steps, 54 rotation keys) at L=20 on the "
                      "library's encodings of a seeded N(0, 0.02) weight; "
                      "HBM fraction against the %d B of plaintexts and keys "
-                     "one evaluation reads" % (hmult_set >> 20, hoist_bytes),
+                     "one evaluation reads" % (NTT_STREAMS, hmult_set >> 20,
+                                               hoist_bytes),
         },
     }
-    nsets = max(4, (2 * MALL_BYTES) // (2 * 32 * LIMB_BYTES) + 1)
     line["config"]["workload"] = line["config"]["workload"].replace(
-        "%d MiB" % 0, "%d MiB" % (2 * nsets * 16))
+        "over 0 MiB", "over %d MiB" % (2 * ntt_sets() * 16))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line))
