@@ -68,7 +68,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU-baseline leg")
-    ap.add_argument("--only", choices=["ntt_fwd", "ntt_inv", "hmult",
+    ap.add_argument("--only", choices=["ntt_fwd", "ntt_inv", "ntt_step",
+                                       "hmult",
                                        "hmult_cold", "bconv", "bconv_cold",
                                        "copy", "hoist"],
                     help="run only this workload's timed loop (for "
@@ -391,6 +392,9 @@ def run_only(chd, what, steps):
         return bench_bconv(chd, steps, cold=True) * 1e3
     if what == "hoist":
         return bench_hoist(chd, steps)[0] * 1e3
+    if what == "ntt_step":
+        # the headline loop (after its per-direction timings): us per step
+        return bench_ntt(chd, steps, 5)[0] / steps * 1e3
     if what == "copy":
         # plain device copy of COPY_BYTES: the reference point that scales
         # the FETCH_SIZE / WRITE_SIZE counters into HBM bytes
