@@ -434,10 +434,9 @@ def traffic_from_profile():
 def main():
     args = parse()
     if args.gpus != 1:
-        print("bench.py measures one GPU: every box in this run has one "
-              "MI355X and the key-switch path is not sharded across GPUs "
-              "(see DESIGN.md, 'More than one GPU'). Run with --gpus 1.",
-              file=sys.stderr)
+        print("bench.py measures one GPU: the key-switch path here runs "
+              "on a single MI355X and is not sharded across GPUs. Run with "
+              "--gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
