@@ -65,6 +65,36 @@ def test_ntt_config2_batch(chd):
     assert np.array_equal(host(y2), want_m)
 
 
+def test_ntt_concurrent_streams(chd):
+    """one plan used from three streams at once on separate buffer sets (the
+    benchmark's headline loop): every forward matches the oracle and every
+    inverse restores its input"""
+    import ctypes
+    import torch
+    primes = Q30[:32]
+    plan = chd.NttPlan(primes)
+    sets = 6
+    xs = [np.stack([uniform_limbs(rng(900 + 2 * i + p), primes)
+                    for p in range(2)]) for i in range(sets)]
+    srcs = [dev(x) for x in xs]
+    fwds = [zeros(2, 32, N) for _ in range(sets)]
+    backs = [zeros(2, 32, N) for _ in range(sets)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    for rep in range(2):
+        for i in range(sets):
+            s = ctypes.c_void_p(streams[i % 3].cuda_stream)
+            plan.forward(fwds[i], srcs[i], 32, 2, stream=s)
+            plan.inverse(backs[i], fwds[i], 32, 2, mont_conv=False, stream=s)
+    torch.cuda.synchronize()
+    for i in range(sets):
+        assert np.array_equal(host(backs[i]), xs[i]), i
+    for i in (0, sets - 1):
+        want = np.stack([_orc.ntt_batch(xs[i][p].reshape(-1), 16, primes)
+                         .reshape(32, N) for p in range(2)])
+        assert np.array_equal(host(fwds[i]), want), i
+
+
 @pytest.mark.parametrize("kind", ["zeros", "max", "impulse", "ramp"])
 def test_ntt_edge_inputs(chd, kind):
     primes = [CFG1_Q, Q31[5], Q30[0], Q30[31]]
