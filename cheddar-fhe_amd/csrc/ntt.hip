@@ -146,7 +146,6 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-
 // Coalesced tile layout of the row passes: a workgroup owns kTileRows
 // consecutive rows (16 KiB contiguous); in store round v (0..3) thread t owns
 // the 16 bytes at tile offset 16 (t + 256 v), i.e. tile elements
