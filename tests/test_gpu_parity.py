@@ -272,6 +272,16 @@ def test_hmult_config4(chd, ks, L, rescale):
     assert np.array_equal(host(res[1]), wa)
 
 
+@pytest.mark.parametrize("L,rescale", [(1, False), (2, True), (8, True),
+                                       (9, True), (9, False), (16, True),
+                                       (17, True)])
+def test_hmult_level_sweep(chd, ks, L, rescale):
+    """HMult at the low levels of the config-4 chain: one dnum group (L <= 8),
+    a partial last group (9, 17), exact multiples (8, 16) and the bottom
+    level without rescale, against the oracle"""
+    test_hmult_config4(chd, ks, L, rescale)
+
+
 def test_hmult_in_place_and_separate_rescale(chd, ks):
     param, ctx, main, aux = ks
     L = 24
