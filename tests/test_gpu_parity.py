@@ -300,10 +300,9 @@ def test_hmult_in_place_and_separate_rescale(chd, ks):
 
 
 @pytest.mark.parametrize("rot", [1, 1234])
-def test_hrot_and_mult_key(chd, ks, rot):
+def test_hrot_and_mult_key(chd, ks, rot, L=20):
     param, ctx, main, aux = ks
-    L = 20
-    r = rng(500 + rot)
+    r = rng(500 + rot + 100 * L)
     b, a = uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L])
     kb, ka = _evk(r, main, aux, 3)
     res = (zeros(L, N), zeros(L, N))
@@ -314,9 +313,18 @@ def test_hrot_and_mult_key(chd, ks, rot):
     assert np.array_equal(host(res[1]), wa)
     ctx.hrot(L - 1, res, (dev(b), dev(a)), [dev(k) for k in kb],
              [dev(k) for k in ka], rot)
-    hb, ha = _orc.hrot(b, a, kb, ka, L, 24, main, aux, 16, rot)
+    # HRot reduces the distance modulo the slot count (Context.cpp:776-791);
+    # the oracle takes the permute amount itself
+    hb, ha = _orc.hrot(b, a, kb, ka, L, 24, main, aux, 16, rot % (N // 2))
     assert np.array_equal(host(res[0]), hb)
     assert np.array_equal(host(res[1]), ha)
+
+
+@pytest.mark.parametrize("L,rot", [(1, 3), (8, -1), (9, 77), (17, 4096)])
+def test_hrot_mult_key_level_sweep(chd, ks, L, rot):
+    """MultKey and HRot at the low levels (one group, partial last groups;
+    negative and large rotations) against the oracle"""
+    test_hrot_and_mult_key(chd, ks, rot, L)
 
 
 def test_permute_conjugate(chd, ks):
