@@ -65,6 +65,25 @@ def test_ntt_config2_batch(chd):
     assert np.array_equal(host(y2), want_m)
 
 
+def test_ntt_31bit_primes_batch(chd):
+    """the config-2 batch shape on 31-bit primes (the reference-form
+    butterflies of every kernel) against the oracle, both directions"""
+    primes = Q31[:32]
+    plan = chd.NttPlan(primes)
+    x = np.stack([uniform_limbs(rng(950 + p), primes) for p in range(2)])
+    y = zeros(2, 32, N)
+    plan.forward(y, dev(x), 32, 2)
+    want = np.stack([_orc.ntt_batch(x[p].reshape(-1), 16, primes).reshape(
+        32, N) for p in range(2)])
+    assert np.array_equal(host(y), want)
+    z = zeros(2, 32, N)
+    plan.inverse(z, y, 32, 2, mont_conv=False)
+    assert np.array_equal(host(z), x)
+    yi = dev(x)
+    plan.forward(yi, yi, 32, 2)          # in place: the two-pass kernels
+    assert np.array_equal(host(yi), want)
+
+
 def test_ntt_concurrent_streams(chd):
     """one plan used from three streams at once on separate buffer sets (the
     benchmark's headline loop): every forward matches the oracle and every
