@@ -1,10 +1,13 @@
 """Builds lib/libcheddar_amd.so (HIP kernels for gfx950 + C++ host + C-ABI).
 
 Usage: python cheddar-fhe_amd/build.py [--jobs N] [--phase-timestamps DIR]
+                                        [--host-asan DIR]
 Compiles every source each time it is called (hipcc, no cache).
 --phase-timestamps builds an instrumented copy into DIR instead (the forward
 NTT records per-wave phase timestamps; tests/cpp/ntt_phase_timeline.cpp reads
-them).
+them). --host-asan builds a copy into DIR whose host code runs under
+AddressSanitizer (device code as in the product; tests/cpp's `asan` target
+links the C++ API test against it).
 """
 import argparse
 import concurrent.futures as cf
@@ -55,8 +58,8 @@ def compile_one(rel, device, extra, obj_dir=OBJ_DIR):
     if device:
         cmd = [HIPCC] + COMMON + DEVICE + extra + ["-c", src, "-o", obj]
     else:
-        cmd = [HIPCC] + COMMON + ["-D__HIP_PLATFORM_AMD__", "-c", src, "-o",
-                                  obj]
+        cmd = [HIPCC] + COMMON + extra + ["-D__HIP_PLATFORM_AMD__", "-c",
+                                          src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError("compile failed: %s\n%s\n%s" %
@@ -64,24 +67,38 @@ def compile_one(rel, device, extra, obj_dir=OBJ_DIR):
     return obj
 
 
-def build(jobs=8, phase_timestamps=None):
+# host code only: each option preceded by -Xarch_host, so no device code
+# is built with the sanitizer
+HOST_ASAN = ["-Xarch_host", "-fsanitize=address",
+             "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def build(jobs=8, phase_timestamps=None, host_asan=None):
     """phase_timestamps: a directory for an instrumented copy of the library
     (the forward NTT's per-wave phase timestamps, for measurement only);
-    the product library is not touched then"""
-    out_dir, obj_dir, lib, extra = OUT_DIR, OBJ_DIR, LIB, []
-    if phase_timestamps:
-        out_dir = os.path.abspath(phase_timestamps)
+    host_asan: a directory for a copy whose host code is built with
+    AddressSanitizer (for testing only); the product library is not touched
+    by either"""
+    out_dir, obj_dir, lib = OUT_DIR, OBJ_DIR, LIB
+    dev_extra, host_extra, link_extra = [], [], []
+    if phase_timestamps or host_asan:
+        out_dir = os.path.abspath(phase_timestamps or host_asan)
         obj_dir = os.path.join(out_dir, "_build")
         lib = os.path.join(out_dir, "libcheddar_amd.so")
-        extra = ["-DCHD_PHASE_TIMESTAMPS"]
+    if phase_timestamps:
+        dev_extra = ["-DCHD_PHASE_TIMESTAMPS"]
+    if host_asan:
+        dev_extra = host_extra = link_extra = HOST_ASAN
     os.makedirs(out_dir, exist_ok=True)
     os.makedirs(obj_dir, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(
-            lambda s: compile_one(s[0], s[1], s[2] + (extra if s[1] else []),
+            lambda s: compile_one(s[0], s[1],
+                                  s[2] + (dev_extra if s[1] else host_extra),
                                   obj_dir), SOURCES))
     tmp = lib + ".tmp"
-    cmd = [HIPCC, "-shared", "--offload-arch=" + ARCH, "-o", tmp] + objs
+    cmd = ([HIPCC, "-shared", "--offload-arch=" + ARCH] + link_extra +
+           ["-o", tmp] + objs)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError("link failed: %s\n%s" % (res.stdout, res.stderr))
@@ -94,6 +111,11 @@ if __name__ == "__main__":
     ap.add_argument("--jobs", type=int, default=8)
     ap.add_argument("--phase-timestamps", metavar="DIR",
                     help="build an instrumented copy into DIR instead")
+    ap.add_argument("--host-asan", metavar="DIR",
+                    help="build a copy with host-side AddressSanitizer into "
+                         "DIR instead")
     a = ap.parse_args()
-    print(build(a.jobs, a.phase_timestamps))
+    if a.phase_timestamps and a.host_asan:
+        ap.error("--phase-timestamps and --host-asan are separate builds")
+    print(build(a.jobs, a.phase_timestamps, a.host_asan))
     sys.exit(0)
