@@ -104,7 +104,7 @@ void MemoryPool::Deallocate(void *p, size_t reserved,
   }
   hipEvent_t e = TakeEvent();
   if (e != nullptr && hipEventRecord(e, stream) != hipSuccess) {
-    spare_events_.push_back(e);
+    (void)hipEventDestroy(e);
     e = nullptr;
   }
   if (e == nullptr) (void)hipStreamSynchronize(stream);
@@ -113,9 +113,10 @@ void MemoryPool::Deallocate(void *p, size_t reserved,
     stats_.cached_bytes += reserved;
   } catch (...) {
     // no room to cache it: give it back once its stream is done with it
+    // (nothing here may throw: this function is noexcept)
     if (e != nullptr) {
       (void)hipEventSynchronize(e);
-      spare_events_.push_back(e);
+      (void)hipEventDestroy(e);
     }
     (void)hipFree(p);
   }
