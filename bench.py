@@ -13,10 +13,11 @@ of one batch, is reported next to it.
 
 The same JSON line carries the other two parts of the metric: the HMult
 key-switch time at config 4 (L = 24, dnum = 3, alpha = 8, merged
-ModDown+Rescale) and the config-3 BConv time, both measured with HIP events,
-the time of a config-5-shaped hoisted BSGS linear transform, plus the
-roofline of the NTT and the CPU baseline (the oracle's scalar Montgomery NTT
-on this host, bounded sample).
+ModDown+Rescale; also without rescale followed by a separate Rescale, and
+independent HMults over three streams) and the config-3 BConv time, all
+measured with HIP events, the time of a config-5-shaped hoisted BSGS linear
+transform, plus the roofline of the NTT and the CPU baseline (the oracle's
+scalar Montgomery NTT on this host, bounded sample).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -70,7 +71,8 @@ def parse():
                     help="skip the CPU-baseline leg")
     ap.add_argument("--only", choices=["ntt_fwd", "ntt_inv", "ntt_step",
                                        "hmult",
-                                       "hmult_cold", "bconv", "bconv_cold",
+                                       "hmult_cold", "hmult_separate",
+                                       "bconv", "bconv_cold",
                                        "copy", "hoist"],
                     help="run only this workload's timed loop (for "
                          "profiling); prints its average time")
@@ -164,11 +166,12 @@ def _config4_context(chd):
     return main, aux, chd.Context(param)
 
 
-def bench_hmult(chd, iters=20, cold=False):
+def bench_hmult(chd, iters=20, cold=False, separate=False):
     """config 4: HMult with merged rescale at L = 24. warm: the same inputs
     and key every step (working set resident in the 256 MB MALL); cold:
     steps rotate over distinct input/key sets spanning more than twice the
-    MALL, so inputs and keys come from HBM"""
+    MALL, so inputs and keys come from HBM. separate: HMult without rescale
+    followed by a separate Rescale (the reference's other form)"""
     import numpy as np
     import torch
     main, aux, ctx = _config4_context(chd)
@@ -184,13 +187,20 @@ def bench_hmult(chd, iters=20, cold=False):
     sets = [base] + [[t.clone() for t in base] for _ in range(nsets - 1)]
     res = (torch.empty(23, N, dtype=torch.int32, device="cuda"),
            torch.empty(23, N, dtype=torch.int32, device="cuda"))
+    full = (torch.empty(24, N, dtype=torch.int32, device="cuda"),
+            torch.empty(24, N, dtype=torch.int32, device="cuda"))
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
 
     def run(i):
         t = sets[i % nsets]
-        ctx.hmult(23, res, (t[0], t[1]), (t[2], t[3]), t[4:7], t[7:10],
-                  rescale=True, stream=sp)
+        if separate:
+            ctx.hmult(23, full, (t[0], t[1]), (t[2], t[3]), t[4:7], t[7:10],
+                      rescale=False, stream=sp)
+            ctx.rescale(23, res, full, stream=sp)
+        else:
+            ctx.hmult(23, res, (t[0], t[1]), (t[2], t[3]), t[4:7], t[7:10],
+                      rescale=True, stream=sp)
     for i in range(3):
         run(i)
     torch.cuda.synchronize()
@@ -433,6 +443,8 @@ def run_only(chd, what, steps):
         return bench_hmult(chd, steps)[0] * 1e3
     if what == "hmult_cold":
         return bench_hmult(chd, steps, cold=True)[0] * 1e3
+    if what == "hmult_separate":
+        return bench_hmult(chd, steps, separate=True)[0] * 1e3
     if what == "bconv":
         return bench_bconv(chd, steps) * 1e3
     if what == "bconv_cold":
@@ -503,6 +515,7 @@ def main():
     hmult_us = bench_hmult(chd)[0] * 1e3
     hmult_cold_us, hmult_set = bench_hmult(chd, cold=True)
     hmult_cold_us *= 1e3
+    hmult_sep_us = bench_hmult(chd, separate=True)[0] * 1e3
     hmult_streams_us = bench_hmult_streams(chd)
     bconv_us = bench_bconv(chd) * 1e3
     bconv_cold_us = bench_bconv(chd, cold=True) * 1e3
@@ -581,6 +594,7 @@ def main():
             "ntt_step_us_one_stream": one_ms * 1e3,
             "hmult_keyswitch_us_config4": hmult_us,
             "hmult_keyswitch_us_config4_cold": hmult_cold_us,
+            "hmult_then_rescale_us_config4": hmult_sep_us,
             "hmult_us_per_op_config4_%d_streams" % NTT_STREAMS:
                 hmult_streams_us,
             "bconv_us_config3_warm": bconv_us,
@@ -599,7 +613,9 @@ def main():
                      "stream (the latency of one batch). "
                      "hmult: warm = same key and inputs each step, cold = "
                      "%d MiB of distinct input/key sets rotated; host "
-                     "enqueue included; hmult_us_per_op_config4_%d_streams: "
+                     "enqueue included; hmult_then_rescale: HMult without "
+                     "rescale, then a separate Rescale (warm); "
+                     "hmult_us_per_op_config4_%d_streams: "
                      "independent HMults alternating over that many "
                      "streams, one Context each, time per HMult over the "
                      "whole span (throughput, not the latency of one). "

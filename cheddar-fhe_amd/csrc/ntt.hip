@@ -1417,35 +1417,49 @@ hipError_t launch_ntt_inv(const NttArgs &a, int num_limbs, int num_polys,
 using namespace chd;
 
 namespace {
-// word span [lo, hi) that num_polys polynomials of num_limbs limbs starting
-// at base cover under limb map m (gaps and skips included)
-void limb_span(const uint32_t *base, long long pstride, int num_limbs,
-               int num_polys, const chd_limb_map &m, bool src_side,
-               uintptr_t *lo, uintptr_t *hi) {
+// limbs one polynomial of a strided operand covers under limb map m (its
+// skipped range and, on the source side, its gap included)
+long long span_limbs(int num_limbs, const chd_limb_map &m, bool src_side) {
   const long long top_logical =
       num_limbs - 1 + (m.skip_lo < num_limbs ? m.skip_len : 0);
   const long long gap = src_side ? std::max(m.src_gap, 0) : 0;
-  const long long limbs = top_logical + 1 + gap;
-  const long long ps = std::max(pstride, 0LL);
-  *lo = reinterpret_cast<uintptr_t>(base);
-  *hi = *lo + 4ull * static_cast<unsigned long long>(
-                        (num_polys - 1) * ps + limbs * static_cast<long long>(kN));
+  return top_logical + 1 + gap;
 }
 bool disjoint(uintptr_t alo, uintptr_t ahi, uintptr_t blo, uintptr_t bhi) {
   return ahi <= blo || bhi <= alo;
 }
+// no polynomial of set a (num_a polynomials of limbs_a limbs, pstride_a
+// words apart, of either sign) overlaps any polynomial of set b: each pair
+// is checked on its own, so a set whose polynomials lie far apart (or in
+// descending order) is judged by the memory it reads, not by its hull
+bool sets_disjoint(const uint32_t *a, long long pstride_a, int num_a,
+                   long long limbs_a, const uint32_t *b, long long pstride_b,
+                   int num_b, long long limbs_b) {
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a);
+  const uintptr_t b0 = reinterpret_cast<uintptr_t>(b);
+  for (int i = 0; i < num_a; i++) {
+    // two's-complement wrap: a negative stride moves the base down
+    const uintptr_t alo = a0 + static_cast<uintptr_t>(4LL * i * pstride_a);
+    const uintptr_t ahi = alo + 4ull * static_cast<unsigned long long>(
+                                           limbs_a * static_cast<long long>(kN));
+    for (int j = 0; j < num_b; j++) {
+      const uintptr_t blo = b0 + static_cast<uintptr_t>(4LL * j * pstride_b);
+      const uintptr_t bhi = blo + 4ull * static_cast<unsigned long long>(
+                                             limbs_b * static_cast<long long>(kN));
+      if (!disjoint(alo, ahi, blo, bhi)) return false;
+    }
+  }
+  return true;
+}
 // the ModDown epilogue operand src2 of num_polys polynomials: limbs
-// [src2_lo, src2_hi) of the output read src2 limbs 0 .. src2_hi - src2_lo
+// [src2_lo, src2_hi) of the output read src2 limbs 0 .. src2_hi - src2_lo;
+// true when none of them overlaps the destination polynomial at dst
 bool src2_disjoint(const uint32_t *src2, long long src2_pstride,
-                   int src2_lo, int src2_hi, int num_polys, uintptr_t dlo,
-                   uintptr_t dhi) {
+                   int src2_lo, int src2_hi, int num_polys,
+                   const uint32_t *dst, long long dst_limbs) {
   if (src2 == nullptr || src2_hi <= src2_lo) return true;
-  const uintptr_t lo = reinterpret_cast<uintptr_t>(src2);
-  const uintptr_t hi =
-      lo + 4ull * static_cast<unsigned long long>(
-                      (num_polys - 1) * std::max(src2_pstride, 0LL) +
-                      static_cast<long long>(src2_hi - src2_lo) * kN);
-  return disjoint(lo, hi, dlo, dhi);
+  return sets_disjoint(src2, src2_pstride, num_polys, src2_hi - src2_lo, dst,
+                       0, 1, dst_limbs);
 }
 }  // namespace
 
@@ -1464,10 +1478,12 @@ extern "C" int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m,
   a.map = *m;
   a.tab = *t;
   a.cst = pre_cst;
-  uintptr_t slo, shi, dlo, dhi;
-  limb_span(src, src_pstride, num_limbs, num_polys, *m, true, &slo, &shi);
-  limb_span(dst, dst_pstride, num_limbs, num_polys, *m, false, &dlo, &dhi);
-  a.src_disjoint = disjoint(slo, shi, dlo, dhi) ? 1 : 0;
+  a.src_disjoint =
+      sets_disjoint(src, src_pstride, num_polys, span_limbs(num_limbs, *m, true),
+                    dst, dst_pstride, num_polys,
+                    span_limbs(num_limbs, *m, false))
+          ? 1
+          : 0;
   hipError_t e = launch_ntt_fwd(a, num_limbs, num_polys, pre_cst != nullptr,
                                 kEpiStore, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
@@ -1501,13 +1517,10 @@ extern "C" int chd_k_ntt_fwd_moddown(const chd_tables *t,
   if (!t || !m || !dst || !inv_prod || num_limbs < 0 ||
       (src2 == nullptr && src2_hi > src2_lo) || src2 == dst)
     return set_error(CHD_ERR_ARG, "chd_k_ntt_fwd_moddown: invalid argument");
-  {
-    uintptr_t dlo, dhi;
-    limb_span(dst, 0, num_limbs, 1, *m, false, &dlo, &dhi);
-    if (!src2_disjoint(src2, 0, src2_lo, src2_hi, 1, dlo, dhi))
-      return set_error(CHD_ERR_ARG,
-                       "chd_k_ntt_fwd_moddown: src2 overlaps the destination");
-  }
+  if (!src2_disjoint(src2, 0, src2_lo, src2_hi, 1, dst,
+                     span_limbs(num_limbs, *m, false)))
+    return set_error(CHD_ERR_ARG,
+                     "chd_k_ntt_fwd_moddown: src2 overlaps the destination");
   NttArgs a{};
   a.src = dst;
   a.dst = dst;
@@ -1711,10 +1724,8 @@ extern "C" int chd_k_ntt_fwd_moddown_multi(
       return set_error(CHD_ERR_ARG,
                        "chd_k_ntt_fwd_moddown_multi: invalid destination");
     // every workgroup reads src2 while others write: no overlap at all
-    uintptr_t dlo, dhi;
-    limb_span(dst[p], 0, num_limbs, 1, *m, false, &dlo, &dhi);
-    if (!src2_disjoint(src2, src2_pstride, src2_lo, src2_hi, num_polys, dlo,
-                       dhi))
+    if (!src2_disjoint(src2, src2_pstride, src2_lo, src2_hi, num_polys,
+                       dst[p], span_limbs(num_limbs, *m, false)))
       return set_error(CHD_ERR_ARG,
                        "chd_k_ntt_fwd_moddown_multi: src2 overlaps a "
                        "destination");
@@ -1726,14 +1737,11 @@ extern "C" int chd_k_ntt_fwd_moddown_multi(
   a.map.src_gap = 0;
   if (src != nullptr) {
     // separate source: single-pass kernel when no destination overlaps it
-    uintptr_t slo, shi;
-    limb_span(src, src_pstride, num_limbs, num_polys, a.map, true, &slo, &shi);
     bool ok = true;
-    for (int p = 0; p < num_polys; p++) {
-      uintptr_t dlo, dhi;
-      limb_span(dst[p], 0, num_limbs, 1, a.map, false, &dlo, &dhi);
-      ok = ok && disjoint(slo, shi, dlo, dhi);
-    }
+    for (int p = 0; p < num_polys; p++)
+      ok = ok && sets_disjoint(src, src_pstride, num_polys,
+                               span_limbs(num_limbs, a.map, true), dst[p], 0,
+                               1, span_limbs(num_limbs, a.map, false));
     if (!ok)
       return set_error(CHD_ERR_ARG,
                        "chd_k_ntt_fwd_moddown_multi: source overlaps a "

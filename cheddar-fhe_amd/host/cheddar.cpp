@@ -1089,8 +1089,11 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
   word *const intt = intt_rows ? intt_rows : intt_buf.data();
   for (int p = 0; p < num_polys; p++) {
     AssertTrue(dst[p] != nullptr, "ModDown: null destination");
-    // INTTForModDown requires src != dst per polynomial
-    AssertTrue(dst[p] != src + p * src_pstride,
+    // INTTForModDown requires src != dst per polynomial (the polynomials
+    // of src may lie in separate allocations, src_pstride of either sign)
+    AssertTrue(reinterpret_cast<uintptr_t>(dst[p]) !=
+                   reinterpret_cast<uintptr_t>(src) +
+                       static_cast<uintptr_t>(4LL * p * src_pstride),
                "ModDown: src and dst should be different");
   }
   // INTTForModDown (NTT.cu:973-1128) of all polynomials: either the top
@@ -1463,9 +1466,21 @@ void Context<uint32_t>::RescaleV(int level, CtRef res, CtCRef a) const {
   const int nq = param_.LevelToNP(level).GetNumQ();
   const int nq1 = param_.LevelToNP(level - 1).GetNumQ();
   const auto &ms = mod_switch_handlers_.at(level);
-  DvView<word> db(res.bx, nq1 * n, 0), da(res.ax, nq1 * n, 0);
-  ms.Rescale(db, DvConstView<word>(a.bx, nq * n, 0));
-  ms.Rescale(da, DvConstView<word>(a.ax, nq * n, 0));
+  if (res.bx != res.ax) {
+    // bx and ax in one launch per phase (INTT of the top limb, BConv, NTT
+    // with the rescale epilogue): polynomial 1 is addressed as a.bx + its
+    // distance to a.ax, whatever the sign or size of that distance
+    const long long stride =
+        (static_cast<long long>(reinterpret_cast<intptr_t>(a.ax)) -
+         static_cast<long long>(reinterpret_cast<intptr_t>(a.bx))) /
+        static_cast<long long>(sizeof(word));
+    ms.ModDownMulti({res.bx, res.ax}, a.bx, stride,
+                    ModSwitchHandler<word>::Kind::Rescale);
+  } else {
+    DvView<word> db(res.bx, nq1 * n, 0), da(res.ax, nq1 * n, 0);
+    ms.Rescale(db, DvConstView<word>(a.bx, nq * n, 0));
+    ms.Rescale(da, DvConstView<word>(a.ax, nq * n, 0));
+  }
   if (a.rx != nullptr && res.rx != nullptr) {
     DvView<word> dr(res.rx, nq1 * n, 0);
     ms.Rescale(dr, DvConstView<word>(a.rx, nq * n, 0));

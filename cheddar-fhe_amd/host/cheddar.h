@@ -634,7 +634,8 @@ class ModSwitchHandler<uint32_t> {
 
   enum class Kind { ModDown, Rescale, ModDownAndRescale };
   // ModDownWorker for several polynomials at once: polynomial p of the
-  // source starts at src + p * src_pstride (words), its result goes to
+  // source starts at src + p * src_pstride (words, either sign: the
+  // polynomials may sit in separate allocations), its result goes to
   // dst[p] (separate buffers allowed).
   // intt_rows: when given, the first pass of the INTT (stages 15..8) of the
   // INTT limbs is already there ([polynomial][limb] of the INTT limbs, as

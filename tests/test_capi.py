@@ -187,6 +187,30 @@ def test_moddown_ntt_rejects_overlapping_src2(chd):
     assert b"src2 overlaps" in chd.lib.chd_last_error()
 
 
+def test_moddown_ntt_checks_each_polynomial_of_a_descending_source(chd):
+    """polynomials of src and src2 may be any distance apart, also below
+    the first one (a negative stride, as when a ciphertext's ax sits below
+    its bx): each polynomial is checked against every destination"""
+    lib = _kernel_lib(chd)
+    t, m = Tables(), LimbMap(num_q=20, skip_lo=1 << 30)
+    n = 1 << 16
+    base = 0x10000000
+    dst = (P * 2)(P(base), P(base + 40 * 4 * n))
+    # polynomial 1 of the source lands on dst[0]; polynomial 0 is clear
+    st = lib.chd_k_ntt_fwd_moddown_multi(t, m, dst, 2, 20,
+                                         P(base + 100 * 4 * n), -100 * n,
+                                         None, 0, 0, 0, FAKE, None, None)
+    assert st == -1
+    assert b"source overlaps" in chd.lib.chd_last_error()
+    # the same for the epilogue operand
+    st = lib.chd_k_ntt_fwd_moddown_multi(t, m, dst, 2, 20,
+                                         P(base + 100 * 4 * n), 20 * n,
+                                         P(base + 200 * 4 * n), -165 * n, 0,
+                                         20, FAKE, None, None)
+    assert st == -1
+    assert b"src2 overlaps" in chd.lib.chd_last_error()
+
+
 def test_binding_handles_released_cleanly_at_exit():
     """handles still alive at interpreter exit are destroyed through the
     function bound when they were made, not through module globals that

@@ -318,6 +318,28 @@ def test_hmult_in_place_and_separate_rescale(chd, ks):
     assert np.array_equal(host(ra), _orc.rescale(wa, main, L, 1, 16))
 
 
+def test_rescale_polynomials_in_any_order(chd, ks):
+    """Rescale runs bx and ax together, addressing ax as bx plus their
+    distance: here ax lies below bx in one buffer and the result's bx sits
+    between them; both polynomials must match the oracle"""
+    import torch
+    param, ctx, main, aux = ks
+    L = 24
+    r = rng(460)
+    b, a = uniform_limbs(r, main), uniform_limbs(r, main)
+    big = zeros(4 * L, N)
+    a_ax, res_bx = big[0:L], big[L:2 * L - 1]
+    a_bx, res_ax = big[2 * L:3 * L], big[3 * L:4 * L - 1]
+    a_ax.copy_(dev(a))
+    a_bx.copy_(dev(b))
+    ctx.rescale(L - 1, (res_bx, res_ax), (a_bx, a_ax))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(res_bx), _orc.rescale(b, main, L, 1, 16))
+    assert np.array_equal(host(res_ax), _orc.rescale(a, main, L, 1, 16))
+    # the sources are untouched
+    assert np.array_equal(host(a_bx), b) and np.array_equal(host(a_ax), a)
+
+
 @pytest.mark.parametrize("rot", [1, 1234])
 def test_hrot_and_mult_key(chd, ks, rot, L=20):
     param, ctx, main, aux = ks
