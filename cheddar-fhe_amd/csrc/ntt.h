@@ -51,6 +51,10 @@ struct NttArgs {
   // single-pass kernel (which reads every quarter of a limb while writing
   // its own) may run
   int src_disjoint;
+  // single-pass ModDown NTT only: every limb of polynomial z reads the one
+  // centred source limb src + z * src_pstride, times its cst[l] (a
+  // one-source BConv fused into the transform's first round)
+  int src_bcast;
 };
 
 // Fused ModUp row pass + evaluation-key inner product (PAccum) + CAccum for

@@ -1110,16 +1110,24 @@ __device__ __forceinline__ void radix16_pre(const A &ar,
   }
 }
 
+// kPre: the input times a per-limb MontMul constant cst[l] on the way in.
+// With the store epilogue that is the Montgomery conversion; with the ModDown
+// epilogue the source is broadcast: every limb of polynomial z transforms the
+// same centred (signed) limb src + z * src_pstride times its cst[l], i.e. the
+// output of a one-source BConv (ModSwitch.cu:23-171 with one source:
+// y_l = c T_l 2^-32 mod q_l) that is never stored.
 template <int kEpi, bool kPre, bool kLazy>
 __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
                                             int z, int j, uint32_t q,
                                             uint32_t qinv, uint32_t *lds) {
   using A = Arith<kLazy>;
   using T = typename A::T;
+  constexpr bool kBcast = kPre && kEpi == kEpiModDown;
   const A ar(q, qinv);
   const uint32_t *tw = a.tab.tw + (static_cast<size_t>(lb.ti) << kLogN);
   const uint32_t *src =
-      a.src + z * a.src_pstride + (static_cast<size_t>(lb.sl) << kLogN);
+      a.src + z * a.src_pstride +
+      (kBcast ? size_t{0} : static_cast<size_t>(lb.sl) << kLogN);
   uint32_t *dst = poly_dst(a, z) + (static_cast<size_t>(lb.l) << kLogN) +
                   j * kQuarter;
   const int t = threadIdx.x;
@@ -1166,7 +1174,8 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
     const uint32_t w01c = umin(w01, w01 - q);
     c[3] = (((j >> 1) ^ j) & 1) ? q - w01c : w01c;
     if constexpr (kPre) {
-      // Montgomery-conversion prologue folded into the constants
+      // the prologue constant (Montgomery conversion, or the one-source
+      // BConv table entry of this limb) folded into the constants
       const uint32_t ce = a.cst[lb.ci];
       const uint32_t cen = ce * qn;
 #pragma unroll
@@ -1182,10 +1191,28 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
       const uint32_t x1 = ld_nt<uint32_t>(src, off + 4u * kQuarter);
       const uint32_t x2 = ld_nt<uint32_t>(src, off + 8u * kQuarter);
       const uint32_t x3 = ld_nt<uint32_t>(src, off + 12u * kQuarter);
-      const uint64_t acc = static_cast<uint64_t>(x0) * c[0] +
-                           static_cast<uint64_t>(x1) * c[1] +
-                           static_cast<uint64_t>(x2) * c[2] +
-                           static_cast<uint64_t>(x3) * c[3];
+      uint64_t acc;
+      if constexpr (kBcast) {
+        // centred inputs, |x| < 2^29: the signed sum lies in (-2^61, 2^61);
+        // q 2^32 (= 0 mod q, > 2^61) makes it positive and below 2^63, and
+        // the reduction below then lands in [0, 2.5 q), inside the [0, 4q)
+        // the butterflies take
+        acc = static_cast<uint64_t>(
+            (static_cast<int64_t>(q) << 32) +
+            static_cast<int64_t>(static_cast<int32_t>(x0)) *
+                static_cast<int32_t>(c[0]) +
+            static_cast<int64_t>(static_cast<int32_t>(x1)) *
+                static_cast<int32_t>(c[1]) +
+            static_cast<int64_t>(static_cast<int32_t>(x2)) *
+                static_cast<int32_t>(c[2]) +
+            static_cast<int64_t>(static_cast<int32_t>(x3)) *
+                static_cast<int32_t>(c[3]));
+      } else {
+        acc = static_cast<uint64_t>(x0) * c[0] +
+              static_cast<uint64_t>(x1) * c[1] +
+              static_cast<uint64_t>(x2) * c[2] +
+              static_cast<uint64_t>(x3) * c[3];
+      }
       const uint32_t m = static_cast<uint32_t>(acc) * qn;
       x[k] = static_cast<uint32_t>((static_cast<uint64_t>(m) * q + acc) >> 32);
     }
@@ -1211,6 +1238,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
       for (int m = 0; m < 4; m++) {
         xm[m] = static_cast<int32_t>(
             ld_nt<uint32_t>(src, off + 4u * kQuarter * m));
+        // (a broadcast source is centred: mont takes signed inputs)
         if constexpr (kPre) xm[m] = mont(xm[m], ce, ceq, qs);
       }
       ct_bfly(xm[0], xm[2], w0s, w0q, qs);
@@ -1363,7 +1391,10 @@ hipError_t launch_ntt_fwd(const NttArgs &a, int num_limbs, int num_polys,
   if (a.src_disjoint) {
     const int items = num_limbs * num_polys;
     dim3 g1(4 * ((items + 7) / 8 * 8));
-    if (epilogue == kEpiModDown)
+    if (epilogue == kEpiModDown && a.src_bcast)
+      hipLaunchKernelGGL((ntt_fwd_1p<kEpiModDown, true>), g1, dim3(1024), 0,
+                         s, a, num_limbs, items);
+    else if (epilogue == kEpiModDown)
       hipLaunchKernelGGL((ntt_fwd_1p<kEpiModDown, false>), g1, dim3(1024), 0,
                          s, a, num_limbs, items);
     else if (pre_const)
@@ -1709,32 +1740,56 @@ extern "C" int chd_k_modup_keyacc_batch(const chd_tables *t,
   return 0;
 }
 
-extern "C" int chd_k_ntt_fwd_moddown_multi(
-    const chd_tables *t, const chd_limb_map *m, uint32_t *const *dst,
-    int num_polys, int num_limbs, const uint32_t *src, long long src_pstride,
-    const uint32_t *src2, long long src2_pstride, int src2_lo, int src2_hi,
-    const uint32_t *inv_prod, const uint32_t *pad, void *stream) {
+namespace {
+// NttArgs of a batched ModDown NTT: destinations, the epilogue operand src2
+// and its constants, after the checks both entry points share
+int moddown_multi_args(const char *who, const chd_tables *t,
+                       const chd_limb_map *m, uint32_t *const *dst,
+                       int num_polys, int num_limbs, const uint32_t *src2,
+                       long long src2_pstride, int src2_lo, int src2_hi,
+                       const uint32_t *inv_prod, const uint32_t *pad,
+                       NttArgs *out) {
   if (!t || !m || !dst || !inv_prod || num_limbs < 0 || num_polys < 1 ||
       num_polys > CHD_MAX_JOBS || (src2 == nullptr && src2_hi > src2_lo))
-    return set_error(CHD_ERR_ARG,
-                     "chd_k_ntt_fwd_moddown_multi: invalid argument");
-  NttArgs a{};
+    return set_error(CHD_ERR_ARG, std::string(who) + ": invalid argument");
+  NttArgs &a = *out;
+  a = NttArgs{};
   for (int p = 0; p < num_polys; p++) {
     if (!dst[p])
       return set_error(CHD_ERR_ARG,
-                       "chd_k_ntt_fwd_moddown_multi: invalid destination");
+                       std::string(who) + ": invalid destination");
     // every workgroup reads src2 while others write: no overlap at all
     if (!src2_disjoint(src2, src2_pstride, src2_lo, src2_hi, num_polys,
                        dst[p], span_limbs(num_limbs, *m, false)))
       return set_error(CHD_ERR_ARG,
-                       "chd_k_ntt_fwd_moddown_multi: src2 overlaps a "
-                       "destination");
+                       std::string(who) + ": src2 overlaps a destination");
     a.dst_list[p] = dst[p];
   }
   a.src = dst[0];
   a.dst = dst[0];
   a.map = *m;
   a.map.src_gap = 0;
+  a.tab = *t;
+  a.src2 = src2;
+  a.src2_pstride = src2_pstride;
+  a.src2_lo = src2_lo;
+  a.src2_hi = src2_hi;
+  a.cst2 = inv_prod;
+  a.pad = pad;
+  return 0;
+}
+}  // namespace
+
+extern "C" int chd_k_ntt_fwd_moddown_multi(
+    const chd_tables *t, const chd_limb_map *m, uint32_t *const *dst,
+    int num_polys, int num_limbs, const uint32_t *src, long long src_pstride,
+    const uint32_t *src2, long long src2_pstride, int src2_lo, int src2_hi,
+    const uint32_t *inv_prod, const uint32_t *pad, void *stream) {
+  NttArgs a;
+  if (int st = moddown_multi_args("chd_k_ntt_fwd_moddown_multi", t, m, dst,
+                                  num_polys, num_limbs, src2, src2_pstride,
+                                  src2_lo, src2_hi, inv_prod, pad, &a))
+    return st;
   if (src != nullptr) {
     // separate source: single-pass kernel when no destination overlaps it
     bool ok = true;
@@ -1750,17 +1805,45 @@ extern "C" int chd_k_ntt_fwd_moddown_multi(
     a.src_pstride = src_pstride;
     a.src_disjoint = 1;
   }
-  a.tab = *t;
-  a.src2 = src2;
-  a.src2_pstride = src2_pstride;
-  a.src2_lo = src2_lo;
-  a.src2_hi = src2_hi;
-  a.cst2 = inv_prod;
-  a.pad = pad;
   hipError_t e = launch_ntt_fwd(a, num_limbs, num_polys, false, kEpiModDown,
                                 static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
     return set_error(CHD_ERR_HIP, std::string("chd_k_ntt_fwd_moddown_multi: ") +
                                       hipGetErrorString(e));
+  return 0;
+}
+
+extern "C" int chd_k_ntt_fwd_moddown_bconv1_multi(
+    const chd_tables *t, const chd_limb_map *m, uint32_t *const *dst,
+    int num_polys, int num_limbs, const int32_t *src1, long long src1_pstride,
+    const uint32_t *bconv1, const uint32_t *src2, long long src2_pstride,
+    int src2_lo, int src2_hi, const uint32_t *inv_prod, const uint32_t *pad,
+    void *stream) {
+  const char *who = "chd_k_ntt_fwd_moddown_bconv1_multi";
+  if (!src1 || !bconv1)
+    return set_error(CHD_ERR_ARG, std::string(who) + ": invalid argument");
+  NttArgs a;
+  if (int st = moddown_multi_args(who, t, m, dst, num_polys, num_limbs, src2,
+                                  src2_pstride, src2_lo, src2_hi, inv_prod,
+                                  pad, &a))
+    return st;
+  // each workgroup reads all of its polynomial's source limb while others
+  // write their destinations: no overlap at all
+  const uint32_t *s1 = reinterpret_cast<const uint32_t *>(src1);
+  for (int p = 0; p < num_polys; p++)
+    if (!sets_disjoint(s1, src1_pstride, num_polys, 1, dst[p], 0, 1,
+                       span_limbs(num_limbs, a.map, false)))
+      return set_error(CHD_ERR_ARG,
+                       std::string(who) + ": source overlaps a destination");
+  a.src = s1;
+  a.src_pstride = src1_pstride;
+  a.src_disjoint = 1;
+  a.src_bcast = 1;
+  a.cst = bconv1;
+  hipError_t e = launch_ntt_fwd(a, num_limbs, num_polys, false, kEpiModDown,
+                                static_cast<hipStream_t>(stream));
+  if (e != hipSuccess)
+    return set_error(CHD_ERR_HIP,
+                     std::string(who) + ": " + hipGetErrorString(e));
   return 0;
 }

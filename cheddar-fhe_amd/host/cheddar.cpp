@@ -809,6 +809,16 @@ void ModSwitchHandler<uint32_t>::BuildSwitch(
   K(chd_bconv_table_pack(packed.data(), c2.data(), dst.data(), sl, dl));
   st.table.Resize(packed.size());
   st.table.Upload(packed.data(), packed.size());
+  if (sl == 1) {
+    std::vector<word> col(dl);
+    for (int k = 0; k < dl; k++)
+      col[k] = c2[k] < 0 ? static_cast<word>(c2[k] + static_cast<int64_t>(dst[k]))
+                         : static_cast<word>(c2[k]);
+    st.bconv1.resize(dl);
+    HipCheck(hipMemcpy(st.bconv1.data(), col.data(), dl * sizeof(word),
+                       hipMemcpyHostToDevice),
+             "hipMemcpy");
+  }
 }
 
 // src/core/ModSwitch.cu:429-485: INTTAndMultConst(centre) of src into intt,
@@ -1127,22 +1137,6 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
                     src_len, num_polys, st.const1.data(), 1, CurrentStream()));
   }
   chd_limb_map m = NoSkipMap(param_, np_dst);
-  chd_bconv_job jobs[CHD_MAX_JOBS] = {};
-  for (int p = 0; p < num_polys; p++) {
-    jobs[p].dst = dst[p];
-    jobs[p].src = reinterpret_cast<const int32_t *>(intt) + p * ilen;
-    jobs[p].table = st.table.as<void>();
-    jobs[p].src_len = src_len;
-    jobs[p].dst_len = dst_len;
-    jobs[p].skip_lo = INT_MAX;
-    jobs[p].skip_len = 0;
-  }
-  // BConv into a temporary so that the NTT below reads it and writes dst in
-  // one pass (the single-pass forward NTT cannot run in place)
-  Scratch conv(ws_, static_cast<size_t>(num_polys) * dst_len * n);
-  for (int p = 0; p < num_polys; p++)
-    jobs[p].dst = conv.data() + static_cast<size_t>(p) * dst_len * n;
-  K(chd_k_bconv_batch(&ntt_.Tables(), &m, jobs, num_polys, CurrentStream()));
   const DeviceVector<word> &ipp =
       kind == Kind::ModDown   ? inv_prime_prod_
       : kind == Kind::Rescale ? rescale_inv_prime_prod_
@@ -1159,6 +1153,32 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
   const int src2_off = std::max(0, np_src.num_ter_ - np_dst.num_ter_);
   const int s2_lo = np_dst.num_ter_ - np_non_intt.num_ter_;
   const int s2_hi = s2_lo + np_non_intt.GetNumQ();
+  if (st.src_len == 1 && st.bconv1.size() == static_cast<size_t>(dst_len)) {
+    // one source (Rescale): the NTT forms each limb's BConv, the source
+    // times that limb's table entry, from the one INTT limb as it reads it
+    K(chd_k_ntt_fwd_moddown_bconv1_multi(
+        &ntt_.Tables(), &m, dst.data(), num_polys, dst_len,
+        reinterpret_cast<const int32_t *>(intt), ilen, st.bconv1.data(),
+        src + static_cast<size_t>(src2_off) * n, src_pstride, s2_lo, s2_hi,
+        ipp.data(), pad, CurrentStream()));
+    return;
+  }
+  chd_bconv_job jobs[CHD_MAX_JOBS] = {};
+  for (int p = 0; p < num_polys; p++) {
+    jobs[p].dst = dst[p];
+    jobs[p].src = reinterpret_cast<const int32_t *>(intt) + p * ilen;
+    jobs[p].table = st.table.as<void>();
+    jobs[p].src_len = src_len;
+    jobs[p].dst_len = dst_len;
+    jobs[p].skip_lo = INT_MAX;
+    jobs[p].skip_len = 0;
+  }
+  // BConv into a temporary so that the NTT below reads it and writes dst in
+  // one pass (the single-pass forward NTT cannot run in place)
+  Scratch conv(ws_, static_cast<size_t>(num_polys) * dst_len * n);
+  for (int p = 0; p < num_polys; p++)
+    jobs[p].dst = conv.data() + static_cast<size_t>(p) * dst_len * n;
+  K(chd_k_bconv_batch(&ntt_.Tables(), &m, jobs, num_polys, CurrentStream()));
   K(chd_k_ntt_fwd_moddown_multi(&ntt_.Tables(), &m, dst.data(), num_polys,
                                 dst_len, conv.data(),
                                 static_cast<long long>(dst_len) * n,

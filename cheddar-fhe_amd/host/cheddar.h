@@ -657,6 +657,9 @@ class ModSwitchHandler<uint32_t> {
   struct SwitchTable {       // one source set -> destination set
     DeviceVector<word> const1;   // (N prod_{j!=i} s_j)^-1 mod s_i
     DevBuf table;                // packed BConv table (chd_bconv_table_pack)
+    // one source only: its table column, canonical per destination (the
+    // NTT of the ModDown tail then forms the BConv itself)
+    DeviceVector<word> bconv1;
     int src_len = 0, dst_len = 0;
   };
   // restore: destination primes [restore_lo, restore_hi) come back without

@@ -67,6 +67,21 @@ int chd_k_ntt_fwd_moddown_multi(const chd_tables *t, const chd_limb_map *m,
                                 int src2_hi, const uint32_t *inv_prod,
                                 const uint32_t *pad, void *stream);
 
+/* The ModDown tail of a one-source switch (Rescale: ModSwitch.cu:529-545
+ * through ModDownWorker 566-684) in one launch: for every limb l of
+ * polynomial p, the one-source BConv (ModSwitch.cu:23-171 with src_len 1)
+ * y_l = MontMul(src1_p, bconv1[l]) of the centred INTT output
+ * src1_p = src1 + p * src1_pstride (one limb, signed), then the forward NTT
+ * and the ModDown epilogue of chd_k_ntt_fwd_moddown_multi. y is never
+ * stored. bconv1[l] is the BConv table entry of destination l, canonical.
+ * No source or src2 limb may overlap a destination. */
+int chd_k_ntt_fwd_moddown_bconv1_multi(
+    const chd_tables *t, const chd_limb_map *m, uint32_t *const *dst,
+    int num_polys, int num_limbs, const int32_t *src1, long long src1_pstride,
+    const uint32_t *bconv1, const uint32_t *src2, long long src2_pstride,
+    int src2_lo, int src2_hi, const uint32_t *inv_prod, const uint32_t *pad,
+    void *stream);
+
 /* Inverse NTT with epilogue MontMul(N*intt(x), cst[limb]), centred into
  * [-(q-1)/2, (q-1)/2] when centre (NTT.cu:673-813, 973-1128). */
 int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,

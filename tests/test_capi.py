@@ -116,6 +116,10 @@ def _kernel_lib(chd):
         ctypes.POINTER(Tables), ctypes.POINTER(LimbMap), ctypes.POINTER(P),
         ctypes.c_int, ctypes.c_int, P, ctypes.c_longlong, P,
         ctypes.c_longlong, ctypes.c_int, ctypes.c_int, P, P, P]
+    lib.chd_k_ntt_fwd_moddown_bconv1_multi.argtypes = [
+        ctypes.POINTER(Tables), ctypes.POINTER(LimbMap), ctypes.POINTER(P),
+        ctypes.c_int, ctypes.c_int, P, ctypes.c_longlong, P, P,
+        ctypes.c_longlong, ctypes.c_int, ctypes.c_int, P, P, P]
     lib.chd_k_ntt_fwd_moddown.argtypes = [
         ctypes.POINTER(Tables), ctypes.POINTER(LimbMap), P, ctypes.c_int, P,
         ctypes.c_int, ctypes.c_int, P, P, P]
@@ -209,6 +213,33 @@ def test_moddown_ntt_checks_each_polynomial_of_a_descending_source(chd):
                                          20, FAKE, None, None)
     assert st == -1
     assert b"src2 overlaps" in chd.lib.chd_last_error()
+
+
+def test_moddown_bconv1_ntt_checks(chd):
+    """the one-source ModDown NTT reads its source limb of each polynomial
+    while other workgroups write: a source limb inside a destination, a
+    src2 limb inside a destination and missing operands are rejected
+    before any launch"""
+    lib = _kernel_lib(chd)
+    t, m = Tables(), LimbMap(num_q=20, skip_lo=1 << 30)
+    n = 1 << 16
+    base = 0x10000000
+    dst = (P * 2)(P(base), P(base + 40 * 4 * n))
+    f = lib.chd_k_ntt_fwd_moddown_bconv1_multi
+    # polynomial 1's source limb (stride -60 limbs) is dst[1]'s limb 5
+    st = f(t, m, dst, 2, 20, P(base + 105 * 4 * n), -60 * n, FAKE, None, 0,
+           0, 0, FAKE, None, None)
+    assert st == -1
+    assert b"source overlaps" in chd.lib.chd_last_error()
+    st = f(t, m, dst, 2, 20, P(base + 100 * 4 * n), n, FAKE,
+           P(base + 30 * 4 * n), 20 * n, 0, 20, FAKE, None, None)
+    assert st == -1
+    assert b"src2 overlaps" in chd.lib.chd_last_error()
+    for src1, table in ((None, FAKE), (P(base + 100 * 4 * n), None)):
+        st = f(t, m, dst, 2, 20, src1, n, table, None, 0, 0, 0, FAKE, None,
+               None)
+        assert st == -1
+        assert b"invalid argument" in chd.lib.chd_last_error()
 
 
 def test_binding_handles_released_cleanly_at_exit():
