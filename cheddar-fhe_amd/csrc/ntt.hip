@@ -1193,10 +1193,11 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
       const uint32_t x3 = ld_nt<uint32_t>(src, off + 12u * kQuarter);
       uint64_t acc;
       if constexpr (kBcast) {
-        // centred inputs, |x| < 2^29: the signed sum lies in (-2^61, 2^61);
-        // q 2^32 (= 0 mod q, > 2^61) makes it positive and below 2^63, and
-        // the reduction below then lands in [0, 2.5 q), inside the [0, 4q)
-        // the butterflies take
+        // centred inputs of a source prime below 2^31, |x| < 2^30, times
+        // constants below q: the signed sum lies in (-q 2^32, q 2^32);
+        // adding q 2^32 (= 0 mod q) makes it positive and below q 2^33 <
+        // 2^63, and the reduction below then lands in [0, 3q), inside the
+        // [0, 4q) the butterflies take
         acc = static_cast<uint64_t>(
             (static_cast<int64_t>(q) << 32) +
             static_cast<int64_t>(static_cast<int32_t>(x0)) *
