@@ -318,6 +318,33 @@ def test_hmult_in_place_and_separate_rescale(chd, ks):
     assert np.array_equal(host(ra), _orc.rescale(wa, main, L, 1, 16))
 
 
+@pytest.mark.parametrize("rescale", [True, False])
+def test_hmult_one_aux_prime(chd, rescale):
+    """alpha = 1 (dnum = L = 4): ModDown then has a single source limb, so
+    its BConv is formed inside the ModDown NTT from the key accumulation's
+    INTT rows; without rescale the result is also rescaled separately (one
+    source again), both against the oracle"""
+    main, aux, L = Q30[:4], Q31[:1], 4
+    param = chd.Param(main, aux, [(i, 0) for i in range(1, L + 1)])
+    ctx = chd.Context(param)
+    r = rng(470 + int(rescale))
+    b1, a1, b2, a2 = (uniform_limbs(r, main) for _ in range(4))
+    kb, ka = _evk(r, main, aux, L)
+    out_l = L - 1 if rescale else L
+    res = (zeros(out_l, N), zeros(out_l, N))
+    ctx.hmult(L - 1, res, (dev(b1), dev(a1)), (dev(b2), dev(a2)),
+              [dev(k) for k in kb], [dev(k) for k in ka], rescale=rescale)
+    wb, wa = _orc.hmult(b1, a1, b2, a2, kb, ka, L, L, main, aux, 16,
+                        1 if rescale else 0)
+    assert np.array_equal(host(res[0]), wb)
+    assert np.array_equal(host(res[1]), wa)
+    if not rescale:
+        out = (zeros(L - 1, N), zeros(L - 1, N))
+        ctx.rescale(L - 1, out, res)
+        assert np.array_equal(host(out[0]), _orc.rescale(wb, main, L, 1, 16))
+        assert np.array_equal(host(out[1]), _orc.rescale(wa, main, L, 1, 16))
+
+
 def test_rescale_polynomials_in_any_order(chd, ks):
     """Rescale runs bx and ax together, addressing ax as bx plus their
     distance: here ax lies below bx in one buffer and the result's bx sits
