@@ -162,7 +162,10 @@ int chd_hmult_noalloc(const chd_context *ctx, int level, uint32_t *res_bx,
                       const uint32_t *b_ax, const uint32_t *const *evk_bx,
                       const uint32_t *const *evk_ax, int evk_beta,
                       int rescale, void *stream);
-/* Context::Rescale of a two-polynomial ciphertext (Context.cpp:739-774) */
+/* Context::Rescale of a two-polynomial ciphertext (Context.cpp:739-774).
+ * Both polynomials go through each phase together; the result may not
+ * overlap the input (such a call fails, chd_last_error naming the
+ * overlap). */
 int chd_rescale(const chd_context *ctx, int level, uint32_t *res_bx,
                 uint32_t *res_ax, const uint32_t *a_bx, const uint32_t *a_ax,
                 void *stream);
