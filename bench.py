@@ -43,6 +43,11 @@ BCONV_TRAFFIC = int((1097.5 * 2 + 10240) * 1024)
 # config 4 HMult compulsory bytes: 4 x 24 input limbs, 3 x 2 x 32 key limbs,
 # 2 x 23 output limbs
 HMULT_BYTES = (96 + 192 + 46) * 4 * (1 << 16)
+# its measured HBM bytes per HMult, the sum over its 8 launches
+# (profiles/hmult_config4_traffic.md; the INTT column pass and the BConv
+# run twice)
+HMULT_TRAFFIC = (25275392 + 2 * 11308096 + 2 * 21158912 + 38176384 +
+                 128372032 + 48663552)
 N = 1 << 16
 LIMB_BYTES = 4 * N
 # one limb-transform moves one limb in and one limb out (algorithmic bytes)
@@ -591,9 +596,10 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": hmult_gbs / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": HMULT_TRAFFIC,
             "note": "achieved = compulsory %d B (96 limbs in, 192 key limbs, "
-                    "46 limbs out) / HMult time" % HMULT_BYTES,
+                    "46 limbs out) / HMult time; traffic = the 8 launches' "
+                    "counted HBM bytes" % HMULT_BYTES,
         },
         "extra": {
             "ntt_forward_us": fwd_ms * 1e3,
