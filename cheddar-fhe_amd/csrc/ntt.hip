@@ -1116,6 +1116,18 @@ __device__ __forceinline__ void radix16_pre(const A &ar,
 // same centred (signed) limb src + z * src_pstride times its cst[l], i.e. the
 // output of a one-source BConv (ModSwitch.cu:23-171 with one source:
 // y_l = c T_l 2^-32 mod q_l) that is never stored.
+// round-1 input word: streaming for a limb's own input (its four
+// workgroups read it together), default caching for a broadcast source,
+// which every workgroup of the polynomial reads and the L2 keeps for them
+template <bool kBcast>
+__device__ __forceinline__ uint32_t ld_src(const uint32_t *src,
+                                           uint32_t byte_off) {
+  if constexpr (kBcast)
+    return ld_at<uint32_t>(src, byte_off);
+  else
+    return ld_nt<uint32_t>(src, byte_off);
+}
+
 template <int kEpi, bool kPre, bool kLazy>
 __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
                                             int z, int j, uint32_t q,
@@ -1187,10 +1199,10 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
     for (int k = 0; k < 16; k++) {
       const uint32_t off = 4u * static_cast<uint32_t>((k << 10) | t);
-      const uint32_t x0 = ld_nt<uint32_t>(src, off);
-      const uint32_t x1 = ld_nt<uint32_t>(src, off + 4u * kQuarter);
-      const uint32_t x2 = ld_nt<uint32_t>(src, off + 8u * kQuarter);
-      const uint32_t x3 = ld_nt<uint32_t>(src, off + 12u * kQuarter);
+      const uint32_t x0 = ld_src<kBcast>(src, off);
+      const uint32_t x1 = ld_src<kBcast>(src, off + 4u * kQuarter);
+      const uint32_t x2 = ld_src<kBcast>(src, off + 8u * kQuarter);
+      const uint32_t x3 = ld_src<kBcast>(src, off + 12u * kQuarter);
       uint64_t acc;
       if constexpr (kBcast) {
         // centred inputs of a source prime below 2^31, |x| < 2^30, times
@@ -1238,7 +1250,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
       for (int m = 0; m < 4; m++) {
         xm[m] = static_cast<int32_t>(
-            ld_nt<uint32_t>(src, off + 4u * kQuarter * m));
+            ld_src<kBcast>(src, off + 4u * kQuarter * m));
         // (a broadcast source is centred: mont takes signed inputs)
         if constexpr (kPre) xm[m] = mont(xm[m], ce, ceq, qs);
       }
