@@ -41,7 +41,9 @@ typedef struct chd_limb_map {
 
 /* Forward NTT of num_limbs x num_polys limbs (NTT.cu:606-671, 815-887).
  * pre_cst != NULL: input first multiplied by MontMul(x, pre_cst[limb])
- * (Montgomery conversion). Strides are in words between polynomials. */
+ * (Montgomery conversion). Strides are in words between polynomials. src
+ * either is dst (in place, same stride: two passes) or overlaps none of
+ * dst's polynomials (one pass); a partial overlap races. */
 int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
                   long long dst_pstride, const uint32_t *src,
                   long long src_pstride, int num_limbs, int num_polys,
@@ -83,7 +85,8 @@ int chd_k_ntt_fwd_moddown_bconv1_multi(
     void *stream);
 
 /* Inverse NTT with epilogue MontMul(N*intt(x), cst[limb]), centred into
- * [-(q-1)/2, (q-1)/2] when centre (NTT.cu:673-813, 973-1128). */
+ * [-(q-1)/2, (q-1)/2] when centre (NTT.cu:673-813, 973-1128). src either
+ * is dst (in place, same stride) or does not overlap it. */
 int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
                   long long dst_pstride, const uint32_t *src,
                   long long src_pstride, int num_limbs, int num_polys,
