@@ -77,6 +77,7 @@ def parse():
     ap.add_argument("--only", choices=["ntt_fwd", "ntt_inv", "ntt_step",
                                        "hmult",
                                        "hmult_cold", "hmult_separate",
+                                       "hmult_levels",
                                        "bconv", "bconv_cold",
                                        "copy", "hoist"],
                     help="run only this workload's timed loop (for "
@@ -210,6 +211,37 @@ def bench_hmult(chd, iters=20, cold=False, separate=False):
         run(i)
     torch.cuda.synchronize()
     return event_time_ms(run, iters, stream) / iters, nsets * set_bytes
+
+
+def bench_hmult_levels(chd, levels=(4, 8, 12, 16, 20, 24), iters=50):
+    """HMult (merged rescale) of the config-4 chain at several levels: L q
+    limbs in, L - 1 out, ceil(L / 8) of the key's 3 dnum groups in use, the
+    same key and inputs every step (warm). Returns {L: microseconds}."""
+    import numpy as np
+    import torch
+    main, aux, ctx = _config4_context(chd)
+    rng = np.random.default_rng(0xC0FFEE24)
+
+    def limbs(primes):
+        a = np.stack([rng.integers(0, p, N, dtype=np.uint64) for p in primes])
+        return torch.from_numpy(a.astype(np.uint32).view(np.int32)).cuda()
+    kb = [limbs(main + aux) for _ in range(3)]
+    ka = [limbs(main + aux) for _ in range(3)]
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    out = {}
+    for L in levels:
+        x = [limbs(main[:L]) for _ in range(4)]
+        res = (torch.empty(L - 1, N, dtype=torch.int32, device="cuda"),
+               torch.empty(L - 1, N, dtype=torch.int32, device="cuda"))
+        def run(i):
+            ctx.hmult(L - 1, res, (x[0], x[1]), (x[2], x[3]), kb, ka,
+                      rescale=True, stream=sp)
+        for i in range(3):
+            run(i)
+        torch.cuda.synchronize()
+        out[L] = event_time_ms(run, iters, stream) / iters * 1e3
+    return out
 
 
 def bench_hmult_streams(chd, iters=150, nstreams=NTT_STREAMS):
@@ -450,6 +482,8 @@ def run_only(chd, what, steps):
         return bench_hmult(chd, steps, cold=True)[0] * 1e3
     if what == "hmult_separate":
         return bench_hmult(chd, steps, separate=True)[0] * 1e3
+    if what == "hmult_levels":
+        return bench_hmult_levels(chd, iters=steps)
     if what == "bconv":
         return bench_bconv(chd, steps) * 1e3
     if what == "bconv_cold":

@@ -24,6 +24,10 @@ void K(int status) {
 
 int DivCeil(int a, int b) { return (a + b - 1) / b; }
 
+#ifndef CHD_SMALL_MODDOWN_LIMBS
+#define CHD_SMALL_MODDOWN_LIMBS 32
+#endif
+
 chd_limb_map NoSkipMap(const Parameter<uint32_t> &param, const NPInfo &np) {
   chd_limb_map m{};
   m.num_q = np.GetNumQ();
@@ -1153,7 +1157,14 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
   const int src2_off = std::max(0, np_src.num_ter_ - np_dst.num_ter_);
   const int s2_lo = np_dst.num_ter_ - np_non_intt.num_ter_;
   const int s2_hi = s2_lo + np_non_intt.GetNumQ();
-  if (st.src_len == 1 && st.bconv1.size() == static_cast<size_t>(dst_len)) {
+  // Few destination limbs: the single-pass NTT's time is one workgroup's
+  // latency (~15 us whatever the limb count), so the BConv writes the
+  // destination and the two-pass NTT runs in place on it, its passes
+  // spread over many small workgroups (HMult at L = 4, 8, 12, 16: 6.4, 5.8,
+  // 3.2 and 2.2 us faster; at 38 and 46 limbs the single pass is ahead)
+  const bool few = num_polys * dst_len <= CHD_SMALL_MODDOWN_LIMBS;
+  if (!few && st.src_len == 1 &&
+      st.bconv1.size() == static_cast<size_t>(dst_len)) {
     // one source (Rescale): the NTT forms each limb's BConv, the source
     // times that limb's table entry, from the one INTT limb as it reads it
     K(chd_k_ntt_fwd_moddown_bconv1_multi(
@@ -1172,6 +1183,16 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
     jobs[p].dst_len = dst_len;
     jobs[p].skip_lo = INT_MAX;
     jobs[p].skip_len = 0;
+  }
+  if (few) {
+    K(chd_k_bconv_batch(&ntt_.Tables(), &m, jobs, num_polys,
+                        CurrentStream()));
+    K(chd_k_ntt_fwd_moddown_multi(&ntt_.Tables(), &m, dst.data(), num_polys,
+                                  dst_len, nullptr, 0,
+                                  src + static_cast<size_t>(src2_off) * n,
+                                  src_pstride, s2_lo, s2_hi, ipp.data(), pad,
+                                  CurrentStream()));
+    return;
   }
   // BConv into a temporary so that the NTT below reads it and writes dst in
   // one pass (the single-pass forward NTT cannot run in place)
