@@ -1401,8 +1401,13 @@ hipError_t launch_modup_keyacc(const KeyAccBatch &a, int num_jobs,
 hipError_t launch_ntt_fwd(const NttArgs &a, int num_limbs, int num_polys,
                           bool pre_const, int epilogue, hipStream_t s) {
   if (num_limbs <= 0 || num_polys <= 0) return hipSuccess;
-  if (a.src_disjoint) {
-    const int items = num_limbs * num_polys;
+  // The single pass takes one workgroup's latency however few limbs there
+  // are (12.3 us for 1 limb, 13.9 for 16, 16-17 for 64); up to 16 limbs
+  // the two passes, spread over many small workgroups, are faster (9.3 us
+  // for 1 limb, 11.3-12.5 for 2-16; from 24 limbs on they are not). The
+  // ModDown epilogue keeps the single pass: its caller makes that choice.
+  const int items = num_limbs * num_polys;
+  if (a.src_disjoint && (epilogue == kEpiModDown || items > 16)) {
     dim3 g1(4 * ((items + 7) / 8 * 8));
     if (epilogue == kEpiModDown && a.src_bcast)
       hipLaunchKernelGGL((ntt_fwd_1p<kEpiModDown, true>), g1, dim3(1024), 0,
