@@ -43,7 +43,8 @@ typedef struct chd_limb_map {
  * pre_cst != NULL: input first multiplied by MontMul(x, pre_cst[limb])
  * (Montgomery conversion). Strides are in words between polynomials. src
  * either is dst (in place, same stride: two passes) or overlaps none of
- * dst's polynomials (one pass); a partial overlap races. */
+ * dst's polynomials (one pass above 16 limbs, two up to 16); a partial
+ * overlap races. */
 int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
                   long long dst_pstride, const uint32_t *src,
                   long long src_pstride, int num_limbs, int num_polys,
