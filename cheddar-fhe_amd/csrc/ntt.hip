@@ -32,6 +32,7 @@
 #include "chd_device.h"
 #include "kernel_common.h"
 #include "ntt.h"
+#include "overlap.h"
 
 namespace chd {
 namespace {
@@ -1474,31 +1475,12 @@ long long span_limbs(int num_limbs, const chd_limb_map &m, bool src_side) {
   const long long gap = src_side ? std::max(m.src_gap, 0) : 0;
   return top_logical + 1 + gap;
 }
-bool disjoint(uintptr_t alo, uintptr_t ahi, uintptr_t blo, uintptr_t bhi) {
-  return ahi <= blo || bhi <= alo;
-}
-// no polynomial of set a (num_a polynomials of limbs_a limbs, pstride_a
-// words apart, of either sign) overlaps any polynomial of set b: each pair
-// is checked on its own, so a set whose polynomials lie far apart (or in
-// descending order) is judged by the memory it reads, not by its hull
+// chd::sets_disjoint_words over polynomials of limbs_a / limbs_b limbs
 bool sets_disjoint(const uint32_t *a, long long pstride_a, int num_a,
                    long long limbs_a, const uint32_t *b, long long pstride_b,
                    int num_b, long long limbs_b) {
-  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a);
-  const uintptr_t b0 = reinterpret_cast<uintptr_t>(b);
-  for (int i = 0; i < num_a; i++) {
-    // two's-complement wrap: a negative stride moves the base down
-    const uintptr_t alo = a0 + static_cast<uintptr_t>(4LL * i * pstride_a);
-    const uintptr_t ahi = alo + 4ull * static_cast<unsigned long long>(
-                                           limbs_a * static_cast<long long>(kN));
-    for (int j = 0; j < num_b; j++) {
-      const uintptr_t blo = b0 + static_cast<uintptr_t>(4LL * j * pstride_b);
-      const uintptr_t bhi = blo + 4ull * static_cast<unsigned long long>(
-                                             limbs_b * static_cast<long long>(kN));
-      if (!disjoint(alo, ahi, blo, bhi)) return false;
-    }
-  }
-  return true;
+  return sets_disjoint_words(a, pstride_a, num_a, limbs_a * kN, b, pstride_b,
+                             num_b, limbs_b * kN);
 }
 // the ModDown epilogue operand src2 of num_polys polynomials: limbs
 // [src2_lo, src2_hi) of the output read src2 limbs 0 .. src2_hi - src2_lo;
@@ -1533,6 +1515,14 @@ extern "C" int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m,
                     span_limbs(num_limbs, *m, false))
           ? 1
           : 0;
+  // the two passes run in place only when every limb is read from where it
+  // is written: the same base, polynomial stride and limb layout
+  if (!a.src_disjoint &&
+      (src != dst || m->src_gap != 0 ||
+       (num_polys > 1 && src_pstride != dst_pstride)))
+    return set_error(CHD_ERR_ARG,
+                     "chd_k_ntt_fwd: source and destination overlap without "
+                     "being the same polynomials");
   hipError_t e = launch_ntt_fwd(a, num_limbs, num_polys, pre_cst != nullptr,
                                 kEpiStore, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)

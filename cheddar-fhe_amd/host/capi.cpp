@@ -347,6 +347,76 @@ extern "C" int chd_mult_key(const chd_context *ctx, int level,
                             MakeEvk(ctx, evk_bx, evk_ax, evk_beta)))
 }
 
+namespace {
+// [a, a + aw) and [b, b + bw) (words) share memory
+bool Overlap(const void *a, size_t aw, const void *b, size_t bw) {
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a);
+  const uintptr_t b0 = reinterpret_cast<uintptr_t>(b);
+  return a0 < b0 + 4 * bw && b0 < a0 + 4 * aw;
+}
+}  // namespace
+
+extern "C" int chd_mult_key_no_mod_down(const chd_context *ctx, int level,
+                                        uint32_t *acc_b, uint32_t *acc_a,
+                                        const uint32_t *a_bx,
+                                        const uint32_t *a_ax,
+                                        const uint32_t *a_rx,
+                                        const uint32_t *const *evk_bx,
+                                        const uint32_t *const *evk_ax,
+                                        int evk_beta, void *stream) {
+  CHD_CALL("chd_mult_key_no_mod_down",
+           LevelOk(ctx, level) && acc_b && acc_a && a_bx && a_ax && evk_bx &&
+               evk_ax && evk_beta > 0,
+           {
+             const auto &p = ctx->c->param_;
+             const size_t qw =
+                 static_cast<size_t>(p.LevelToNP(level).GetNumQ()) * p.degree_;
+             const size_t tw = qw + static_cast<size_t>(p.alpha_) * p.degree_;
+             // Context.cpp:657-658: no in-place operation
+             bool bad = Overlap(acc_b, tw, acc_a, tw);
+             for (const uint32_t *in : {a_bx, a_ax, a_rx})
+               bad = bad || (in != nullptr && (Overlap(acc_b, tw, in, qw) ||
+                                               Overlap(acc_a, tw, in, qw)));
+             if (bad)
+               throw cheddar::Error(
+                   "In-place operation is not supported for "
+                   "MultKeyNoModDown (the accumulator overlaps an input)");
+             const auto key = MakeEvk(ctx, evk_bx, evk_ax, evk_beta);
+             if (a_rx != nullptr)
+               ctx->c->KeyMultNoModDownV(level, acc_b, acc_a, a_rx, a_bx, a_ax,
+                                         key);
+             else
+               ctx->c->KeyMultNoModDownV(level, acc_b, acc_a, a_ax, a_bx,
+                                         nullptr, key);
+           })
+}
+
+extern "C" int chd_mult_key_no_mod_down_mod_up(
+    const chd_context *ctx, int level, uint32_t *acc_b, uint32_t *acc_a,
+    const uint32_t *const *a_modup, const uint32_t *const *evk_bx,
+    const uint32_t *const *evk_ax, int evk_beta, void *stream) {
+  CHD_CALL("chd_mult_key_no_mod_down_mod_up",
+           LevelOk(ctx, level) && acc_b && acc_a && a_modup && evk_bx &&
+               evk_ax && evk_beta > 0,
+           {
+             const auto &p = ctx->c->param_;
+             const size_t tw =
+                 static_cast<size_t>(p.LevelToNP(level).GetNumQ() + p.alpha_) *
+                 p.degree_;
+             const auto &ms = ctx->c->mod_switch_handlers_.at(level);
+             bool bad = Overlap(acc_b, tw, acc_a, tw);
+             for (int g = ms.FirstGroup(); g < ms.GetBeta(); g++)
+               bad = bad || (a_modup[g] != nullptr &&
+                             (Overlap(acc_b, tw, a_modup[g], tw) ||
+                              Overlap(acc_a, tw, a_modup[g], tw)));
+             if (bad)
+               throw cheddar::Error(
+                   "MultKeyNoModDown: the accumulator overlaps a ModUp group");
+             ctx->c->KeyMultModUpV(level, acc_b, acc_a, a_modup,
+                                   MakeEvk(ctx, evk_bx, evk_ax, evk_beta));
+           })
+}
+
 extern "C" int chd_hrot(const chd_context *ctx, int level, uint32_t *res_bx,
                         uint32_t *res_ax, const uint32_t *a_bx,
                         const uint32_t *a_ax, const uint32_t *const *evk_bx,

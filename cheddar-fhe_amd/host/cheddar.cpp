@@ -11,6 +11,7 @@
 
 #include "cheddar_amd.h"
 #include "chd_device.h"
+#include "overlap.h"
 #include "prime_math.h"
 
 namespace cheddar {
@@ -1110,6 +1111,20 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
                        static_cast<uintptr_t>(4LL * p * src_pstride),
                "ModDown: src and dst should be different");
   }
+  // NTTForModDown's epilogue operand src2 (the kept limbs of the source) is
+  // read while other workgroups write the destinations, and with few
+  // destination limbs the BConv writes them before that: no destination
+  // may overlap any polynomial's src2, checked before anything is launched
+  const int src2_off = std::max(0, np_src.num_ter_ - np_dst.num_ter_);
+  const int s2_lo = np_dst.num_ter_ - np_non_intt.num_ter_;
+  const int s2_hi = s2_lo + np_non_intt.GetNumQ();
+  if (s2_hi > s2_lo)
+    for (int p = 0; p < num_polys; p++)
+      AssertTrue(chd::sets_disjoint_words(
+                     src + static_cast<size_t>(src2_off) * n, src_pstride,
+                     num_polys, static_cast<long long>(s2_hi - s2_lo) * n,
+                     dst[p], 0, 1, static_cast<long long>(dst_len) * n),
+                 "ModDown: the kept source limbs overlap a destination");
   // INTTForModDown (NTT.cu:973-1128) of all polynomials: either the top
   // main limbs (case 1) or the leading terminal limbs (case 2), then the
   // aux limbs when the source has them
@@ -1154,10 +1169,7 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
   const word *pad =
       kind != Kind::ModDown && padv.size() != 0 ? padv.data() : nullptr;
   // NTTForModDown (NTT.cu:417-604) with src2 = the untouched low limbs
-  const int src2_off = std::max(0, np_src.num_ter_ - np_dst.num_ter_);
-  const int s2_lo = np_dst.num_ter_ - np_non_intt.num_ter_;
-  const int s2_hi = s2_lo + np_non_intt.GetNumQ();
-  // Few destination limbs: the single-pass NTT's time is one workgroup's
+  // (src2_off, s2_lo, s2_hi above). Few destination limbs: the single-pass NTT's time is one workgroup's
   // latency (~15 us whatever the limb count), so the BConv writes the
   // destination and the two-pass NTT runs in place on it, its passes
   // spread over many small workgroups (HMult at L = 4, 8, 12, 16: 6.4, 5.8,
@@ -1359,6 +1371,110 @@ void Context<uint32_t>::KeyMultExtV(int level, word *acc_b, word *acc_a,
                                     const EvkRef &key) const {
   KeyAccumulate(level, acc_b, acc_a, d, nullptr, nullptr, nullptr, nullptr,
                 key, add_b);
+}
+
+// src/core/Context.cpp:609-643 on views: the PAccum of the non-empty dnum
+// groups of a caller-held ModUp with the key read from the level's first
+// chain position (the key's extra_ view, Context.cpp:640)
+void Context<uint32_t>::KeyMultModUpV(int level, word *acc_b, word *acc_a,
+                                      const word *const *modup,
+                                      const EvkRef &key) const {
+  const NPInfo a_np = param_.LevelToNP(level);
+  const int n = param_.degree_;
+  const int num_q = a_np.GetNumQ();
+  const int num_aux = key.np.num_aux_;
+  AssertTrue(num_aux == param_.alpha_, "Invalid setting for MultKeyNoModDown");
+  const int prime_offset = param_.GetMaxNumTer() - a_np.num_ter_;
+  const int padded_num_q = num_q + prime_offset;
+  const int beta = DivCeil(padded_num_q, num_aux);
+  AssertTrue(static_cast<int>(key.bx.size()) >= beta &&
+                 key.bx.size() == key.ax.size(),
+             "Beta mismatch");
+  const int key_q = key.np.GetNumQ() - prime_offset;
+  AssertTrue(key_q >= num_q, "MultKeyNoModDown: key level below input level");
+  const NPInfo np(a_np.num_main_, a_np.num_ter_, num_aux);
+  const int total = np.GetNumTotal() * n;
+  const int aux_words = num_aux * n;
+  std::vector<std::vector<DvConstView<word>>> key_views;
+  std::vector<DvConstView<word>> modup_views;
+  for (int i = 0; i < beta; i++) {
+    if (std::min((i + 1) * num_aux, padded_num_q) <= prime_offset) continue;
+    AssertTrue(modup[i] != nullptr, "MultKeyNoModDown: null ModUp group");
+    const int key_words = (key_q + num_aux) * n;
+    key_views.push_back(
+        {DvConstView<word>(key.bx[i] + static_cast<size_t>(prime_offset) * n,
+                           key_words, aux_words),
+         DvConstView<word>(key.ax[i] + static_cast<size_t>(prime_offset) * n,
+                           key_words, aux_words)});
+    modup_views.emplace_back(modup[i], total, aux_words);
+  }
+  std::vector<DvView<word>> acc{DvView<word>(acc_b, total, aux_words),
+                                DvView<word>(acc_a, total, aux_words)};
+  elem_handler_.PAccum(acc, np, key_views, modup_views);
+}
+
+// src/core/Context.cpp:609-643
+void Context<uint32_t>::MultKeyNoModDown(Ct &accum,
+                                         const std::vector<Dv> &a_modup,
+                                         const Ct &a_orig,
+                                         const Evk &key) const {
+  const NPInfo a_np = a_orig.GetNP();
+  const int level = param_.NPToLevel(a_np);
+  AssertTrue(key.GetNP().num_aux_ == param_.alpha_,
+             "Invalid setting for MultKeyNoModDown");
+  AssertTrue(&accum != &a_orig,
+             "In-place operation is not supported for MultKeyNoModDown");
+  const int num_aux = param_.alpha_;
+  const int prime_offset = param_.GetMaxNumTer() - a_np.num_ter_;
+  const int padded_num_q = a_np.GetNumQ() + prime_offset;
+  const int beta = DivCeil(padded_num_q, num_aux);
+  AssertTrue(key.GetBeta() >= beta && static_cast<int>(a_modup.size()) == beta,
+             "Beta mismatch");
+  const NPInfo np(a_np.num_main_, a_np.num_ter_, num_aux);
+  const size_t total = static_cast<size_t>(np.GetNumTotal()) * param_.degree_;
+  std::vector<const word *> modup(beta, nullptr);
+  for (int i = 0; i < beta; i++) {
+    if (std::min((i + 1) * num_aux, padded_num_q) <= prime_offset) continue;
+    AssertTrue(a_modup[i].size() == total,
+               "MultKeyNoModDown: ModUp group size mismatch");
+    modup[i] = a_modup[i].data();
+  }
+  const double scale = a_orig.GetScale();
+  const int slots = a_orig.GetNumSlots();
+  accum.RemoveRx();
+  accum.ModifyNP(np);
+  accum.SetScale(scale);
+  accum.SetNumSlots(slots);
+  KeyMultModUpV(level, accum.bx_.data(), accum.ax_.data(), modup.data(),
+                RefOfKey(key));
+}
+
+// src/core/Context.cpp:645-712: ModUp, PAccum and CAccum in the fused key
+// accumulation (one launch after the ModUp's INTT, BConv and column pass)
+void Context<uint32_t>::MultKeyNoModDown(Ct &accum, const Ct &a,
+                                         const Evk &key) const {
+  const NPInfo a_np = a.GetNP();
+  AssertTrue(a_np.num_aux_ == 0,
+             "MultKeyNoModDown is not supported for ciphertexts with p "
+             "primes");
+  AssertTrue(&accum != &a,
+             "In-place operation is not supported for MultKeyNoModDown");
+  const int level = param_.NPToLevel(a_np);
+  AssertTrue(key.GetNP().num_aux_ == param_.alpha_,
+             "Invalid setting for MultKeyNoModDown");
+  const double scale = a.GetScale();
+  const int slots = a.GetNumSlots();
+  accum.RemoveRx();
+  accum.ModifyNP(NPInfo(a_np.num_main_, a_np.num_ter_, param_.alpha_));
+  accum.SetScale(scale);
+  accum.SetNumSlots(slots);
+  const EvkRef k = RefOfKey(key);
+  if (a.HasRx())  // relinearisation: ModUp(rx), p_prod * (bx, ax)
+    KeyMultNoModDownV(level, accum.bx_.data(), accum.ax_.data(),
+                      a.rx_.data(), a.bx_.data(), a.ax_.data(), k);
+  else  // MultKey: ModUp(ax), p_prod * bx
+    KeyMultNoModDownV(level, accum.bx_.data(), accum.ax_.data(),
+                      a.ax_.data(), a.bx_.data(), nullptr, k);
 }
 
 void Context<uint32_t>::KeyAccumulate(int level, word *acc_b, word *acc_a,

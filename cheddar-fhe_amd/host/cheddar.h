@@ -749,6 +749,7 @@ template <>
 class Context<uint32_t> {
  public:
   using word = uint32_t;
+  using Dv = DeviceVector<word>;
   using Ct = Ciphertext<word>;
   using Evk = EvaluationKey<word>;
   static std::shared_ptr<Context<word>> Create(const Parameter<word> &param);
@@ -763,6 +764,20 @@ class Context<uint32_t> {
   void Rescale(Ct &res, const Ct &a) const;
   void HRot(Ct &res, const Ct &a, const Evk &rot_key, int rot_dist) const;
   void Permute(Ct &res, const Ct &a, int rot_dist) const;
+  // Special-purpose key products for bootstrapping and hoisting
+  // (Context.h:420-423, Context.cpp:609-712): the key switch without its
+  // ModDown. accum gets the level's q primes plus alpha aux primes, a's
+  // scale and slot count, and no rx; it may not be a (or a_orig).
+  // PAccum of a caller-held ModUp: a_modup[g] is dnum group g of the ModUp
+  // (ModSwitchHandler::ModUp's output, num_q + alpha limbs; groups holding
+  // no limb of a_orig's level may be empty), multiplied by the key's group g
+  // and summed over the extended basis.
+  void MultKeyNoModDown(Ct &accum, const std::vector<Dv> &a_modup,
+                        const Ct &a_orig, const Evk &key) const;
+  // ModUp of a's rx (relinearisation) or of its ax (MultKey), the PAccum
+  // above, then p_prod * (bx, ax) (or bx alone) added on the q limbs.
+  // a may not carry aux primes.
+  void MultKeyNoModDown(Ct &accum, const Ct &a, const Evk &key) const;
 
   // element-wise entry points (Context.h:95-300, Context.cpp:132-560,
   // 794-929); operands share the primes (and scale, where added)
@@ -831,6 +846,12 @@ class Context<uint32_t> {
   // groups, plus add_b (q + alpha limbs) on the b part.
   void KeyMultExtV(int level, word *acc_b, word *acc_a, const word *d,
                    const word *add_b, const EvkRef &key) const;
+  // the PAccum of MultKeyNoModDown(accum, a_modup, a_orig, key) on views:
+  // modup[g] for g < GetBeta() of the level's ModSwitchHandler, each
+  // num_q + alpha limbs (unread, and may be null, for groups before its
+  // FirstGroup()); acc_b / acc_a get num_q + alpha limbs
+  void KeyMultModUpV(int level, word *acc_b, word *acc_a,
+                     const word *const *modup, const EvkRef &key) const;
   // KeyMultExtV of num (<= CHD_MAX_JOBS) independent inputs at one level,
   // each with its own key: input i is d + i * d_stride, its add_b is
   // add_b + i * add_stride and its result goes to (acc_b[i], acc_a[i]).

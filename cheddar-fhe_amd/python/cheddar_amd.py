@@ -69,6 +69,10 @@ _SIGS = {
                                                      _vp]),
     "chd_rescale": (_i, [_vp, _i] + [_vp] * 4 + [_vp]),
     "chd_mult_key": (_i, [_vp, _i] + [_vp] * 4 + [_pp, _pp, _i, _vp]),
+    "chd_mult_key_no_mod_down": (_i, [_vp, _i] + [_vp] * 5 + [_pp, _pp, _i,
+                                                             _vp]),
+    "chd_mult_key_no_mod_down_mod_up": (_i, [_vp, _i, _vp, _vp, _pp, _pp, _pp,
+                                             _i, _vp]),
     "chd_hrot": (_i, [_vp, _i] + [_vp] * 4 + [_pp, _pp, _i, _i, _i, _vp]),
     "chd_permute": (_i, [_vp, _i] + [_vp] * 4 + [_i, _vp]),
     "chd_hoist_baby_steps": (_i, [_vp, _i, _vp, _vp, _i, _ip, _pp, _pp, _i,
@@ -124,7 +128,9 @@ def ptr(t):
 
 
 def ptr_array(ts):
-    return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+    """device pointers of torch tensors (None gives NULL)"""
+    return (ctypes.c_void_p * len(ts))(
+        *[None if t is None else t.data_ptr() for t in ts])
 
 
 def _own(obj, h, destroy):
@@ -317,6 +323,23 @@ class Context:
                                 ptr(a[0]), ptr(a[1]), ptr_array(evk_b),
                                 ptr_array(evk_a), len(evk_b),
                                 self._s(stream)))
+
+    def mult_key_no_mod_down(self, level, acc, a, evk_b, evk_a, stream=None):
+        """Context::MultKeyNoModDown(accum, a, key): acc = (acc_b, acc_a) of
+        num_q + alpha limbs; a = (bx, ax) or (bx, ax, rx)"""
+        rx = a[2] if len(a) > 2 else None
+        _check(lib.chd_mult_key_no_mod_down(
+            self.h, level, ptr(acc[0]), ptr(acc[1]), ptr(a[0]), ptr(a[1]),
+            ptr(rx), ptr_array(evk_b), ptr_array(evk_a), len(evk_b),
+            self._s(stream)))
+
+    def mult_key_no_mod_down_mod_up(self, level, acc, a_modup, evk_b, evk_a,
+                                    stream=None):
+        """Context::MultKeyNoModDown(accum, a_modup, a_orig, key): a_modup is
+        the list mod_up wrote (None for groups holding no limb of level)"""
+        _check(lib.chd_mult_key_no_mod_down_mod_up(
+            self.h, level, ptr(acc[0]), ptr(acc[1]), ptr_array(a_modup),
+            ptr_array(evk_b), ptr_array(evk_a), len(evk_b), self._s(stream)))
 
     def hrot(self, level, res, a, evk_b, evk_a, rot, num_slots=N // 2,
              stream=None):

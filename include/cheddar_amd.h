@@ -153,9 +153,12 @@ int chd_hmult(const chd_context *ctx, int level, uint32_t *res_bx,
  * instead of the context's arena, and the call makes no hipMalloc, hipFree
  * or other allocating call. A level whose HMult needs more than 64 MiB of
  * temporaries (more than 24 q limbs with alpha = 8, dnum 3) is rejected
- * with CHD_ERR_INVALID_ARGUMENT. Every call on one GPU shares that array:
- * calls that overlap on one GPU (other streams, threads or contexts) race;
- * order them. */
+ * with CHD_ERR_INVALID_ARGUMENT. Every call on one GPU shares that array,
+ * and the library orders those calls itself: host threads take a
+ * per-GPU lock, and a call on another stream than the previous call (of
+ * any context) first makes its stream wait for that call's end, so calls
+ * from several contexts and streams run one after another on the device
+ * rather than at the same time. */
 int chd_hmult_noalloc(const chd_context *ctx, int level, uint32_t *res_bx,
                       uint32_t *res_ax, const uint32_t *a_bx,
                       const uint32_t *a_ax, const uint32_t *b_bx,
@@ -174,6 +177,33 @@ int chd_mult_key(const chd_context *ctx, int level, uint32_t *res_bx,
                  uint32_t *res_ax, const uint32_t *a_bx, const uint32_t *a_ax,
                  const uint32_t *const *evk_bx, const uint32_t *const *evk_ax,
                  int evk_beta, void *stream);
+/* Context::MultKeyNoModDown(accum, a, key) (Context.h:423,
+ * Context.cpp:645-712): the key switch without its ModDown, for hoisting and
+ * bootstrapping callers (Hoist.cu:676, 771, 849). acc_b / acc_a get
+ * num_q(level) + alpha limbs: sum_g ModUp(d)_g * evk_g over the extended
+ * basis, plus P * a_bx on the q limbs of acc_b, and P * a_ax on those of
+ * acc_a when a_rx is given. d = a_rx when a_rx is not NULL
+ * (relinearisation of a tensor), else a_ax (MultKey). The accumulators may
+ * not overlap each other or an input (the reference's no-in-place rule). */
+int chd_mult_key_no_mod_down(const chd_context *ctx, int level,
+                             uint32_t *acc_b, uint32_t *acc_a,
+                             const uint32_t *a_bx, const uint32_t *a_ax,
+                             const uint32_t *a_rx,
+                             const uint32_t *const *evk_bx,
+                             const uint32_t *const *evk_ax, int evk_beta,
+                             void *stream);
+/* Context::MultKeyNoModDown(accum, a_modup, a_orig, key) (Context.h:421-422,
+ * Context.cpp:609-643): the PAccum of a caller-held ModUp with the key,
+ * a_modup[g] for g < chd_context_beta(level) as chd_mod_up writes it
+ * (num_q + alpha limbs each; groups holding no limb of the level are not
+ * read and may be NULL) -> acc_b / acc_a (num_q(level) + alpha limbs),
+ * which may not overlap each other or a ModUp group. */
+int chd_mult_key_no_mod_down_mod_up(const chd_context *ctx, int level,
+                                    uint32_t *acc_b, uint32_t *acc_a,
+                                    const uint32_t *const *a_modup,
+                                    const uint32_t *const *evk_bx,
+                                    const uint32_t *const *evk_ax,
+                                    int evk_beta, void *stream);
 /* Context::HRot (Context.cpp:776-791): MultKey then Permute by 5^rot;
  * num_slots as Ciphertext::GetNumSlots (N/2 for a fresh ciphertext).
  * res must not alias a. */

@@ -42,9 +42,10 @@ typedef struct chd_limb_map {
 /* Forward NTT of num_limbs x num_polys limbs (NTT.cu:606-671, 815-887).
  * pre_cst != NULL: input first multiplied by MontMul(x, pre_cst[limb])
  * (Montgomery conversion). Strides are in words between polynomials. src
- * either is dst (in place, same stride: two passes) or overlaps none of
- * dst's polynomials (one pass above 16 limbs, two up to 16); a partial
- * overlap races. */
+ * either is dst (in place: same stride and src_gap 0; two passes) or
+ * overlaps none of dst's polynomials (one pass above 16 limbs, two up to
+ * 16); any other overlap is rejected with CHD_ERR_INVALID_ARGUMENT before
+ * a launch. */
 int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
                   long long dst_pstride, const uint32_t *src,
                   long long src_pstride, int num_limbs, int num_polys,

@@ -253,6 +253,91 @@ int main() {
     check("HRot(5)", same(download(rot.bx_.data(), qw), hrb) &&
                          same(download(rot.ax_.data(), qw), hra));
   }
+  // Context::MultKeyNoModDown, both overloads (Context.h:420-423,
+  // Context.cpp:609-712), shaped as the reference's hoisting calls them
+  // (Hoist.cu:676, 771, 849): a caller-held ModUp of a.ax, a.ax itself (the
+  // MultKey branch) and a tensor with rx (the relinearisation branch),
+  // against orc_mod_up + orc_paccum (+ orc_caccum)
+  {
+    std::vector<word> pp(L);
+    orc_p_prod(pp.data(), main_p.data(), L, aux_p.data(), alpha);
+    auto key_mult = [&](const std::vector<word> &d, std::vector<word> &ob,
+                        std::vector<word> &oa) {
+      std::vector<word> up(static_cast<size_t>(beta) * kw);
+      orc_mod_up(up.data(), d.data(), L, main_p.data(), aux_p.data(), alpha,
+                 kLogN);
+      ob.assign(kw, 0);
+      oa.assign(kw, 0);
+      orc_paccum(ob.data(), oa.data(), up.data(), beta, kb.data(), ka.data(),
+                 L, alpha, L, chain_k.data(), kLogN);
+    };
+    const NPInfo np_acc(L, 0, alpha);
+    std::vector<word> pb, pa;
+    key_mult(ha1, pb, pa);
+
+    // (accum, a_modup, a_orig, key): the PAccum of a ModUp the caller holds
+    const auto &ms = ctx->mod_switch_handlers_[L - 1];
+    std::vector<DeviceVector<word>> up(ms.GetBeta());
+    std::vector<DvView<word>> upv;
+    for (auto &u : up) {
+      u.resize(kw);
+      upv.push_back(u.View(alpha * static_cast<int>(kN)));
+    }
+    ms.ModUp(upv, a.ax_.ConstView());
+    Ct acc;
+    ctx->MultKeyNoModDown(acc, up, a, key);
+    check("MultKeyNoModDown(accum, a_modup, a_orig, key)",
+          acc.GetNP() == np_acc && !acc.HasRx() &&
+              acc.GetScale() == a.GetScale() &&
+              same(download(acc.bx_.data(), kw), pb) &&
+              same(download(acc.ax_.data(), kw), pa));
+
+    // (accum, a, key) without rx: ModUp(ax), PAccum, P * bx on the q limbs
+    std::vector<word> wb2 = pb;
+    orc_caccum(wb2.data(), hb1.data(), pp.data(), L, main_p.data(), kLogN);
+    ctx->MultKeyNoModDown(acc, a, key);
+    check("MultKeyNoModDown(accum, a, key), MultKey branch",
+          acc.GetNP() == np_acc && same(download(acc.bx_.data(), kw), wb2) &&
+              same(download(acc.ax_.data(), kw), pa));
+
+    // (accum, a, key) with rx: ModUp(rx), PAccum, P * (bx, ax)
+    Ct t;
+    ctx->Mult(t, a, b);
+    std::vector<word> tb(qw), ta(qw), tr(qw), rb, ra;
+    orc_tensor(tb.data(), ta.data(), tr.data(), hb1.data(), ha1.data(),
+               hb2.data(), ha2.data(), L, main_p.data(), kLogN);
+    key_mult(tr, rb, ra);
+    orc_caccum(rb.data(), tb.data(), pp.data(), L, main_p.data(), kLogN);
+    orc_caccum(ra.data(), ta.data(), pp.data(), L, main_p.data(), kLogN);
+    ctx->MultKeyNoModDown(acc, t, key);
+    check("MultKeyNoModDown(accum, a, key), relinearisation branch",
+          acc.GetNP() == np_acc && acc.GetScale() == t.GetScale() &&
+              same(download(acc.bx_.data(), kw), rb) &&
+              same(download(acc.ax_.data(), kw), ra));
+    // ModDown of that accumulator is Relinearize (Context.cpp:584-607 with
+    // 645-712)
+    DeviceVector<word> md(qw);
+    DvView<word> mdv = md.View();
+    ms.ModDown(mdv, acc.bx_.ConstView(alpha * static_cast<int>(kN)));
+    check("ModDown(MultKeyNoModDown(a * b)) == HMult(rescale=false)",
+          same(download(md.data(), qw), wb));
+
+    // the reference's asserts: no in-place, no aux primes in a
+    bool in_place = false, with_aux = false;
+    try {
+      ctx->MultKeyNoModDown(t, t, key);
+    } catch (const Error &) {
+      in_place = true;
+    }
+    try {
+      Ct acc2;
+      ctx->MultKeyNoModDown(acc2, acc, key);
+    } catch (const Error &) {
+      with_aux = true;
+    }
+    check("MultKeyNoModDown rejects in-place and aux-prime inputs",
+          in_place && with_aux);
+  }
   // public handler members (Context.h:83-92), used directly by extensions
   {
     DeviceVector<word> y(qw);

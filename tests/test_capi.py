@@ -242,6 +242,32 @@ def test_moddown_bconv1_ntt_checks(chd):
         assert b"invalid argument" in chd.lib.chd_last_error()
 
 
+def test_forward_ntt_rejects_partial_overlap(chd):
+    """the forward NTT runs in place (two passes) or out of place into
+    disjoint memory; any other overlap would race between workgroups and is
+    rejected before a launch: a shifted destination, the same base with
+    another polynomial stride, and an in-place call whose source has a gap"""
+    lib = chd.lib
+    lib.chd_k_ntt_fwd.argtypes = [ctypes.POINTER(Tables),
+                                  ctypes.POINTER(LimbMap), P,
+                                  ctypes.c_longlong, P, ctypes.c_longlong,
+                                  ctypes.c_int, ctypes.c_int, P, P]
+    t, m = Tables(), LimbMap(num_q=20, skip_lo=1 << 30)
+    n = 1 << 16
+    base = 0x10000000
+    cases = [
+        (P(base + 3 * 4 * n), 20 * n, P(base), 20 * n, 1, m),
+        (P(base), 24 * n, P(base), 20 * n, 2, m),
+        (P(base), 20 * n, P(base), 20 * n, 1,
+         LimbMap(num_q=16, skip_lo=1 << 30, src_gap=4)),
+    ]
+    for dst, dps, src, sps, polys, mm in cases:
+        st = lib.chd_k_ntt_fwd(t, mm, dst, dps, src, sps, 20, polys, None,
+                               None)
+        assert st == -1
+        assert b"overlap" in chd.lib.chd_last_error()
+
+
 def test_binding_handles_released_cleanly_at_exit():
     """handles still alive at interpreter exit are destroyed through the
     function bound when they were made, not through module globals that

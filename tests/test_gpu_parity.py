@@ -320,10 +320,13 @@ def test_hmult_in_place_and_separate_rescale(chd, ks):
 
 @pytest.mark.parametrize("rescale", [True, False])
 def test_hmult_one_aux_prime(chd, rescale):
-    """alpha = 1 (dnum = L = 4): ModDown then has a single source limb, so
-    its BConv is formed inside the ModDown NTT from the key accumulation's
-    INTT rows; without rescale the result is also rescaled separately (one
-    source again), both against the oracle"""
+    """alpha = 1 (dnum = L = 4): ModDown has a single source limb. With so
+    few destination limbs (at most 32 polynomial-limbs) the one-source BConv
+    writes the destination and the two-pass ModDown NTT runs in place on it;
+    without rescale the result is also rescaled separately (one source
+    again, the same path), both against the oracle. The one-source BConv
+    formed inside the single-pass NTT serves Rescale above 16 limbs and is
+    pinned by the L = 24 Rescale tests."""
     main, aux, L = Q30[:4], Q31[:1], 4
     param = chd.Param(main, aux, [(i, 0) for i in range(1, L + 1)])
     ctx = chd.Context(param)
@@ -343,6 +346,22 @@ def test_hmult_one_aux_prime(chd, rescale):
         ctx.rescale(L - 1, out, res)
         assert np.array_equal(host(out[0]), _orc.rescale(wb, main, L, 1, 16))
         assert np.array_equal(host(out[1]), _orc.rescale(wa, main, L, 1, 16))
+
+
+@pytest.mark.parametrize("L", [4, 24])
+def test_rescale_rejects_result_overlapping_kept_limbs(chd, ks, L):
+    """a Rescale whose result bx is the input's ax overlaps the kept source
+    limbs the ModDown epilogue reads: the call fails before any launch
+    (also where few destination limbs let the BConv write the destination
+    first) and the input is left as it was"""
+    param, ctx, main, aux = ks
+    r = rng(480 + L)
+    b, a = uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L])
+    tb, ta = dev(b), dev(a)
+    out_a = zeros(L - 1, N)
+    with pytest.raises(chd.ChdError, match="overlap"):
+        ctx.rescale(L - 1, (ta[:L - 1], out_a), (tb, ta))
+    assert np.array_equal(host(ta), a) and np.array_equal(host(tb), b)
 
 
 def test_rescale_polynomials_in_any_order(chd, ks):

@@ -140,6 +140,44 @@ def test_hrot_and_mod_up_at_offset_levels(setup):
             assert np.array_equal(host(dst[g]), want[g]), (name, level, g)
 
 
+def test_mult_key_no_mod_down_at_offset_levels(setup):
+    """Context::MultKeyNoModDown through the C-ABI, both forms
+    (Context.cpp:609-712): the MultKey branch (ModUp of ax, P * bx), the
+    relinearisation branch (ModUp of rx, P * (bx, ax)) and the PAccum of a
+    caller-held ModUp, at the top level and at a level whose dnum groups
+    start part-way into a chain group (terminal primes missing)"""
+    name, ctx, chain, (kb, ka), (dkb, dka), r = setup
+    top = chain_top(chain)
+    shifted = [lv for lv in range(1, top + 1)
+               if chain.offset(lv) % chain.alpha]
+    for level in sorted({top} | set(shifted[-1:])):
+        q = chain.q(level)
+        t = len(q) + chain.alpha
+        b, a, rx = (_uniform(r, q) for _ in range(3))
+        acc = (zeros(t, N), zeros(t, N))
+        print(name, "mult_key_no_mod_down level", level, chain.np(level),
+              flush=True)
+        ctx.mult_key_no_mod_down(level, acc, (dev(b), dev(a)), dkb, dka)
+        wb, wa = chain.key_mult(a, level, kb, ka)
+        assert np.array_equal(host(acc[0]), chain.caccum(wb, b, level)), (
+            name, level)
+        assert np.array_equal(host(acc[1]), wa), (name, level)
+        ctx.mult_key_no_mod_down(level, acc, (dev(b), dev(a), dev(rx)), dkb,
+                                 dka)
+        wb, wa = chain.key_mult(rx, level, kb, ka)
+        assert np.array_equal(host(acc[0]), chain.caccum(wb, b, level)), (
+            name, level, "rx")
+        assert np.array_equal(host(acc[1]), chain.caccum(wa, a, level)), (
+            name, level, "rx")
+        groups = chain.groups(level)
+        up = [zeros(t, N) if g in groups else None
+              for g in range(ctx.beta(level))]
+        ctx.mod_up(level, up, dev(rx))
+        ctx.mult_key_no_mod_down_mod_up(level, acc, up, dkb, dka)
+        assert np.array_equal(host(acc[0]), wb), (name, level, "modup")
+        assert np.array_equal(host(acc[1]), wa), (name, level, "modup")
+
+
 def test_encode_decode_at_terminal_level(setup):
     name, ctx, chain, _, _, r = setup
     level = next((lv for lv in range(len(chain.levels))
