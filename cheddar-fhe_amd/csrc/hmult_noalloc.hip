@@ -3,6 +3,7 @@
 // cannot allocate (code under HIP graph capture, tight serving loops,
 // harnesses that forbid hipMalloc). It runs the same kernels as chd_hmult;
 // only where their scratch operands point differs.
+#include <memory>
 #include <mutex>
 #include <vector>
 
@@ -19,13 +20,25 @@ constexpr size_t kScratchWords = kScratchBytes / sizeof(uint32_t);
 static __device__ __align__(256) uint32_t scratch[kScratchWords];
 
 namespace {
+// Per device: the address of that device's copy of `scratch` (the array's
+// name is a host-side stand-in, never a device address), and what orders
+// the calls that share it. Every context, stream and host thread of the
+// process shares one device's array, so its calls are serialised on the
+// host by `mu` and on the device by `done`: a call on another stream than
+// the previous call first makes its stream wait for that call's end.
+struct DeviceScratch {
+  uint32_t *ptr = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool has_last = false;
+  std::mutex mu;
+};
 std::mutex g_mu;
-// per device: the address of that device's copy of `scratch` (the array's
-// name is a host-side stand-in, never a device address)
-std::vector<uint32_t *> g_scratch_ptr;
+std::vector<std::unique_ptr<DeviceScratch>> g_scratch;
 
-// looked up once per device, with that device current
-int ScratchOfCurrentDevice(uint32_t **out) {
+// set up once per device, with that device current: the array's address
+// and the ordering event (no device memory is allocated)
+int ScratchOfCurrentDevice(DeviceScratch **out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess)
@@ -33,9 +46,9 @@ int ScratchOfCurrentDevice(uint32_t **out) {
                                                    "hipGetDevice: ") +
                                            hipGetErrorString(e));
   std::lock_guard<std::mutex> lock(g_mu);
-  if (dev >= static_cast<int>(g_scratch_ptr.size()))
-    g_scratch_ptr.resize(dev + 1, nullptr);
-  if (g_scratch_ptr[dev] == nullptr) {
+  if (dev >= static_cast<int>(g_scratch.size())) g_scratch.resize(dev + 1);
+  if (g_scratch[dev] == nullptr) {
+    std::unique_ptr<DeviceScratch> d(new DeviceScratch);
     void *p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr)
@@ -43,9 +56,16 @@ int ScratchOfCurrentDevice(uint32_t **out) {
                             std::string("chd_hmult_noalloc: "
                                         "hipGetSymbolAddress: ") +
                                 hipGetErrorString(e));
-    g_scratch_ptr[dev] = static_cast<uint32_t *>(p);
+    e = hipEventCreateWithFlags(&d->done, hipEventDisableTiming);
+    if (e != hipSuccess)
+      return chd::set_error(CHD_ERR_HIP,
+                            std::string("chd_hmult_noalloc: "
+                                        "hipEventCreateWithFlags: ") +
+                                hipGetErrorString(e));
+    d->ptr = static_cast<uint32_t *>(p);
+    g_scratch[dev] = std::move(d);
   }
-  *out = g_scratch_ptr[dev];
+  *out = g_scratch[dev].get();
   return 0;
 }
 }  // namespace
@@ -61,8 +81,10 @@ extern "C" int chd_hmult_noalloc(const chd_context *ctx, int level,
   if (!(LevelOk(ctx, level) && (!rescale || level > 0) && res_bx && res_ax &&
         a_bx && a_ax && b_bx && b_ax && evk_bx && evk_ax && evk_beta > 0))
     return chd::set_error(CHD_ERR_ARG, "chd_hmult_noalloc: invalid argument");
-  uint32_t *buf = nullptr;
-  if (int st = ScratchOfCurrentDevice(&buf)) return st;
+  DeviceScratch *ds = nullptr;
+  if (int st = ScratchOfCurrentDevice(&ds)) return st;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::mutex> lock(ds->mu);
   CHD_TRY
   const size_t need = ctx->c->KeySwitchScratchWords(level, rescale != 0);
   if (need > kScratchWords)
@@ -75,13 +97,35 @@ extern "C" int chd_hmult_noalloc(const chd_context *ctx, int level,
   cheddar::Workspace *ws = ctx->c->GetWorkspace();
   if (ws == nullptr)
     return chd::set_error(CHD_ERR_STATE, "chd_hmult_noalloc: no workspace");
-  cheddar::StreamScope scope(static_cast<hipStream_t>(stream));
-  cheddar::Workspace::Use use(ws);
-  cheddar::Workspace::External ext(ws, buf, kScratchWords);
-  ctx->c->HMultV(level, {res_bx, res_ax, nullptr}, {a_bx, a_ax, nullptr},
-                 {b_bx, b_ax, nullptr},
-                 chd_capi::MakeEvk(ctx, evk_bx, evk_ax, evk_beta),
-                 rescale != 0);
+  const auto key = chd_capi::MakeEvk(ctx, evk_bx, evk_ax, evk_beta);
+  // after the previous user of the array, whatever its context or stream
+  if (ds->has_last && ds->last != s)
+    cheddar::HipCheck(hipStreamWaitEvent(s, ds->done, 0),
+                      "hipStreamWaitEvent");
+  // this call becomes the array's last user once its kernels are enqueued,
+  // also when it throws after some of them
+  struct Record {
+    DeviceScratch *d;
+    hipStream_t s;
+    ~Record() {
+      if (hipEventRecord(d->done, s) == hipSuccess) {
+        d->last = s;
+        d->has_last = true;
+      } else {
+        // no event to order the next call after this one: finish this one
+        (void)hipStreamSynchronize(s);
+        d->has_last = false;
+      }
+    }
+  };
+  {
+    Record rec{ds, s};
+    cheddar::StreamScope scope(s);
+    cheddar::Workspace::Use use(ws);
+    cheddar::Workspace::External ext(ws, ds->ptr, kScratchWords);
+    ctx->c->HMultV(level, {res_bx, res_ax, nullptr}, {a_bx, a_ax, nullptr},
+                   {b_bx, b_ax, nullptr}, key, rescale != 0);
+  }
   return chd::check_launch("chd_hmult_noalloc");
   CHD_CATCH("chd_hmult_noalloc")
 }

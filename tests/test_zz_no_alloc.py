@@ -70,6 +70,37 @@ def test_hmult_noalloc_result_may_alias_input(chd):
     assert np.array_equal(host(a[1])[:level], host(want[1]))
 
 
+def test_hmult_noalloc_two_contexts_two_streams(chd):
+    """two contexts share the GPU's one static array; their calls, issued
+    back to back on two streams without any ordering by the caller, are
+    ordered by the library and stay bit-exact against chd_hmult"""
+    import ctypes
+    import torch
+    main, aux, levels = config4()
+    ctxs = [chd.Context(chd.Param(main, aux, levels)) for _ in range(2)]
+    r = np.random.default_rng(0xA110F)
+    jobs = []
+    for ctx, level in zip(ctxs, (23, 20)):
+        a, b, kb, ka = _inputs(r, main, aux, level + 1)
+        want = (zeros(level, N), zeros(level, N))
+        ctx.hmult(level, want, a, b, kb, ka)
+        jobs.append((ctx, level, a, b, kb, ka, want,
+                     [(zeros(level, N), zeros(level, N)) for _ in range(3)]))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    for rep in range(3):
+        for (ctx, level, a, b, kb, ka, _, got), st in zip(jobs, streams):
+            print("hmult_noalloc two contexts: level", level, "call", rep,
+                  flush=True)
+            ctx.hmult_noalloc(level, got[rep], a, b, kb, ka,
+                              stream=ctypes.c_void_p(st.cuda_stream))
+    torch.cuda.synchronize()
+    for ctx, level, a, b, kb, ka, want, got in jobs:
+        for g in got:
+            assert np.array_equal(host(g[0]), host(want[0])), level
+            assert np.array_equal(host(g[1]), host(want[1])), level
+
+
 def test_hmult_noalloc_rejects_levels_beyond_its_scratch(chd):
     """30 q limbs with alpha = 8 need about 69 MiB of temporaries"""
     main, aux = Q30[:30], Q31[:8]
