@@ -69,6 +69,16 @@ __device__ __forceinline__ int32_t mont(int32_t b, int32_t w, int32_t wq,
   return hi - __mulhi(t, q);
 }
 
+// the same for a per-lane twiddle, without the companion w q^-1: b w as one
+// 64-bit product (v_mad_i64_i32), t = (b w mod 2^32) q^-1
+__device__ __forceinline__ int32_t mont_s(int32_t b, int32_t w, uint32_t qinv,
+                                          int32_t q) {
+  const int64_t p = static_cast<int64_t>(b) * w;
+  const int32_t t =
+      static_cast<int32_t>(static_cast<uint32_t>(p) * qinv);
+  return static_cast<int32_t>(p >> 32) - __mulhi(t, q);
+}
+
 // [-q, q) -> [0, q) with one add and an unsigned min
 __device__ __forceinline__ int32_t norm(int32_t a, int32_t q) {
   uint32_t ua = static_cast<uint32_t>(a);
@@ -76,23 +86,30 @@ __device__ __forceinline__ int32_t norm(int32_t a, int32_t q) {
   return static_cast<int32_t>(ua < uq ? ua : uq);
 }
 
-// ButterflyNTT (NTTUtils.cuh:19-34): a, b in [-q, q)
-__device__ __forceinline__ void ct_bfly(int32_t &a, int32_t &b, int32_t w,
-                                        int32_t wq, int32_t q) {
-  int32_t m = norm(mont(b, w, wq, q), q);
+// ButterflyNTT (NTTUtils.cuh:19-34): a, b in [-q, q); m = MontMul(b, w)
+__device__ __forceinline__ void ct_bfly_m(int32_t &a, int32_t &b, int32_t m,
+                                          int32_t q) {
+  m = norm(m, q);
   int32_t an = norm(a, q);
   b = an - m;
   a = (an - q) + m;
 }
-
-// ButterflyINTT (NTTUtils.cuh:46-60)
-__device__ __forceinline__ void gs_bfly(int32_t &a, int32_t &b, int32_t w,
+__device__ __forceinline__ void ct_bfly(int32_t &a, int32_t &b, int32_t w,
                                         int32_t wq, int32_t q) {
+  ct_bfly_m(a, b, mont(b, w, wq, q), q);
+}
+
+// ButterflyINTT (NTTUtils.cuh:46-60); returns an - bn for the product
+__device__ __forceinline__ int32_t gs_bfly_sum(int32_t &a, int32_t b,
+                                               int32_t q) {
   int32_t an = norm(a, q);
   int32_t bn = norm(b, q);
-  int32_t d = an - bn;
   a = (an - q) + bn;
-  b = mont(d, w, wq, q);
+  return an - bn;
+}
+__device__ __forceinline__ void gs_bfly(int32_t &a, int32_t &b, int32_t w,
+                                        int32_t wq, int32_t q) {
+  b = mont(gs_bfly_sum(a, b, q), w, wq, q);
 }
 
 // Lazy butterflies for q < 2^30 (4q < 2^32), unsigned values: CT keeps
@@ -112,22 +129,52 @@ __device__ __forceinline__ uint32_t mont_mad(uint32_t b, uint32_t w,
   return static_cast<uint32_t>((static_cast<uint64_t>(m) * q + t) >> 32);
 }
 
+// The same product for a per-lane twiddle: m = (b w mod 2^32) qn equals
+// b wn mod 2^32, so no companion of w is needed (the multiply waits for the
+// low word of b w instead of running beside it).
+__device__ __forceinline__ uint32_t mont_lo(uint32_t b, uint32_t w,
+                                            uint32_t qn, uint32_t q) {
+  const uint64_t t = static_cast<uint64_t>(b) * w;
+  const uint32_t m = static_cast<uint32_t>(t) * qn;
+  return static_cast<uint32_t>((static_cast<uint64_t>(m) * q + t) >> 32);
+}
+
+// |x - y| + z in one v_sad_u32 (full VALU rate on gfx950). With x >= y it
+// is x - y + z, which otherwise takes a subtract and an add. Written as an
+// instruction: with a wave-uniform x the compiler expands the max - min + z
+// pattern into four instructions instead.
+__device__ __forceinline__ uint32_t sad(uint32_t x, uint32_t y, uint32_t z) {
+  uint32_t r;
+  asm("v_sad_u32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(y), "v"(z));
+  return r;
+}
+
 // CT: a, b in [0, 4q) -> a + d, a + 2q - d with a reduced to [0, 2q)
+// (kRed false: the caller knows a < 2q already). d = b w 2^-32 in [0, 2q).
+template <bool kRed = true>
+__device__ __forceinline__ void ct_lazy_d(uint32_t &a, uint32_t &b,
+                                          uint32_t d, uint32_t q) {
+  const uint32_t ar = kRed ? umin(a, a - 2 * q) : a;  // [0, 2q)
+  b = sad(2 * q, d, ar);                             // (0, 4q)
+  a = ar + d;                                        // [0, 4q)
+}
+template <bool kRed = true>
 __device__ __forceinline__ void ct_lazy(uint32_t &a, uint32_t &b, uint32_t w,
                                         uint32_t wn, uint32_t q) {
-  const uint32_t ar = umin(a, a - 2 * q);   // [0, 2q)
-  const uint32_t d = mont_mad(b, w, wn, q);  // [0, 2q)
-  b = ar + 2 * q - d;                        // (0, 4q)
-  a = ar + d;                                // [0, 4q)
+  ct_lazy_d<kRed>(a, b, mont_mad(b, w, wn, q), q);
 }
 
 // GS: a, b in [0, 2q) -> a + b (reduced), (a - b) w
+__device__ __forceinline__ uint32_t gs_lazy_sum(uint32_t &a, uint32_t b,
+                                                uint32_t q) {
+  const uint32_t s = a + b;                  // [0, 4q)
+  const uint32_t t = sad(2 * q, b, a);       // a + 2q - b in (0, 4q)
+  a = umin(s, s - 2 * q);                    // [0, 2q)
+  return t;
+}
 __device__ __forceinline__ void gs_lazy(uint32_t &a, uint32_t &b, uint32_t w,
                                         uint32_t wn, uint32_t q) {
-  const uint32_t s = a + b;                  // [0, 4q)
-  const uint32_t t = a + 2 * q - b;          // (0, 4q)
-  a = umin(s, s - 2 * q);                    // [0, 2q)
-  b = mont_mad(t, w, wn, q);                 // [0, 2q)
+  b = mont_mad(gs_lazy_sum(a, b, q), w, wn, q);  // [0, 2q)
 }
 
 // [0, 4q) -> [0, q)
@@ -206,6 +253,40 @@ __device__ __forceinline__ void st_nt(void *base, uint32_t byte_off, T v) {
       v, reinterpret_cast<T *>(static_cast<char *>(base) + byte_off));
 }
 
+// Buffer-resource access (raw buffer, stride 0): address = base + soffset
+// (an SGPR) + voffset (a VGPR) + a 12-bit immediate, so a load whose
+// per-lane part repeats costs no VALU address arithmetic; the scalar part is
+// formed by SALU. The range (bytes) is checked by the hardware: loads beyond
+// it return 0 and stores beyond it are dropped. Word 3 0x00020000 is the
+// gfx9 dword data format. Cache policy kAux: 0 default, 2 nontemporal.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0,
+                                           static_cast<int>(bytes),
+                                           0x00020000);
+}
+template <int kAux = 0>
+__device__ __forceinline__ uint32_t bld1(rsrc_t r, uint32_t voff,
+                                         uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kAux);
+}
+template <int kAux = 0>
+__device__ __forceinline__ u32x2 bld2(rsrc_t r, uint32_t voff,
+                                      uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kAux);
+}
+template <int kAux = 0>
+__device__ __forceinline__ u32x4 bld4(rsrc_t r, uint32_t voff,
+                                      uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kAux);
+}
+template <int kAux = 0>
+__device__ __forceinline__ void bst4(rsrc_t r, uint32_t voff, uint32_t soff,
+                                     u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, kAux);
+}
+
 // the 4 words of store round v (tile_lane_byte) from the padded LDS tile
 // (rows of kRowPad words, column i at pidx(i))
 __device__ __forceinline__ u32x4 tile_lds4(const uint32_t *xt, int v) {
@@ -225,7 +306,10 @@ template <bool kLazy>
 struct Arith;
 
 // twq(w) is the per-twiddle companion of w that ct / gs / mul take:
-// w (-q^-1) for the lazy form, w q^-1 for the reference form.
+// w (-q^-1) for the lazy form, w q^-1 for the reference form. Wave-uniform
+// twiddles use it (a scalar multiply); per-lane twiddles use ctv / gsv,
+// which derive the Montgomery factor from the product instead.
+// ct<false> skips the reduction of a, for a known to lie in [0, 2q).
 template <>
 struct Arith<true> {
   using T = uint32_t;
@@ -233,11 +317,19 @@ struct Arith<true> {
   uint32_t qn;  // -q^-1 mod 2^32
   __device__ Arith(uint32_t q_, uint32_t qinv) : q(q_), qn(0u - qinv) {}
   __device__ uint32_t twq(uint32_t w) const { return w * qn; }
+  template <bool kRed = true>
   __device__ void ct(T &a, T &b, uint32_t w, uint32_t wn) const {
-    ct_lazy(a, b, w, wn, q);
+    ct_lazy<kRed>(a, b, w, wn, q);
+  }
+  template <bool kRed = true>
+  __device__ void ctv(T &a, T &b, uint32_t w) const {
+    ct_lazy_d<kRed>(a, b, mont_lo(b, w, qn, q), q);
   }
   __device__ void gs(T &a, T &b, uint32_t w, uint32_t wn) const {
     gs_lazy(a, b, w, wn, q);
+  }
+  __device__ void gsv(T &a, T &b, uint32_t w) const {
+    b = mont_lo(gs_lazy_sum(a, b, q), w, qn, q);
   }
   // MontMul(x, c) for any representable input, result in [0, 2q)
   __device__ T mul(T x, uint32_t c, uint32_t cn) const {
@@ -255,11 +347,19 @@ struct Arith<false> {
   __device__ Arith(uint32_t q_, uint32_t qinv_)
       : q(static_cast<int32_t>(q_)), qinv(qinv_) {}
   __device__ uint32_t twq(uint32_t w) const { return w * qinv; }
+  template <bool kRed = true>
   __device__ void ct(T &a, T &b, uint32_t w, uint32_t wq) const {
     ct_bfly(a, b, static_cast<int32_t>(w), static_cast<int32_t>(wq), q);
   }
+  template <bool kRed = true>
+  __device__ void ctv(T &a, T &b, uint32_t w) const {
+    ct_bfly_m(a, b, mont_s(b, static_cast<int32_t>(w), qinv, q), q);
+  }
   __device__ void gs(T &a, T &b, uint32_t w, uint32_t wq) const {
     gs_bfly(a, b, static_cast<int32_t>(w), static_cast<int32_t>(wq), q);
+  }
+  __device__ void gsv(T &a, T &b, uint32_t w) const {
+    b = mont_s(gs_bfly_sum(a, b, q), static_cast<int32_t>(w), qinv, q);
   }
   __device__ T mul(T x, uint32_t c, uint32_t cq) const {
     return mont(x, static_cast<int32_t>(c), static_cast<int32_t>(cq), q);
@@ -1072,8 +1172,9 @@ __device__ __forceinline__ int qidx(int n) { return n + ((n >> 6) << 2); }
 
 
 // radix-16 over the 16 registers; stage t (0..3) has 2^t groups and group g
-// uses tw[base[t] + g]; kUniform: the twiddles are wave-uniform
-template <bool kUniform, typename A>
+// uses tw[base[t] + g]; kUniform: the twiddles are wave-uniform; kRed0
+// false: the inputs lie in [0, 2q), so stage 0 needs no reduction
+template <bool kUniform, bool kRed0, typename A>
 __device__ __forceinline__ void radix16_1p(const A &ar,
                                            typename A::T (&x)[16],
                                            const uint32_t *tw,
@@ -1086,14 +1187,20 @@ __device__ __forceinline__ void radix16_1p(const A &ar,
       const uint32_t w = kUniform ? ld_uniform(tw, base[t] + g) : tw[base[t] + g];
       const uint32_t wq = ar.twq(w);
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) {
+        if (t == 0 && !kRed0)
+          ar.template ct<false>(x[k], x[k + h], w, wq);
+        else
+          ar.ct(x[k], x[k + h], w, wq);
+      }
     }
   }
 }
 
 // radix-16 with the 15 twiddles of its four stages preloaded:
-// w[(1 << t) - 1 + g] is group g of stage t
-template <typename A>
+// w[(1 << t) - 1 + g] is group g of stage t. kVec: the twiddles are per lane
+// (no companion multiply); otherwise wave-uniform (scalar companion).
+template <bool kVec, typename A>
 __device__ __forceinline__ void radix16_pre(const A &ar,
                                             typename A::T (&x)[16],
                                             const uint32_t (&w)[15]) {
@@ -1103,10 +1210,16 @@ __device__ __forceinline__ void radix16_pre(const A &ar,
 #pragma unroll
     for (int g = 0; g < (1 << t); g++) {
       const uint32_t wv = w[(1 << t) - 1 + g];
-      const uint32_t wq = ar.twq(wv);
+      if constexpr (kVec) {
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++)
-        ar.ct(x[k], x[k + h], wv, wq);
+        for (int k = g * 2 * h; k < g * 2 * h + h; k++)
+          ar.ctv(x[k], x[k + h], wv);
+      } else {
+        const uint32_t wq = ar.twq(wv);
+#pragma unroll
+        for (int k = g * 2 * h; k < g * 2 * h + h; k++)
+          ar.ct(x[k], x[k + h], wv, wq);
+      }
     }
   }
 }
@@ -1120,15 +1233,6 @@ __device__ __forceinline__ void radix16_pre(const A &ar,
 // round-1 input word: streaming for a limb's own input (its four
 // workgroups read it together), default caching for a broadcast source,
 // which every workgroup of the polynomial reads and the L2 keeps for them
-template <bool kBcast>
-__device__ __forceinline__ uint32_t ld_src(const uint32_t *src,
-                                           uint32_t byte_off) {
-  if constexpr (kBcast)
-    return ld_at<uint32_t>(src, byte_off);
-  else
-    return ld_nt<uint32_t>(src, byte_off);
-}
-
 template <int kEpi, bool kPre, bool kLazy>
 __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
                                             int z, int j, uint32_t q,
@@ -1136,6 +1240,10 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   using A = Arith<kLazy>;
   using T = typename A::T;
   constexpr bool kBcast = kPre && kEpi == kEpiModDown;
+  // round-1 input words: streaming for a limb's own input (its four
+  // workgroups read it together), default caching for a broadcast source,
+  // which every workgroup of the polynomial reads and the L2 keeps for them
+  constexpr int kSrcAux = kBcast ? 0 : 2;
   const A ar(q, qinv);
   const uint32_t *tw = a.tab.tw + (static_cast<size_t>(lb.ti) << kLogN);
   const uint32_t *src =
@@ -1143,6 +1251,9 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
       (kBcast ? size_t{0} : static_cast<size_t>(lb.sl) << kLogN);
   uint32_t *dst = poly_dst(a, z) + (static_cast<size_t>(lb.l) << kLogN) +
                   j * kQuarter;
+  const rsrc_t rtw = make_rsrc(tw, 4u * kN);
+  const rsrc_t rsrc = make_rsrc(src, 4u * kN);
+  const rsrc_t rdst = make_rsrc(dst, 4u * kQuarter);
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -1151,28 +1262,53 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   // workgroup barrier every wave of the CU computes at once, and a round
   // that first waited for its twiddles would leave the VALUs idle
   // (round 2: wave-uniform, w[(1 << s) - 1 + g] = psi_rev[((64 + hi) << s)
-  // + g]; round 3: per lane, the same from 1024; round 4: per store round).
+  // + g]; round 3: per lane, the same from 1024, the 2^s words of stage s
+  // contiguous and 2^s-aligned, so one or two vector loads each; round 4:
+  // per store round v, psi_rev[16384 + hi4] and the pair at
+  // psi_rev[32768 + 2 hi4]). Per-lane offsets in the VGPR operand, the
+  // wave-uniform rest in the scalar one.
   uint32_t w2[15], w3[15], w4[4][3];
   {
-    const int hi2 = (j << 4) | wave;                       // bits 15..10
-    const int hi3 = (j << 8) | (wave << 4) | (lane >> 2);  // bits 15..6
+    const int hi2 = (j << 4) | wave;              // bits 15..10
+    const uint32_t u3 = 1024u + ((j << 8) | (wave << 4));  // + (lane >> 2)
+    const uint32_t l3 = static_cast<uint32_t>(lane >> 2);
 #pragma unroll
     for (int s = 0; s < 4; s++)
 #pragma unroll
-      for (int g = 0; g < (1 << s); g++) {
+      for (int g = 0; g < (1 << s); g++)
         w2[(1 << s) - 1 + g] = ld_uniform(tw, ((64 + hi2) << s) + g);
-        w3[(1 << s) - 1 + g] = tw[((1024 + hi3) << s) + g];
-      }
+    w3[0] = bld1(rtw, l3 << 2, u3 << 2);
+    const u32x2 p1 = bld2(rtw, l3 << 3, u3 << 3);
+    w3[1] = p1[0];
+    w3[2] = p1[1];
+    const u32x4 p2 = bld4(rtw, l3 << 4, u3 << 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++) w3[3 + i] = p2[i];
+    const u32x4 p3a = bld4(rtw, l3 << 5, u3 << 5);
+    const u32x4 p3b = bld4(rtw, (l3 << 5) + 16u, u3 << 5);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      w3[7 + i] = p3a[i];
+      w3[11 + i] = p3b[i];
+    }
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-      const int hi4 = (j << 12) | (wave << 8) | (v << 6) | lane;  // 15..2
-      w4[v][0] = tw[16384 + hi4];
-      w4[v][1] = tw[32768 + 2 * hi4];
-      w4[v][2] = tw[32768 + 2 * hi4 + 1];
+      // hi4 = (j << 12) | (wave << 8) | (v << 6) | lane: bits 15..2
+      const uint32_t u4 =
+          static_cast<uint32_t>((j << 12) | (wave << 8) | (v << 6));
+      w4[v][0] = bld1(rtw, static_cast<uint32_t>(lane) << 2,
+                      (16384u + u4) << 2);
+      const u32x2 pb = bld2(rtw, static_cast<uint32_t>(lane) << 3,
+                            (32768u + 2u * u4) << 2);
+      w4[v][1] = pb[0];
+      w4[v][2] = pb[1];
     }
   }
   const uint32_t w0 = ld_uniform(tw, 1);
   const uint32_t w1 = ld_uniform(tw, 2 + (j >> 1));
+  // lane part of every round-1 input offset; quarter m and row k of the
+  // lane's 16 go in the scalar offset
+  const uint32_t vt = 4u * static_cast<uint32_t>(t);
   T x[16];
   // ---- round 1: stages 0, 1 of quarter j (bits 15, 14), then 2..5
   if constexpr (kLazy) {
@@ -1199,11 +1335,11 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
     }
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-      const uint32_t off = 4u * static_cast<uint32_t>((k << 10) | t);
-      const uint32_t x0 = ld_src<kBcast>(src, off);
-      const uint32_t x1 = ld_src<kBcast>(src, off + 4u * kQuarter);
-      const uint32_t x2 = ld_src<kBcast>(src, off + 8u * kQuarter);
-      const uint32_t x3 = ld_src<kBcast>(src, off + 12u * kQuarter);
+      const uint32_t so = 4u * static_cast<uint32_t>(k << 10);
+      const uint32_t x0 = bld1<kSrcAux>(rsrc, vt, so);
+      const uint32_t x1 = bld1<kSrcAux>(rsrc, vt, so + 4u * kQuarter);
+      const uint32_t x2 = bld1<kSrcAux>(rsrc, vt, so + 8u * kQuarter);
+      const uint32_t x3 = bld1<kSrcAux>(rsrc, vt, so + 12u * kQuarter);
       uint64_t acc;
       if constexpr (kBcast) {
         // centred inputs of a source prime below 2^31, |x| < 2^30, times
@@ -1246,12 +1382,12 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
     const bool hi0 = j >= 2, hi1 = j & 1;
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-      const uint32_t off = 4u * static_cast<uint32_t>((k << 10) | t);
+      const uint32_t so = 4u * static_cast<uint32_t>(k << 10);
       int32_t xm[4];
 #pragma unroll
       for (int m = 0; m < 4; m++) {
         xm[m] = static_cast<int32_t>(
-            ld_src<kBcast>(src, off + 4u * kQuarter * m));
+            bld1<kSrcAux>(rsrc, vt, so + 4u * kQuarter * m));
         // (a broadcast source is centred: mont takes signed inputs)
         if constexpr (kPre) xm[m] = mont(xm[m], ce, ceq, qs);
       }
@@ -1265,8 +1401,10 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   }
   CHD_PHASE(1);
   {
+    // the lazy prologue's outputs lie in [0, 2q) (dot product of canonical
+    // values below q 2^32 reduced), except for the broadcast form's [0, 3q)
     const int base[4] = {4 + j, 8 + 2 * j, 16 + 4 * j, 32 + 8 * j};
-    radix16_1p<true>(ar, x, tw, base);
+    radix16_1p<true, kBcast>(ar, x, tw, base);
   }
   CHD_PHASE(2);
   T *xs = reinterpret_cast<T *>(lds);
@@ -1280,7 +1418,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   // ---- round 2: stages 6..9 (bits 9..6); lane = bits 5..0, wave = 13..10
 #pragma unroll
   for (int k = 0; k < 16; k++) x[k] = xs[qidx((wave << 10) | (k << 6) | lane)];
-  radix16_pre(ar, x, w2);
+  radix16_pre<false>(ar, x, w2);
 #pragma unroll
   for (int k = 0; k < 16; k++) xs[qidx((wave << 10) | (k << 6) | lane)] = x[k];
   wave_lds_sync();
@@ -1290,7 +1428,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
 #pragma unroll
   for (int k = 0; k < 16; k++)
     x[k] = xs[qidx((wave << 10) | (b96 << 6) | (k << 2) | b10)];
-  radix16_pre(ar, x, w3);
+  radix16_pre<true>(ar, x, w3);
 #pragma unroll
   for (int k = 0; k < 16; k++)
     xs[qidx((wave << 10) | (b96 << 6) | (k << 2) | b10)] = x[k];
@@ -1301,13 +1439,17 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   const int32_t qs = static_cast<int32_t>(q);
   [[maybe_unused]] int32_t c2 = 0, c2q = 0, pe = 0, peq = 0;
   [[maybe_unused]] bool has_pad = false;
-  [[maybe_unused]] const uint32_t *s2p = nullptr;
+  [[maybe_unused]] bool has_s2 = false;
+  [[maybe_unused]] rsrc_t rs2 = make_rsrc(dst, 0);
   if constexpr (kEpi == kEpiModDown) {
     c2 = static_cast<int32_t>(a.cst2[lb.l]);
     c2q = static_cast<int32_t>(static_cast<uint32_t>(c2) * qinv);
     if (lb.l >= a.src2_lo && lb.l < a.src2_hi) {
-      s2p = a.src2 + z * a.src2_pstride +
-            (static_cast<size_t>(lb.l - a.src2_lo) << kLogN) + j * kQuarter;
+      has_s2 = true;
+      rs2 = make_rsrc(a.src2 + z * a.src2_pstride +
+                          (static_cast<size_t>(lb.l - a.src2_lo) << kLogN) +
+                          j * kQuarter,
+                      4u * kQuarter);
       if (a.pad != nullptr) {
         has_pad = true;
         pe = static_cast<int32_t>(a.pad[lb.l - a.src2_lo]);
@@ -1315,25 +1457,23 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
       }
     }
   }
+  const uint32_t vl = static_cast<uint32_t>(lane) << 4;
 #pragma unroll
   for (int v = 0; v < 4; v++) {
     const int n = (wave << 10) | (v << 8) | (lane << 2);
-    const uint32_t boff = 4u * static_cast<uint32_t>(n);
+    const uint32_t sn = 4u * static_cast<uint32_t>((wave << 10) | (v << 8));
     u32x4 s2 = {0, 0, 0, 0};
     if constexpr (kEpi == kEpiModDown)
-      if (s2p != nullptr) s2 = ld_nt<u32x4>(s2p, boff);
+      if (has_s2) s2 = bld4<2>(rs2, vl, sn);
     const u32x4 u = *reinterpret_cast<const u32x4 *>(&lds[qidx(n)]);
     T y[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) y[i] = static_cast<T>(u[i]);
     const uint32_t wa = w4[v][0];
-    const uint32_t waq = ar.twq(wa);
-    ar.ct(y[0], y[2], wa, waq);
-    ar.ct(y[1], y[3], wa, waq);
-    const uint32_t wb0 = w4[v][1];
-    const uint32_t wb1 = w4[v][2];
-    ar.ct(y[0], y[1], wb0, ar.twq(wb0));
-    ar.ct(y[2], y[3], wb1, ar.twq(wb1));
+    ar.ctv(y[0], y[2], wa);
+    ar.ctv(y[1], y[3], wa);
+    ar.ctv(y[0], y[1], w4[v][1]);
+    ar.ctv(y[2], y[3], w4[v][2]);
     u32x4 o;
 #pragma unroll
     for (int i = 0; i < 4; i++) o[i] = ar.canon_fwd(y[i]);
@@ -1349,7 +1489,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
         o[i] = static_cast<uint32_t>(norm(mont(dv, c2, c2q, qs), qs));
       }
     }
-    st_nt<u32x4>(dst, boff, o);
+    bst4<2>(rdst, vl, sn, o);
   }
   CHD_PHASE(6);
 }

@@ -56,6 +56,13 @@ __global__ __launch_bounds__(256) void chains(uint32_t *out, uint32_t seed,
           asm volatile("v_min_u32 %0, %0, %1" : "+v"(a[i]) : "v"(b));
         if constexpr (kOp == 6)
           asm volatile("v_add3_u32 %0, %0, %1, %0" : "+v"(a[i]) : "v"(b));
+        if constexpr (kOp == 7)
+          asm volatile("v_sad_u32 %0, %0, %1, %0" : "+v"(a[i]) : "v"(b));
+        if constexpr (kOp == 8)
+          asm volatile("v_mad_i64_i32 %0, vcc, %1, %2, %0"
+                       : "+v"(w[i])
+                       : "v"(a[i]), "v"(b)
+                       : "vcc");
       }
     }
   }
@@ -98,6 +105,8 @@ int main() {
   run(chains<4>, "v_sub_u32");
   run(chains<5>, "v_min_u32");
   run(chains<6>, "v_add3_u32");
+  run(chains<7>, "v_sad_u32");
+  run(chains<8>, "v_mad_i64_i32");
   CK(hipFree(out));
   return 0;
 }
