@@ -253,12 +253,18 @@ __device__ __forceinline__ void st_nt(void *base, uint32_t byte_off, T v) {
       v, reinterpret_cast<T *>(static_cast<char *>(base) + byte_off));
 }
 
-// Buffer-resource access (raw buffer, stride 0): address = base + soffset
+// Buffer-resource loads (raw buffer, stride 0): address = base + soffset
 // (an SGPR) + voffset (a VGPR) + a 12-bit immediate, so a load whose
 // per-lane part repeats costs no VALU address arithmetic; the scalar part is
 // formed by SALU. The range (bytes) is checked by the hardware: loads beyond
-// it return 0 and stores beyond it are dropped. Word 3 0x00020000 is the
-// gfx9 dword data format. Cache policy kAux: 0 default, 2 nontemporal.
+// it return 0. Word 3 0x00020000 is the gfx9 dword data format. Cache policy
+// kAux: 0 default, 2 nontemporal.
+// Loads only: a buffer store of more than 8 bytes with an SGPR soffset reads
+// its data VGPRs after the next instructions have issued, and the compiler
+// inserts no wait state for that form (it does for global stores). On gfx950
+// a VALU write of the data registers right after such a store put the new
+// value into memory under load (measured: the next round's index in the
+// first word of a 16-byte output). Stores stay global stores.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
@@ -281,11 +287,7 @@ __device__ __forceinline__ u32x4 bld4(rsrc_t r, uint32_t voff,
                                       uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kAux);
 }
-template <int kAux = 0>
-__device__ __forceinline__ void bst4(rsrc_t r, uint32_t voff, uint32_t soff,
-                                     u32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, kAux);
-}
+
 
 // the 4 words of store round v (tile_lane_byte) from the padded LDS tile
 // (rows of kRowPad words, column i at pidx(i))
@@ -438,10 +440,9 @@ __device__ __forceinline__ void fwd_cols_body(const NttArgs &a, const Limb &lb,
     const int h = 8 >> (s - 4);
 #pragma unroll
     for (int g = 0; g < (1 << (s - 4)); g++, i++) {
-      const uint32_t w = w2[i];
-      const uint32_t wq = ar.twq(w);
+      const uint32_t w = w2[i];  // per lane
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ctv(x[k], x[k + h], w);
     }
   }
 #pragma unroll
@@ -516,10 +517,9 @@ __device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++, i++) {
-      const uint32_t w = w1[i];
-      const uint32_t wq = ar.twq(w);
+      const uint32_t w = w1[i];  // per lane
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ctv(x[k], x[k + h], w);
     }
   }
 #pragma unroll
@@ -533,10 +533,9 @@ __device__ __forceinline__ void fwd_rows_body(const NttArgs &a, const Limb &lb,
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++, i++) {
-      const uint32_t w = w2[i];
-      const uint32_t wq = ar.twq(w);
+      const uint32_t w = w2[i];  // per lane
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ct(x[k], x[k + h], w, wq);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.ctv(x[k], x[k + h], w);
     }
   }
   // canonical values back through LDS: each wave then stores 1 KiB of the
@@ -676,10 +675,9 @@ __device__ __forceinline__ void inv_rows_body(const uint32_t (&w1)[15],
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
-      const uint32_t w = w2[(1 << s) - 1 + g];
-      const uint32_t wq = ar.twq(w);
+      const uint32_t w = w2[(1 << s) - 1 + g];  // per lane
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gsv(x[k], x[k + h], w);
     }
   }
 #pragma unroll
@@ -693,10 +691,9 @@ __device__ __forceinline__ void inv_rows_body(const uint32_t (&w1)[15],
     const int h = 8 >> s;
 #pragma unroll
     for (int g = 0; g < (1 << s); g++) {
-      const uint32_t w = w1[(1 << s) - 1 + g];
-      const uint32_t wq = ar.twq(w);
+      const uint32_t w = w1[(1 << s) - 1 + g];  // per lane
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gsv(x[k], x[k + h], w);
     }
   }
   // through LDS again so each wave stores 1 KiB contiguous per instruction
@@ -802,10 +799,9 @@ __device__ __forceinline__ void inv_cols_body(const NttArgs &a, const Limb &lb,
     const int h = 8 >> (s - 4);
 #pragma unroll
     for (int g = 0; g < (1 << (s - 4)); g++) {
-      const uint32_t w = w2[(1 << (s - 4)) - 1 + g];
-      const uint32_t wq = ar.twq(w);
+      const uint32_t w = w2[(1 << (s - 4)) - 1 + g];  // per lane
 #pragma unroll
-      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gs(x[k], x[k + h], w, wq);
+      for (int k = g * 2 * h; k < g * 2 * h + h; k++) ar.gsv(x[k], x[k + h], w);
     }
   }
   T *xt = reinterpret_cast<T *>(xch);
@@ -995,11 +991,10 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
         const int h = 8 >> s;
 #pragma unroll
         for (int gg = 0; gg < (1 << s); gg++, i++) {
-          const uint32_t w = w1[i];
-          const uint32_t wq = ar.twq(w);
+          const uint32_t w = w1[i];  // per lane
 #pragma unroll
           for (int k = gg * 2 * h; k < gg * 2 * h + h; k++)
-            ar.ct(x[k], x[k + h], w, wq);
+            ar.ctv(x[k], x[k + h], w);
         }
       }
 #pragma unroll
@@ -1013,11 +1008,10 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
         const int h = 8 >> s;
 #pragma unroll
         for (int gg = 0; gg < (1 << s); gg++, i++) {
-          const uint32_t w = w2[i];
-          const uint32_t wq = ar.twq(w);
+          const uint32_t w = w2[i];  // per lane
 #pragma unroll
           for (int k = gg * 2 * h; k < gg * 2 * h + h; k++)
-            ar.ct(x[k], x[k + h], w, wq);
+            ar.ctv(x[k], x[k + h], w);
         }
       }
       // columns 16c + k -> the product ownership 4c + 64v + j
@@ -1253,7 +1247,6 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
                   j * kQuarter;
   const rsrc_t rtw = make_rsrc(tw, 4u * kN);
   const rsrc_t rsrc = make_rsrc(src, 4u * kN);
-  const rsrc_t rdst = make_rsrc(dst, 4u * kQuarter);
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -1440,7 +1433,7 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
   [[maybe_unused]] int32_t c2 = 0, c2q = 0, pe = 0, peq = 0;
   [[maybe_unused]] bool has_pad = false;
   [[maybe_unused]] bool has_s2 = false;
-  [[maybe_unused]] rsrc_t rs2 = make_rsrc(dst, 0);
+  [[maybe_unused]] rsrc_t rs2 = make_rsrc(src, 0);
   if constexpr (kEpi == kEpiModDown) {
     c2 = static_cast<int32_t>(a.cst2[lb.l]);
     c2q = static_cast<int32_t>(static_cast<uint32_t>(c2) * qinv);
@@ -1489,16 +1482,16 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
         o[i] = static_cast<uint32_t>(norm(mont(dv, c2, c2q, qs), qs));
       }
     }
-    bst4<2>(rdst, vl, sn, o);
+    // the wave-uniform part of the address in the scalar base
+    st_nt<u32x4>(dst + (sn >> 2), vl, o);
   }
   CHD_PHASE(6);
 }
 
 // grid: 1D, 4 * roundup(limbs * polys, 8) blocks of 1024 threads
 template <int kEpi, bool kPre>
-__global__ __launch_bounds__(1024) void ntt_fwd_1p(NttArgs a, int num_limbs,
-                                                   int num_items) {
-  __shared__ __align__(16) uint32_t lds[kQLdsWords];
+__device__ __forceinline__ void fwd_1p_entry(const NttArgs &a, int num_limbs,
+                                             int num_items, uint32_t *lds) {
   const int b = blockIdx.x;
   const int slot = b >> 3;
   const int j = slot & 3;
@@ -1512,6 +1505,24 @@ __global__ __launch_bounds__(1024) void ntt_fwd_1p(NttArgs a, int num_limbs,
     fwd_1p_body<kEpi, kPre, true>(a, lb, z, j, q, qinv, lds);
   else
     fwd_1p_body<kEpi, kPre, false>(a, lb, z, j, q, qinv, lds);
+}
+
+// At most 64 VGPRs (8 waves per SIMD): two of these workgroups (16 waves,
+// 68 KiB of LDS each) fit on one CU, so a launch on another stream can run
+// its loads beside this one's butterflies. The broadcast ModDown form needs
+// more registers and keeps the default limit (ntt_fwd_1p_bcast).
+template <int kEpi, bool kPre>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8)))
+void ntt_fwd_1p(NttArgs a, int num_limbs, int num_items) {
+  __shared__ __align__(16) uint32_t lds[kQLdsWords];
+  fwd_1p_entry<kEpi, kPre>(a, num_limbs, num_items, lds);
+}
+
+__global__ __launch_bounds__(1024) void ntt_fwd_1p_bcast(NttArgs a,
+                                                         int num_limbs,
+                                                         int num_items) {
+  __shared__ __align__(16) uint32_t lds[kQLdsWords];
+  fwd_1p_entry<kEpiModDown, true>(a, num_limbs, num_items, lds);
 }
 
 }  // namespace
@@ -1551,8 +1562,8 @@ hipError_t launch_ntt_fwd(const NttArgs &a, int num_limbs, int num_polys,
   if (a.src_disjoint && (epilogue == kEpiModDown || items > 16)) {
     dim3 g1(4 * ((items + 7) / 8 * 8));
     if (epilogue == kEpiModDown && a.src_bcast)
-      hipLaunchKernelGGL((ntt_fwd_1p<kEpiModDown, true>), g1, dim3(1024), 0,
-                         s, a, num_limbs, items);
+      hipLaunchKernelGGL(ntt_fwd_1p_bcast, g1, dim3(1024), 0, s, a,
+                         num_limbs, items);
     else if (epilogue == kEpiModDown)
       hipLaunchKernelGGL((ntt_fwd_1p<kEpiModDown, false>), g1, dim3(1024), 0,
                          s, a, num_limbs, items);

@@ -114,6 +114,41 @@ def test_ntt_concurrent_streams(chd):
         assert np.array_equal(host(fwds[i]), want), i
 
 
+def test_ntt_three_streams_in_place_rounds(chd):
+    """the benchmark's headline loop at its size: 33 buffer sets (> 1 GiB,
+    more than twice the MALL) rotated over three streams, each step a
+    forward into the set's second buffer and the inverse back into its
+    source, checked after every round. Under this load a store-data hazard
+    once put index values into single words of the forward's output (a
+    16-byte buffer store whose data registers were rewritten right after
+    it); every forward must equal the first one and every source must come
+    back."""
+    import ctypes
+    import torch
+    primes = Q30[:32]
+    plan = chd.NttPlan(primes)
+    x = np.stack([uniform_limbs(rng(950 + p), primes) for p in range(2)])
+    base = dev(x)
+    want = zeros(2, 32, N)
+    plan.forward(want, base, 32, 2)
+    torch.cuda.synchronize()
+    sets = 33
+    srcs = [base.clone() for _ in range(sets)]
+    dsts = [zeros(2, 32, N) for _ in range(sets)]
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    sps = [ctypes.c_void_p(s.cuda_stream) for s in streams]
+    for rnd in range(8):
+        for i in range(sets):
+            plan.forward(dsts[i], srcs[i], 32, 2, stream=sps[i % 3])
+            plan.inverse(srcs[i], dsts[i], 32, 2, mont_conv=False,
+                         stream=sps[i % 3])
+        torch.cuda.synchronize()
+        bad = [i for i in range(sets)
+               if not (torch.equal(dsts[i], want) and
+                       torch.equal(srcs[i], base))]
+        assert not bad, (rnd, bad)
+
+
 @pytest.mark.parametrize("kind", ["zeros", "max", "impulse", "ramp"])
 def test_ntt_edge_inputs(chd, kind):
     primes = [CFG1_Q, Q31[5], Q30[0], Q30[31]]
