@@ -61,7 +61,17 @@ constexpr int kCoefPerBlock = (kThreads / 64) * kTilesPerWave * 16;
 constexpr int kPlaneBytes = 64 * 16;   // one digit plane of a 16-dst tile
 static_assert(kTilesPerWave == 2,
               "a packed last tile carries exactly the wave's two coefficient "
-              "tiles");
+              "tiles, and a wave's 32 coefficients are one 128-byte line");
+constexpr int kLdsRow = 36;  // words per LDS row: 32 coefficients + pad
+
+// orders a wave's LDS writes before its reads of other lanes' words (a
+// wave's LDS instructions execute in order; only the compiler must not move
+// them)
+__device__ __forceinline__ void wave_lds_sync_bc() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 struct BconvBatch {
   chd_bconv_job job[CHD_MAX_BCONV_JOBS];
@@ -112,6 +122,7 @@ template <int kChunks, bool kStream>
 __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
                                                        chd_limb_map m,
                                                        BconvBatch b) {
+  __shared__ __align__(16) uint32_t lds[(kThreads / 64) * 16 * kLdsRow];
   // the job by value: its fields stay in scalar registers
   const chd_bconv_job jb = b.job[blockIdx.z];
   const int lane = threadIdx.x & 63;
@@ -124,11 +135,12 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
   // this job's K chunks (its table holds exactly that many per tile)
   const int nk = kChunks == 1 ? 1 : (jb.src_len + kChunkSrc - 1) / kChunkSrc;
   const int tiles = (jb.dst_len + 15) >> 4;
+  // the grid covers the batch's largest job; a smaller one has fewer tiles
+  if (static_cast<int>(blockIdx.y) >= tiles) return;
   // at most 8 sources: lanes 32..63 (K 32..63, zero rows of B in the other
   // tiles) hold the sources of the second coefficient group instead
   const bool narrow = jb.src_len <= 8;
   const bool packed = packed_last_tile(jb.src_len, jb.dst_len);
-  const int regular = packed ? tiles - 1 : tiles;
   // Source words of this wave's coefficient tiles, per K chunk. Every load
   // is issued (sources beyond src_len read the last source and are zeroed
   // after), so they are all in flight together instead of one guarded load
@@ -162,13 +174,15 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
     p = t.q[ti];
     pinv = t.qinv[ti];
   };
-  // destination tile 0's primes and planes, requested with the sources
+  // this workgroup's destination tile: its primes and planes, requested
+  // with the sources
+  const int tt = blockIdx.y;
   uint32_t p;
   int32_t pinv;
   int pos;
-  prime_of(0, p, pinv, pos);
+  prime_of(tt, p, pinv, pos);
   v4i bp[kChunks][4];
-  load_planes<kChunks>(bp, tab, 0, nk, lane);
+  load_planes<kChunks>(bp, tab, tt, nk, lane);
   // A operands (the sources' signed digits)
   v4i a[kChunks][kTilesPerWave];
 #pragma unroll
@@ -182,36 +196,53 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
   // one destination): pairs of planes in int32 (|acc_c| <= 2^21, so |lo|,
   // |hi| < 2^30), one 64-bit multiply-add y = lo + 2^16 hi (|y| < 2^47, far
   // inside the (-p 2^31, p 2^31) a signed Montgomery reduction takes),
-  // reduced to y 2^-32 in (-p, p), then made canonical. Stores: inside a
-  // key switch (the batch entry) the next launch, the NTT, reads the result
-  // right away, so it is written with default (temporal) stores and stays in
-  // the caches (3 % faster per HMult than streaming stores, measured); a
-  // standalone conversion (kStream) writes with the streaming hint (config 3
-  // 6.0 -> 5.5 us in the kernel trace, measured).
-  auto finish = [&](const v4i (&d)[4], uint32_t pc, int32_t pinvc, int posc,
-                    int n) {
-    uint32_t o[4];
+  // reduced to y 2^-32 in (-p, p), then made canonical.
+  auto finish = [&](const v4i (&d)[4]) {
+    v4u o;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int32_t lo = d[0][i] + d[1][i] * 256;
       const int32_t hi = d[2][i] + d[3][i] * 256;
       const int64_t y = static_cast<int64_t>(hi) * 65536 + lo;
-      const uint32_t u = static_cast<uint32_t>(mont_reduce_lazy(y, pc, pinvc));
-      const uint32_t up = u + pc;
+      const uint32_t u = static_cast<uint32_t>(mont_reduce_lazy(y, p, pinv));
+      const uint32_t up = u + p;
       o[i] = u < up ? u : up;  // unsigned min: u + p when negative
     }
-    const v4u ov = {o[0], o[1], o[2], o[3]};
-    v4u *dp = reinterpret_cast<v4u *>(jb.dst +
-                                      (static_cast<size_t>(posc) << kLogN) + n);
-    if constexpr (kStream)
-      __builtin_nontemporal_store(ov, dp);
-    else
-      *dp = ov;
+    return o;
   };
-  for (int tt = 0; tt < regular; tt++) {
-    const bool live = tt * 16 + r < jb.dst_len;
-    // the MFMAs of this tile, then the next tile's primes and planes go out
-    // while this tile is recombined and stored
+  // Results go out through this wave's LDS tile, [destination column][32
+  // coefficients] (rows padded to 36 words), so that 8 lanes store the 128
+  // contiguous bytes of one destination limb: each store instruction writes
+  // 8 whole lines instead of 16 half lines. Inside a key switch (the batch
+  // entry) the next launch, the NTT, reads the result right away, so it is
+  // written with default (temporal) stores and stays in the caches (3 %
+  // faster per HMult than streaming stores, measured); a standalone
+  // conversion (kStream) writes with the streaming hint.
+  uint32_t *xt = lds + wave * (16 * kLdsRow);
+  auto store_rows = [&](int dst_base, int rows) {
+    // rows destinations (8 or 16) of this tile, 8 per store instruction;
+    // dst_base is the destination index of LDS row 0
+    wave_lds_sync_bc();
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      if (h * 8 >= rows) break;
+      const int row = h * 8 + (lane >> 3);
+      const int piece = lane & 7;
+      const v4u v = *reinterpret_cast<const v4u *>(xt + row * kLdsRow +
+                                                  4 * piece);
+      const int k = dst_base + row;
+      if (k < jb.dst_len) {
+        const int kp = k + (k >= jb.skip_lo ? jb.skip_len : 0);
+        v4u *dp = reinterpret_cast<v4u *>(
+            jb.dst + (static_cast<size_t>(kp) << kLogN) + n_wave + 4 * piece);
+        if constexpr (kStream)
+          __builtin_nontemporal_store(v, dp);
+        else
+          *dp = v;
+      }
+    }
+  };
+  if (!(packed && tt == tiles - 1)) {
     v4i d[kTilesPerWave][4];
 #pragma unroll
     for (int mt = 0; mt < kTilesPerWave; mt++)
@@ -225,22 +256,16 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
           d[mt][pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
               a[ch][mt], bp[ch][pl], d[mt][pl], 0, 0, 0);
       }
-    const uint32_t pc = p;
-    const int32_t pinvc = pinv;
-    const int posc = pos;
-    if (tt + 1 < tiles) {
-      prime_of(tt + 1, p, pinv, pos);
-      load_planes<kChunks>(bp, tab, tt + 1, nk, lane);
-    }
-    if (live) {
+    // lane: destination column r, coefficients 16 mt + 4 g .. + 3
 #pragma unroll
-      for (int mt = 0; mt < kTilesPerWave; mt++)
-        finish(d[mt], pc, pinvc, posc, n_wave + mt * 16 + 4 * g);
-    }
-  }
-  if (packed) {
-    // the last tile, both coefficient groups at once (one K chunk: nk is 1
-    // for at most 8 sources); its primes and planes are already loaded
+    for (int mt = 0; mt < kTilesPerWave; mt++)
+      *reinterpret_cast<v4u *>(xt + r * kLdsRow + 16 * mt + 4 * g) =
+          finish(d[mt]);
+    store_rows(tt * 16, 16);
+  } else {
+    // the packed last tile, both coefficient groups at once (one K chunk:
+    // nk is 1 for at most 8 sources): column r is destination
+    // 16 tt + (r & 7) for coefficient group r >> 3
     v4i d[4];
 #pragma unroll
     for (int pl = 0; pl < 4; pl++) {
@@ -248,8 +273,9 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
       d[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[0][0], bp[0][pl], z, 0,
                                                     0, 0);
     }
-    if ((tiles - 1) * 16 + (r & 7) < jb.dst_len)
-      finish(d, p, pinv, pos, n_wave + (r >> 3) * 16 + 4 * g);
+    *reinterpret_cast<v4u *>(xt + (r & 7) * kLdsRow + 16 * (r >> 3) +
+                             4 * g) = finish(d);
+    store_rows(tt * 16, 8);
   }
 }
 
@@ -336,9 +362,16 @@ int launch_bconv(const chd_tables *t, const chd_limb_map *m,
       return set_error(CHD_ERR_ARG, "chd_k_bconv_batch: invalid job");
     b.job[j] = jb;
   }
-  int max_src = 0;
-  for (int j = 0; j < num_jobs; j++) max_src = std::max(max_src, jobs[j].src_len);
-  dim3 g(kN / kCoefPerBlock, 1, num_jobs);
+  int max_src = 0, max_tiles = 0;
+  for (int j = 0; j < num_jobs; j++) {
+    max_src = std::max(max_src, jobs[j].src_len);
+    max_tiles = std::max(max_tiles, (jobs[j].dst_len + 15) / 16);
+  }
+  // one destination tile per workgroup (blockIdx.y): the coefficient blocks
+  // of a tile are consecutive block ids, and the tiles of one coefficient
+  // block land on the same XCD (kN / kCoefPerBlock is a multiple of 8), whose
+  // L2 keeps the sources for them
+  dim3 g(kN / kCoefPerBlock, max_tiles, num_jobs);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (max_src <= kChunkSrc) {
     if (stream_out)
