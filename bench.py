@@ -74,7 +74,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU-baseline leg")
-    ap.add_argument("--only", choices=["ntt_fwd", "ntt_inv", "ntt_step",
+    ap.add_argument("--only", choices=["ntt_fwd", "ntt_inv", "ntt_inv_1p",
+                                       "ntt_step",
                                        "hmult",
                                        "hmult_cold", "hmult_separate",
                                        "hmult_levels",
@@ -134,6 +135,13 @@ def bench_ntt(chd, steps, warmup):
         lambda i: plan.inverse(srcs[i % nsets], dsts[i % nsets], 32, 2,
                                mont_conv=False, stream=sp), sub,
         stream) / sub
+    # the single-pass inverse (one HBM read and write per limb), for
+    # comparison: the same results, not used by the headline loop
+    inv1_ms = event_time_ms(
+        lambda i: plan.inverse(srcs[i % nsets], dsts[i % nsets], 32, 2,
+                               mont_conv=False, stream=sp,
+                               single_pass=True), sub,
+        stream) / sub
     # warm (MALL-resident) figure on one buffer set
     warm_ms = event_time_ms(lambda i: plan.forward(dsts[0], srcs[0], 32, 2,
                                                    stream=sp), sub,
@@ -162,7 +170,7 @@ def bench_ntt(chd, steps, warmup):
           min([0.0] + [t0.elapsed_time(ev) for ev in starts[1:]]))
     # the inverse with mont_conv=False returns the input: check it stayed put
     ok = all(torch.equal(srcs[i], base) for i in range(nsets))
-    return ms, fwd_ms, inv_ms, warm_ms, one_ms, ok
+    return ms, fwd_ms, inv_ms, warm_ms, one_ms, ok, inv1_ms
 
 
 def _config4_context(chd):
@@ -521,8 +529,11 @@ def run_only(chd, what, steps):
         def fn(i):
             plan.forward(dsts[i % nsets], srcs[i % nsets], 32, 2, stream=sp)
     else:
+        one = what == "ntt_inv_1p"
+
         def fn(i):
-            plan.inverse(dsts[i % nsets], srcs[i % nsets], 32, 2, stream=sp)
+            plan.inverse(dsts[i % nsets], srcs[i % nsets], 32, 2, stream=sp,
+                         single_pass=one)
     for i in range(nsets):
         fn(i)
     torch.cuda.synchronize()
@@ -566,8 +577,8 @@ def main():
     hmult_streams_us = bench_hmult_streams(chd)
     bconv_us = bench_bconv(chd) * 1e3
     bconv_cold_us = bench_bconv(chd, cold=True) * 1e3
-    ms, fwd_ms, inv_ms, warm_ms, one_ms, ok = bench_ntt(chd, args.steps,
-                                                        args.warmup)
+    ms, fwd_ms, inv_ms, warm_ms, one_ms, ok, inv1_ms = bench_ntt(
+        chd, args.steps, args.warmup)
     if not ok:
         print("NTT round trip changed the data", file=sys.stderr)
         sys.exit(1)
@@ -638,6 +649,7 @@ def main():
         "extra": {
             "ntt_forward_us": fwd_ms * 1e3,
             "ntt_inverse_us": inv_ms * 1e3,
+            "ntt_inverse_single_pass_us": inv1_ms * 1e3,
             "ntt_forward_warm_mall_us": warm_ms * 1e3,
             "ntt_step_us_one_stream": one_ms * 1e3,
             "hmult_keyswitch_us_config4": hmult_us,

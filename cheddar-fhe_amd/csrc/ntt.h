@@ -51,6 +51,9 @@ struct NttArgs {
   // single-pass kernel (which reads every quarter of a limb while writing
   // its own) may run
   int src_disjoint;
+  // inverse only: run the single pass over residue classes (src_disjoint
+  // set, no src_mul, tab.twist present; checked by the caller)
+  int inv_one_pass;
   // single-pass ModDown NTT only: every limb of polynomial z reads the one
   // centred source limb src + z * src_pstride, times its cst[l] (a
   // one-source BConv fused into the transform's first round)

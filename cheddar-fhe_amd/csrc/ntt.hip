@@ -1525,6 +1525,266 @@ __global__ __launch_bounds__(1024) void ntt_fwd_1p_bcast(NttArgs a,
   fwd_1p_entry<kEpiModDown, true>(a, num_limbs, num_items, lds);
 }
 
+// ------------------------------------------------------------------------
+// Single-pass inverse over residue classes of the output.
+// With input index i = 4k + r (r < 4, k < N/4), brev(i) = brev2(r) 2^14 +
+// brev14(k), so the kernels' N intt (INTT of NTT.cu:23-229 without N^-1) is
+//   S[4u + s] = sum_k psi^-(e_k (4u + s)) D_s[k],   e_k = 2 brev14(k) + 1,
+//   D_s[k]    = sum_r y[4k + r] I^-(brev2(r) s),    I = psi^(N/2)
+//             = sum_k (psi^4)^-(e_k u) Z_s[k],      Z_s[k] = psi^-(s e_k) D_s[k]:
+// for each residue class s of the output, the N/4-point inverse with root
+// psi^4, whose twiddles (psi^4)^-brev14(m) are psi_inv_rev[m] for m < N/4,
+// of the four adjacent input words combined with constants and twisted.
+// Workgroup s of a limb computes class s: it reads the whole limb (16-byte
+// loads of y[4k .. 4k + 3]) and writes every fourth word of it. The
+// epilogue constant is folded into the four combination constants, so the
+// last round only makes the values canonical (or centred).
+// The four register rounds mirror the forward single pass's, in reverse:
+// stage bits 1..0 and 5..2 (per-lane twiddles), 9..6 (wave-uniform) and
+// 13..10 (uniform), through the same LDS layouts; only the last exchange
+// crosses waves.
+// ------------------------------------------------------------------------
+
+// GS radix-16 over the 16 registers: stage t (0..3) pairs registers j and
+// j + 2^t (bit t of j clear); group gg = j >> (t + 1) of stage t uses
+// w[16 - (16 >> t) + gg]. kVec: per-lane twiddles (no companion multiply).
+template <bool kVec, typename A>
+__device__ __forceinline__ void radix16_gs(const A &ar,
+                                           typename A::T (&x)[16],
+                                           const uint32_t (&w)[15]) {
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const int h = 1 << t;
+#pragma unroll
+    for (int gg = 0; gg < (8 >> t); gg++) {
+      const uint32_t wv = w[16 - (16 >> t) + gg];
+      if constexpr (kVec) {
+#pragma unroll
+        for (int p = 0; p < h; p++)
+          ar.gsv(x[gg * 2 * h + p], x[gg * 2 * h + p + h], wv);
+      } else {
+        const uint32_t wq = ar.twq(wv);
+#pragma unroll
+        for (int p = 0; p < h; p++)
+          ar.gs(x[gg * 2 * h + p], x[gg * 2 * h + p + h], wv, wq);
+      }
+    }
+  }
+}
+
+template <int kEpi, bool kLazy>
+__device__ __forceinline__ void inv_1p_body(const NttArgs &a, const Limb &lb,
+                                            int z, int s, uint32_t q,
+                                            uint32_t qinv, uint32_t *lds) {
+  using A = Arith<kLazy>;
+  using T = typename A::T;
+  const A ar(q, qinv);
+  const uint32_t *itw = a.tab.itw + (static_cast<size_t>(lb.ti) << kLogN);
+  const uint32_t *src = a.src + z * a.src_pstride +
+                        (static_cast<size_t>(lb.sl) << kLogN);
+  // output class s: word 4u + s of the limb
+  uint32_t *dst = poly_dst(a, z) + (static_cast<size_t>(lb.l) << kLogN) + s;
+  const rsrc_t ritw = make_rsrc(itw, 4u * kN);
+  const rsrc_t rsrc = make_rsrc(src, 4u * kN);
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int32_t qs = static_cast<int32_t>(q);
+  const uint32_t qn = 0u - qinv;
+  // Per-lane twiddles of rounds 1 and 2 and the twists, requested before
+  // the input (round 1, store round v: hi4 = k >> 2 = (wave << 8) |
+  // (v << 6) | lane, psi_inv_rev[8192 + 2 hi4 + {0, 1}] and [4096 + hi4];
+  // round 2: hi = k >> 6 = (wave << 4) | (lane >> 2), stage t's 8 >> t
+  // words at psi_inv_rev[2^(11 - t) + (hi << (3 - t))]).
+  uint32_t w1[4][3], w2[15];
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const uint32_t u4 = static_cast<uint32_t>((wave << 8) | (v << 6));
+    const u32x2 pb = bld2(ritw, static_cast<uint32_t>(lane) << 3,
+                          (8192u + 2u * u4) << 2);
+    w1[v][0] = pb[0];
+    w1[v][1] = pb[1];
+    w1[v][2] = bld1(ritw, static_cast<uint32_t>(lane) << 2, (4096u + u4) << 2);
+  }
+  {
+    const uint32_t b96 = static_cast<uint32_t>(lane >> 2);
+    const uint32_t u2 = static_cast<uint32_t>(wave << 4);
+    const u32x4 pa = bld4(ritw, b96 << 5, (2048u + 8u * u2) << 2);
+    const u32x4 pb = bld4(ritw, (b96 << 5) + 16u, (2048u + 8u * u2) << 2);
+    const u32x4 pc = bld4(ritw, b96 << 4, (1024u + 4u * u2) << 2);
+    const u32x2 pd = bld2(ritw, b96 << 3, (512u + 2u * u2) << 2);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      w2[i] = pa[i];
+      w2[4 + i] = pb[i];
+      w2[8 + i] = pc[i];
+    }
+    w2[12] = pd[0];
+    w2[13] = pd[1];
+    w2[14] = bld1(ritw, b96 << 2, (256u + u2) << 2);
+  }
+  // round-1 input layout (the forward's round-2 layout): register rho =
+  // k bits 9..6, lane = bits 5..0, wave = bits 13..10; element k reads the
+  // 16 bytes y[4k .. 4k + 3]
+  // twists of this class (ToMont(1) for class 0: no branch in the loop
+  // below, whose loads then stay in flight together)
+  uint32_t tau[16];
+  {
+    const rsrc_t rtau = make_rsrc(
+        a.tab.twist + (static_cast<size_t>(lb.ti) * 4 + s) * kQuarter,
+        4u * kQuarter);
+#pragma unroll
+    for (int rho = 0; rho < 16; rho++)
+      tau[rho] = bld1(rtau, static_cast<uint32_t>(lane) << 2,
+                      4u * static_cast<uint32_t>((wave << 10) | (rho << 6)));
+  }
+  // combination constants c_r = I^-(brev2(r) s) times the epilogue
+  // constant, canonical: I^-e for e = 0..3 is ToMont(1), psi_inv_rev[1],
+  // -ToMont(1), -psi_inv_rev[1]
+  uint32_t cc[4];
+  {
+    const uint32_t one = ld_uniform(itw, 0), ii = ld_uniform(itw, 1);
+    const uint32_t ce = a.cst[lb.ci];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int br = ((r & 1) << 1) | (r >> 1);
+      const int e = (br * s) & 3;
+      const uint32_t c = e == 0 ? one : e == 1 ? ii : e == 2 ? q - one : q - ii;
+      const uint32_t v = mont_mad(c, ce, ce * qn, q);  // [0, 2q) for q < 2^31
+      cc[r] = v >= q ? v - q : v;
+    }
+  }
+  T x[16];
+#pragma unroll
+  for (int rho = 0; rho < 16; rho++) {
+    const u32x4 y = bld4<2>(rsrc, static_cast<uint32_t>(lane) << 4,
+                            16u * static_cast<uint32_t>((wave << 10) |
+                                                        (rho << 6)));
+    if constexpr (kLazy) {
+      // inputs below 2q: the sum is below 8 q^2, its reduction below 3q, and
+      // the twist's product reduces into [0, 2q)
+      const uint64_t acc = static_cast<uint64_t>(y[0]) * cc[0] +
+                           static_cast<uint64_t>(y[1]) * cc[1] +
+                           static_cast<uint64_t>(y[2]) * cc[2] +
+                           static_cast<uint64_t>(y[3]) * cc[3];
+      const uint32_t m = static_cast<uint32_t>(acc) * qn;
+      uint32_t d =
+          static_cast<uint32_t>((static_cast<uint64_t>(m) * q + acc) >> 32);
+      x[rho] = mont_lo(d, tau[rho], qn, q);  // [0, 2q)
+    } else {
+      // reference form: canonical inputs (signed ones in (-q, q) as well)
+      uint64_t acc = 0;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        acc += static_cast<uint64_t>(
+                   static_cast<uint32_t>(norm(static_cast<int32_t>(y[i]), qs))) *
+               cc[i];
+      const int32_t d = static_cast<int32_t>(reduce_sum4(acc, q, qn));
+      x[rho] = mont_s(d, static_cast<int32_t>(tau[rho]), qinv, qs);  // (-q, q)
+    }
+  }
+  T *xs = reinterpret_cast<T *>(lds);
+#pragma unroll
+  for (int rho = 0; rho < 16; rho++)
+    xs[qidx((wave << 10) | (rho << 6) | lane)] = x[rho];
+  wave_lds_sync();
+  // ---- round 1: stages on bits 1..0 (the forward's round-4 layout: lane =
+  // bits 7..2, store round v = bits 9..8, the four words of a lane = bits
+  // 1..0)
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int n = (wave << 10) | (v << 8) | (lane << 2);
+    u32x4 u = *reinterpret_cast<const u32x4 *>(&lds[qidx(n)]);
+    T y[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) y[i] = static_cast<T>(u[i]);
+    ar.gsv(y[0], y[1], w1[v][0]);
+    ar.gsv(y[2], y[3], w1[v][1]);
+    ar.gsv(y[0], y[2], w1[v][2]);
+    ar.gsv(y[1], y[3], w1[v][2]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) u[i] = static_cast<uint32_t>(y[i]);
+    *reinterpret_cast<u32x4 *>(&lds[qidx(n)]) = u;
+  }
+  wave_lds_sync();
+  // ---- round 2: stages on bits 5..2 (the forward's round-3 layout)
+  {
+    const int b96 = lane >> 2, b10 = lane & 3;
+#pragma unroll
+    for (int rho = 0; rho < 16; rho++)
+      x[rho] = xs[qidx((wave << 10) | (b96 << 6) | (rho << 2) | b10)];
+    radix16_gs<true>(ar, x, w2);
+#pragma unroll
+    for (int rho = 0; rho < 16; rho++)
+      xs[qidx((wave << 10) | (b96 << 6) | (rho << 2) | b10)] = x[rho];
+  }
+  wave_lds_sync();
+  // ---- round 3: stages on bits 9..6 (the forward's round-2 layout);
+  // twiddles wave-uniform: psi_inv_rev[2^(7 - t) + (wave << (3 - t)) + gg]
+  {
+    uint32_t w3[15];
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+      for (int gg = 0; gg < (8 >> tt); gg++)
+        w3[16 - (16 >> tt) + gg] =
+            ld_uniform(itw, (128 >> tt) + (wave << (3 - tt)) + gg);
+#pragma unroll
+    for (int rho = 0; rho < 16; rho++)
+      x[rho] = xs[qidx((wave << 10) | (rho << 6) | lane)];
+    radix16_gs<false>(ar, x, w3);
+#pragma unroll
+    for (int rho = 0; rho < 16; rho++)
+      xs[qidx((wave << 10) | (rho << 6) | lane)] = x[rho];
+  }
+  __syncthreads();
+  // ---- round 4: stages on bits 13..10 (the forward's round-1 layout: the
+  // register is bits 13..10, the thread bits 9..0); twiddles uniform:
+  // psi_inv_rev[2^(3 - t) + gg]
+  {
+    uint32_t w4[15];
+#pragma unroll
+    for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+      for (int gg = 0; gg < (8 >> tt); gg++)
+        w4[16 - (16 >> tt) + gg] = ld_uniform(itw, (8 >> tt) + gg);
+#pragma unroll
+    for (int rho = 0; rho < 16; rho++) x[rho] = xs[qidx((rho << 10) | t)];
+    radix16_gs<false>(ar, x, w4);
+  }
+  // output u = (rho << 10) | t is word 4u + s: every fourth word, written
+  // with default caching so that the limb's four workgroups (one XCD, one
+  // L2) complete each line before it leaves the L2
+#pragma unroll
+  for (int rho = 0; rho < 16; rho++) {
+    int32_t v = static_cast<int32_t>(ar.canon_inv(x[rho]));
+    if constexpr (kEpi == kEpiConstCentre)
+      if (v > (qs >> 1)) v -= qs;
+    st_at<int32_t>(dst + (rho << 12), 16u * static_cast<uint32_t>(t), v);
+  }
+}
+
+// grid: 1D, 4 * roundup(limbs * polys, 8) blocks of 1024 threads (the four
+// classes of a limb 8 block ids apart: one XCD)
+template <int kEpi>
+__global__ __launch_bounds__(1024) void ntt_inv_1p(NttArgs a, int num_limbs,
+                                                   int num_items) {
+  __shared__ __align__(16) uint32_t lds[kQLdsWords];
+  const int b = blockIdx.x;
+  const int slot = b >> 3;
+  const int s = slot & 3;
+  const int li = (slot >> 2) * 8 + (b & 7);
+  if (li >= num_items) return;
+  const int z = li / num_limbs;
+  const Limb lb = decode(a.map, li - z * num_limbs);
+  const uint32_t q = a.tab.q[lb.ti];
+  const uint32_t qinv = static_cast<uint32_t>(a.tab.qinv[lb.ti]);
+  if (q < (1u << 30))
+    inv_1p_body<kEpi, true>(a, lb, z, s, q, qinv, lds);
+  else
+    inv_1p_body<kEpi, false>(a, lb, z, s, q, qinv, lds);
+}
+
 }  // namespace
 
 hipError_t launch_ntt_fwd_cols(const NttArgs &a, int num_limbs, int num_z,
@@ -1603,6 +1863,22 @@ hipError_t launch_ntt_inv_cols(const NttArgs &a, int num_limbs, int num_polys,
 hipError_t launch_ntt_inv(const NttArgs &a, int num_limbs, int num_polys,
                           int epilogue, hipStream_t s) {
   if (num_limbs <= 0 || num_polys <= 0) return hipSuccess;
+  // The single pass over residue classes (one HBM read and write of each
+  // limb instead of two: 43 MB against 76 MB at config 2) runs only when
+  // asked for (chd_k_ntt_inv_1p): at config 2 it takes 21.5 us against
+  // 19 us for the two passes, and the three-stream headline step 30.3 us
+  // against 27.7 us (its every-fourth-word stores cost ~3 us).
+  const int items = num_limbs * num_polys;
+  if (a.inv_one_pass) {
+    dim3 g1(4 * ((items + 7) / 8 * 8));
+    if (epilogue == kEpiConstCentre)
+      hipLaunchKernelGGL(ntt_inv_1p<kEpiConstCentre>, g1, dim3(1024), 0, s, a,
+                         num_limbs, items);
+    else
+      hipLaunchKernelGGL(ntt_inv_1p<kEpiConst>, g1, dim3(1024), 0, s, a,
+                         num_limbs, items);
+    return hipGetLastError();
+  }
   dim3 gr(kRows / kTileRows, num_limbs, num_polys);
   hipLaunchKernelGGL(ntt_inv_rows, gr, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
@@ -1735,8 +2011,9 @@ static int ntt_inv_common(const char *name, const chd_tables *t,
                           long long dst_pstride, const uint32_t *src,
                           const uint32_t *src_mul, long long src_pstride,
                           int num_limbs, int num_polys, const uint32_t *cst,
-                          int centre, void *stream) {
-  if (!t || !m || !dst || !src || !cst || num_limbs < 0 || num_polys < 0)
+                          int centre, void *stream, bool one_pass = false) {
+  if (!t || !m || !dst || !src || !cst || num_limbs < 0 || num_polys < 0 ||
+      (one_pass && (src_mul != nullptr || t->twist == nullptr)))
     return set_error(CHD_ERR_ARG, std::string(name) + ": invalid argument");
   NttArgs a{};
   a.src = src;
@@ -1747,6 +2024,18 @@ static int ntt_inv_common(const char *name, const chd_tables *t,
   a.map = *m;
   a.tab = *t;
   a.cst = cst;
+  a.src_disjoint =
+      sets_disjoint(src, src_pstride, num_polys, span_limbs(num_limbs, *m, true),
+                    dst, dst_pstride, num_polys,
+                    span_limbs(num_limbs, *m, false))
+          ? 1
+          : 0;
+  if (one_pass && !a.src_disjoint)
+    return set_error(CHD_ERR_ARG,
+                     std::string(name) +
+                         ": the single pass needs a source apart from the "
+                         "destination");
+  a.inv_one_pass = one_pass ? 1 : 0;
   hipError_t e =
       launch_ntt_inv(a, num_limbs, num_polys,
                      centre ? kEpiConstCentre : kEpiConst,
@@ -1765,6 +2054,17 @@ extern "C" int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m,
   return ntt_inv_common("chd_k_ntt_inv", t, m, dst, dst_pstride, src, nullptr,
                         src_pstride, num_limbs, num_polys, cst, centre,
                         stream);
+}
+
+extern "C" int chd_k_ntt_inv_1p(const chd_tables *t, const chd_limb_map *m,
+                                uint32_t *dst, long long dst_pstride,
+                                const uint32_t *src, long long src_pstride,
+                                int num_limbs, int num_polys,
+                                const uint32_t *cst, int centre,
+                                void *stream) {
+  return ntt_inv_common("chd_k_ntt_inv_1p", t, m, dst, dst_pstride, src,
+                        nullptr, src_pstride, num_limbs, num_polys, cst,
+                        centre, stream, true);
 }
 
 extern "C" int chd_k_ntt_inv_cols(const chd_tables *t, const chd_limb_map *m,

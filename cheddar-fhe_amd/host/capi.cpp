@@ -110,6 +110,23 @@ extern "C" int chd_ntt_inverse(const chd_ntt_plan *plan, uint32_t *dst,
                        0, stream);
 }
 
+extern "C" int chd_ntt_inverse_single_pass(const chd_ntt_plan *plan,
+                                           uint32_t *dst, const uint32_t *src,
+                                           int num_limbs, int num_polys,
+                                           int mont_conv, void *stream) {
+  if (!plan || !dst || !src || num_limbs < 1 ||
+      num_limbs > plan->chain->size() || num_polys < 1)
+    return set_error(CHD_ERR_ARG,
+                     "chd_ntt_inverse_single_pass: invalid argument");
+  chd_limb_map m = PlainMap(num_limbs);
+  const long long ps = static_cast<long long>(num_limbs) << 16;
+  return chd_k_ntt_inv_1p(&plan->chain->tables(), &m, dst, ps, src, ps,
+                          num_limbs, num_polys,
+                          mont_conv ? plan->chain->inv_degree()
+                                    : plan->chain->inv_degree_mont(),
+                          0, stream);
+}
+
 // ---------------------------------------------------------- BConv plans --
 extern "C" int chd_bconv_plan_create(chd_bconv_plan **out, int log_degree,
                                      const uint32_t *src_primes, int src_len,

@@ -38,6 +38,12 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
   std::vector<int32_t> qinv(T);
   std::vector<uint32_t> ninv(T), ninv_mont(T), r2(T);
   std::vector<uint32_t> tw(T * n), itw(T * n);
+  // the single-pass inverse's twists: psi^-(s e_k), e_k = 2 brev(k) + 1
+  // over log N - 2 bits, for the residue classes s = 0..3 of its output
+  // (class 0's row is ToMont(1): every class runs the same code)
+  const int m4 = n / 4;
+  std::vector<uint32_t> twist(T * 4 * m4);
+  std::vector<uint32_t> ipow(2 * n);
   for (size_t i = 0; i < T; i++) {
     const uint32_t q = primes[i];
     if (q >= (1u << 31) || q % (2u * n) != 1)
@@ -59,11 +65,25 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
       p = p * psi % q;
       pi = pi * psi_inv % q;
     }
+    // psi^-e for e < 2N (psi has order 2N)
+    uint64_t e1 = 1;
+    for (int e = 0; e < 2 * n; e++) {
+      ipow[e] = static_cast<uint32_t>(e1);
+      e1 = e1 * psi_inv % q;
+    }
+    for (int s = 0; s < 4; s++)
+      for (int k = 0; k < m4; k++) {
+        const uint32_t ek =
+            2u * pm::bitrev(static_cast<uint32_t>(k), log_degree - 2) + 1u;
+        twist[(i * 4 + s) * m4 + k] =
+            pm::to_mont(ipow[(s * ek) % (2u * n)], q);
+      }
   }
   q_.Upload(primes);
   qinv_.Upload(qinv);
   tw_.Upload(tw);
   itw_.Upload(itw);
+  twist_.Upload(twist);
   ninv_.Upload(ninv);
   ninv_mont_.Upload(ninv_mont);
   r2_.Upload(r2);
@@ -71,6 +91,7 @@ ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
   tab_.qinv = qinv_.as<int32_t>();
   tab_.tw = tw_.as<uint32_t>();
   tab_.itw = itw_.as<uint32_t>();
+  tab_.twist = twist_.as<uint32_t>();
 }
 
 }  // namespace cheddar

@@ -72,7 +72,7 @@ class ChainTables {
  private:
   int log_degree_;
   std::vector<uint32_t> primes_;
-  DevBuf q_, qinv_, tw_, itw_;
+  DevBuf q_, qinv_, tw_, itw_, twist_;
   DevBuf ninv_, ninv_mont_, r2_;
   chd_tables tab_{};
 };

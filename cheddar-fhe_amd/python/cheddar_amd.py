@@ -43,6 +43,7 @@ _SIGS = {
     "chd_ntt_plan_tables": (_vp, [_vp]),
     "chd_ntt_forward": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "chd_ntt_inverse": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "chd_ntt_inverse_single_pass": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "chd_bconv_plan_create": (_i, [_pp, _i, _c_u32p, _i, _c_u32p, _i]),
     "chd_bconv_plan_destroy": (None, [_vp]),
     "chd_bconv_plan_constants": (_i, [_vp, _c_u32p, _c_i32p]),
@@ -166,11 +167,14 @@ class NttPlan:
                                    current_stream()))
 
     def inverse(self, dst, src, num_limbs, num_polys=1, mont_conv=True,
-                stream=None):
-        _check(lib.chd_ntt_inverse(self.h, ptr(dst), ptr(src), num_limbs,
-                                   num_polys, int(bool(mont_conv)),
-                                   stream if stream is not None else
-                                   current_stream()))
+                stream=None, single_pass=False):
+        """single_pass: the one-pass kernel over residue classes (dst apart
+        from src; the default two passes are faster)"""
+        fn = (lib.chd_ntt_inverse_single_pass if single_pass
+              else lib.chd_ntt_inverse)
+        _check(fn(self.h, ptr(dst), ptr(src), num_limbs, num_polys,
+                  int(bool(mont_conv)),
+                  stream if stream is not None else current_stream()))
 
 
 class BconvPlan:

@@ -26,6 +26,11 @@ typedef struct chd_tables {
   const int32_t *qinv;      /* [T] q^-1 mod 2^32 (signed)                 */
   const uint32_t *tw;       /* [T][N] ToMont(psi^brev(j))                 */
   const uint32_t *itw;      /* [T][N] ToMont(psi^-brev(j))                */
+  /* [T][4][N/4] ToMont(psi^-(s (2 brev_{log N - 2}(k) + 1))), s = 0..3: the
+   * per-element twist of the single-pass inverse NTT's residue class s
+   * (row 0 is ToMont(1)); optional: NULL keeps every inverse on the
+   * two-pass kernels */
+  const uint32_t *twist;
 } chd_tables;
 
 /* launch limb j -> logical limb l = j + (j >= skip_lo ? skip_len : 0);
@@ -93,6 +98,18 @@ int chd_k_ntt_inv(const chd_tables *t, const chd_limb_map *m, uint32_t *dst,
                   long long dst_pstride, const uint32_t *src,
                   long long src_pstride, int num_limbs, int num_polys,
                   const uint32_t *cst, int centre, void *stream);
+
+/* chd_k_ntt_inv in one pass over residue classes of the output: workgroup
+ * s of a limb reads the whole limb and writes its words 4u + s (one HBM read
+ * and write per limb; the two passes read and write twice). src must not
+ * overlap dst (else CHD_ERR_INVALID_ARGUMENT before any launch) and t->twist
+ * must be set. Same results as chd_k_ntt_inv; slower at config 2 (21.5 us
+ * against 19 us), kept for that comparison. No reference counterpart: an
+ * alternative layout of INTT (NTT.cu:673-741). */
+int chd_k_ntt_inv_1p(const chd_tables *t, const chd_limb_map *m,
+                     uint32_t *dst, long long dst_pstride, const uint32_t *src,
+                     long long src_pstride, int num_limbs, int num_polys,
+                     const uint32_t *cst, int centre, void *stream);
 
 /* Second pass of chd_k_ntt_inv alone (stages 7..0 and the epilogue, in
  * place on dst), for data whose first pass another kernel produced

@@ -9,6 +9,7 @@
 // test; exit status 0 only if every test passes. Needs a HIP device.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -772,6 +773,59 @@ int main() {
         err = std::max(err, std::abs(dec[i] - msg[i]));
       check("Context::LevelDown (oracle, and the encoding survives)",
             ok && err < 1e-3);
+    }
+  }
+  // kernel ABI: the inverse NTT of 2 x 32 limbs out of place (the single
+  // pass over residue classes) and in place (the two passes), plain and
+  // centred, on the chain's 30- and 31-bit primes with arbitrary epilogue
+  // constants, against the oracle's INTTAndMultConst (NTT.cu:743-813)
+  {
+    const ChainTables chain(kLogN, chain_k);
+    const int nl = L + alpha, npoly = 2;
+    const size_t w = static_cast<size_t>(nl) * kN;
+    std::vector<word> x(npoly * w);
+    for (int p = 0; p < npoly; p++) {
+      const std::vector<word> v = uniform(chain_k, nl);
+      std::copy(v.begin(), v.end(), x.begin() + p * w);
+    }
+    std::vector<word> cst(nl);
+    for (int l = 0; l < nl; l++) cst[l] = next64() % chain_k[l];
+    DevBuf dsrc(npoly * w * sizeof(word)), ddst(npoly * w * sizeof(word)),
+        dcst(nl * sizeof(word));
+    dcst.Upload(cst);
+    chd_limb_map m{};
+    m.num_q = nl;
+    m.skip_lo = INT_MAX;
+    for (int centre = 0; centre < 2; centre++) {
+      std::vector<word> want(npoly * w);
+      for (int p = 0; p < npoly; p++)
+        for (int l = 0; l < nl; l++)
+          orc_intt_mult_const(
+              reinterpret_cast<int32_t *>(want.data() + p * w + l * kN),
+              x.data() + p * w + l * kN, kLogN, chain_k[l], cst[l], centre);
+      upload(dsrc.as<word>(), x);
+      bool ok = chd_k_ntt_inv(&chain.tables(), &m, ddst.as<word>(),
+                              static_cast<long long>(w), dsrc.as<word>(),
+                              static_cast<long long>(w), nl, npoly,
+                              dcst.as<word>(), centre, nullptr) == 0;
+      ok = ok && same(download(ddst.as<word>(), npoly * w), want) &&
+           same(download(dsrc.as<word>(), npoly * w), x);
+      upload(ddst.as<word>(), x);
+      ok = ok && chd_k_ntt_inv(&chain.tables(), &m, ddst.as<word>(),
+                               static_cast<long long>(w), ddst.as<word>(),
+                               static_cast<long long>(w), nl, npoly,
+                               dcst.as<word>(), centre, nullptr) == 0;
+      ok = ok && same(download(ddst.as<word>(), npoly * w), want);
+      // the single pass over residue classes: the same words
+      HipCheck(hipMemset(ddst.as<void>(), 0, npoly * w * sizeof(word)),
+               "hipMemset");
+      ok = ok && chd_k_ntt_inv_1p(&chain.tables(), &m, ddst.as<word>(),
+                                  static_cast<long long>(w), dsrc.as<word>(),
+                                  static_cast<long long>(w), nl, npoly,
+                                  dcst.as<word>(), centre, nullptr) == 0;
+      ok = ok && same(download(ddst.as<word>(), npoly * w), want);
+      check(std::string("chd_k_ntt_inv 2 x 32 limbs, out of place, in place "
+                        "and single pass") + (centre ? ", centred" : ""), ok);
     }
   }
   // an invalid call throws cheddar::Error instead of exiting

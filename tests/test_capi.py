@@ -81,7 +81,7 @@ P = ctypes.c_void_p
 
 
 class Tables(ctypes.Structure):
-    _fields_ = [(n, P) for n in ("q", "qinv", "tw", "itw")]
+    _fields_ = [(n, P) for n in ("q", "qinv", "tw", "itw", "twist")]
 
 
 class LimbMap(ctypes.Structure):
@@ -124,6 +124,28 @@ def _kernel_lib(chd):
         ctypes.POINTER(Tables), ctypes.POINTER(LimbMap), P, ctypes.c_int, P,
         ctypes.c_int, ctypes.c_int, P, P, P]
     return lib
+
+
+def test_ntt_inv_single_pass_checks(chd):
+    """chd_k_ntt_inv_1p refuses an overlapping destination and tables
+    without the twist table, before any launch"""
+    lib = chd.lib
+    lib.chd_k_ntt_inv_1p.argtypes = [
+        ctypes.POINTER(Tables), ctypes.POINTER(LimbMap), P, ctypes.c_longlong,
+        P, ctypes.c_longlong, ctypes.c_int, ctypes.c_int, P, ctypes.c_int, P]
+    m = LimbMap(num_q=32, skip_lo=1 << 30)
+    ps = 32 << 16
+    t = Tables(twist=FAKE)
+    assert lib.chd_k_ntt_inv_1p(t, m, FAKE, ps, FAKE, ps, 32, 2, FAKE, 0,
+                                None) == -1
+    assert b"apart from the destination" in lib.chd_last_error()
+    # half a limb apart: still overlapping
+    assert lib.chd_k_ntt_inv_1p(t, m, P(0x1000 + 4 * (1 << 15)), ps, FAKE,
+                                ps, 32, 2, FAKE, 0, None) == -1
+    t = Tables()
+    assert lib.chd_k_ntt_inv_1p(t, m, P(1 << 40), ps, FAKE, ps, 32, 2, FAKE,
+                                0, None) == -1
+    assert b"invalid argument" in lib.chd_last_error()
 
 
 def test_gs_fused_wide_checks(chd):

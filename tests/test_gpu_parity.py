@@ -65,6 +65,32 @@ def test_ntt_config2_batch(chd):
     assert np.array_equal(host(y2), want_m)
 
 
+@pytest.mark.parametrize("bits", [30, 31])
+def test_ntt_inverse_single_pass(chd, bits):
+    """the single-pass inverse over residue classes (chd_ntt_inverse_single_
+    pass) at the config-2 shape, on 30-bit primes (lazy butterflies) and
+    31-bit primes (reference-form butterflies), both epilogue constants,
+    against the oracle; an overlapping destination is refused"""
+    primes = (Q30 if bits == 30 else Q31)[:32]
+    plan = chd.NttPlan(primes)
+    x = np.stack([uniform_limbs(rng(960 + bits + p), primes)
+                  for p in range(2)])
+    y = np.stack([_orc.ntt_batch(x[p].reshape(-1), 16, primes).reshape(32, N)
+                  for p in range(2)])
+    src = dev(y)
+    z = zeros(2, 32, N)
+    plan.inverse(z, src, 32, 2, mont_conv=False, single_pass=True)
+    assert np.array_equal(host(z), x)
+    assert np.array_equal(host(src), y)
+    want = np.stack([_orc.intt_batch(y[p].reshape(-1), 16, primes,
+                                     1).reshape(32, N) for p in range(2)])
+    plan.inverse(z, src, 32, 2, mont_conv=True, single_pass=True)
+    assert np.array_equal(host(z), want)
+    with pytest.raises(chd.ChdError, match="apart from the destination"):
+        plan.inverse(src, src, 32, 2, single_pass=True)
+    assert np.array_equal(host(src), y)
+
+
 def test_ntt_31bit_primes_batch(chd):
     """the config-2 batch shape on 31-bit primes (the reference-form
     butterflies of every kernel) against the oracle, both directions"""
