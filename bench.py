@@ -38,16 +38,15 @@ INT8_PEAK_TOPS = 5000.0     # dense int8 MFMA, MI355X
 BCONV_BYTES = 48 * 4 * (1 << 16)
 BCONV_INT8_OPS = 2 * 16 * (1 << 16) * 8 * 40
 # its measured HBM bytes per launch (profiles/bconv_config3_traffic.md:
-# FETCH_SIZE 1100.5 KiB x 2 + WRITE_SIZE 12751.6 KiB)
-BCONV_TRAFFIC = 15311424
+# FETCH_SIZE 1101.0 KiB x 2 + WRITE_SIZE 10240.0 KiB)
+BCONV_TRAFFIC = 12740608
 # config 4 HMult compulsory bytes: 4 x 24 input limbs, 3 x 2 x 32 key limbs,
 # 2 x 23 output limbs
 HMULT_BYTES = (96 + 192 + 46) * 4 * (1 << 16)
 # its measured HBM bytes per HMult, the sum over its 8 launches
-# (profiles/hmult_config4_traffic.md; the INTT column pass and the BConv
-# run twice)
-HMULT_TRAFFIC = (25275392 + 2 * 11308096 + 2 * 21158912 + 38176384 +
-                 128372032 + 48663552)
+# (profiles/hmult_config4_traffic.md, one row per launch)
+HMULT_TRAFFIC = (25288704 + 12902464 + 25420800 + 38170624 + 128376256 +
+                 9694976 + 16901120 + 48668672)
 N = 1 << 16
 LIMB_BYTES = 4 * N
 # one limb-transform moves one limb in and one limb out (algorithmic bytes)

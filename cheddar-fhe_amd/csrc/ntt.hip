@@ -1510,9 +1510,15 @@ __device__ __forceinline__ void fwd_1p_entry(const NttArgs &a, int num_limbs,
 // At most 64 VGPRs (8 waves per SIMD): two of these workgroups (16 waves,
 // 68 KiB of LDS each) fit on one CU, so a launch on another stream can run
 // its loads beside this one's butterflies. The broadcast ModDown form needs
-// more registers and keeps the default limit (ntt_fwd_1p_bcast).
+// more registers and keeps the default limit (ntt_fwd_1p_bcast), and so does
+// the phase-timestamp build, whose marks would otherwise spill.
+#ifdef CHD_PHASE_TIMESTAMPS
+#define CHD_FWD_1P_WAVES
+#else
+#define CHD_FWD_1P_WAVES __attribute__((amdgpu_waves_per_eu(8)))
+#endif
 template <int kEpi, bool kPre>
-__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(8)))
+__global__ __launch_bounds__(1024) CHD_FWD_1P_WAVES
 void ntt_fwd_1p(NttArgs a, int num_limbs, int num_items) {
   __shared__ __align__(16) uint32_t lds[kQLdsWords];
   fwd_1p_entry<kEpi, kPre>(a, num_limbs, num_items, lds);

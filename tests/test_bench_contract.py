@@ -48,12 +48,19 @@ def test_bconv_traffic_matches_profile():
 
 
 def test_hmult_traffic_matches_profile():
-    name = "hmult_config4_traffic.md"
-    launches = {"ntt_inv_rows": 1, "ntt_inv_cols<3>": 2,
-                "bconv_mfma<1, false>": 2, "ntt_fwd_cols<false>": 1,
-                "modup_keyacc": 1, "ntt_fwd_1p<1, false>": 1}
-    total = sum(n * _table_row(name, k)[2] for k, n in launches.items())
-    assert bench.HMULT_TRAFFIC == total
+    """the bench's figure is the sum of the profile's eight per-launch rows
+    (| # | kernel | ... | HBM bytes |), each consistent with its counters"""
+    rows = []
+    with open(os.path.join(ROOT, "profiles", "hmult_config4_traffic.md")) as f:
+        for line in f:
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) == 8 and cells[0].isdigit():
+                rows.append(cells)
+    assert [int(c[0]) for c in rows] == list(range(1, 9))
+    for c in rows:
+        fetch, write, total = float(c[3]), float(c[4]), int(c[7])
+        assert abs(total - (fetch * 2 + write) * 1024) < 1024
+    assert bench.HMULT_TRAFFIC == sum(int(c[7]) for c in rows)
 
 
 def test_ntt_traffic_from_profile():
