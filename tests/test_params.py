@@ -63,6 +63,17 @@ def test_malformed_files_are_rejected(chd, mutate, match):
         chd.Param.from_json(json.dumps(d))
 
 
+@pytest.mark.parametrize("log_degree", [12, 15, 17])
+def test_degrees_other_than_2_16_are_rejected(chd, log_degree):
+    """the reference documents only log_degree 16 (Parameter.h:33); every
+    kernel here is built for N = 2^16, so another degree is refused with a
+    reason instead of running wrong (its primes stay NTT-friendly for it)"""
+    d = json.loads(_text("bootparam_30.json"))
+    d["log_degree"] = log_degree
+    with pytest.raises(chd.ChdError, match="only log_degree 16"):
+        chd.Param.from_json(json.dumps(d))
+
+
 def test_syntax_error_is_reported(chd):
     with pytest.raises(chd.ChdError, match="JSON"):
         chd.Param.from_json('{"log_degree": 16,')
