@@ -25,8 +25,22 @@ void K(int status) {
 
 int DivCeil(int a, int b) { return (a + b - 1) / b; }
 
+// ModDown's destination-limb counts (polynomials x limbs) up to which the
+// BConv writes the destination and a two-pass NTT runs in place on it; above
+// them a single-pass NTT does. The one-source case (Rescale) has its own,
+// lower limit: there the single pass forms the BConv itself and saves a
+// launch. Measured on MI355X, warm, microseconds (threshold 32 / single pass
+// everywhere / two passes everywhere):
+//   ModDown, 1 poly, 8..24 limbs: 28.2..33.2 / 32.4..37.8 / 28.2..33.2
+//   HMult (merged rescale), 2 x 19 and 2 x 23 limbs: 86.9, 89.0 / 86.8,
+//     88.9 / 88.1, 91.2; 2 x 15: 70.4 (two passes) / 70.9 (single)
+//   Rescale, 1 poly, 7 / 11 / 15 / 19 / 23 limbs: two passes 25.8 / 27.0 /
+//     28.2 / 30.5 / 31.3, single pass 27.6 / 27.5 / 27.7 / 28.1 / 27.8
 #ifndef CHD_SMALL_MODDOWN_LIMBS
 #define CHD_SMALL_MODDOWN_LIMBS 32
+#endif
+#ifndef CHD_SMALL_RESCALE_LIMBS
+#define CHD_SMALL_RESCALE_LIMBS 12
 #endif
 
 chd_limb_map NoSkipMap(const Parameter<uint32_t> &param, const NPInfo &np) {
@@ -1174,9 +1188,11 @@ void ModSwitchHandler<uint32_t>::ModDownMulti(const std::vector<word *> &dst,
   // destination and the two-pass NTT runs in place on it, its passes
   // spread over many small workgroups (HMult at L = 4, 8, 12, 16: 6.4, 5.8,
   // 3.2 and 2.2 us faster; at 38 and 46 limbs the single pass is ahead)
-  const bool few = num_polys * dst_len <= CHD_SMALL_MODDOWN_LIMBS;
-  if (!few && st.src_len == 1 &&
-      st.bconv1.size() == static_cast<size_t>(dst_len)) {
+  const bool one_src =
+      st.src_len == 1 && st.bconv1.size() == static_cast<size_t>(dst_len);
+  const bool few = num_polys * dst_len <= (one_src ? CHD_SMALL_RESCALE_LIMBS
+                                                   : CHD_SMALL_MODDOWN_LIMBS);
+  if (!few && one_src) {
     // one source (Rescale): the NTT forms each limb's BConv, the source
     // times that limb's table entry, from the one INTT limb as it reads it
     K(chd_k_ntt_fwd_moddown_bconv1_multi(

@@ -382,12 +382,13 @@ def test_hmult_in_place_and_separate_rescale(chd, ks):
 @pytest.mark.parametrize("rescale", [True, False])
 def test_hmult_one_aux_prime(chd, rescale):
     """alpha = 1 (dnum = L = 4): ModDown has a single source limb. With so
-    few destination limbs (at most 32 polynomial-limbs) the one-source BConv
-    writes the destination and the two-pass ModDown NTT runs in place on it;
-    without rescale the result is also rescaled separately (one source
-    again, the same path), both against the oracle. The one-source BConv
-    formed inside the single-pass NTT serves Rescale above 16 limbs and is
-    pinned by the L = 24 Rescale tests."""
+    few destination limbs (at most 12 polynomial-limbs for one source) the
+    one-source BConv writes the destination and the two-pass ModDown NTT
+    runs in place on it; without rescale the result is also rescaled
+    separately (one source again, the same path), both against the oracle.
+    The one-source BConv formed inside the single-pass NTT serves more
+    destination limbs and is pinned by the L = 24 Rescale tests and
+    test_rescale_either_side_of_the_one_source_limit."""
     main, aux, L = Q30[:4], Q31[:1], 4
     param = chd.Param(main, aux, [(i, 0) for i in range(1, L + 1)])
     ctx = chd.Context(param)
@@ -407,6 +408,26 @@ def test_hmult_one_aux_prime(chd, rescale):
         ctx.rescale(L - 1, out, res)
         assert np.array_equal(host(out[0]), _orc.rescale(wb, main, L, 1, 16))
         assert np.array_equal(host(out[1]), _orc.rescale(wa, main, L, 1, 16))
+
+
+@pytest.mark.parametrize("L", [7, 8, 13, 14])
+def test_rescale_either_side_of_the_one_source_limit(chd, ks, L):
+    """Rescale has one source limb: up to 12 destination polynomial-limbs
+    the BConv writes the destination and a two-pass NTT runs in place on
+    it, above that the single-pass NTT forms the BConv as it reads. The
+    ciphertext (2 x 6 = 12 limbs at L = 7, 2 x 7 = 14 at L = 8) and the
+    single polynomial (12 at L = 13, 13 at L = 14) on both sides, against
+    the oracle"""
+    param, ctx, main, aux = ks
+    r = rng(490 + L)
+    b, a = uniform_limbs(r, main[:L]), uniform_limbs(r, main[:L])
+    out = (zeros(L - 1, N), zeros(L - 1, N))
+    ctx.rescale(L - 1, out, (dev(b), dev(a)))
+    assert np.array_equal(host(out[0]), _orc.rescale(b, main, L, 1, 16))
+    assert np.array_equal(host(out[1]), _orc.rescale(a, main, L, 1, 16))
+    one = zeros(L - 1, N)
+    ctx.rescale_poly(L - 1, one, dev(b))
+    assert np.array_equal(host(one), _orc.rescale(b, main, L, 1, 16))
 
 
 @pytest.mark.parametrize("L", [4, 24])
