@@ -397,7 +397,7 @@ __global__ __launch_bounds__(kThreads) void gs_fused_kernel(chd_tables t,
 // [0, 2q), and the accumulators stay in [0, 2q) until the final store.
 // Otherwise (q < 2^31) the sum is reduced by reduce_sum4 to [0, q) and
 // accumulated canonically.
-template <int kGw, bool kSmall>
+template <int kGw, bool kSmall, bool kTiled>
 __device__ __forceinline__ void gs_wide_body(const chd_gs_wide_args &a,
                                              const LimbIdx &li) {
   const uint32_t q = li.q;
@@ -406,6 +406,17 @@ __device__ __forceinline__ void gs_wide_body(const chd_gs_wide_args &a,
   const size_t o = (static_cast<size_t>(li.l) << kLogN) +
                    blockIdx.x * (64 * kPerThread) + (threadIdx.x & 63) * kPerThread;
   const int g0 = wave * kGw;
+  // tiled plaintexts (chd_k_gs_pack_tiled): this workgroup's block of this
+  // limb, every (giant, baby) pair 256 words apart, lane part included
+  [[maybe_unused]] const int tiled_rows = a.tiled_rows;
+  [[maybe_unused]] const uint32_t *tile =
+      kTiled ? a.pt_tiled +
+                   ((static_cast<size_t>(li.l) * (kN / (64 * kPerThread)) +
+                     blockIdx.x) *
+                        static_cast<size_t>(tiled_rows) * a.pt_stride
+                    << 8) +
+                   (threadIdx.x & 63) * kPerThread
+             : nullptr;
   uint32_t rb[kGw][4], ra[kGw][4];
 #pragma unroll
   for (int g = 0; g < kGw; g++) {
@@ -443,8 +454,20 @@ __device__ __forceinline__ void gs_wide_body(const chd_gs_wide_args &a,
 #pragma unroll
     for (int g = 0; g < kGw; g++) {
       uint4 mv[4];
+      if constexpr (kTiled) {
+        // giant steps past tiled_rows (padding) are not computed
+        if (g0 + g >= tiled_rows) continue;
+        // this pair's 256 coefficients of the block; the next baby step
+        // 256 words on
+        const uint32_t *p =
+            tile + (static_cast<size_t>((g0 + g) * a.pt_stride + b0) << 8);
 #pragma unroll
-      for (int j = 0; j < 4; j++) mv[j] = ld4_once(row[g * a.pt_stride + j] + o);
+        for (int j = 0; j < 4; j++) mv[j] = ld4_once(p + (j << 8));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          mv[j] = ld4_once(row[g * a.pt_stride + j] + o);
+      }
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         uint64_t tb = 0, ta = 0;
@@ -461,6 +484,8 @@ __device__ __forceinline__ void gs_wide_body(const chd_gs_wide_args &a,
   }
 #pragma unroll
   for (int g = 0; g < kGw; g++) {
+    if constexpr (kTiled)
+      if (g0 + g >= tiled_rows) break;
     if constexpr (kSmall) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
@@ -473,15 +498,52 @@ __device__ __forceinline__ void gs_wide_body(const chd_gs_wide_args &a,
   }
 }
 
-template <int kGw>
+template <int kGw, bool kTiled>
 __global__ __launch_bounds__(kThreads) void gs_wide_kernel(chd_tables t,
                                                          chd_limb_map m,
                                                          chd_gs_wide_args a) {
   const LimbIdx li = limb_of(t, m);
   if (li.q < (1u << 30))
-    gs_wide_body<kGw, true>(a, li);
+    gs_wide_body<kGw, true, kTiled>(a, li);
   else
-    gs_wide_body<kGw, false>(a, li);
+    gs_wide_body<kGw, false, kTiled>(a, li);
+}
+
+// Tiled plaintext copy for gs_wide_kernel: grid (N / 256 blocks, limbs,
+// rows); the 4 waves of a workgroup copy the row's pt_stride baby steps of
+// one 256-coefficient block, 1 KiB per wave instruction.
+__global__ __launch_bounds__(kThreads) void gs_pack_tiled_kernel(
+    const uint32_t *const *pt_table, int rows, int pt_stride,
+    uint32_t *dst) {
+  const int k = blockIdx.x, l = blockIdx.y, g = blockIdx.z;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const size_t so = (static_cast<size_t>(l) << kLogN) + (k << 8) + lane * 4;
+  uint32_t *d = dst +
+                ((((static_cast<size_t>(l) * (kN >> 8) + k) * rows + g) *
+                  pt_stride)
+                 << 8) +
+                lane * 4;
+  for (int b = wave; b < pt_stride; b += kThreads / 64)
+    st4(d + (static_cast<size_t>(b) << 8),
+        ld4_once(pt_table[g * pt_stride + b] + so));
+}
+
+// One row back out of the tiled copy: grid (N / 256 blocks, dst limbs), the
+// row's pt_stride baby steps of one block, 1 KiB per wave instruction.
+__global__ __launch_bounds__(kThreads) void gs_untile_row_kernel(
+    const uint32_t *tiled, int rows, int pt_stride, int g, int dst_limbs,
+    uint32_t *dst) {
+  const int k = blockIdx.x, l = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t *s = tiled +
+                      ((((static_cast<size_t>(l) * (kN >> 8) + k) * rows + g) *
+                        pt_stride)
+                       << 8) +
+                      lane * 4;
+  uint32_t *d = dst + (static_cast<size_t>(l) << kLogN) + (k << 8) + lane * 4;
+  for (int b = wave; b < pt_stride; b += kThreads / 64)
+    st4(d + (static_cast<size_t>(b) * dst_limbs << kLogN),
+        ld4_once(s + (static_cast<size_t>(b) << 8)));
 }
 
 // Element-wise arithmetic (ElementWise.cu:33-220 Sum / Sub / Neg / Mult /
@@ -757,28 +819,62 @@ extern "C" int chd_k_gs_fused_wide(const chd_tables *t, const chd_limb_map *m,
   for (int g = 0; g < ng; g++)
     if (!args->dst_b[g] || !args->dst_a[g])
       return set_error(CHD_ERR_ARG, "chd_k_gs_fused_wide: null destination");
+  if (args->pt_tiled != nullptr &&
+      (args->tiled_rows < 0 || args->tiled_rows > ng))
+    return set_error(CHD_ERR_ARG,
+                     "chd_k_gs_fused_wide: tiled_rows outside [0, num_gs]");
   if (num_limbs == 0) return 0;
   static_assert(kThreads == 256, "gs_wide_kernel splits giant steps over 4 waves");
   dim3 g(kN / (64 * kPerThread), num_limbs);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool tiled = args->pt_tiled != nullptr;
+#define CHD_GS_WIDE_LAUNCH(kGw)                                               \
+  if (tiled)                                                                  \
+    hipLaunchKernelGGL((gs_wide_kernel<kGw, true>), g, dim3(kThreads), 0, s,  \
+                       *t, *m, *args);                                        \
+  else                                                                        \
+    hipLaunchKernelGGL((gs_wide_kernel<kGw, false>), g, dim3(kThreads), 0, s, \
+                       *t, *m, *args)
   switch (ng) {
-    case 8:
-      hipLaunchKernelGGL(gs_wide_kernel<2>, g, dim3(kThreads), 0, s, *t, *m, *args);
-      break;
-    case 16:
-      hipLaunchKernelGGL(gs_wide_kernel<4>, g, dim3(kThreads), 0, s, *t, *m, *args);
-      break;
-    case 24:
-      hipLaunchKernelGGL(gs_wide_kernel<6>, g, dim3(kThreads), 0, s, *t, *m, *args);
-      break;
-    case 28:
-      hipLaunchKernelGGL(gs_wide_kernel<7>, g, dim3(kThreads), 0, s, *t, *m, *args);
-      break;
-    default:
-      hipLaunchKernelGGL(gs_wide_kernel<8>, g, dim3(kThreads), 0, s, *t, *m, *args);
-      break;
+    case 8: CHD_GS_WIDE_LAUNCH(2); break;
+    case 16: CHD_GS_WIDE_LAUNCH(4); break;
+    case 24: CHD_GS_WIDE_LAUNCH(6); break;
+    case 28: CHD_GS_WIDE_LAUNCH(7); break;
+    default: CHD_GS_WIDE_LAUNCH(8); break;
   }
+#undef CHD_GS_WIDE_LAUNCH
   return check_launch("chd_k_gs_fused_wide");
+}
+
+extern "C" int chd_k_gs_pack_tiled(const uint32_t *const *pt_table, int rows,
+                                   int pt_stride, int num_limbs, uint32_t *dst,
+                                   void *stream) {
+  if (!pt_table || !dst || rows < 1 || rows > CHD_GS_WIDE_GS ||
+      pt_stride < 1 || pt_stride > CHD_GS_MAX_BS || num_limbs < 0 ||
+      num_limbs > 65535)
+    return set_error(CHD_ERR_ARG, "chd_k_gs_pack_tiled: invalid argument");
+  if (num_limbs == 0) return 0;
+  dim3 g(kN >> 8, num_limbs, rows);
+  hipLaunchKernelGGL(gs_pack_tiled_kernel, g, dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), pt_table, rows,
+                     pt_stride, dst);
+  return check_launch("chd_k_gs_pack_tiled");
+}
+
+extern "C" int chd_k_gs_untile_row(const uint32_t *tiled, int rows,
+                                   int pt_stride, int num_limbs, int g,
+                                   int dst_limbs, uint32_t *dst,
+                                   void *stream) {
+  if (!tiled || !dst || rows < 1 || rows > CHD_GS_WIDE_GS || pt_stride < 1 ||
+      pt_stride > CHD_GS_MAX_BS || num_limbs < 0 || num_limbs > 65535 ||
+      g < 0 || g >= rows || dst_limbs < 0 || dst_limbs > num_limbs)
+    return set_error(CHD_ERR_ARG, "chd_k_gs_untile_row: invalid argument");
+  if (dst_limbs == 0) return 0;
+  dim3 grid(kN >> 8, dst_limbs);
+  hipLaunchKernelGGL(gs_untile_row_kernel, grid, dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), tiled, rows, pt_stride,
+                     g, dst_limbs, dst);
+  return check_launch("chd_k_gs_untile_row");
 }
 
 extern "C" int chd_k_elementwise(const chd_tables *t, const chd_limb_map *m,

@@ -42,6 +42,12 @@ int DivCeil(int a, int b) { return (a + b - 1) / b; }
 #ifndef CHD_SMALL_RESCALE_LIMBS
 #define CHD_SMALL_RESCALE_LIMBS 12
 #endif
+// 1: a hoisting handle with a wide giant-step accumulation keeps a tiled
+// copy of its plaintexts beside the per-pair ones (twice their memory); 0:
+// the accumulation reads the per-pair plaintexts in place
+#ifndef CHD_GS_TILED
+#define CHD_GS_TILED 1
+#endif
 
 chd_limb_map NoSkipMap(const Parameter<uint32_t> &param, const NPInfo &np) {
   chd_limb_map m{};
@@ -2000,6 +2006,25 @@ HoistHandler<uint32_t>::HoistHandler(ConstContextPtr<word> context,
       for (; j < wide_bs_; j++) table.push_back(zero_pt_.as<const word>());
     }
     pt_table_.Upload(table);
+#if CHD_GS_TILED
+    // the real giant steps' plaintexts move into one tiled array, so that
+    // each accumulation workgroup streams one contiguous run (one block of
+    // one limb, every pair) instead of 1 KiB from each pair's allocation;
+    // the per-pair copies are then given back (to the memory pool) and the
+    // table points only at the zero plaintext: the wide accumulation reads
+    // the tiled array, MinKS takes rows back out of it
+    tiled_rows_ = num_gs;
+    pt_tiled_.Resize(static_cast<size_t>(tiled_rows_) * wide_bs_ * pt_words *
+                     sizeof(word));
+    K(chd_k_gs_pack_tiled(pt_table_.as<const word *>(), tiled_rows_,
+                          wide_bs_, np.GetNumTotal(), pt_tiled_.as<word>(),
+                          CurrentStream()));
+    HipCheck(hipStreamSynchronize(CurrentStream()), "hipStreamSynchronize");
+    for (auto &[g, bs_map] : pt_map_)
+      for (auto &[b, pt] : bs_map) pt.mx_ = DeviceVector<word>();
+    std::fill(table.begin(), table.end(), zero_pt_.as<const word>());
+    pt_table_.Upload(table);
+#endif
   }
 }
 
@@ -2161,12 +2186,28 @@ void HoistHandler<uint32_t>::MinKSGiantStep(const Context<word> &ctx, Ct &res,
   Workspace *ws = ctx.GetWorkspace();
   Workspace::Use use_ws(ws);
   Scratch acc(ws, 2 * qw);
+  // plaintexts held only in the tiled array: each giant step's row is
+  // taken back out (its q limbs, one plaintext per baby-step column)
+  Scratch row(ws, tiled_rows_ > 0 ? static_cast<size_t>(wide_bs_) * qw : 0);
   const chd_limb_map m = NoSkipMap(param, np);
   bool first = true;
   int prev = 0;
   for (auto it = pt_map_.rbegin(); it != pt_map_.rend(); ++it) {
     const int g = it->first;
     const std::map<int, Pt> &pmap = it->second;
+    if (tiled_rows_ > 0) {
+      const int gi = static_cast<int>(
+          std::find(gs_indices_.begin(), gs_indices_.end(), g) -
+          gs_indices_.begin());
+      K(chd_k_gs_untile_row(pt_tiled_.as<const word>(), tiled_rows_,
+                            wide_bs_, np.GetNumTotal(), gi, np.GetNumQ(),
+                            row.data(), CurrentStream()));
+    }
+    auto pt_of = [&](int b) -> const word * {
+      if (tiled_rows_ == 0) return pmap.at(b).mx_.data();
+      const auto col = std::distance(bs_indices_.begin(), bs_indices_.find(b));
+      return row.data() + static_cast<size_t>(col) * qw;
+    };
     // accumulation over this giant step's baby steps (q limbs of each
     // plaintext), onto the rotated running sum after the first
     std::vector<int> bsv;
@@ -2182,7 +2223,7 @@ void HoistHandler<uint32_t>::MinKSGiantStep(const Context<word> &ctx, Ct &res,
         const Ct &ct = bs.at(bsv[b0 + j]);
         a.bs_b[j] = ct.bx_.data();
         a.bs_a[j] = ct.ax_.data();
-        a.pt[0][j] = pmap.at(bsv[b0 + j]).mx_.data();
+        a.pt[0][j] = pt_of(bsv[b0 + j]);
       }
       a.dst_b[0] = acc.data();
       a.dst_a[0] = acc.data() + qw;
@@ -2382,6 +2423,8 @@ void HoistHandler<uint32_t>::GiantStep(const Context<word> &ctx, Ct &res,
     a.add_to_dst = 0;
     a.pt_stride = wide_bs_;
     a.pt_table = pt_table_.as<const word *>();
+    a.pt_tiled = tiled_rows_ > 0 ? pt_tiled_.as<const word>() : nullptr;
+    a.tiled_rows = tiled_rows_;
     for (int j = 0; j < wide_bs_; j++) {
       const bool real = j < static_cast<int>(bsv.size());
       a.bs_b[j] = real ? bs.at(bsv[j]).bx_.data() : zero_pt_.as<word>();

@@ -979,6 +979,10 @@ class HoistHandler<uint32_t> {
   // write to dummy_out_ (never read). Built once at construction.
   int wide_gs_ = 0, wide_bs_ = 0;
   DevBuf pt_table_, zero_pt_, dummy_out_;
+  // tiled copy of the first tiled_rows_ giant steps' plaintexts
+  // (chd_k_gs_pack_tiled), read by the wide accumulation; 0 rows: none
+  int tiled_rows_ = 0;
+  DevBuf pt_tiled_;
 };
 
 // Square matrix by its generalised diagonals (include/extension/

@@ -308,16 +308,42 @@ int chd_k_gs_fused(const chd_tables *t, const chd_limb_map *m,
  * each baby step is read once for all of them. num_bs must be a multiple of
  * 4 (pad with zero baby steps). The plaintext addresses are a device array
  * pt_table[g * pt_stride + b]; every entry must be a valid plaintext (point
- * absent pairs at a zero plaintext). Inputs must be canonical residues. */
+ * absent pairs at a zero plaintext). Inputs must be canonical residues.
+ * pt_tiled (optional, NULL for none): the plaintexts of giant steps
+ * g < tiled_rows in the tiled layout chd_k_gs_pack_tiled writes (rows =
+ * tiled_rows); they are read from it instead of through pt_table, and the
+ * giant steps from tiled_rows on (padding) are neither computed nor
+ * written. */
 #define CHD_GS_WIDE_GS 32
 typedef struct chd_gs_wide_args {
   int num_bs, num_gs, add_to_dst, pt_stride;
   const uint32_t *bs_b[CHD_GS_MAX_BS], *bs_a[CHD_GS_MAX_BS];
   const uint32_t *const *pt_table;
   uint32_t *dst_b[CHD_GS_WIDE_GS], *dst_a[CHD_GS_WIDE_GS];
+  const uint32_t *pt_tiled;
+  int tiled_rows;
 } chd_gs_wide_args;
 int chd_k_gs_fused_wide(const chd_tables *t, const chd_limb_map *m,
                         const chd_gs_wide_args *args, int num_limbs,
+                        void *stream);
+
+/* Tiled copy of a giant-step plaintext table for chd_k_gs_fused_wide (no
+ * counterpart in the reference, whose GSFusedKernel reads each plaintext of
+ * its map in place, Hoist.cu:80-118): word c of 256-coefficient block k of
+ * limb l of the plaintext pt_table[g * pt_stride + b] goes to
+ *   dst[((((l * (N / 256) + k) * rows + g) * pt_stride + b) << 8) + c]
+ * for g < rows, b < pt_stride, l < num_limbs, so the plaintexts one
+ * accumulation workgroup reads (one block of one limb, every pair) are one
+ * contiguous run. dst holds rows * pt_stride * num_limbs * N words. */
+int chd_k_gs_pack_tiled(const uint32_t *const *pt_table, int rows,
+                        int pt_stride, int num_limbs, uint32_t *dst,
+                        void *stream);
+/* The inverse for one row g of such a tiled array (rows x pt_stride
+ * plaintexts of num_limbs limbs): the first dst_limbs limbs of plaintext
+ * (g, b) go to dst + b * dst_limbs * N, for b < pt_stride (no counterpart in
+ * the reference; it gives back the per-pair plaintexts of one giant step). */
+int chd_k_gs_untile_row(const uint32_t *tiled, int rows, int pt_stride,
+                        int num_limbs, int g, int dst_limbs, uint32_t *dst,
                         void *stream);
 
 #define CHD_MAX_BS 8

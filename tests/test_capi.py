@@ -94,7 +94,8 @@ class GsWideArgs(ctypes.Structure):
     _fields_ = [("num_bs", ctypes.c_int), ("num_gs", ctypes.c_int),
                 ("add_to_dst", ctypes.c_int), ("pt_stride", ctypes.c_int),
                 ("bs_b", P * 32), ("bs_a", P * 32), ("pt_table", P),
-                ("dst_b", P * 32), ("dst_a", P * 32)]
+                ("dst_b", P * 32), ("dst_a", P * 32), ("pt_tiled", P),
+                ("tiled_rows", ctypes.c_int)]
 
 
 FAKE = P(0x1000)  # never dereferenced: the calls fail their checks first
@@ -164,6 +165,37 @@ def test_gs_fused_wide_checks(chd):
     assert lib.chd_k_gs_fused_wide(t, m, a, 28, None) == -1
     a.num_bs, a.pt_table = 4, None
     assert lib.chd_k_gs_fused_wide(t, m, a, 28, None) == -1
+
+
+def test_gs_tiled_copy_checks(chd):
+    lib = chd.lib
+    lib.chd_k_gs_pack_tiled.argtypes = [P, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, P, P]
+    lib.chd_k_gs_untile_row.argtypes = [P, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, P, P]
+    # rows in [1, 32], stride in [1, 32], pointers given
+    for rows, stride, tab, dst in ((0, 4, FAKE, FAKE), (33, 4, FAKE, FAKE),
+                                   (2, 0, FAKE, FAKE), (2, 33, FAKE, FAKE),
+                                   (2, 4, None, FAKE), (2, 4, FAKE, None)):
+        assert lib.chd_k_gs_pack_tiled(tab, rows, stride, 28, dst, None) == -1
+        assert b"chd_k_gs_pack_tiled" in lib.chd_last_error()
+    # the row inside the array, no more limbs out than it holds
+    for g, dl in ((-1, 4), (2, 4), (0, 29), (0, -1)):
+        assert lib.chd_k_gs_untile_row(FAKE, 2, 4, 28, g, dl, FAKE,
+                                       None) == -1
+        assert b"chd_k_gs_untile_row" in lib.chd_last_error()
+    # a tiled array with more rows than the launch computes is refused
+    a = GsWideArgs(num_bs=4, num_gs=16, pt_stride=4, pt_table=FAKE,
+                   pt_tiled=FAKE, tiled_rows=17)
+    for j in range(4):
+        a.bs_b[j] = a.bs_a[j] = FAKE
+    for g in range(32):
+        a.dst_b[g] = a.dst_a[g] = FAKE
+    k = _kernel_lib(chd)
+    t, m = Tables(), LimbMap(num_q=20)
+    assert k.chd_k_gs_fused_wide(t, m, a, 28, None) == -1
+    assert b"tiled_rows" in chd.lib.chd_last_error()
 
 
 def test_batched_entry_points_reject_bad_counts(chd):

@@ -1,5 +1,7 @@
 """GPU parity: the HIP path through the C-ABI against the CPU oracle,
 bit-exact, on seeded inputs at the BASELINE configurations' real sizes."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -618,6 +620,54 @@ def test_hoist_evaluate_many_giant_steps(chd, ks):
     h.run(out, (dev(b), dev(a)), dkeys)
     assert np.array_equal(host(out[0]), wb)
     assert np.array_equal(host(out[1]), wa)
+    # the handle keeps these plaintexts only in its tiled array: the min_ks
+    # order takes each giant step's row back out of it
+    mb, ma = hoist_ref.evaluate_min_ks(b, a, pts, keys, L, 24, main, aux, 16)
+    assert h.required_rotations(min_ks=True) == [1, 3]
+    out = (zeros(L - 1, N), zeros(L - 1, N))
+    h.run(out, (dev(b), dev(a)), dkeys, min_ks=True)
+    assert np.array_equal(host(out[0]), mb)
+    assert np.array_equal(host(out[1]), ma)
+
+
+def test_gs_tiled_pack_and_untile(chd):
+    """chd_k_gs_pack_tiled puts word c of block k of limb l of plaintext
+    (g, b) at ((((l * 256 + k) * rows + g) * stride + b) << 8) + c (checked
+    word by word on the host), and chd_k_gs_untile_row gives each row's
+    plaintexts back, whole or their first limbs"""
+    import torch
+    lib = chd.lib
+    P = ctypes.c_void_p
+    lib.chd_k_gs_pack_tiled.argtypes = [P, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, P, P]
+    lib.chd_k_gs_untile_row.argtypes = [P, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, P, P]
+    rows, stride, limbs = 3, 4, 5
+    r = rng(540)
+    pts = [[r.integers(0, 1 << 32, (limbs, N), dtype=np.uint64).astype(
+        np.uint32) for _ in range(stride)] for _ in range(rows)]
+    dpts = [[dev(x) for x in row] for row in pts]
+    table = torch.tensor([t.data_ptr() for row in dpts for t in row],
+                         dtype=torch.int64, device="cuda")
+    tiled = torch.empty(rows * stride * limbs * N, dtype=torch.int32,
+                        device="cuda")
+    assert lib.chd_k_gs_pack_tiled(P(table.data_ptr()), rows, stride, limbs,
+                                   P(tiled.data_ptr()), None) == 0
+    got = host(tiled).reshape(limbs, N >> 8, rows, stride, 256)
+    want = np.stack([np.stack(row) for row in pts])  # g, b, l, n
+    want = want.reshape(rows, stride, limbs, N >> 8, 256).transpose(2, 3, 0,
+                                                                  1, 4)
+    assert np.array_equal(got, want)
+    for g in range(rows):
+        for dl in (limbs, 2):
+            out = zeros(stride * dl, N)
+            assert lib.chd_k_gs_untile_row(P(tiled.data_ptr()), rows, stride,
+                                           limbs, g, dl, P(out.data_ptr()),
+                                           None) == 0
+            back = host(out).reshape(stride, dl, N)
+            for b in range(stride):
+                assert np.array_equal(back[b], pts[g][b][:dl]), (g, dl, b)
 
 
 def test_hoist_evaluate_chunked_accumulation(chd, ks):
