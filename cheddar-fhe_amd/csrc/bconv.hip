@@ -35,8 +35,8 @@
 // 4 (l / 16) .. + 3 of coefficient l % 16, and finishes four consecutive
 // coefficients of destination 16 t + l % 16.
 //
-// Grid (N / kCoefPerBlock, 1, jobs), 256 threads; a wave takes kTilesPerWave
-// 16-coefficient tiles. The packed table (4 KiB per 16 destinations and K
+// Grid (N / kCoefPerBlock, destination tiles or 1, jobs), 256 threads; a wave
+// takes kTilesPerWave 16-coefficient tiles. The packed table (4 KiB per 16 destinations and K
 // chunk) is read through the caches by every wave.
 #include <algorithm>
 #include <cstring>
@@ -174,16 +174,8 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
     p = t.q[ti];
     pinv = t.qinv[ti];
   };
-  // this workgroup's destination tile: its primes and planes, requested
-  // with the sources
-  const int tt = blockIdx.y;
-  uint32_t p;
-  int32_t pinv;
-  int pos;
-  prime_of(tt, p, pinv, pos);
-  v4i bp[kChunks][4];
-  load_planes<kChunks>(bp, tab, tt, nk, lane);
-  // A operands (the sources' signed digits)
+  // A operands (the sources' signed digits), shared by every destination
+  // tile this workgroup computes
   v4i a[kChunks][kTilesPerWave];
 #pragma unroll
   for (int ch = 0; ch < kChunks; ch++)
@@ -192,6 +184,16 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
 #pragma unroll
       for (int j = 0; j < 4; j++)
         a[ch][mt][j] = digits(si[ch][j] < jb.src_len ? cw[ch][mt][j] : 0);
+  // the workgroup's destination tiles: blockIdx.y, then every gridDim.y-th
+  // (a single conversion has a workgroup per tile, a batch one workgroup
+  // for all of a job's tiles); each tile's primes and planes
+  for (int tt = blockIdx.y; tt < tiles; tt += gridDim.y) {
+  uint32_t p;
+  int32_t pinv;
+  int pos;
+  prime_of(tt, p, pinv, pos);
+  v4i bp[kChunks][4];
+  load_planes<kChunks>(bp, tab, tt, nk, lane);
   // Recombination of the four planes of one MFMA output (4 coefficients of
   // one destination): pairs of planes in int32 (|acc_c| <= 2^21, so |lo|,
   // |hi| < 2^30), one 64-bit multiply-add y = lo + 2^16 hi (|y| < 2^47, far
@@ -276,6 +278,9 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
     *reinterpret_cast<v4u *>(xt + (r & 7) * kLdsRow + 16 * (r >> 3) +
                              4 * g) = finish(d);
     store_rows(tt * 16, 8);
+  }
+  // the next tile rewrites this wave's LDS tile after its lanes' reads
+  wave_lds_sync_bc();
   }
 }
 
@@ -367,11 +372,17 @@ int launch_bconv(const chd_tables *t, const chd_limb_map *m,
     max_src = std::max(max_src, jobs[j].src_len);
     max_tiles = std::max(max_tiles, (jobs[j].dst_len + 15) / 16);
   }
-  // one destination tile per workgroup (blockIdx.y): the coefficient blocks
-  // of a tile are consecutive block ids, and the tiles of one coefficient
-  // block land on the same XCD (kN / kCoefPerBlock is a multiple of 8), whose
-  // L2 keeps the sources for them
-  dim3 g(kN / kCoefPerBlock, max_tiles, num_jobs);
+  // A single conversion: one destination tile per workgroup (blockIdx.y),
+  // the coefficient blocks of a tile consecutive block ids, so the tiles of
+  // one coefficient block land on the same XCD (kN / kCoefPerBlock is a
+  // multiple of 8), whose L2 keeps the sources for them (config 3, 1,536
+  // workgroups). A batch (key-switch ModUp and ModDown, at least 2 jobs)
+  // already has enough workgroups: each one computes all of its job's tiles
+  // from one load of the sources (the hoisted config-5 batches of 8 to 24
+  // jobs 25.9 -> 23.4 us per launch on average, HMult's 8.7 -> 8.0 us;
+  // walking two or four coefficient blocks per workgroup as well was
+  // slower, 27.0 and 29.3 us).
+  dim3 g(kN / kCoefPerBlock, num_jobs >= 2 ? 1 : max_tiles, num_jobs);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (max_src <= kChunkSrc) {
     if (stream_out)
