@@ -39,7 +39,7 @@ BCONV_BYTES = 48 * 4 * (1 << 16)
 BCONV_INT8_OPS = 2 * 16 * (1 << 16) * 8 * 40
 # its measured HBM bytes per launch (profiles/bconv_config3_traffic.md:
 # FETCH_SIZE 1101.0 KiB x 2 + WRITE_SIZE 10240.0 KiB)
-BCONV_TRAFFIC = 12740608
+BCONV_TRAFFIC = 12741632
 # config 4 HMult compulsory bytes: 4 x 24 input limbs, 3 x 2 x 32 key limbs,
 # 2 x 23 output limbs
 HMULT_BYTES = (96 + 192 + 46) * 4 * (1 << 16)
