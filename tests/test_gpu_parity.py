@@ -598,14 +598,16 @@ def test_hoist_evaluate_config5_level(chd, ks):
         assert np.array_equal(host(out[1]), wa)
 
 
-def test_hoist_evaluate_many_giant_steps(chd, ks):
-    """12 giant steps at L = 20: the wide giant-step accumulation (one launch
-    for every giant step, padded to 16 with zero plaintexts) and the batched
-    giant-step key switches (a batch of 8 and one of 3), with absent pairs"""
+@pytest.mark.parametrize("L", [20, 21])
+def test_hoist_evaluate_many_giant_steps(chd, ks, L):
+    """12 giant steps at L = 20 and 21: the wide giant-step accumulation
+    (every giant step in each launch, padded to 16 rows that are skipped;
+    launches of two limbs, the last of one limb at L = 21's 29 limbs) and
+    the batched giant-step key switches (a batch of 8 and one of 3), with
+    absent pairs"""
     import hoist_ref
     param, ctx, main, aux = ks
-    L = 20
-    r = rng(520)
+    r = rng(520 + L)
     bsi, gsi = [0, 1, 2], [3 * k for k in range(12)]
     pts = {(g, s): uniform_limbs(r, main[:L] + aux) for g in gsi for s in bsi
            if (g, s) not in ((6, 1), (33, 2))}
