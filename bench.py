@@ -116,9 +116,9 @@ def bench_ntt(chd, steps, warmup):
     streams = [torch.cuda.Stream() for _ in range(NTT_STREAMS)]
     sps = [ctypes.c_void_p(x.cuda_stream) for x in streams]
 
-    def step_on(i, p):
+    def step_on(i, p, two_pass=False):
         s, d = srcs[i % nsets], dsts[i % nsets]
-        plan.forward(d, s, 32, 2, stream=p)
+        plan.forward(d, s, 32, 2, stream=p, two_pass=two_pass)
         plan.inverse(s, d, 32, 2, mont_conv=False, stream=p)
 
     # Per-direction timings (reported, and the forward one is the roofline's)
@@ -141,6 +141,10 @@ def bench_ntt(chd, steps, warmup):
                                mont_conv=False, stream=sp,
                                single_pass=True), sub,
         stream) / sub
+    # the forward on the two-pass kernels (chd_ntt_forward_two_pass)
+    fwd2_ms = event_time_ms(
+        lambda i: plan.forward(dsts[i % nsets], srcs[i % nsets], 32, 2,
+                               stream=sp, two_pass=True), sub, stream) / sub
     # warm (MALL-resident) figure on one buffer set
     warm_ms = event_time_ms(lambda i: plan.forward(dsts[0], srcs[0], 32, 2,
                                                    stream=sp), sub,
@@ -164,12 +168,25 @@ def bench_ntt(chd, steps, warmup):
     for ev, x in zip(ends, streams):
         ev.record(x)
     torch.cuda.synchronize()
-    t0 = starts[0]
-    ms = (max(t0.elapsed_time(ev) for ev in ends) -
-          min([0.0] + [t0.elapsed_time(ev) for ev in starts[1:]]))
+
+    def span(starts, ends):
+        t0 = starts[0]
+        return (max(t0.elapsed_time(ev) for ev in ends) -
+                min([0.0] + [t0.elapsed_time(ev) for ev in starts[1:]]))
+    ms = span(starts, ends)
+    # the same loop with the forward on the two-pass kernels, after the
+    # headline (reported beside it, not the headline)
+    for ev, x in zip(starts, streams):
+        ev.record(x)
+    for i in range(steps):
+        step_on(i, sps[i % NTT_STREAMS], two_pass=True)
+    for ev, x in zip(ends, streams):
+        ev.record(x)
+    torch.cuda.synchronize()
+    ms2 = span(starts, ends)
     # the inverse with mont_conv=False returns the input: check it stayed put
     ok = all(torch.equal(srcs[i], base) for i in range(nsets))
-    return ms, fwd_ms, inv_ms, warm_ms, one_ms, ok, inv1_ms
+    return ms, fwd_ms, inv_ms, warm_ms, one_ms, ok, inv1_ms, fwd2_ms, ms2
 
 
 def _config4_context(chd):
@@ -576,8 +593,8 @@ def main():
     hmult_streams_us = bench_hmult_streams(chd)
     bconv_us = bench_bconv(chd) * 1e3
     bconv_cold_us = bench_bconv(chd, cold=True) * 1e3
-    ms, fwd_ms, inv_ms, warm_ms, one_ms, ok, inv1_ms = bench_ntt(
-        chd, args.steps, args.warmup)
+    (ms, fwd_ms, inv_ms, warm_ms, one_ms, ok, inv1_ms, fwd2_ms,
+     ms2) = bench_ntt(chd, args.steps, args.warmup)
     if not ok:
         print("NTT round trip changed the data", file=sys.stderr)
         sys.exit(1)
@@ -649,6 +666,9 @@ def main():
             "ntt_forward_us": fwd_ms * 1e3,
             "ntt_inverse_us": inv_ms * 1e3,
             "ntt_inverse_single_pass_us": inv1_ms * 1e3,
+            "ntt_forward_two_pass_us": fwd2_ms * 1e3,
+            "ntt_step_us_%d_streams_two_pass_forward" % NTT_STREAMS:
+                ms2 / args.steps * 1e3,
             "ntt_forward_warm_mall_us": warm_ms * 1e3,
             "ntt_step_us_one_stream": one_ms * 1e3,
             "hmult_keyswitch_us_config4": hmult_us,
@@ -670,6 +690,12 @@ def main():
                      "run beside another's butterflies; "
                      "ntt_step_us_one_stream is one step at a time on one "
                      "stream (the latency of one batch). "
+                     "ntt_step_us_%d_streams_two_pass_forward: the same "
+                     "loop (after the headline) with the forward on the "
+                     "two-pass kernels (chd_ntt_forward_two_pass), slower "
+                     "alone (ntt_forward_two_pass_us) but sharing the GPU "
+                     "better with the other streams' kernels; the headline "
+                     "keeps the default chd_ntt_forward. "
                      "hmult: warm = same key and inputs each step, cold = "
                      "%d MiB of distinct input/key sets rotated; host "
                      "enqueue included; hmult_then_rescale: HMult without "
@@ -682,7 +708,8 @@ def main():
                      "giant steps, 54 rotation keys) at L=20 on the "
                      "library's encodings of a seeded N(0, 0.02) weight; "
                      "HBM fraction against the %d B of plaintexts and keys "
-                     "one evaluation reads" % (NTT_STREAMS, hmult_set >> 20,
+                     "one evaluation reads" % (NTT_STREAMS, NTT_STREAMS,
+                                               hmult_set >> 20,
                                                NTT_STREAMS, hoist_bytes),
         },
     }

@@ -54,6 +54,8 @@ struct NttArgs {
   // inverse only: run the single pass over residue classes (src_disjoint
   // set, no src_mul, tab.twist present; checked by the caller)
   int inv_one_pass;
+  // forward only: run the two passes even where the single pass would
+  int fwd_two_pass;
   // single-pass ModDown NTT only: every limb of polynomial z reads the one
   // centred source limb src + z * src_pstride, times its cst[l] (a
   // one-source BConv fused into the transform's first round)

@@ -1825,7 +1825,8 @@ hipError_t launch_ntt_fwd(const NttArgs &a, int num_limbs, int num_polys,
   // for 1 limb, 11.3-12.5 for 2-16; from 24 limbs on they are not). The
   // ModDown epilogue keeps the single pass: its caller makes that choice.
   const int items = num_limbs * num_polys;
-  if (a.src_disjoint && (epilogue == kEpiModDown || items > 16)) {
+  if (a.src_disjoint && !a.fwd_two_pass &&
+      (epilogue == kEpiModDown || items > 16)) {
     dim3 g1(4 * ((items + 7) / 8 * 8));
     if (epilogue == kEpiModDown && a.src_bcast)
       hipLaunchKernelGGL(ntt_fwd_1p_bcast, g1, dim3(1024), 0, s, a,
@@ -1927,14 +1928,16 @@ bool src2_disjoint(const uint32_t *src2, long long src2_pstride,
 }
 }  // namespace
 
-extern "C" int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m,
-                             uint32_t *dst, long long dst_pstride,
-                             const uint32_t *src, long long src_pstride,
-                             int num_limbs, int num_polys,
-                             const uint32_t *pre_cst, void *stream) {
+namespace {
+int ntt_fwd_common(const char *name, const chd_tables *t,
+                   const chd_limb_map *m, uint32_t *dst,
+                   long long dst_pstride, const uint32_t *src,
+                   long long src_pstride, int num_limbs, int num_polys,
+                   const uint32_t *pre_cst, void *stream, bool two_pass) {
   if (!t || !m || !dst || !src || num_limbs < 0 || num_polys < 0)
-    return set_error(CHD_ERR_ARG, "chd_k_ntt_fwd: invalid argument");
+    return set_error(CHD_ERR_ARG, std::string(name) + ": invalid argument");
   NttArgs a{};
+  a.fwd_two_pass = two_pass ? 1 : 0;
   a.src = src;
   a.dst = dst;
   a.src_pstride = src_pstride;
@@ -1954,14 +1957,36 @@ extern "C" int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m,
       (src != dst || m->src_gap != 0 ||
        (num_polys > 1 && src_pstride != dst_pstride)))
     return set_error(CHD_ERR_ARG,
-                     "chd_k_ntt_fwd: source and destination overlap without "
-                     "being the same polynomials");
+                     std::string(name) +
+                         ": source and destination overlap without being the "
+                         "same polynomials");
   hipError_t e = launch_ntt_fwd(a, num_limbs, num_polys, pre_cst != nullptr,
                                 kEpiStore, static_cast<hipStream_t>(stream));
   if (e != hipSuccess)
-    return set_error(CHD_ERR_HIP, std::string("chd_k_ntt_fwd: ") +
-                                      hipGetErrorString(e));
+    return set_error(CHD_ERR_HIP,
+                     std::string(name) + ": " + hipGetErrorString(e));
   return 0;
+}
+}  // namespace
+
+extern "C" int chd_k_ntt_fwd(const chd_tables *t, const chd_limb_map *m,
+                             uint32_t *dst, long long dst_pstride,
+                             const uint32_t *src, long long src_pstride,
+                             int num_limbs, int num_polys,
+                             const uint32_t *pre_cst, void *stream) {
+  return ntt_fwd_common("chd_k_ntt_fwd", t, m, dst, dst_pstride, src,
+                        src_pstride, num_limbs, num_polys, pre_cst, stream,
+                        false);
+}
+
+extern "C" int chd_k_ntt_fwd_2p(const chd_tables *t, const chd_limb_map *m,
+                                uint32_t *dst, long long dst_pstride,
+                                const uint32_t *src, long long src_pstride,
+                                int num_limbs, int num_polys,
+                                const uint32_t *pre_cst, void *stream) {
+  return ntt_fwd_common("chd_k_ntt_fwd_2p", t, m, dst, dst_pstride, src,
+                        src_pstride, num_limbs, num_polys, pre_cst, stream,
+                        true);
 }
 
 #ifdef CHD_PHASE_TIMESTAMPS

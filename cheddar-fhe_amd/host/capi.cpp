@@ -95,6 +95,22 @@ extern "C" int chd_ntt_forward(const chd_ntt_plan *plan, uint32_t *dst,
                        stream);
 }
 
+extern "C" int chd_ntt_forward_two_pass(const chd_ntt_plan *plan,
+                                        uint32_t *dst, const uint32_t *src,
+                                        int num_limbs, int num_polys,
+                                        int mont_conv, void *stream) {
+  if (!plan || !dst || !src || num_limbs < 1 ||
+      num_limbs > plan->chain->size() || num_polys < 1)
+    return set_error(CHD_ERR_ARG,
+                     "chd_ntt_forward_two_pass: invalid argument");
+  chd_limb_map m = PlainMap(num_limbs);
+  const long long ps = static_cast<long long>(num_limbs) << 16;
+  return chd_k_ntt_fwd_2p(&plan->chain->tables(), &m, dst, ps, src, ps,
+                          num_limbs, num_polys,
+                          mont_conv ? plan->chain->mont_converter() : nullptr,
+                          stream);
+}
+
 extern "C" int chd_ntt_inverse(const chd_ntt_plan *plan, uint32_t *dst,
                                const uint32_t *src, int num_limbs,
                                int num_polys, int mont_conv, void *stream) {

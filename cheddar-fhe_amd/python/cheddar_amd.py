@@ -44,6 +44,7 @@ _SIGS = {
     "chd_ntt_forward": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "chd_ntt_inverse": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "chd_ntt_inverse_single_pass": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
+    "chd_ntt_forward_two_pass": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp]),
     "chd_bconv_plan_create": (_i, [_pp, _i, _c_u32p, _i, _c_u32p, _i]),
     "chd_bconv_plan_destroy": (None, [_vp]),
     "chd_bconv_plan_constants": (_i, [_vp, _c_u32p, _c_i32p]),
@@ -160,11 +161,13 @@ class NttPlan:
 
 
     def forward(self, dst, src, num_limbs, num_polys=1, mont_conv=False,
-                stream=None):
-        _check(lib.chd_ntt_forward(self.h, ptr(dst), ptr(src), num_limbs,
-                                   num_polys, int(bool(mont_conv)),
-                                   stream if stream is not None else
-                                   current_stream()))
+                stream=None, two_pass=False):
+        """two_pass: always the two-pass kernels (the same results; for
+        throughput over several streams, where they share the GPU better)"""
+        fn = lib.chd_ntt_forward_two_pass if two_pass else lib.chd_ntt_forward
+        _check(fn(self.h, ptr(dst), ptr(src), num_limbs, num_polys,
+                  int(bool(mont_conv)),
+                  stream if stream is not None else current_stream()))
 
     def inverse(self, dst, src, num_limbs, num_polys=1, mont_conv=True,
                 stream=None, single_pass=False):

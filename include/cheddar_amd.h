@@ -59,6 +59,12 @@ int chd_ntt_forward(const chd_ntt_plan *plan, uint32_t *dst,
 int chd_ntt_inverse(const chd_ntt_plan *plan, uint32_t *dst,
                     const uint32_t *src, int num_limbs, int num_polys,
                     int mont_conv, void *stream);
+/* chd_ntt_forward on the two passes (chd_k_ntt_fwd_2p): the same results;
+ * slower for one call at a time, faster in throughput when several streams
+ * keep the GPU busy. No reference counterpart. */
+int chd_ntt_forward_two_pass(const chd_ntt_plan *plan, uint32_t *dst,
+                             const uint32_t *src, int num_limbs,
+                             int num_polys, int mont_conv, void *stream);
 /* chd_ntt_inverse on the single-pass kernel (chd_k_ntt_inv_1p): the same
  * results, one HBM read and write per limb; dst must not overlap src. For
  * comparison with the default two-pass inverse, which is faster at config 2.

@@ -315,11 +315,12 @@ def test_forward_ntt_rejects_partial_overlap(chd):
         (P(base), 20 * n, P(base), 20 * n, 1,
          LimbMap(num_q=16, skip_lo=1 << 30, src_gap=4)),
     ]
-    for dst, dps, src, sps, polys, mm in cases:
-        st = lib.chd_k_ntt_fwd(t, mm, dst, dps, src, sps, 20, polys, None,
-                               None)
-        assert st == -1
-        assert b"overlap" in chd.lib.chd_last_error()
+    lib.chd_k_ntt_fwd_2p.argtypes = lib.chd_k_ntt_fwd.argtypes
+    for fn in (lib.chd_k_ntt_fwd, lib.chd_k_ntt_fwd_2p):
+        for dst, dps, src, sps, polys, mm in cases:
+            st = fn(t, mm, dst, dps, src, sps, 20, polys, None, None)
+            assert st == -1
+            assert b"overlap" in chd.lib.chd_last_error()
 
 
 def test_binding_handles_released_cleanly_at_exit():

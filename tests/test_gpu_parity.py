@@ -67,6 +67,29 @@ def test_ntt_config2_batch(chd):
     assert np.array_equal(host(y2), want_m)
 
 
+def test_ntt_forward_two_pass_config2(chd):
+    """chd_ntt_forward_two_pass (the two-pass kernels at any size) gives the
+    default forward's residues at config 2: out of place, in place, and
+    with the Montgomery conversion on input"""
+    primes = Q30[:32]
+    plan = chd.NttPlan(primes)
+    x = np.stack([uniform_limbs(rng(15 + p), primes) for p in range(2)])
+    src = dev(x)
+    want = np.stack([_orc.ntt_batch(x[p].reshape(-1), 16, primes).reshape(
+        32, N) for p in range(2)])
+    y = zeros(2, 32, N)
+    plan.forward(y, src, 32, 2, two_pass=True)
+    assert np.array_equal(host(y), want)
+    assert np.array_equal(host(src), x)
+    want_m = np.stack([_orc.ntt_batch(x[p].reshape(-1), 16, primes, 1)
+                       .reshape(32, N) for p in range(2)])
+    plan.forward(y, src, 32, 2, mont_conv=True, two_pass=True)
+    assert np.array_equal(host(y), want_m)
+    y2 = dev(x)
+    plan.forward(y2, y2, 32, 2, two_pass=True)
+    assert np.array_equal(host(y2), want)
+
+
 @pytest.mark.parametrize("bits", [30, 31])
 def test_ntt_inverse_single_pass(chd, bits):
     """the single-pass inverse over residue classes (chd_ntt_inverse_single_
