@@ -122,19 +122,22 @@ class Keys:
         v = self._add(b, self._mul(a, self.s_ntt[:L], primes), primes)
         return from_ntt_mont(v, primes, self.log_n)
 
-    def switch_key(self, s_new, max_q, s_enc=None, rng=None):
+    def switch_key(self, s_new, max_q, s_enc=None, rng=None, s_new_ntt=None):
         """evk for target secret s_new (coefficients) encrypted under s_enc
         (default s), beta groups of (max_q + alpha) limbs;
         bx_g = -a_g s_enc + e_g + P s_new on group g (UserInterface.cu:366).
         Vectorised over all limbs of a group (one modulus per row); rng
-        (default: the secret's generator) draws a and the errors."""
+        (default: the secret's generator) draws a and the errors.
+        s_new_ntt: s_new already in NTT-Montgomery form over those primes
+        (then s_new is not read)."""
         alpha = len(self.p)
         primes = self.q[:max_q] + self.p
         beta = (max_q + alpha - 1) // alpha
         total = len(primes)
         own = np.concatenate([self.s_ntt[:max_q], self.s_ntt[len(self.q):]])
         s_cur = own if s_enc is None else self.ntt_of(s_enc, primes)
-        t = own if s_new is self.s else self.ntt_of(s_new, primes)
+        t = (s_new_ntt if s_new_ntt is not None else
+             own if s_new is self.s else self.ntt_of(s_new, primes))
         pc = np.array(primes, np.uint64)[:, None]
         r_inv = np.array([pow(R, -1, p) for p in primes], np.uint64)[:, None]
         P = 1
@@ -164,6 +167,16 @@ class Keys:
     def mult_key(self, max_q):
         s2 = negacyclic_mul(self.s, self.s)
         return self.switch_key(s2, max_q)
+
+    def mult_key_ntt(self, max_q, rng=None):
+        """the same key with s^2 formed pointwise in the NTT domain
+        (MontMul of s's NTT-Montgomery limbs with themselves is the NTT of
+        the negacyclic square): no O(N^2) product, for N = 2^16"""
+        own = np.concatenate([self.s_ntt[:max_q], self.s_ntt[len(self.q):]])
+        primes = self.q[:max_q] + self.p
+        s2 = np.stack([mont_mul_vec(own[i], own[i], p)
+                       for i, p in enumerate(primes)])
+        return self.switch_key(None, max_q, rng=rng, s_new_ntt=s2)
 
     def rot_key(self, galois, max_q, rng=None):
         """HRot key-switches first and permutes after (Context.cpp:776-791),
