@@ -9,6 +9,8 @@ within the reference's 1e-3 (Testbed.h:93). The residues of the same
 operations are pinned bit-exactly against the oracle elsewhere
 (test_gpu_parity.py); these tests check what the reference's own tests
 check: that the results decrypt to the right messages."""
+import os
+
 import numpy as np
 import pytest
 
@@ -98,4 +100,90 @@ def test_hrot_1234_decrypts(sem, level):
     res = (zeros(level + 1, N), zeros(level + 1, N))
     sem["ctx"].hrot(level, res, c, *sem["rk"], 1234)
     got = _decrypt(sem, res, level, DELTA)
+    assert np.max(np.abs(got - np.roll(m, -1234))) < 1e-3
+
+
+# --------------------------------------------------------------------------
+# the reference's parameter files, as BasicTest is instantiated
+# (BasicTest.cpp:421-429): terminal primes, 20-bit primes, two-prime rescales
+# --------------------------------------------------------------------------
+PARAMS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                      "params")
+
+
+@pytest.fixture(scope="module", params=["bootparam_30.json",
+                                        "bootparam_35.json",
+                                        "bootparam_40.json"])
+def tsem(request):
+    import json
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("no HIP device visible")
+    import cheddar_amd
+    import ckks_host as ck
+    from ks_ref import Chain
+    _orc.lib.orc_set_threads(16)
+    text = open(os.path.join(PARAMS, request.param)).read()
+    d = json.loads(text)
+    ctx = cheddar_amd.Context(cheddar_amd.Param.from_json(text))
+    chain = Chain(d["main_primes"], d["terminal_primes"],
+                  d["auxiliary_primes"], d["level_config"], 16)
+    keys = ck.Keys(16, chain.chain, chain.aux, seed=0x7E5)
+    dk = lambda k: ([dev(t) for t in k[0]], [dev(t) for t in k[1]])
+    mk = dk(keys.mult_key_ntt(chain.max_q, rng=np.random.default_rng(1)))
+    g = _orc.lib.orc_galois_factor(1234, 16)
+    rk = dk(keys.rot_key(g, chain.max_q, rng=np.random.default_rng(2)))
+    print("parameter set", request.param, flush=True)
+    return dict(ctx=ctx, chain=chain, keys=keys, mk=mk, rk=rk,
+                level=d["default_encryption_level"],
+                scale=2.0 ** d["log_default_scale"])
+
+
+def _t_s(t, level):
+    off = t["chain"].offset(level)
+    return t["keys"].s_ntt[off: off + len(t["chain"].q(level))]
+
+
+def _t_encrypt(t, msg, level):
+    keys, q = t["keys"], t["chain"].q(level)
+    pt = zeros(len(q), N)
+    t["ctx"].encode(level, 0, t["scale"], msg, pt)
+    a = keys.uniform(q)
+    b = keys._add(keys._add(keys._neg(keys._mul(a, _t_s(t, level), q), q),
+                            host(pt), q), keys.ntt_of(keys.small(), q), q)
+    return dev(b), dev(a)
+
+
+def _t_decrypt(t, ct, level, scale):
+    keys, q = t["keys"], t["chain"].q(level)
+    v = keys._add(host(ct[0]), keys._mul(host(ct[1]), _t_s(t, level), q), q)
+    return t["ctx"].decode(level, scale, SLOTS, dev(v))
+
+
+def test_param_files_hmult_decrypts(tsem):
+    """HMult with the merged rescale at the default encryption level: the
+    result's scale is scale^2 times the primes the rescale restores over
+    the ones it drops"""
+    import math
+    chain, lv = tsem["chain"], tsem["level"]
+    m1, m2 = _msg(11), _msg(12)
+    c1, c2 = _t_encrypt(tsem, m1, lv), _t_encrypt(tsem, m2, lv)
+    nq = len(chain.q(lv - 1))
+    res = (zeros(nq, N), zeros(nq, N))
+    tsem["ctx"].hmult(lv, res, c1, c2, *tsem["mk"], rescale=True)
+    up, lo = chain.q(lv), chain.q(lv - 1)
+    num = math.prod(p for p in lo if p not in up)
+    den = math.prod(p for p in up if p not in lo)
+    got = _t_decrypt(tsem, res, lv - 1, tsem["scale"] ** 2 * num / den)
+    assert np.max(np.abs(got - m1 * m2)) < 1e-3
+
+
+def test_param_files_hrot_1234_decrypts(tsem):
+    lv = tsem["level"]
+    m = _msg(13)
+    c = _t_encrypt(tsem, m, lv)
+    nq = len(tsem["chain"].q(lv))
+    res = (zeros(nq, N), zeros(nq, N))
+    tsem["ctx"].hrot(lv, res, c, *tsem["rk"], 1234)
+    got = _t_decrypt(tsem, res, lv, tsem["scale"])
     assert np.max(np.abs(got - np.roll(m, -1234))) < 1e-3
