@@ -1,6 +1,8 @@
 """End-to-end semantic tests on the GPU in the shape of the reference's
 unittest/BasicTest.cpp (HMult merged and non-merged with a separate
-Rescale, :327-374; HRot with r = 1234, :376-399): messages encoded by the
+Rescale, :327-374; HRot with r = 1234, :376-399; the encode / encrypt
+round trips, the element-wise ciphertext ops and HConj, :10-325 and
+:401-419): messages encoded by the
 library, encrypted on the host under a known ternary secret (the
 structure of UserInterface.cu:366-458), key-switched on the GPU at the full
 N = 2^16 config-4 chain (24 main primes, 8 aux primes, dnum 3), decrypted
@@ -37,8 +39,10 @@ def sem():
     mk = keys.mult_key_ntt(24, rng=np.random.default_rng(0x5E3B))
     g = _orc.lib.orc_galois_factor(1234, 16)
     rk = keys.rot_key(g, 24, rng=np.random.default_rng(0x5E3C))
+    ck_ = keys.rot_key(2 * N - 1, 24, rng=np.random.default_rng(0x5E3D))
     dk = lambda k: ([dev(t) for t in k[0]], [dev(t) for t in k[1]])
-    return dict(ctx=ctx, keys=keys, main=main, mk=dk(mk), rk=dk(rk))
+    return dict(ctx=ctx, keys=keys, main=main, mk=dk(mk), rk=dk(rk),
+                ck=dk(ck_))
 
 
 def _encrypt(s, msg, level, scale):
@@ -101,6 +105,127 @@ def test_hrot_1234_decrypts(sem, level):
     sem["ctx"].hrot(level, res, c, *sem["rk"], 1234)
     got = _decrypt(sem, res, level, DELTA)
     assert np.max(np.abs(got - np.roll(m, -1234))) < 1e-3
+
+
+# --------------------------------------------------------------------------
+# the rest of BasicTest at config 4 (BasicTest.cpp:10-325, 401-419): encode /
+# encrypt round trips, the ciphertext-ciphertext, -plaintext and -constant
+# ops through chd_elementwise composed as Context::Add / Sub / Neg / Mult /
+# MultImaginaryUnit compose them (Context.cpp; b op operand, a copied for a
+# plaintext or constant operand), and HConj = MultKey with the conjugation
+# key, then PermuteConjugate (Context.cpp:794-798). Two levels: the top one
+# and one whose modulus (4 primes) still holds a product at scale 2^60.
+# --------------------------------------------------------------------------
+BASIC_LEVELS = [L - 1, 3]
+
+
+def _ct(level):
+    return (zeros(level + 1, N), zeros(level + 1, N))
+
+
+def _pt(s, msg, level, scale=DELTA):
+    pt = zeros(level + 1, N)
+    s["ctx"].encode(level, 0, scale, msg, pt)
+    return pt
+
+
+def _const(s, value, level, scale=DELTA):
+    cx = zeros(level + 1)
+    s["ctx"].encode_constant(level, 0, scale, value, cx)
+    return cx
+
+
+@pytest.mark.parametrize("level", BASIC_LEVELS)
+def test_encode_decode_and_encrypt_decrypt(sem, level):
+    m = _msg(20)
+    got = sem["ctx"].decode(level, DELTA, SLOTS, _pt(sem, m, level))
+    assert np.max(np.abs(got - m)) < 1e-3
+    got = _decrypt(sem, _encrypt(sem, m, level, DELTA), level, DELTA)
+    assert np.max(np.abs(got - m)) < 1e-3
+
+
+@pytest.mark.parametrize("level", BASIC_LEVELS)
+@pytest.mark.parametrize("op", ["add", "sub"])
+def test_ct_ct_add_sub_decrypts(sem, level, op):
+    m1, m2 = _msg(21), _msg(22)
+    c1, c2 = _encrypt(sem, m1, level, DELTA), _encrypt(sem, m2, level, DELTA)
+    res = _ct(level)
+    sem["ctx"].elementwise(level, 0, op, list(res), list(c1), list(c2))
+    want = m1 + m2 if op == "add" else m1 - m2
+    assert np.max(np.abs(_decrypt(sem, res, level, DELTA) - want)) < 1e-3
+
+
+@pytest.mark.parametrize("level", BASIC_LEVELS)
+@pytest.mark.parametrize("op", ["add", "sub"])
+def test_ct_pt_add_sub_decrypts(sem, level, op):
+    m1, m2 = _msg(23), _msg(24)
+    c1 = _encrypt(sem, m1, level, DELTA)
+    res = _ct(level)
+    sem["ctx"].elementwise(level, 0, op, [res[0]], [c1[0]],
+                           [_pt(sem, m2, level)])
+    sem["ctx"].elementwise(level, 0, "copy", [res[1]], [c1[1]])
+    want = m1 + m2 if op == "add" else m1 - m2
+    assert np.max(np.abs(_decrypt(sem, res, level, DELTA) - want)) < 1e-3
+
+
+@pytest.mark.parametrize("level", BASIC_LEVELS)
+@pytest.mark.parametrize("op", ["add_const", "sub_const"])
+def test_ct_const_add_sub_decrypts(sem, level, op):
+    m1 = _msg(25)
+    value = _msg(26)[0].real
+    c1 = _encrypt(sem, m1, level, DELTA)
+    res = _ct(level)
+    sem["ctx"].elementwise(level, 0, op, [res[0]], [c1[0]],
+                           cst=_const(sem, value, level))
+    sem["ctx"].elementwise(level, 0, "copy", [res[1]], [c1[1]])
+    want = m1 + value if op == "add_const" else m1 - value
+    assert np.max(np.abs(_decrypt(sem, res, level, DELTA) - want)) < 1e-3
+
+
+@pytest.mark.parametrize("level", BASIC_LEVELS)
+def test_neg_ct_decrypts(sem, level):
+    m1 = _msg(27)
+    c1 = _encrypt(sem, m1, level, DELTA)
+    res = _ct(level)
+    sem["ctx"].elementwise(level, 0, "neg", list(res), list(c1))
+    assert np.max(np.abs(_decrypt(sem, res, level, DELTA) + m1)) < 1e-3
+
+
+@pytest.mark.parametrize("level", BASIC_LEVELS)
+def test_ct_mult_pt_and_const_decrypt(sem, level):
+    """without rescaling: the products decrypt at scale^2"""
+    m1, m2 = _msg(28), _msg(29)
+    value = _msg(30)[0].real
+    c1 = _encrypt(sem, m1, level, DELTA)
+    res = _ct(level)
+    sem["ctx"].elementwise(level, 0, "pmult", list(res), list(c1),
+                           [_pt(sem, m2, level)])
+    got = _decrypt(sem, res, level, DELTA * DELTA)
+    assert np.max(np.abs(got - m1 * m2)) < 1e-3
+    sem["ctx"].elementwise(level, 0, "mult_const", list(res), list(c1),
+                           cst=_const(sem, value, level))
+    got = _decrypt(sem, res, level, DELTA * DELTA)
+    assert np.max(np.abs(got - m1 * value)) < 1e-3
+
+
+@pytest.mark.parametrize("level", BASIC_LEVELS)
+def test_ct_mult_imaginary_unit_decrypts(sem, level):
+    m1 = _msg(31)
+    c1 = _encrypt(sem, m1, level, DELTA)
+    res = _ct(level)
+    sem["ctx"].elementwise(level, 0, "mult_i", list(res), list(c1))
+    assert np.max(np.abs(_decrypt(sem, res, level, DELTA) - 1j * m1)) < 1e-3
+
+
+@pytest.mark.parametrize("level", BASIC_LEVELS)
+def test_hconj_decrypts(sem, level):
+    m1 = _msg(32)
+    c1 = _encrypt(sem, m1, level, DELTA)
+    tmp, res = _ct(level), _ct(level)
+    sem["ctx"].mult_key(level, tmp, c1, *sem["ck"])
+    sem["ctx"].permute(level, res, tmp, -1)
+    got = _decrypt(sem, res, level, DELTA)
+    assert np.max(np.abs(got - np.conj(m1))) < 1e-3
 
 
 # --------------------------------------------------------------------------
