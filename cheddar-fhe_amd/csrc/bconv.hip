@@ -63,6 +63,7 @@ static_assert(kTilesPerWave == 2,
               "a packed last tile carries exactly the wave's two coefficient "
               "tiles, and a wave's 32 coefficients are one 128-byte line");
 constexpr int kLdsRow = 36;  // words per LDS row: 32 coefficients + pad
+constexpr int kFewJobs = 4;   // a batch of at most this many jobs: kFew
 
 // orders a wave's LDS writes before its reads of other lanes' words (a
 // wave's LDS instructions execute in order; only the compiler must not move
@@ -118,7 +119,7 @@ __device__ __forceinline__ void load_planes(v4i (&bp)[kChunks][4],
   }
 }
 
-template <int kChunks, bool kStream>
+template <int kChunks, bool kStream, bool kFew>
 __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
                                                        chd_limb_map m,
                                                        BconvBatch b) {
@@ -129,7 +130,15 @@ __global__ __launch_bounds__(kThreads) void bconv_mfma(chd_tables t,
   const int r = lane & 15;
   const int g = lane >> 4;
   const int wave = threadIdx.x >> 6;
-  const int n_wave = blockIdx.x * kCoefPerBlock + wave * kTilesPerWave * 16;
+  // a wave's 32 coefficients: 128 consecutive ones per workgroup, or with
+  // kFew (a batch of a few jobs, one generation of workgroups) four rows of
+  // one 32-coefficient column tile, so that the workgroup runs on the XCD
+  // (block id mod 8) of the column-pass workgroups that write its sources
+  // and read its output
+  const int n_wave =
+      kFew ? (((static_cast<int>(blockIdx.x) >> 3) * 4 + wave) << 8) +
+                 (static_cast<int>(blockIdx.x) & 7) * (kTilesPerWave * 16)
+           : blockIdx.x * kCoefPerBlock + wave * kTilesPerWave * 16;
   const int32_t *__restrict__ src = jb.src;
   const v4i *__restrict__ tab = static_cast<const v4i *>(jb.table);
   // this job's K chunks (its table holds exactly that many per tile)
@@ -382,18 +391,31 @@ int launch_bconv(const chd_tables *t, const chd_limb_map *m,
   // jobs 25.9 -> 23.4 us per launch on average, HMult's 8.7 -> 8.0 us;
   // walking two or four coefficient blocks per workgroup as well was
   // slower, 27.0 and 29.3 us).
+  //
+  // A batch of at most kFewJobs jobs (one key switch's ModUp or ModDown)
+  // maps its workgroups onto the column tiles of the NTT passes around it
+  // (kFew): about 1 us less per HMult with merged rescale at L = 4, 20 and
+  // 24 (53.4-53.6 against 54.4-54.5, 87.6-88.3 against 88.6-89.8,
+  // 90.2-90.3 against 91.0-91.3 us; three A/B pairs in one call); the
+  // larger hoisting batches measured 0.6 % slower with that mapping and
+  // keep the consecutive one.
   dim3 g(kN / kCoefPerBlock, num_jobs >= 2 ? 1 : max_tiles, num_jobs);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool few = num_jobs >= 2 && num_jobs <= kFewJobs;
   if (max_src <= kChunkSrc) {
     if (stream_out)
-      hipLaunchKernelGGL((bconv_mfma<1, true>), g, dim3(kThreads), 0, s, *t, *m, b);
+      hipLaunchKernelGGL((bconv_mfma<1, true, false>), g, dim3(kThreads), 0, s, *t, *m, b);
+    else if (few)
+      hipLaunchKernelGGL((bconv_mfma<1, false, true>), g, dim3(kThreads), 0, s, *t, *m, b);
     else
-      hipLaunchKernelGGL((bconv_mfma<1, false>), g, dim3(kThreads), 0, s, *t, *m, b);
+      hipLaunchKernelGGL((bconv_mfma<1, false, false>), g, dim3(kThreads), 0, s, *t, *m, b);
   } else {
     if (stream_out)
-      hipLaunchKernelGGL((bconv_mfma<2, true>), g, dim3(kThreads), 0, s, *t, *m, b);
+      hipLaunchKernelGGL((bconv_mfma<2, true, false>), g, dim3(kThreads), 0, s, *t, *m, b);
+    else if (few)
+      hipLaunchKernelGGL((bconv_mfma<2, false, true>), g, dim3(kThreads), 0, s, *t, *m, b);
     else
-      hipLaunchKernelGGL((bconv_mfma<2, false>), g, dim3(kThreads), 0, s, *t, *m, b);
+      hipLaunchKernelGGL((bconv_mfma<2, false, false>), g, dim3(kThreads), 0, s, *t, *m, b);
   }
   return check_launch("chd_k_bconv_batch");
 }
