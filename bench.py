@@ -77,7 +77,7 @@ def parse():
                                        "ntt_step",
                                        "hmult",
                                        "hmult_cold", "hmult_separate",
-                                       "hmult_levels",
+                                       "hmult_levels", "hrot",
                                        "bconv", "bconv_cold",
                                        "copy", "hoist"],
                     help="run only this workload's timed loop (for "
@@ -235,6 +235,34 @@ def bench_hmult(chd, iters=20, cold=False, separate=False):
         run(i)
     torch.cuda.synchronize()
     return event_time_ms(run, iters, stream) / iters, nsets * set_bytes
+
+
+def bench_hrot(chd, iters=20):
+    """config 4: HRot by 1234 slots at L = 24 (MultKey, whose key
+    accumulation adds P times bx, then Permute), the same input and key
+    every step"""
+    import numpy as np
+    import torch
+    main, aux, ctx = _config4_context(chd)
+    rng = np.random.default_rng(0xC0FFEE06)
+
+    def limbs(primes):
+        a = np.stack([rng.integers(0, p, N, dtype=np.uint64) for p in primes])
+        return torch.from_numpy(a.astype(np.uint32).view(np.int32)).cuda()
+    a = (limbs(main), limbs(main))
+    kb = [limbs(main + aux) for _ in range(3)]
+    ka = [limbs(main + aux) for _ in range(3)]
+    res = (torch.empty(24, N, dtype=torch.int32, device="cuda"),
+           torch.empty(24, N, dtype=torch.int32, device="cuda"))
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def run(i):
+        ctx.hrot(23, res, a, kb, ka, 1234, stream=sp)
+    for i in range(3):
+        run(i)
+    torch.cuda.synchronize()
+    return event_time_ms(run, iters, stream) / iters
 
 
 def bench_hmult_levels(chd, levels=(4, 8, 12, 16, 20, 24), iters=50):
@@ -508,6 +536,8 @@ def run_only(chd, what, steps):
         return bench_hmult(chd, steps, separate=True)[0] * 1e3
     if what == "hmult_levels":
         return bench_hmult_levels(chd, iters=steps)
+    if what == "hrot":
+        return bench_hrot(chd, steps) * 1e3
     if what == "bconv":
         return bench_bconv(chd, steps) * 1e3
     if what == "bconv_cold":
@@ -591,6 +621,7 @@ def main():
     hmult_cold_us *= 1e3
     hmult_sep_us = bench_hmult(chd, separate=True)[0] * 1e3
     hmult_streams_us = bench_hmult_streams(chd)
+    hrot_us = bench_hrot(chd) * 1e3
     bconv_us = bench_bconv(chd) * 1e3
     bconv_cold_us = bench_bconv(chd, cold=True) * 1e3
     (ms, fwd_ms, inv_ms, warm_ms, one_ms, ok, inv1_ms, fwd2_ms,
@@ -674,6 +705,7 @@ def main():
             "hmult_keyswitch_us_config4": hmult_us,
             "hmult_keyswitch_us_config4_cold": hmult_cold_us,
             "hmult_then_rescale_us_config4": hmult_sep_us,
+            "hrot_1234_us_config4": hrot_us,
             "hmult_us_per_op_config4_%d_streams" % NTT_STREAMS:
                 hmult_streams_us,
             "bconv_us_config3_warm": bconv_us,
@@ -700,6 +732,8 @@ def main():
                      "%d MiB of distinct input/key sets rotated; host "
                      "enqueue included; hmult_then_rescale: HMult without "
                      "rescale, then a separate Rescale (warm); "
+                     "hrot_1234_us_config4: HRot by 1234 slots at L=24 "
+                     "(warm); "
                      "hmult_us_per_op_config4_%d_streams: "
                      "independent HMults alternating over that many "
                      "streams, one Context each, time per HMult over the "

@@ -1044,15 +1044,26 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
     if (nprod + 1 > 4) fold();
     nprod += 1;
     const uint64_t pp = a.p_prod[l];
+    // every load of both polynomials is issued before the first product
+    // (a guarded load inside the product loop waited for each in turn)
+    const bool with_a = a.ca != nullptr;
+    uint4 tb[4], ta[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) tb[v] = ld_at<uint4>(a.cb + loff, obase + 256u * v);
+    if (with_a) {
+#pragma unroll
+      for (int v = 0; v < 4; v++) ta[v] = ld_at<uint4>(a.ca + loff, obase + 256u * v);
+    }
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-      uint4 tb = ld_at<uint4>(a.cb + loff, obase + 256u * v);
-      const uint32_t cbv[4] = {tb.x, tb.y, tb.z, tb.w};
+      const uint32_t cbv[4] = {tb[v].x, tb[v].y, tb[v].z, tb[v].w};
 #pragma unroll
       for (int j = 0; j < 4; j++) sb[4 * v + j] += pp * cbv[j];
-      if (a.ca != nullptr) {
-        uint4 ta = ld_at<uint4>(a.ca + loff, obase + 256u * v);
-        const uint32_t cav[4] = {ta.x, ta.y, ta.z, ta.w};
+    }
+    if (with_a) {
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const uint32_t cav[4] = {ta[v].x, ta[v].y, ta[v].z, ta[v].w};
 #pragma unroll
         for (int j = 0; j < 4; j++) sa[4 * v + j] += pp * cav[j];
       }
