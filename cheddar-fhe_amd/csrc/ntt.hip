@@ -1462,13 +1462,25 @@ __device__ __forceinline__ void fwd_1p_body(const NttArgs &a, const Limb &lb,
     }
   }
   const uint32_t vl = static_cast<uint32_t>(lane) << 4;
+  // the epilogue's src2 words of all four store rounds, requested together
+  // (one guarded load per round waited for each in turn)
+  [[maybe_unused]] u32x4 s2v[4];
+  if constexpr (kEpi == kEpiModDown) {
+#pragma unroll
+    for (int v = 0; v < 4; v++) s2v[v] = u32x4{0, 0, 0, 0};
+    if (has_s2) {
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+        s2v[v] = bld4<2>(rs2, vl,
+                         4u * static_cast<uint32_t>((wave << 10) | (v << 8)));
+    }
+  }
 #pragma unroll
   for (int v = 0; v < 4; v++) {
     const int n = (wave << 10) | (v << 8) | (lane << 2);
     const uint32_t sn = 4u * static_cast<uint32_t>((wave << 10) | (v << 8));
-    u32x4 s2 = {0, 0, 0, 0};
-    if constexpr (kEpi == kEpiModDown)
-      if (has_s2) s2 = bld4<2>(rs2, vl, sn);
+    [[maybe_unused]] u32x4 s2 = {0, 0, 0, 0};
+    if constexpr (kEpi == kEpiModDown) s2 = s2v[v];
     const u32x4 u = *reinterpret_cast<const u32x4 *>(&lds[qidx(n)]);
     T y[4];
 #pragma unroll
