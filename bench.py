@@ -45,8 +45,8 @@ BCONV_TRAFFIC = 12741632
 HMULT_BYTES = (96 + 192 + 46) * 4 * (1 << 16)
 # its measured HBM bytes per HMult, the sum over its 8 launches
 # (profiles/hmult_config4_traffic.md, one row per launch)
-HMULT_TRAFFIC = (25288704 + 12907584 + 25409536 + 38171456 + 128234432 +
-                 9695808 + 16889856 + 48668672)
+HMULT_TRAFFIC = (25288704 + 12904384 + 25421824 + 38169344 + 128323392 +
+                 9696448 + 16902144 + 48662528)
 N = 1 << 16
 LIMB_BYTES = 4 * N
 # one limb-transform moves one limb in and one limb out (algorithmic bytes)

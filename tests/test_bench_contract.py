@@ -42,7 +42,7 @@ def _table_row(name, kernel):
 
 def test_bconv_traffic_matches_profile():
     fetch, write, total = _table_row("bconv_config3_traffic.md",
-                                     "bconv_mfma<1, true>")
+                                     "bconv_mfma<1, true, false>")
     assert bench.BCONV_TRAFFIC == total
     assert abs(total - (fetch * 2 + write) * 1024) < 1024
 
