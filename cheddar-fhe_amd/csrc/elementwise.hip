@@ -833,8 +833,8 @@ extern "C" int chd_k_gs_fused_wide(const chd_tables *t, const chd_limb_map *m,
   // that are still streaming plaintexts (config 5: 14 launches take 1,253
   // us of kernel time against 1,281-1,289 us for one, the evaluation 3.07
   // against 3.13 ms; one limb per launch, 28 launches, 3.33 ms; three and
-  // four limbs per launch 3.09-3.10 and 3.08-3.09 ms against 3.08-3.09 ms
-  // for two, four A/B rounds in one call). A limb
+  // four limbs per launch 3,090-3,100 and 3,083-3,091 us against
+  // 3,079-3,086 us for two, four A/B rounds in one call). A limb
   // range [a0, a0 + n) is the caller's map (skip_len 0, checked above) with
   // the launch's limbs shifted by a0 through its skip fields.
   constexpr int kGsWideLimbs = 2;
