@@ -64,6 +64,10 @@ static_assert(kTilesPerWave == 2,
               "tiles, and a wave's 32 coefficients are one 128-byte line");
 constexpr int kLdsRow = 36;  // words per LDS row: 32 coefficients + pad
 constexpr int kFewJobs = 4;   // a batch of at most this many jobs: kFew
+static_assert(kN == 256 * 256 && kCoefPerBlock == 4 * kTilesPerWave * 16 &&
+                  kTilesPerWave * 16 == 32,
+              "kFew maps the N / kCoefPerBlock workgroups onto 8 column tiles "
+              "of 32 coefficients x 64 groups of four 256-coefficient rows");
 
 // orders a wave's LDS writes before its reads of other lanes' words (a
 // wave's LDS instructions execute in order; only the compiler must not move
