@@ -902,6 +902,12 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
     sb[k] = sa[k] = 0;
     accb[k] = acca[k] = 0;
   }
+  // the ModDown INTT row pass's twiddles of an aux limb, requested before
+  // the group loop so that the last phase does not wait for them
+  const bool intt_here = a.intt_b != nullptr && l >= a.intt_lo;
+  uint32_t iw1[15], iw2[15];
+  if (intt_here)
+    inv_row_twiddles(tab.itw + (static_cast<size_t>(ti) << kLogN), iw1, iw2);
   int nprod = 0;        // products in sb / sa (uniform)
   bool folded = false;  // accb / acca hold earlier products
   auto fold = [&]() {
@@ -1081,12 +1087,12 @@ __device__ __forceinline__ void keyacc_body(const chd_keyacc_args &a,
     }
   }
   (void)qs;
-  if (a.intt_b != nullptr && l >= a.intt_lo) {
+  if (intt_here) {
     // first pass of ModDown's INTT (INTTForModDown, NTT.cu:973-1128) on
     // this limb of both accumulators, straight from the registers; the
     // accumulator itself is not stored
-    uint32_t w1[15], w2[15];
-    inv_row_twiddles(tab.itw + (static_cast<size_t>(ti) << kLogN), w1, w2);
+    const uint32_t (&w1)[15] = iw1;
+    const uint32_t (&w2)[15] = iw2;
     const size_t ioff = static_cast<size_t>(l - a.intt_lo) << kLogN;
     // back to columns 16c + k, the row pass's input ownership (the group
     // row passes' LDS accesses were this wave's own)
