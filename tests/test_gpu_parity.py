@@ -284,6 +284,86 @@ def test_bconv_tile_shapes(chd, src_len, dst_len):
     assert np.array_equal(host(out), _orc.bconv(x, o2, dst_p, 16))
 
 
+class _Tables(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("q", "qinv", "tw", "itw",
+                                               "twist")]
+
+
+class _LimbMap(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("num_q", "skip_lo", "skip_len",
+                                            "src_gap", "tab_off", "tab_gap",
+                                            "cst_gap")]
+
+
+class _BconvJob(ctypes.Structure):
+    _fields_ = [("dst", ctypes.c_void_p), ("src", ctypes.c_void_p),
+                ("table", ctypes.c_void_p), ("src_len", ctypes.c_int),
+                ("dst_len", ctypes.c_int), ("skip_lo", ctypes.c_int),
+                ("skip_len", ctypes.c_int)]
+
+
+# (src_len, dst_len, skip_lo, skip_len) per job: one to three destination
+# tiles, packed and plain last tiles, two K chunks, skip ranges before,
+# inside and past the destinations
+_BATCHES = {
+    2: [(8, 24, 8, 8), (8, 23, 0, 0)],
+    3: [(8, 24, 0, 8), (8, 24, 8, 8), (5, 27, 16, 5)],
+    4: [(17, 40, 0, 0), (32, 9, 3, 2), (8, 16, 0, 0), (1, 5, 2, 30)],
+    5: [(8, 24, 0, 8), (8, 24, 8, 8), (17, 40, 0, 0), (5, 27, 16, 5),
+        (32, 9, 3, 2)],
+    9: [(8, 21, 8, 8)] * 6 + [(9, 33, 1, 1), (16, 8, 0, 0), (2, 17, 20, 4)],
+}
+
+
+@pytest.mark.parametrize("num_jobs", sorted(_BATCHES))
+def test_bconv_batch_job_counts(chd, num_jobs):
+    """chd_k_bconv_batch (the key switch's entry) against the oracle, each
+    job with its own sources, table, lengths and skip range; a batch of two
+    to four jobs takes the column-tile workgroup mapping, a larger one the
+    consecutive mapping, and both walk every destination tile of a job in
+    one workgroup"""
+    import torch
+    lib = chd.lib
+    P = ctypes.c_void_p
+    lib.chd_k_bconv_batch.argtypes = [P, P, P, ctypes.c_int, P]
+    lib.chd_bconv_table_size.restype = ctypes.c_longlong
+    lib.chd_bconv_table_pack.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int]
+    dst_q = Q31[:48]
+    qinv = np.array([pow(p, -1, 1 << 32) for p in dst_q], np.uint32)
+    dq = torch.from_numpy(np.array(dst_q, np.uint32).view(np.int32)).cuda()
+    dqi = torch.from_numpy(qinv.view(np.int32)).cuda()
+    tabs = _Tables(q=dq.data_ptr(), qinv=dqi.data_ptr())
+    lmap = _LimbMap(num_q=1 << 20)
+    r = rng(900 + num_jobs)
+    jobs, keep, want = (_BconvJob * num_jobs)(), [], []
+    for j, (src_len, dst_len, lo, ln) in enumerate(_BATCHES[num_jobs]):
+        pos = [k + (ln if k >= lo else 0) for k in range(dst_len)]
+        src_p = Q30[:src_len]
+        dst_p = [dst_q[p] for p in pos]
+        _, t2 = _orc.modswitch_consts(src_p, dst_p, 16)
+        x = centred_limbs(r, src_p)
+        x[:, :64] = np.array([(p - 1) // 2 for p in src_p], np.int32)[:, None]
+        size = lib.chd_bconv_table_size(src_len, dst_len)
+        packed = np.zeros(size, np.int8)
+        assert lib.chd_bconv_table_pack(
+            packed.ctypes.data, np.ascontiguousarray(t2, np.int32).ctypes.data,
+            np.array(dst_p, np.uint32).ctypes.data, src_len, dst_len) == 0
+        dtab = torch.from_numpy(packed).cuda()
+        dsrc = dev(x.view(np.uint32))
+        out = zeros(max(pos) + 1, N)
+        keep += [dtab, dsrc, out]
+        jobs[j] = _BconvJob(out.data_ptr(), dsrc.data_ptr(), dtab.data_ptr(),
+                            src_len, dst_len, lo, ln)
+        want.append((out, pos, _orc.bconv(x, t2, dst_p, 16)))
+    assert lib.chd_k_bconv_batch(ctypes.byref(tabs), ctypes.byref(lmap), jobs,
+                                 num_jobs, None) == 0
+    torch.cuda.synchronize()
+    for j, (out, pos, w) in enumerate(want):
+        got = host(out)
+        for k, p in enumerate(pos):
+            assert np.array_equal(got[p], w[k]), (num_jobs, j, k)
+
+
 # --------------------------------------------------- key-switch pipeline ----
 @pytest.fixture(scope="module")
 def ks(chd):
