@@ -72,14 +72,17 @@ def _msg(seed):
     return (r.uniform(-1, 1, SLOTS) + 1j * r.uniform(-1, 1, SLOTS))
 
 
-def test_hmult_merged_rescale_decrypts(sem):
+@pytest.mark.parametrize("level", [L - 1, 12, 2])
+def test_hmult_merged_rescale_decrypts(sem, level):
+    """BasicTest's HMult loops over the levels; here the top one, a middle
+    one and the lowest whose modulus (3 primes) holds the scale^2 product"""
     m1, m2 = _msg(1), _msg(2)
-    c1 = _encrypt(sem, m1, L - 1, DELTA)
-    c2 = _encrypt(sem, m2, L - 1, DELTA)
-    res = (zeros(L - 1, N), zeros(L - 1, N))
-    sem["ctx"].hmult(L - 1, res, c1, c2, *sem["mk"], rescale=True)
-    scale = DELTA * DELTA / sem["main"][L - 1]
-    got = _decrypt(sem, res, L - 2, scale)
+    c1 = _encrypt(sem, m1, level, DELTA)
+    c2 = _encrypt(sem, m2, level, DELTA)
+    res = (zeros(level, N), zeros(level, N))
+    sem["ctx"].hmult(level, res, c1, c2, *sem["mk"], rescale=True)
+    scale = DELTA * DELTA / sem["main"][level]
+    got = _decrypt(sem, res, level - 1, scale)
     assert np.max(np.abs(got - m1 * m2)) < 1e-3
 
 
