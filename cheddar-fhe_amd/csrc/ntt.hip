@@ -374,11 +374,6 @@ struct Arith<false> {
   }
 };
 
-// signed (-q, q) value of a policy value (for epilogue arithmetic)
-__device__ __forceinline__ int32_t to_signed_canon(uint32_t canon) {
-  return static_cast<int32_t>(canon);
-}
-
 // ------------------------------------------------------------------------
 // Kernel skeleton: each kernel decodes its limb, issues the data loads of the
 // whole tile first (they depend on kernel arguments only), then reads the

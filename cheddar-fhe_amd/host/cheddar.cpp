@@ -712,9 +712,11 @@ ModSwitchHandler<uint32_t>::ModSwitchHandler(
       first_group_(prime_offset_ / param.alpha_),
       group_shift_(prime_offset_ % param.alpha_),
       param_(param),
-      elem_(elem),
       ntt_(ntt),
       ws_(ws) {
+  // the reference's constructor also takes the element-wise handler; this
+  // one keeps none of its state
+  (void)elem;
   const NPInfo np = param_.LevelToNP(level_, num_aux_);
   const int num_q = np.GetNumQ();
   const std::vector<word> lp = param_.GetPrimeVector(np);
@@ -2620,12 +2622,9 @@ LinearTransform<uint32_t>::LinearTransform(ConstContextPtr<word> context,
                                            int pt_level, double pt_scale,
                                            int bs, int gs, int pre_rotation,
                                            int additional_pt_rot)
-    : pt_level_(pt_level),
-      pt_scale_(pt_scale),
-      bs_(bs),
+    : bs_(bs),
       gs_(gs),
       pre_rotation_(pre_rotation),
-      additional_pt_rot_(additional_pt_rot),
       hoist_(context,
              ConstructPlainHoistMap(matrix, bs, gs, pre_rotation,
                                     additional_pt_rot),

@@ -677,7 +677,6 @@ class ModSwitchHandler<uint32_t> {
   const int beta_;
   const int prime_offset_, first_group_, group_shift_;
   const Parameter<word> &param_;
-  const ElementWiseHandler<word> &elem_;
   const NTTHandler<word> &ntt_;
   Workspace *ws_;
   DeviceVector<word> mod_up1_;
@@ -1035,9 +1034,7 @@ class LinearTransform<uint32_t> {
  private:
   static int DetermineStride(const StripedMatrix &matrix, int bs, int gs,
                              int pre_rotation);
-  int pt_level_;
-  double pt_scale_;
-  int bs_, gs_, pre_rotation_, additional_pt_rot_;
+  int bs_, gs_, pre_rotation_;
   HoistHandler<word> hoist_;
 };
 

@@ -30,7 +30,7 @@ void DevBuf::Release() {
 
 // twiddle tables as in NTTHandler::PopulateTwiddleFactors (NTT.cu:1233-1299)
 ChainTables::ChainTables(int log_degree, const std::vector<uint32_t> &primes)
-    : log_degree_(log_degree), primes_(primes) {
+    : primes_(primes) {
   if (log_degree != 16)
     throw std::invalid_argument("only log_degree 16 is supported");
   const int n = 1 << log_degree;

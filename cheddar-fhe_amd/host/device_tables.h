@@ -70,7 +70,6 @@ class ChainTables {
   const uint32_t *mont_converter() const { return r2_.as<uint32_t>(); }
 
  private:
-  int log_degree_;
   std::vector<uint32_t> primes_;
   DevBuf q_, qinv_, tw_, itw_, twist_;
   DevBuf ninv_, ninv_mont_, r2_;
